@@ -1,0 +1,142 @@
+/*
+ * zw_gpu.h — C ABI of the MI355X (gfx950) attention library for zwhisper.
+ *
+ * It replaces the bodies of zwhisper's `ops.attentionEx` (src/ops.zig:562-590) and
+ * `ops.attention` (src/ops.zig:593-605).  Those Zig functions keep their signatures; their
+ * bodies call the entry points below (the Zig binding is spelt out in INTEGRATION.md).
+ * The whisper C ABI (include/zwhisper.h) is untouched: attention is internal to it.
+ *
+ * Conventions (those of include/zwhisper.h:34-42):
+ *   - every function returning int gives ZWG_OK (0) on success, ZWG_ERROR (2) on failure;
+ *     zwg_last_error() then says why.  No C++ exception crosses this boundary.
+ *   - the caller owns every buffer it passes; a context owns its stream and device workspace
+ *     and frees them in zwg_close().
+ *   - one context per host thread; calls on one context are not thread-safe
+ *     (as the zw_* handles, src/capi.zig:3-4).
+ *
+ * Arithmetic is f32 throughout (fp32 MFMA for the dense kernel, f32 FMA for the streaming
+ * decode kernel); results match the reference's f32 attention within max abs 2e-4.
+ */
+#ifndef ZW_GPU_H
+#define ZW_GPU_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ZWG_OK 0
+#define ZWG_ERROR 2
+#define ZWG_VERSION 1
+
+typedef struct zwg_ctx zwg_ctx;
+
+/*
+ * Mirror of ops.AttnShape (src/ops.zig:477-492), field for field.  Query head h reads key/value
+ * head h / (n_head / n_head_kv).  Strides are in floats.  kt_stride == 0 stands for Zig's
+ * `null`: k is row-major [n_kv][kv_stride] like v.  kt_stride > 0: k is transposed,
+ * [n_head_kv][d][kt_stride] (keys along the last axis, as the LLM's cache, src/llm.zig:27).
+ * causal: query i sees keys j <= n_kv - n_q + i (src/ops.zig:466), so n_kv >= n_q is required.
+ *
+ * Limits of this build (checked; ZWG_ERROR otherwise): d in {32, 64, 128}; q_stride, kv_stride,
+ * out_stride and kt_stride multiples of 4; q, k, v, out 16-byte aligned; every count < 2^31.
+ * Device buffers: with kt_stride, the last transposed row is read in 16-byte groups, so k must
+ * hold (n_head_kv*d - 1)*kt_stride + round_up(n_kv, 4) floats -- no more than the reference
+ * itself reads (round_up(n_kv, V) columns of every row, src/ops.zig:529-530).
+ */
+typedef struct zwg_attn_shape {
+    uint64_t n_q;
+    uint64_t n_kv;
+    uint64_t n_head;
+    uint64_t n_head_kv;
+    uint64_t d;
+    uint64_t q_stride;
+    uint64_t kv_stride;
+    uint64_t out_stride;
+    uint64_t kt_stride;
+    uint32_t causal;
+    uint32_t reserved; /* must be 0 */
+} zwg_attn_shape;
+
+/*
+ * A batch of independent attention problems of one shape, laid out at fixed strides (in floats)
+ * from the base pointers: item b uses q + b*q_bstride, k + b*k_bstride, v + b*v_bstride,
+ * out + b*out_bstride.  n_kv_dev, if not NULL, is a device array of n_batch int32 key counts
+ * (each 0 <= n_kv_dev[b] <= shape.n_kv, the capacity): per-item cache lengths, as the decoder
+ * windows or LLM sequences of one step have.  Causal items need n_kv_dev[b] >= n_q.
+ */
+typedef struct zwg_batch {
+    uint64_t n_batch;
+    uint64_t q_bstride;
+    uint64_t k_bstride;
+    uint64_t v_bstride;
+    uint64_t out_bstride;
+    const int32_t *n_kv_dev;
+} zwg_batch;
+
+/* Sizes fixed when a context opens.  Zero fields take the defaults. */
+typedef struct zwg_limits {
+    uint64_t workspace_bytes; /* device memory for split-KV partial results; default 256 MiB */
+} zwg_limits;
+
+/* How a call will run (zwg_plan): which kernel, how the keys are split. */
+typedef struct zwg_plan_info {
+    uint32_t kernel;        /* 1 = dense MFMA flash kernel, 2 = split-K streaming decode kernel */
+    uint32_t rows_per_unit; /* query rows one work unit covers (q-block, or heads x queries) */
+    uint64_t chunk_len;     /* keys per split (a multiple of the kernel's key tile) */
+    uint64_t max_chunks;    /* splits of the longest row; 1 = no combine pass */
+    uint64_t grid_blocks;   /* workgroups launched by the main kernel */
+    uint64_t workspace_bytes; /* partial results the call writes (0 when max_chunks == 1) */
+} zwg_plan_info;
+
+/* Open a context on HIP device `device` (limits may be NULL).  *out is NULL on failure. */
+int zwg_open(int device, const zwg_limits *limits, zwg_ctx **out);
+void zwg_close(zwg_ctx *ctx);
+
+/* Why the last call on ctx failed; with ctx == NULL, the last failure on this thread. */
+const char *zwg_last_error(const zwg_ctx *ctx);
+
+/* Run on a caller's hipStream_t (NULL: the context's own stream) / the stream in use. */
+int zwg_set_stream(zwg_ctx *ctx, void *hip_stream);
+void *zwg_get_stream(const zwg_ctx *ctx);
+/* Wait for all work queued on the context's stream. */
+int zwg_sync(zwg_ctx *ctx);
+
+/*
+ * Drop-in for ops.attentionEx (src/ops.zig:562): host pointers, synchronous — `out` holds the
+ * result on return, and only each query row's n_head*d columns are written, as in the
+ * reference.  Stages q/k/v through device buffers the context keeps (grown on first need).
+ */
+int zwg_attention_ex(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_attn_shape *shape,
+                     float *out);
+
+/* Drop-in for ops.attention (src/ops.zig:593): n_head_kv = n_head, d = n_state / n_head,
+ * all strides n_state, row-major K. */
+int zwg_attention(zwg_ctx *ctx, const float *q, const float *k, const float *v, uint64_t n_q, uint64_t n_kv,
+                  uint64_t n_state, uint64_t n_head, int causal, float *out);
+
+/* Device pointers (inputs already in HBM): queued on the context's stream, asynchronous. */
+int zwg_attention_dev(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_attn_shape *shape,
+                      float *out);
+
+/* A batch of problems (see zwg_batch), device pointers, asynchronous. */
+int zwg_attention_batch_dev(zwg_ctx *ctx, const float *q, const float *k, const float *v,
+                            const zwg_attn_shape *shape, const zwg_batch *batch, float *out);
+
+/*
+ * The plan a call with this shape and batch (NULL = one item) would use, for a context opened
+ * with `workspace_bytes` of workspace (0 = default).  Host-only: needs no device.
+ */
+int zwg_plan(const zwg_attn_shape *shape, const zwg_batch *batch, uint64_t workspace_bytes, zwg_plan_info *out);
+
+/* Shape check alone (same rules as the calls), host-only.  0 ok, 2 with a message. */
+int zwg_check_shape(const zwg_attn_shape *shape, char *msg, size_t msg_len);
+
+int zwg_version(void); /* ZWG_VERSION */
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ZW_GPU_H */

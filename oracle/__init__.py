@@ -1,0 +1,205 @@
+"""The CPU oracle for zwhisper's attention hot path — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package,
+and only as the checker (or, in bench.py, as the timed CPU baseline).  The product — the HIP
+library under zwhisper_amd/ — never imports, links or calls anything here.
+
+Contents:
+* ``Oracle``: ctypes front end to liboracle_v{3,4}.so, the C restatement of the reference's
+  ops.attentionEx / attention / pvBlock / expVec / softmaxRow / Pool (oracle/attn_oracle.c,
+  which cites src/ops.zig and src/gemm.zig line by line).
+* ``naive``: the f64 closed form (oracle/naive.py).
+
+Parity pinning of each function lives in tests/test_oracle.py.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+from . import naive  # noqa: F401
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_c_size = ctypes.c_size_t
+_fp = ctypes.POINTER(ctypes.c_float)
+
+V = 16
+Q_BLOCK = 64
+
+
+class OraShape(ctypes.Structure):
+    """Mirror of AttnShape (src/ops.zig:477-492); kt_stride 0 stands for null."""
+
+    _fields_ = [
+        ("n_q", ctypes.c_uint64),
+        ("n_kv", ctypes.c_uint64),
+        ("n_head", ctypes.c_uint64),
+        ("n_head_kv", ctypes.c_uint64),
+        ("d", ctypes.c_uint64),
+        ("q_stride", ctypes.c_uint64),
+        ("kv_stride", ctypes.c_uint64),
+        ("out_stride", ctypes.c_uint64),
+        ("kt_stride", ctypes.c_uint64),
+        ("causal", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+    ]
+
+
+def _host_has_avx512() -> bool:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("flags"):
+                    flags = set(line.split(":", 1)[1].split())
+                    return {"avx512f", "avx512bw", "avx512cd", "avx512dq", "avx512vl"} <= flags
+    except OSError:
+        pass
+    return False
+
+
+def build() -> None:
+    """Compile liboracle_v3.so / liboracle_v4.so from attn_oracle.c (oracle/Makefile)."""
+    subprocess.run(["make", "-s", "-C", _HERE, "-j2"], check=True)
+
+
+def library_path() -> str:
+    return os.path.join(_HERE, "liboracle_v4.so" if _host_has_avx512() else "liboracle_v3.so")
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        path = library_path()
+        if not os.path.exists(path):
+            build()
+        L = ctypes.CDLL(path)
+        L.ora_pool_new.restype = ctypes.c_void_p
+        L.ora_pool_new.argtypes = [_c_size]
+        L.ora_pool_free.argtypes = [ctypes.c_void_p]
+        L.ora_pool_size.restype = _c_size
+        L.ora_pool_size.argtypes = [ctypes.c_void_p]
+        L.ora_attention_ex.restype = ctypes.c_int
+        L.ora_attention_ex.argtypes = [ctypes.c_void_p, _fp, _fp, _fp, ctypes.POINTER(OraShape), _fp, _c_size, _fp]
+        L.ora_attention.restype = ctypes.c_int
+        L.ora_attention.argtypes = [ctypes.c_void_p, _fp, _fp, _fp, _c_size, _c_size, _c_size, _c_size, ctypes.c_int,
+                                    _fp, _c_size, _fp]
+        for name in ("ora_attention_scratch_ex",):
+            getattr(L, name).restype = _c_size
+            getattr(L, name).argtypes = [_c_size] * 5
+        L.ora_attention_scratch_kt.restype = _c_size
+        L.ora_attention_scratch_kt.argtypes = [_c_size] * 3
+        L.ora_attention_scratch.restype = _c_size
+        L.ora_attention_scratch.argtypes = [_c_size] * 4
+        L.ora_exp_vec.argtypes = [_fp, _fp, _c_size]
+        L.ora_softmax_row.argtypes = [_fp, _c_size]
+        L.ora_pv_block.argtypes = [_fp, _c_size, _fp, _c_size, _fp, _c_size, _c_size, _c_size, _c_size]
+        L.ora_vector_width.restype = ctypes.c_int
+        L.ora_q_block.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _ptr(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(_fp)
+
+
+def to_ora_shape(sh) -> OraShape:
+    return OraShape(sh.n_q, sh.n_kv, sh.n_head, sh.n_head_kv, sh.d, sh.q_stride, sh.kv_stride, sh.out_stride,
+                    sh.kt_stride or 0, 1 if sh.causal else 0, 0)
+
+
+def scratch_floats(sh) -> int:
+    L = lib()
+    if sh.kt_stride:
+        return int(L.ora_attention_scratch_kt(sh.n_q, sh.kt_stride, sh.n_head))
+    return int(L.ora_attention_scratch_ex(sh.n_q, sh.n_kv, sh.n_head, sh.n_head_kv, sh.d))
+
+
+class Oracle:
+    """The reference's multithreaded f32 attention, restated in C, with its own Pool."""
+
+    def __init__(self, threads: int = 1):
+        self._L = lib()
+        self._pool = self._L.ora_pool_new(max(1, int(threads)))
+        self.threads = int(self._L.ora_pool_size(self._pool))
+
+    def close(self) -> None:
+        if self._pool:
+            self._L.ora_pool_free(self._pool)
+            self._pool = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def attention_ex(self, q, k, v, sh, out=None, scratch=None) -> np.ndarray:
+        """ops.attentionEx on numpy f32 buffers; returns out (flat, [n_q][out_stride])."""
+        q = np.ascontiguousarray(q, dtype=np.float32).reshape(-1)
+        k = np.ascontiguousarray(k, dtype=np.float32).reshape(-1)
+        v = np.ascontiguousarray(v, dtype=np.float32).reshape(-1)
+        n_out = (sh.n_q - 1) * sh.out_stride + sh.n_head * sh.d if sh.n_q else 0
+        if out is None:
+            out = np.zeros(max(n_out, 1), dtype=np.float32)
+        if scratch is None:
+            scratch = np.empty(max(scratch_floats(sh), 1), dtype=np.float32)
+        shape = to_ora_shape(sh)
+        rc = self._L.ora_attention_ex(self._pool, _ptr(q), _ptr(k), _ptr(v), ctypes.byref(shape), _ptr(scratch),
+                                      scratch.size, _ptr(out))
+        if rc != 0:
+            raise ValueError(f"oracle rejected shape {sh}")
+        return out
+
+    def attention(self, q, k, v, n_q, n_kv, n_state, n_head, causal, out=None) -> np.ndarray:
+        """ops.attention (src/ops.zig:593-605)."""
+        q = np.ascontiguousarray(q, dtype=np.float32).reshape(-1)
+        k = np.ascontiguousarray(k, dtype=np.float32).reshape(-1)
+        v = np.ascontiguousarray(v, dtype=np.float32).reshape(-1)
+        if out is None:
+            out = np.zeros(max(n_q * n_state, 1), dtype=np.float32)
+        scratch = np.empty(max(int(self._L.ora_attention_scratch(n_q, n_kv, n_head, n_state)), 1), dtype=np.float32)
+        rc = self._L.ora_attention(self._pool, _ptr(q), _ptr(k), _ptr(v), n_q, n_kv, n_state, n_head,
+                                   1 if causal else 0, _ptr(scratch), scratch.size, _ptr(out))
+        if rc != 0:
+            raise ValueError("oracle rejected shape")
+        return out
+
+
+def exp_vec(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    assert x.size % V == 0
+    y = np.empty_like(x)
+    lib().ora_exp_vec(_ptr(x), _ptr(y), x.size)
+    return y
+
+
+def softmax_row(x: np.ndarray) -> np.ndarray:
+    y = np.ascontiguousarray(x, dtype=np.float32).copy()
+    lib().ora_softmax_row(_ptr(y), y.size)
+    return y
+
+
+def pv_block(p: np.ndarray, v: np.ndarray) -> np.ndarray:
+    """C[m][d] = P[m][t] . V[t][d] (gemm.pvBlock)."""
+    p = np.ascontiguousarray(p, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    m, t = p.shape
+    t2, d = v.shape
+    assert t == t2 and d % V == 0
+    c = np.empty((m, d), dtype=np.float32)
+    lib().ora_pv_block(_ptr(p), t, _ptr(v), d, _ptr(c), d, m, t, d)
+    return c

@@ -1,0 +1,123 @@
+"""ctypes binding of include/zw_gpu.h (libzwgpu.so, built in-tree by zwhisper_amd/build.py).
+
+Loading fails loudly when the library has not been built: there is no fallback path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(PKG)
+LIB_PATH = os.path.join(PKG, "libzwgpu.so")
+HEADER = os.path.join(ROOT, "include", "zw_gpu.h")
+
+ZWG_OK = 0
+ZWG_ERROR = 2
+
+_u64 = ctypes.c_uint64
+_fp = ctypes.c_void_p  # device or host float pointers travel as addresses
+
+
+class ZwgError(RuntimeError):
+    """A call into the library returned ZWG_ERROR (the message is zwg_last_error)."""
+
+
+class ShapeC(ctypes.Structure):
+    _fields_ = [
+        ("n_q", _u64),
+        ("n_kv", _u64),
+        ("n_head", _u64),
+        ("n_head_kv", _u64),
+        ("d", _u64),
+        ("q_stride", _u64),
+        ("kv_stride", _u64),
+        ("out_stride", _u64),
+        ("kt_stride", _u64),
+        ("causal", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+    ]
+
+
+class BatchC(ctypes.Structure):
+    _fields_ = [
+        ("n_batch", _u64),
+        ("q_bstride", _u64),
+        ("k_bstride", _u64),
+        ("v_bstride", _u64),
+        ("out_bstride", _u64),
+        ("n_kv_dev", ctypes.c_void_p),
+    ]
+
+
+class LimitsC(ctypes.Structure):
+    _fields_ = [("workspace_bytes", _u64)]
+
+
+class PlanC(ctypes.Structure):
+    _fields_ = [
+        ("kernel", ctypes.c_uint32),
+        ("rows_per_unit", ctypes.c_uint32),
+        ("chunk_len", _u64),
+        ("max_chunks", _u64),
+        ("grid_blocks", _u64),
+        ("workspace_bytes", _u64),
+    ]
+
+
+def declared_symbols() -> list[str]:
+    """Every function the C header declares."""
+    with open(HEADER) as f:
+        text = f.read()
+    return sorted(set(re.findall(r"\b(zwg_[a-z_0-9]+)\s*\(", text)))
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built; run `python -m zwhisper_amd.build` (hipcc, gfx950)")
+    L = ctypes.CDLL(LIB_PATH)
+    c_int, vp = ctypes.c_int, ctypes.c_void_p
+    L.zwg_version.restype = c_int
+    L.zwg_last_error.restype = ctypes.c_char_p
+    L.zwg_last_error.argtypes = [vp]
+    L.zwg_open.restype = c_int
+    L.zwg_open.argtypes = [c_int, ctypes.POINTER(LimitsC), ctypes.POINTER(vp)]
+    L.zwg_close.restype = None
+    L.zwg_close.argtypes = [vp]
+    L.zwg_set_stream.restype = c_int
+    L.zwg_set_stream.argtypes = [vp, vp]
+    L.zwg_get_stream.restype = vp
+    L.zwg_get_stream.argtypes = [vp]
+    L.zwg_sync.restype = c_int
+    L.zwg_sync.argtypes = [vp]
+    L.zwg_attention_ex.restype = c_int
+    L.zwg_attention_ex.argtypes = [vp, _fp, _fp, _fp, ctypes.POINTER(ShapeC), _fp]
+    L.zwg_attention.restype = c_int
+    L.zwg_attention.argtypes = [vp, _fp, _fp, _fp, _u64, _u64, _u64, _u64, c_int, _fp]
+    L.zwg_attention_dev.restype = c_int
+    L.zwg_attention_dev.argtypes = [vp, _fp, _fp, _fp, ctypes.POINTER(ShapeC), _fp]
+    L.zwg_attention_batch_dev.restype = c_int
+    L.zwg_attention_batch_dev.argtypes = [vp, _fp, _fp, _fp, ctypes.POINTER(ShapeC), ctypes.POINTER(BatchC), _fp]
+    L.zwg_plan.restype = c_int
+    L.zwg_plan.argtypes = [ctypes.POINTER(ShapeC), ctypes.POINTER(BatchC), _u64, ctypes.POINTER(PlanC)]
+    L.zwg_check_shape.restype = c_int
+    L.zwg_check_shape.argtypes = [ctypes.POINTER(ShapeC), ctypes.c_char_p, ctypes.c_size_t]
+    _lib = L
+    return L
+
+
+def last_error(ctx=None) -> str:
+    msg = lib().zwg_last_error(ctx)
+    return msg.decode() if msg else ""
+
+
+def check(rc: int, ctx=None) -> None:
+    if rc != ZWG_OK:
+        raise ZwgError(last_error(ctx))

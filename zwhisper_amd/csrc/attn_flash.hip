@@ -1,0 +1,314 @@
+// Dense attention on gfx950 fp32 MFMA: one workgroup = 4 waves x 32 query rows of one head,
+// streaming 32-key tiles of K and V through LDS, online softmax in registers.
+//
+// Replaces the per-(head, 64-row q-block) task of the reference (AttnJob.run,
+// src/ops.zig:517-541: S = Q.KT by broadcast FMA, scale, causal limit, softmaxRow, O = S.V)
+// without materialising S: each wave keeps its 32x32 score tile in MFMA accumulators.
+//
+// Layout trick.  The wave computes S^T = K . Q^T with v_mfma_f32_32x32x2_f32 (M = keys,
+// N = queries, K = head dims).  Its accumulator register r of lane l holds
+// S^T[8*(r/4) + 4*(l/32) + r%4][l%32]: query l%32, a key picked by (r, l/32).  That is exactly
+// the B-operand layout of the next product O^T = V^T . P^T (K = keys) if the MFMA at step r
+// contracts key 8*(r/4) + 4*(l/32) + r%4 for lane half l/32 -- so the exponentiated scores feed
+// the P.V MFMA straight from registers, and only the V^T operand is read in that key order
+// (from an LDS tile stored transposed, four consecutive keys per 16-byte read).
+// The QK contraction is order-free as well: lane half h contracts dims h*D/2 + s at step s,
+// so each lane reads D/2 contiguous floats of its key row and keeps D/2 query values in VGPRs.
+//
+// Scores are pre-scaled by f32(1/sqrt(d)) * log2(e) (folded into Q) so softmax uses exp2.
+#include "attn_kernels.hpp"
+
+namespace zwg {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+static __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <int D, bool KT>
+__global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
+    constexpr int BM = kFlashBM;
+    constexpr int BN = kFlashBN;
+    constexpr int HD = D / 2;   // dims per lane half in the QK contraction
+    constexpr int KS = D + 4;   // LDS row stride of the K tile [key][dim]
+    constexpr int VS = BN + 4;  // LDS row stride of the V^T tile [dim][key]
+    constexpr int NDB = D / 32; // 32-dim output tiles
+    constexpr int LD = BN * D / 4 / 256; // float4 loads per thread per tile, per tensor
+    static_assert(LD >= 1, "tile too small for the workgroup");
+
+    __shared__ __align__(16) float Ks[2][BN * KS];
+    __shared__ __align__(16) float Vt[2][D * VS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int col = lane & 31;
+    const int half = lane >> 5;
+
+    const int chunk = blockIdx.x;
+    const int qb = blockIdx.y;
+    const int item = blockIdx.z / a.n_head;
+    const int head = blockIdx.z - item * a.n_head;
+    const int hk = head / a.group;
+
+    const int n_q = a.n_q;
+    const int n_kv = item_kv(a, item);
+    const int q_first = qb * BM;
+    const int q_end_blk = min(q_first + BM, n_q);
+    const int kv_hi = a.causal ? max(0, n_kv - n_q + q_end_blk) : n_kv;
+    const int n_chunks = max(1, (kv_hi + a.chunk_len - 1) / a.chunk_len);
+    if (chunk >= n_chunks) return;
+    const int k_begin = chunk * a.chunk_len;
+    const int k_end = min(kv_hi, k_begin + a.chunk_len);
+
+    const float *qp = a.q + item * a.q_bstride + head * D;
+    const float *kp = a.k + item * a.k_bstride + (KT ? (int64_t)hk * D * a.kt_stride : (int64_t)hk * D);
+    const float *vp = a.v + item * a.v_bstride + hk * D;
+
+    // This lane's query row and the wave's key window.
+    const int q_wave = q_first + wave * 32;
+    const int query = q_wave + col;
+    const bool q_valid = query < n_q;
+    const bool wave_active = q_wave < n_q;
+    const int q_wave_last = min(q_wave + 31, n_q - 1);
+    const int diag = n_kv - n_q; // query i sees keys j <= diag + i
+    // keys the wave needs at all (exclusive), and keys every query of the wave sees
+    const int wave_hi = min(k_end, a.causal ? diag + q_wave_last + 1 : n_kv);
+    const int wave_full = min(k_end, a.causal ? diag + q_wave + 1 : n_kv);
+
+    float qreg[HD];
+    if (q_valid) {
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(qp + (int64_t)query * a.q_stride + half * HD);
+#pragma unroll
+        for (int i = 0; i < HD / 4; ++i) {
+            const f32x4 t = src[i];
+            qreg[4 * i + 0] = t[0] * a.scale_log2;
+            qreg[4 * i + 1] = t[1] * a.scale_log2;
+            qreg[4 * i + 2] = t[2] * a.scale_log2;
+            qreg[4 * i + 3] = t[3] * a.scale_log2;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < HD; ++i) qreg[i] = 0.f;
+    }
+
+    f32x16 o[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) o[db] = (f32x16){0};
+    float m_run = -INFINITY;
+    float l_run = 0.f;
+
+    f32x4 kr[LD], vr[LD];
+    auto load_tile = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < LD; ++i) {
+            const int f = tid + 256 * i;
+            if (KT) {
+                const int dim = f / (BN / 4);
+                const int gk = k0 + 4 * (f % (BN / 4));
+                kr[i] = gk < n_kv ? *reinterpret_cast<const f32x4 *>(kp + (int64_t)dim * a.kt_stride + gk)
+                                  : (f32x4){0};
+            } else {
+                const int gk = k0 + f / (D / 4);
+                kr[i] = gk < n_kv ? *reinterpret_cast<const f32x4 *>(kp + (int64_t)gk * a.kv_stride + 4 * (f % (D / 4)))
+                                  : (f32x4){0};
+            }
+            const int gv = k0 + f / (D / 4);
+            vr[i] = gv < n_kv ? *reinterpret_cast<const f32x4 *>(vp + (int64_t)gv * a.kv_stride + 4 * (f % (D / 4)))
+                              : (f32x4){0};
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < LD; ++i) {
+            const int f = tid + 256 * i;
+            if (KT) {
+                const int dim = f / (BN / 4);
+                const int key = 4 * (f % (BN / 4));
+#pragma unroll
+                for (int j = 0; j < 4; ++j) Ks[buf][(key + j) * KS + dim] = kr[i][j];
+            } else {
+                const int key = f / (D / 4);
+                *reinterpret_cast<f32x4 *>(&Ks[buf][key * KS + 4 * (f % (D / 4))]) = kr[i];
+            }
+            const int key = f / (D / 4);
+            const int dim = 4 * (f % (D / 4));
+#pragma unroll
+            for (int j = 0; j < 4; ++j) Vt[buf][(dim + j) * VS + key] = vr[i][j];
+        }
+    };
+
+    const int n_tiles = k_end > k_begin ? (k_end - k_begin + BN - 1) / BN : 0;
+    if (n_tiles > 0) {
+        load_tile(k_begin);
+        store_tile(0);
+    }
+    __syncthreads();
+
+    for (int t = 0; t < n_tiles; ++t) {
+        const int buf = t & 1;
+        const int k0 = k_begin + t * BN;
+        if (t + 1 < n_tiles) load_tile(k0 + BN);
+
+        if (wave_active && k0 < wave_hi) {
+            // S^T tile = K . Q^T  (32 keys x 32 queries)
+            f32x16 s = (f32x16){0};
+            const float *krow = &Ks[buf][col * KS + half * HD];
+#pragma unroll
+            for (int j = 0; j < HD; j += 4) {
+                const f32x4 kk = *reinterpret_cast<const f32x4 *>(krow + j);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[0], qreg[j + 0], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[1], qreg[j + 1], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[2], qreg[j + 2], s, 0, 0, 0);
+                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[3], qreg[j + 3], s, 0, 0, 0);
+            }
+            // mask keys past the chunk end or past this query's causal limit
+            if (k0 + BN > wave_full) {
+                const int lim = min(k_end, a.causal ? diag + query + 1 : n_kv);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = k0 + 8 * (r >> 2) + 4 * half + (r & 3);
+                    s[r] = key < lim ? s[r] : -INFINITY;
+                }
+            }
+            // online softmax over keys: this lane holds 16 of the query's 32 keys, the
+            // partner lane (l ^ 32) the other 16
+            float mt = s[0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            const float m_new = fmaxf(m_run, mt);
+            const float m_use = m_new == -INFINITY ? 0.f : m_new;
+            const float alpha = exp2_fast(m_run - m_use);
+            float ls = 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                s[r] = exp2_fast(s[r] - m_use);
+                ls += s[r];
+            }
+            l_run = l_run * alpha + ls;
+            m_run = m_new;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+            // O^T += V^T . P^T
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+                const float *vrow = &Vt[buf][(db * 32 + col) * VS + 4 * half];
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x4 vv = *reinterpret_cast<const f32x4 *>(vrow + 8 * g);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[0], s[4 * g + 0], o[db], 0, 0, 0);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[1], s[4 * g + 1], o[db], 0, 0, 0);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[2], s[4 * g + 2], o[db], 0, 0, 0);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[3], s[4 * g + 3], o[db], 0, 0, 0);
+                }
+            }
+        }
+        if (t + 1 < n_tiles) store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    if (!q_valid) return;
+    // lane holds dims db*32 + 8*g + 4*half + {0..3} in registers 4g..4g+3 of o[db]
+    if (a.max_chunks == 1) {
+        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+        float *op = a.out + item * a.out_bstride + (int64_t)query * a.out_stride + head * D;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                f32x4 w = {o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv};
+                *reinterpret_cast<f32x4 *>(op + db * 32 + 8 * g + 4 * half) = w;
+            }
+    } else {
+        const int64_t slot = row_index(a, item, head, query) * a.max_chunks + chunk;
+        float *po = a.part_o + slot * D;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                f32x4 w = {o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2], o[db][4 * g + 3]};
+                *reinterpret_cast<f32x4 *>(po + db * 32 + 8 * g + 4 * half) = w;
+            }
+        if (half == 0) {
+            a.part_ml[2 * slot] = m_run;
+            a.part_ml[2 * slot + 1] = l_tot;
+        }
+    }
+}
+
+// Merge the split-KV partials of each row: out = sum_c 2^(m_c - M) o_c / sum_c 2^(m_c - M) l_c.
+// One wave per row; lane covers dims lane, lane + 64 (D = 128).
+template <int D>
+__global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t n_rows = (int64_t)a.n_batch * a.n_head * a.n_q;
+    if (row >= n_rows) return;
+    const int query = (int)(row % a.n_q);
+    const int64_t ih = row / a.n_q;
+    const int head = (int)(ih % a.n_head);
+    const int item = (int)(ih / a.n_head);
+    const int n_kv = item_kv(a, item);
+    const int q_end = min((query / a.rows_per_unit + 1) * a.rows_per_unit, a.n_q);
+    const int kv_hi = a.causal ? max(0, n_kv - a.n_q + q_end) : n_kv;
+    const int n_chunks = max(1, (kv_hi + a.chunk_len - 1) / a.chunk_len);
+
+    const float *ml = a.part_ml + row * a.max_chunks * 2;
+    const float *po = a.part_o + row * a.max_chunks * D;
+    float M = -INFINITY;
+    for (int c = 0; c < n_chunks; ++c) M = fmaxf(M, ml[2 * c]);
+    float L = 0.f;
+    float acc0 = 0.f, acc1 = 0.f;
+    if (M != -INFINITY) {
+        for (int c = 0; c < n_chunks; ++c) {
+            const float m = ml[2 * c];
+            const float w = m == -INFINITY ? 0.f : exp2_fast(m - M);
+            L += w * ml[2 * c + 1];
+            if (lane < D) acc0 += w * po[c * D + lane];
+            if (D > 64) acc1 += w * po[c * D + 64 + lane];
+        }
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    float *op = a.out + item * a.out_bstride + (int64_t)query * a.out_stride + head * D;
+    if (lane < D) op[lane] = acc0 * inv;
+    if (D > 64) op[64 + lane] = acc1 * inv;
+}
+
+hipError_t launch_flash(const AttnArgs &a, int d, hipStream_t stream, int *grid_blocks) {
+    const int n_qblocks = (a.n_q + kFlashBM - 1) / kFlashBM;
+    const int max_chunks = a.max_chunks;
+    dim3 grid(max_chunks, n_qblocks, a.n_batch * a.n_head);
+    dim3 block(256);
+    if (grid_blocks) *grid_blocks = (int)(grid.x * grid.y * grid.z);
+    const bool kt = a.kt_stride != 0;
+#define ZWG_FLASH(DD)                                                                                            \
+    if (kt)                                                                                                      \
+        flash_attn_kernel<DD, true><<<grid, block, 0, stream>>>(a);                                              \
+    else                                                                                                         \
+        flash_attn_kernel<DD, false><<<grid, block, 0, stream>>>(a);
+    switch (d) {
+    case 32: ZWG_FLASH(32) break;
+    case 64: ZWG_FLASH(64) break;
+    case 128: ZWG_FLASH(128) break;
+    default: return hipErrorInvalidValue;
+    }
+#undef ZWG_FLASH
+    return hipGetLastError();
+}
+
+hipError_t launch_combine(const AttnArgs &a, int d, hipStream_t stream) {
+    const int64_t n_rows = (int64_t)a.n_batch * a.n_head * a.n_q;
+    dim3 grid((unsigned)((n_rows + 3) / 4));
+    dim3 block(256);
+    switch (d) {
+    case 32: combine_kernel<32><<<grid, block, 0, stream>>>(a); break;
+    case 64: combine_kernel<64><<<grid, block, 0, stream>>>(a); break;
+    case 128: combine_kernel<128><<<grid, block, 0, stream>>>(a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+} // namespace zwg

@@ -1,0 +1,58 @@
+// Kernel arguments and launch entry points shared by the host layer (zw_gpu.hip) and the
+// kernels (attn_flash.hip, attn_decode.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace zwg {
+
+// Everything a kernel needs for one call, passed by value.  Counts are int32 (checked on
+// the host), strides int64, all in floats.
+struct AttnArgs {
+    const float *q;
+    const float *k;
+    const float *v;
+    float *out;
+    int64_t q_stride, kv_stride, out_stride, kt_stride; // kt_stride 0: row-major K
+    int64_t q_bstride, k_bstride, v_bstride, out_bstride;
+    const int32_t *n_kv_item; // per-item key counts, or nullptr (then n_kv for all)
+    int32_t n_q, n_kv, n_head, n_head_kv, group; // group = n_head / n_head_kv
+    int32_t n_batch;
+    int32_t causal;
+    float scale_log2; // f32(1/sqrt(d)) * log2(e): scores go straight into exp2
+    // split-KV
+    int32_t chunk_len;  // keys per split, a multiple of the kernel's key tile
+    int32_t max_chunks; // partial slots per row; 1 = the kernel writes `out` itself
+    int32_t rows_per_unit; // query rows sharing one key range (flash: BM; decode: n_q)
+    float *part_o;      // [row][max_chunks][d]   unnormalised sum of p*v
+    float *part_ml;     // [row][max_chunks][2]   (running max in log2 units, sum of p)
+};
+
+// Rows of a call are numbered ((item * n_head + head) * n_q + query).
+__host__ __device__ inline int64_t row_index(const AttnArgs &a, int item, int head, int query) {
+    return ((int64_t)item * a.n_head + head) * a.n_q + query;
+}
+
+// Keys of batch item `item`: its own count when the call has per-item counts, clamped to the
+// capacity n_kv the buffers were sized for.
+__device__ inline int item_kv(const AttnArgs &a, int item) {
+    return a.n_kv_item ? min(max(a.n_kv_item[item], 0), a.n_kv) : a.n_kv;
+}
+
+// Flash (dense, MFMA) kernel geometry.
+constexpr int kFlashWaves = 4;
+constexpr int kFlashRowsPerWave = 32;
+constexpr int kFlashBM = kFlashWaves * kFlashRowsPerWave; // query rows per workgroup
+constexpr int kFlashBN = 32;                              // keys per MFMA tile
+
+// Decode (split-K streaming) kernel geometry.
+constexpr int kDecodeThreads = 256;
+constexpr int kDecodeTile = 256; // keys per inner tile
+constexpr int kDecodeMaxRows = 8; // heads-per-KV-group x queries a block can carry
+
+hipError_t launch_flash(const AttnArgs &a, int d, hipStream_t stream, int *grid_blocks);
+hipError_t launch_decode(const AttnArgs &a, int d, int rows, hipStream_t stream, int *grid_blocks);
+hipError_t launch_combine(const AttnArgs &a, int d, hipStream_t stream);
+
+} // namespace zwg

@@ -1,0 +1,385 @@
+// C ABI of the attention library (include/zw_gpu.h): contexts, shape checks, planning and
+// dispatch to the dense MFMA kernel (attn_flash.hip) or the split-K decode kernel
+// (attn_decode.hip).
+#include "zw_gpu.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "attn_kernels.hpp"
+
+struct zwg_ctx {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    float *workspace = nullptr;
+    uint64_t workspace_bytes = 0;
+    // device staging for the host-pointer calls: q, k, v, out
+    float *stage[4] = {nullptr, nullptr, nullptr, nullptr};
+    uint64_t stage_bytes[4] = {0, 0, 0, 0};
+    std::string err;
+};
+
+namespace {
+
+constexpr uint64_t kDefaultWorkspace = 256ull << 20;
+constexpr int kNumCUs = 256;
+
+thread_local std::string t_err;
+
+int fail(zwg_ctx *ctx, const std::string &msg) {
+    t_err = msg;
+    if (ctx) ctx->err = msg;
+    return ZWG_ERROR;
+}
+
+int fail_hip(zwg_ctx *ctx, const char *what, hipError_t e) {
+    return fail(ctx, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Shape rules: the reference's asserts (src/ops.zig:564, :568; causal needs n_kv >= n_q,
+// src/ops.zig:534) plus this build's limits.
+std::string check_shape(const zwg_attn_shape &s) {
+    const uint64_t lim = 0x7fffffffull;
+    char buf[256];
+    if (s.reserved != 0) return "shape.reserved must be 0";
+    if (s.d != 32 && s.d != 64 && s.d != 128) {
+        snprintf(buf, sizeof buf, "head dim d=%llu unsupported (this build: 32, 64, 128)", (unsigned long long)s.d);
+        return buf;
+    }
+    if (s.n_head == 0 || s.n_head_kv == 0 || s.n_head % s.n_head_kv != 0) {
+        snprintf(buf, sizeof buf, "n_head=%llu must be a positive multiple of n_head_kv=%llu",
+                 (unsigned long long)s.n_head, (unsigned long long)s.n_head_kv);
+        return buf;
+    }
+    if (s.n_q > lim || s.n_kv > lim || s.n_head > lim) return "n_q, n_kv and n_head must be below 2^31";
+    if (s.causal && s.n_kv < s.n_q) {
+        snprintf(buf, sizeof buf, "causal attention needs n_kv >= n_q (n_kv=%llu, n_q=%llu)",
+                 (unsigned long long)s.n_kv, (unsigned long long)s.n_q);
+        return buf;
+    }
+    if (s.q_stride % 4 || s.kv_stride % 4 || s.out_stride % 4 || s.kt_stride % 4)
+        return "q_stride, kv_stride, out_stride and kt_stride must be multiples of 4 floats";
+    if (s.n_q > 1 && s.q_stride < s.n_head * s.d) return "q_stride is smaller than n_head * d";
+    if (s.n_q > 1 && s.out_stride < s.n_head * s.d) return "out_stride is smaller than n_head * d";
+    if (s.n_kv > 1 && s.kv_stride < s.n_head_kv * s.d) return "kv_stride is smaller than n_head_kv * d";
+    if (s.kt_stride && s.kt_stride < s.n_kv) return "kt_stride is smaller than n_kv";
+    return "";
+}
+
+std::string check_batch(const zwg_attn_shape &s, const zwg_batch &b) {
+    if (b.n_batch == 0 || b.n_batch > 65535) return "n_batch must be in 1..65535";
+    if (b.q_bstride % 4 || b.k_bstride % 4 || b.v_bstride % 4 || b.out_bstride % 4)
+        return "batch strides must be multiples of 4 floats";
+    if (s.n_head * b.n_batch > 0x7fffffffull) return "n_head * n_batch must be below 2^31";
+    return "";
+}
+
+struct Plan {
+    int kernel = 0; // 1 flash, 2 decode
+    int rows_per_unit = 0;
+    int chunk_len = 0;
+    int max_chunks = 1;
+    uint64_t grid_blocks = 0;
+    uint64_t ws_bytes = 0;
+};
+
+uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+
+// Work units and key splits.  Decode: one unit per (item, KV head), keys split so the grid
+// has ~8 workgroups per CU.  Dense: one unit per (item, head, 128-row q-block); keys are
+// split only when the units alone cannot fill the machine (short or few sequences, causal
+// triangles), in chunks large enough to keep the partial traffic small.
+Plan make_plan(const zwg_attn_shape &s, const zwg_batch &b, uint64_t ws_cap) {
+    Plan p;
+    const uint64_t group = s.n_head / s.n_head_kv;
+    const uint64_t n_rows_total = b.n_batch * s.n_head * s.n_q;
+    const uint64_t row_bytes = (s.d + 2) * sizeof(float);
+    if (s.n_q * group <= (uint64_t)zwg::kDecodeMaxRows) {
+        p.kernel = 2;
+        p.rows_per_unit = (int)s.n_q;
+        const uint64_t T = zwg::kDecodeTile;
+        const uint64_t units = b.n_batch * s.n_head_kv;
+        const uint64_t tiles = std::max<uint64_t>(1, ceil_div(s.n_kv, T));
+        const uint64_t want_chunks = std::min<uint64_t>(tiles, std::max<uint64_t>(1, ceil_div(8 * kNumCUs, units)));
+        uint64_t chunk_tiles = ceil_div(tiles, want_chunks);
+        uint64_t chunks = ceil_div(tiles, chunk_tiles);
+        while (chunks > 1 && n_rows_total * chunks * row_bytes > ws_cap) {
+            ++chunk_tiles;
+            chunks = ceil_div(tiles, chunk_tiles);
+        }
+        p.chunk_len = (int)(chunk_tiles * T);
+        p.max_chunks = (int)chunks;
+        p.grid_blocks = chunks * s.n_head_kv * b.n_batch;
+    } else {
+        p.kernel = 1;
+        const uint64_t BM = zwg::kFlashBM, BN = zwg::kFlashBN;
+        p.rows_per_unit = (int)BM;
+        const uint64_t n_qb = ceil_div(s.n_q, BM);
+        // key tiles the whole call visits (causal blocks stop at their diagonal)
+        uint64_t tiles = 0;
+        for (uint64_t qb = 0; qb < n_qb; ++qb) {
+            const uint64_t q_end = std::min(s.n_q, (qb + 1) * BM);
+            const uint64_t hi = s.causal ? s.n_kv - s.n_q + q_end : s.n_kv;
+            tiles += ceil_div(hi, BN);
+        }
+        tiles *= s.n_head * b.n_batch;
+        const uint64_t slots = 2 * kNumCUs; // workgroups resident at once
+        const uint64_t units = n_qb * s.n_head * b.n_batch;
+        const uint64_t kv_tiles = std::max<uint64_t>(1, ceil_div(s.n_kv, BN));
+        uint64_t chunk_tiles = kv_tiles;
+        if (units < 4 * slots || s.causal) {
+            // aim for two chunks per resident slot, at least 8 tiles (256 keys) each
+            chunk_tiles = std::max<uint64_t>(8, ceil_div(tiles, 2 * slots));
+            chunk_tiles = std::min(chunk_tiles, kv_tiles);
+        }
+        uint64_t chunks = ceil_div(kv_tiles, chunk_tiles);
+        while (chunks > 1 && n_rows_total * chunks * row_bytes > ws_cap) {
+            ++chunk_tiles;
+            chunks = ceil_div(kv_tiles, chunk_tiles);
+        }
+        p.chunk_len = (int)(chunk_tiles * BN);
+        p.max_chunks = (int)chunks;
+        p.grid_blocks = chunks * n_qb * s.n_head * b.n_batch;
+    }
+    p.ws_bytes = p.max_chunks > 1 ? n_rows_total * p.max_chunks * row_bytes : 0;
+    return p;
+}
+
+int run(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_attn_shape &s, const zwg_batch &b,
+        float *out) {
+    std::string msg = check_shape(s);
+    if (msg.empty()) msg = check_batch(s, b);
+    if (!msg.empty()) return fail(ctx, msg);
+    if (s.n_q == 0) return ZWG_OK;
+    if (!q || !out || (s.n_kv && (!k || !v))) return fail(ctx, "null tensor pointer");
+    if (!aligned16(q) || !aligned16(out) || (s.n_kv && (!aligned16(k) || !aligned16(v))))
+        return fail(ctx, "q, k, v and out must be 16-byte aligned");
+    const Plan p = make_plan(s, b, ctx->workspace_bytes);
+    if (p.ws_bytes > ctx->workspace_bytes) return fail(ctx, "workspace too small for this call");
+
+    zwg::AttnArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.out = out;
+    a.q_stride = (int64_t)s.q_stride;
+    a.kv_stride = (int64_t)s.kv_stride;
+    a.out_stride = (int64_t)s.out_stride;
+    a.kt_stride = (int64_t)s.kt_stride;
+    a.q_bstride = (int64_t)b.q_bstride;
+    a.k_bstride = (int64_t)b.k_bstride;
+    a.v_bstride = (int64_t)b.v_bstride;
+    a.out_bstride = (int64_t)b.out_bstride;
+    a.n_kv_item = b.n_kv_dev;
+    a.n_q = (int32_t)s.n_q;
+    a.n_kv = (int32_t)s.n_kv;
+    a.n_head = (int32_t)s.n_head;
+    a.n_head_kv = (int32_t)s.n_head_kv;
+    a.group = (int32_t)(s.n_head / s.n_head_kv);
+    a.n_batch = (int32_t)b.n_batch;
+    a.causal = s.causal ? 1 : 0;
+    // f32(1/sqrt(d)) as the reference computes it (src/ops.zig:531), then to log2 units
+    const float scl = 1.0f / std::sqrt((float)s.d);
+    a.scale_log2 = scl * 1.4426950408889634f;
+    a.chunk_len = p.chunk_len;
+    a.max_chunks = p.max_chunks;
+    a.rows_per_unit = p.rows_per_unit;
+    a.part_ml = ctx->workspace;
+    a.part_o = ctx->workspace + (p.max_chunks > 1 ? 2 * b.n_batch * s.n_head * s.n_q * (uint64_t)p.max_chunks : 0);
+
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
+    int blocks = 0;
+    e = p.kernel == 1 ? zwg::launch_flash(a, (int)s.d, ctx->stream, &blocks)
+                      : zwg::launch_decode(a, (int)s.d, (int)(s.n_q * a.group), ctx->stream, &blocks);
+    if (e != hipSuccess) return fail_hip(ctx, "attention kernel launch", e);
+    if (p.max_chunks > 1) {
+        e = zwg::launch_combine(a, (int)s.d, ctx->stream);
+        if (e != hipSuccess) return fail_hip(ctx, "combine kernel launch", e);
+    }
+    return ZWG_OK;
+}
+
+int ensure_stage(zwg_ctx *ctx, int i, uint64_t bytes) {
+    bytes = std::max<uint64_t>(bytes, 256);
+    if (ctx->stage_bytes[i] >= bytes) return ZWG_OK;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return fail_hip(ctx, "hipStreamSynchronize", e);
+    if (ctx->stage[i]) {
+        (void)hipFree(ctx->stage[i]);
+        ctx->stage[i] = nullptr;
+        ctx->stage_bytes[i] = 0;
+    }
+    void *p = nullptr;
+    e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return fail_hip(ctx, "hipMalloc (staging)", e);
+    ctx->stage[i] = static_cast<float *>(p);
+    ctx->stage_bytes[i] = bytes;
+    return ZWG_OK;
+}
+
+} // namespace
+
+extern "C" {
+
+int zwg_version(void) { return ZWG_VERSION; }
+
+const char *zwg_last_error(const zwg_ctx *ctx) { return ctx ? ctx->err.c_str() : t_err.c_str(); }
+
+int zwg_check_shape(const zwg_attn_shape *shape, char *msg, size_t msg_len) {
+    if (!shape) {
+        if (msg && msg_len) snprintf(msg, msg_len, "null shape");
+        return ZWG_ERROR;
+    }
+    const std::string m = check_shape(*shape);
+    if (msg && msg_len) snprintf(msg, msg_len, "%s", m.c_str());
+    return m.empty() ? ZWG_OK : ZWG_ERROR;
+}
+
+int zwg_plan(const zwg_attn_shape *shape, const zwg_batch *batch, uint64_t workspace_bytes, zwg_plan_info *out) {
+    if (!shape || !out) return fail(nullptr, "null argument");
+    zwg_batch one{1, 0, 0, 0, 0, nullptr};
+    const zwg_batch &b = batch ? *batch : one;
+    std::string msg = check_shape(*shape);
+    if (msg.empty()) msg = check_batch(*shape, b);
+    if (!msg.empty()) return fail(nullptr, msg);
+    const Plan p = make_plan(*shape, b, workspace_bytes ? workspace_bytes : kDefaultWorkspace);
+    out->kernel = (uint32_t)p.kernel;
+    out->rows_per_unit = (uint32_t)p.rows_per_unit;
+    out->chunk_len = (uint64_t)p.chunk_len;
+    out->max_chunks = (uint64_t)p.max_chunks;
+    out->grid_blocks = p.grid_blocks;
+    out->workspace_bytes = p.ws_bytes;
+    return ZWG_OK;
+}
+
+int zwg_open(int device, const zwg_limits *limits, zwg_ctx **out) {
+    if (!out) return fail(nullptr, "null output pointer");
+    *out = nullptr;
+    int n_dev = 0;
+    hipError_t e = hipGetDeviceCount(&n_dev);
+    if (e != hipSuccess || n_dev == 0) return fail(nullptr, "no HIP device available");
+    if (device < 0 || device >= n_dev) return fail(nullptr, "device index out of range");
+    e = hipSetDevice(device);
+    if (e != hipSuccess) return fail_hip(nullptr, "hipSetDevice", e);
+    zwg_ctx *ctx = new zwg_ctx();
+    ctx->device = device;
+    e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete ctx;
+        return fail_hip(nullptr, "hipStreamCreate", e);
+    }
+    ctx->stream = ctx->own_stream;
+    ctx->workspace_bytes = (limits && limits->workspace_bytes) ? limits->workspace_bytes : kDefaultWorkspace;
+    void *ws = nullptr;
+    e = hipMalloc(&ws, ctx->workspace_bytes);
+    if (e != hipSuccess) {
+        (void)hipStreamDestroy(ctx->own_stream);
+        delete ctx;
+        return fail_hip(nullptr, "hipMalloc (workspace)", e);
+    }
+    ctx->workspace = static_cast<float *>(ws);
+    *out = ctx;
+    return ZWG_OK;
+}
+
+void zwg_close(zwg_ctx *ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    for (auto &s : ctx->stage)
+        if (s) (void)hipFree(s);
+    if (ctx->workspace) (void)hipFree(ctx->workspace);
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+}
+
+int zwg_set_stream(zwg_ctx *ctx, void *hip_stream) {
+    if (!ctx) return fail(nullptr, "null context");
+    ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own_stream;
+    return ZWG_OK;
+}
+
+void *zwg_get_stream(const zwg_ctx *ctx) { return ctx ? static_cast<void *>(ctx->stream) : nullptr; }
+
+int zwg_sync(zwg_ctx *ctx) {
+    if (!ctx) return fail(nullptr, "null context");
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return fail_hip(ctx, "hipStreamSynchronize", e);
+    return ZWG_OK;
+}
+
+int zwg_attention_dev(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_attn_shape *shape,
+                      float *out) {
+    if (!ctx || !shape) return fail(ctx, "null context or shape");
+    const zwg_batch one{1, 0, 0, 0, 0, nullptr};
+    return run(ctx, q, k, v, *shape, one, out);
+}
+
+int zwg_attention_batch_dev(zwg_ctx *ctx, const float *q, const float *k, const float *v,
+                            const zwg_attn_shape *shape, const zwg_batch *batch, float *out) {
+    if (!ctx || !shape || !batch) return fail(ctx, "null context, shape or batch");
+    return run(ctx, q, k, v, *shape, *batch, out);
+}
+
+int zwg_attention_ex(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_attn_shape *shape,
+                     float *out) {
+    if (!ctx || !shape) return fail(ctx, "null context or shape");
+    const zwg_attn_shape &s = *shape;
+    const std::string msg = check_shape(s);
+    if (!msg.empty()) return fail(ctx, msg);
+    if (s.n_q == 0) return ZWG_OK;
+    if (!q || !out || (s.n_kv && (!k || !v))) return fail(ctx, "null tensor pointer");
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
+    const uint64_t F = sizeof(float);
+    const uint64_t hd = s.n_head * s.d, kvd = s.n_head_kv * s.d;
+    // spans the reference reads: q rows, K rows or KT rows (n_kv columns of the last one), V rows
+    const uint64_t q_n = (s.n_q - 1) * s.q_stride + hd;
+    const uint64_t k_n = s.n_kv == 0 ? 0 : s.kt_stride ? (kvd - 1) * s.kt_stride + s.n_kv : (s.n_kv - 1) * s.kv_stride + kvd;
+    const uint64_t v_n = s.n_kv == 0 ? 0 : (s.n_kv - 1) * s.kv_stride + kvd;
+    const uint64_t o_n = (s.n_q - 1) * s.out_stride + hd;
+    // +4 floats: a 16-byte key load at the end of the last transposed row stays in the buffer
+    if (ensure_stage(ctx, 0, q_n * F) || ensure_stage(ctx, 1, (k_n + 4) * F) || ensure_stage(ctx, 2, (v_n + 4) * F) ||
+        ensure_stage(ctx, 3, o_n * F))
+        return ZWG_ERROR;
+    e = hipMemcpyAsync(ctx->stage[0], q, q_n * F, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess && k_n) e = hipMemcpyAsync(ctx->stage[1], k, k_n * F, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess && v_n) e = hipMemcpyAsync(ctx->stage[2], v, v_n * F, hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess) return fail_hip(ctx, "hipMemcpyAsync (upload)", e);
+    const zwg_batch one{1, 0, 0, 0, 0, nullptr};
+    int rc = run(ctx, ctx->stage[0], ctx->stage[1], ctx->stage[2], s, one, ctx->stage[3]);
+    if (rc != ZWG_OK) return rc;
+    // copy back only each row's n_head*d columns: out's other columns stay the caller's
+    e = hipMemcpy2DAsync(out, s.out_stride * F, ctx->stage[3], s.out_stride * F, hd * F, s.n_q, hipMemcpyDeviceToHost,
+                         ctx->stream);
+    if (e != hipSuccess) return fail_hip(ctx, "hipMemcpy2DAsync (download)", e);
+    e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return fail_hip(ctx, "hipStreamSynchronize", e);
+    return ZWG_OK;
+}
+
+int zwg_attention(zwg_ctx *ctx, const float *q, const float *k, const float *v, uint64_t n_q, uint64_t n_kv,
+                  uint64_t n_state, uint64_t n_head, int causal, float *out) {
+    if (n_head == 0) return fail(ctx, "n_head must be positive");
+    zwg_attn_shape s{};
+    s.n_q = n_q;
+    s.n_kv = n_kv;
+    s.n_head = n_head;
+    s.n_head_kv = n_head;
+    s.d = n_state / n_head;
+    s.q_stride = n_state;
+    s.kv_stride = n_state;
+    s.out_stride = n_state;
+    s.kt_stride = 0;
+    s.causal = causal ? 1u : 0u;
+    return zwg_attention_ex(ctx, q, k, v, &s, out);
+}
+
+} // extern "C"

@@ -1,0 +1,230 @@
+"""Python mirror of zwhisper's attention interface (src/ops.zig:464-605) on the gfx950 library.
+
+Same names and argument meaning as the Zig module:
+
+* ``q_block``, ``V`` (src/ops.zig:473, src/gemm.zig:15-24);
+* ``AttnShape`` (src/ops.zig:477-492), ``kt_stride=None`` for row-major keys;
+* ``attentionScratchEx`` / ``attentionScratchKT`` / ``attentionScratch`` (src/ops.zig:545-560);
+* ``attentionEx(pool, q, k, v, sh, scratch, out)`` and
+  ``attention(pool, q, k, v, n_q, n_kv, n_state, n_head, causal, scratch, out)`` on host
+  (numpy float32) buffers: synchronous, `out` complete on return, only each row's
+  n_head*d columns written (src/ops.zig:540).
+
+Where the reference asserts (src/ops.zig:564, :568) these raise ``ZwgError``.  ``pool`` and
+``scratch`` are accepted and unused.  ``Context`` adds the device-pointer calls (torch CUDA
+tensors already in HBM, on torch's current stream) that the benchmarks and batched callers use.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from dataclasses import dataclass
+from typing import Optional
+
+import numpy as np
+
+from . import _lib
+from ._lib import ZwgError
+
+V = 16
+q_block = 64
+
+
+@dataclass(frozen=True)
+class AttnShape:
+    n_q: int
+    n_kv: int
+    n_head: int
+    n_head_kv: int
+    d: int
+    q_stride: int
+    kv_stride: int
+    out_stride: int
+    causal: bool
+    kt_stride: Optional[int] = None
+
+    def to_c(self) -> _lib.ShapeC:
+        return _lib.ShapeC(self.n_q, self.n_kv, self.n_head, self.n_head_kv, self.d, self.q_stride, self.kv_stride,
+                           self.out_stride, self.kt_stride or 0, 1 if self.causal else 0, 0)
+
+    # extents (in floats) the reference reads or writes
+    def q_len(self) -> int:
+        return (self.n_q - 1) * self.q_stride + self.n_head * self.d if self.n_q else 0
+
+    def out_len(self) -> int:
+        return (self.n_q - 1) * self.out_stride + self.n_head * self.d if self.n_q else 0
+
+    def k_len(self) -> int:
+        if self.n_kv == 0:
+            return 0
+        kvd = self.n_head_kv * self.d
+        if self.kt_stride:
+            return (kvd - 1) * self.kt_stride + self.n_kv
+        return (self.n_kv - 1) * self.kv_stride + kvd
+
+    def v_len(self) -> int:
+        return (self.n_kv - 1) * self.kv_stride + self.n_head_kv * self.d if self.n_kv else 0
+
+
+def attentionScratchEx(n_q: int, n_kv: int, n_head: int, n_head_kv: int, d: int) -> int:
+    n_kv_pad = (n_kv + V - 1) // V * V
+    n_qblocks = (n_q + q_block - 1) // q_block
+    return n_head_kv * d * n_kv_pad + n_head * n_qblocks * q_block * n_kv_pad
+
+
+def attentionScratchKT(n_q: int, kt_stride: int, n_head: int) -> int:
+    n_qblocks = (n_q + q_block - 1) // q_block
+    return n_head * n_qblocks * q_block * kt_stride
+
+
+def attentionScratch(n_q: int, n_kv: int, n_head: int, n_state: int) -> int:
+    return attentionScratchEx(n_q, n_kv, n_head, n_head, n_state // n_head)
+
+
+def check_shape(sh: AttnShape) -> None:
+    """Raises ZwgError with the library's message if `sh` is not accepted."""
+    buf = ctypes.create_string_buffer(256)
+    c = sh.to_c()
+    if _lib.lib().zwg_check_shape(ctypes.byref(c), buf, 256) != _lib.ZWG_OK:
+        raise ZwgError(buf.value.decode())
+
+
+def plan(sh: AttnShape, n_batch: int = 1, workspace_bytes: int = 0) -> _lib.PlanC:
+    """Which kernel and key split a call would use (host-only)."""
+    c = sh.to_c()
+    b = _lib.BatchC(n_batch, 0, 0, 0, 0, None)
+    p = _lib.PlanC()
+    _lib.check(_lib.lib().zwg_plan(ctypes.byref(c), ctypes.byref(b), workspace_bytes, ctypes.byref(p)))
+    return p
+
+
+class Context:
+    """One library context (zwg_ctx): a device, a workspace, staging buffers."""
+
+    def __init__(self, device: int = 0, workspace_bytes: int = 0):
+        L = _lib.lib()
+        self._L = L
+        h = ctypes.c_void_p()
+        lim = _lib.LimitsC(workspace_bytes)
+        rc = L.zwg_open(device, ctypes.byref(lim), ctypes.byref(h))
+        if rc != _lib.ZWG_OK:
+            raise ZwgError(_lib.last_error(None))
+        self._h = h
+        self.device = device
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._L.zwg_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def handle(self):
+        return self._h
+
+    def _check(self, rc: int) -> None:
+        if rc != _lib.ZWG_OK:
+            raise ZwgError(_lib.last_error(self._h))
+
+    def set_stream(self, stream_ptr: int | None) -> None:
+        self._check(self._L.zwg_set_stream(self._h, stream_ptr))
+
+    def sync(self) -> None:
+        self._check(self._L.zwg_sync(self._h))
+
+    # ---- host buffers: the drop-in
+    def attention_ex_host(self, q: np.ndarray, k: np.ndarray, v: np.ndarray, sh: AttnShape, out: np.ndarray) -> None:
+        for name, a in (("q", q), ("k", k), ("v", v), ("out", out)):
+            if a.dtype != np.float32 or not a.flags["C_CONTIGUOUS"]:
+                raise ZwgError(f"{name} must be a contiguous float32 array")
+        if q.size < sh.q_len() or out.size < sh.out_len() or k.size < sh.k_len() or v.size < sh.v_len():
+            raise ZwgError("a buffer is shorter than the shape needs")
+        c = sh.to_c()
+        self._check(self._L.zwg_attention_ex(self._h, q.ctypes.data, k.ctypes.data, v.ctypes.data, ctypes.byref(c),
+                                             out.ctypes.data))
+
+    # ---- device buffers (torch CUDA tensors, float32), on torch's current stream
+    def _bind_torch_stream(self):
+        import torch
+
+        self.set_stream(torch.cuda.current_stream(self.device).cuda_stream)
+
+    @staticmethod
+    def _dev_ptr(t, name: str) -> int:
+        import torch
+
+        if t is None:
+            return 0
+        if not isinstance(t, torch.Tensor) or not t.is_cuda or t.dtype != torch.float32:
+            raise ZwgError(f"{name} must be a CUDA float32 tensor")
+        return t.data_ptr()
+
+    def attention_dev(self, q, k, v, sh: AttnShape, out) -> None:
+        self._bind_torch_stream()
+        c = sh.to_c()
+        self._check(self._L.zwg_attention_dev(self._h, self._dev_ptr(q, "q"), self._dev_ptr(k, "k"),
+                                              self._dev_ptr(v, "v"), ctypes.byref(c), self._dev_ptr(out, "out")))
+
+    def attention_batch_dev(self, q, k, v, sh: AttnShape, out, n_batch: int, q_bstride: int, k_bstride: int,
+                            v_bstride: int, out_bstride: int, n_kv_dev=None) -> None:
+        """A batch of n_batch problems at fixed strides (floats); n_kv_dev: int32 CUDA tensor or None."""
+        import torch
+
+        self._bind_torch_stream()
+        nkv = 0
+        if n_kv_dev is not None:
+            if not n_kv_dev.is_cuda or n_kv_dev.dtype != torch.int32 or n_kv_dev.numel() < n_batch:
+                raise ZwgError("n_kv_dev must be a CUDA int32 tensor with n_batch entries")
+            nkv = n_kv_dev.data_ptr()
+        c = sh.to_c()
+        b = _lib.BatchC(n_batch, q_bstride, k_bstride, v_bstride, out_bstride, nkv)
+        self._check(self._L.zwg_attention_batch_dev(self._h, self._dev_ptr(q, "q"), self._dev_ptr(k, "k"),
+                                                    self._dev_ptr(v, "v"), ctypes.byref(c), ctypes.byref(b),
+                                                    self._dev_ptr(out, "out")))
+
+
+_tls = threading.local()
+
+
+def default_context() -> Context:
+    """The calling thread's context on device 0, opened on first use."""
+    ctx = getattr(_tls, "ctx", None)
+    if ctx is None:
+        ctx = Context(0)
+        _tls.ctx = ctx
+    return ctx
+
+
+def _as_f32(a, name: str) -> np.ndarray:
+    a = np.asarray(a)
+    if a.dtype != np.float32:
+        raise ZwgError(f"{name} must be float32")
+    return np.ascontiguousarray(a).reshape(-1)
+
+
+def attentionEx(pool, q, k, v, sh: AttnShape, scratch, out) -> None:
+    """ops.attentionEx (src/ops.zig:562) on host buffers; `out` (float32, contiguous) is written in place."""
+    del pool, scratch
+    if not isinstance(out, np.ndarray) or out.dtype != np.float32 or not out.flags["C_CONTIGUOUS"]:
+        raise ZwgError("out must be a contiguous float32 numpy array")
+    default_context().attention_ex_host(_as_f32(q, "q"), _as_f32(k, "k"), _as_f32(v, "v"), sh, out.reshape(-1))
+
+
+def attention(pool, q, k, v, n_q: int, n_kv: int, n_state: int, n_head: int, causal: bool, scratch, out) -> None:
+    """ops.attention (src/ops.zig:593)."""
+    if n_head == 0:
+        raise ZwgError("n_head must be positive")
+    d = n_state // n_head
+    attentionEx(pool, q, k, v, AttnShape(n_q, n_kv, n_head, n_head, d, n_state, n_state, n_state, causal), scratch,
+                out)
