@@ -1,0 +1,353 @@
+#!/usr/bin/env python3
+"""Benchmark of zwhisper's attention hot path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--workload N] [--only] [--no-cpu]
+
+A step is one pass of the attention path over one batch of synthetic input, already resident
+in HBM.  The headline line (one JSON object on stdout) is workload 2, Whisper base.en encoder
+self-attention over 16 windows x 1500 frames (8 heads x 64, K transposed), in TFLOP/s of
+algorithmic work (4*d*H per visible (q, k) pair, src/bench.zig:76).  The other four workloads
+are measured too (unless --only) and reported under "workloads" in the same line, each with its
+own roofline: fp32 MFMA (157.3 TFLOP/s) for the dense ones, HBM (8 TB/s) for the decode ones.
+
+Timing: W untimed warm-up steps, then exactly K steps bracketed by torch.cuda.synchronize();
+each step's launches are also bracketed by HIP events on the stream they run on, whose mean is
+the kernel time used for the roofline.  Decode workloads rotate between two copies of their
+inputs so no step finds its K/V in the 256 MB last-level cache left by the previous one.
+The CPU baseline is the C restatement of the reference's multithreaded attention (oracle/),
+timed on this host's cores on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_MFMA_F32 = 157.3e12  # FLOP/s, MI355X dense fp32 matrix
+PEAK_HBM = 8.0e12  # B/s, MI355X HBM3E
+
+
+def host_threads() -> int:
+    """The reference's default thread count, CPUs - 1 (src/main.zig:126), on this host's share."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16) - 1)
+
+
+class Workload:
+    """Device inputs for one benchmark workload and a step that runs it."""
+
+    def __init__(self, number: int, torch, ctx, copies: int):
+        from zwhisper_amd import workloads as W
+
+        self.W = W
+        self.number = number
+        self.spec = W.WORKLOADS[number]
+        self.torch = torch
+        self.ctx = ctx
+        self.copies = copies
+        self.lengths = W.kv_lengths(number)
+        self.work = W.algorithmic_work(number, self.lengths)
+        self.sets = []
+        self._setup()
+
+    # ---- inputs
+    def _dev(self, a):
+        return self.torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+    def _setup(self):
+        from zwhisper_amd.ops import AttnShape
+
+        W, w, n = self.W, self.spec, self.number
+        t = self.torch
+        if n in (1, 2, 4):
+            kt = W.kt_stride_for(w.n_kv_cap) if n != 4 else w.n_kv_cap
+            qs, ks, vs = [], [], []
+            for item in range(w.n_items):
+                q, kl, v = W.make_dense(n, item)
+                qs.append(q)
+                ks.append(W.to_kt(kl, kt))
+                vs.append(v)
+            q, k, v = np.stack(qs), np.stack(ks), np.stack(vs)
+            self.shape = AttnShape(w.n_q, w.n_kv_cap, w.n_head, w.n_head_kv, w.d, w.n_head * w.d,
+                                   w.n_head_kv * w.d, w.n_head * w.d, w.causal, kt)
+            base = {"q": self._dev(q), "k": self._dev(k), "v": self._dev(v)}
+            base["out"] = t.empty((w.n_items, w.n_q, w.n_head * w.d), dtype=t.float32, device="cuda")
+            self.bstrides = (q[0].size, k[0].size, v[0].size, w.n_q * w.n_head * w.d)
+            self.sets = [base] + [{kk: (vv.clone() if kk != "out" else vv) for kk, vv in base.items()}
+                                  for _ in range(self.copies - 1)]
+        elif n == 3:
+            ns = w.n_head * w.d
+            cap, n_cross = w.n_kv_cap, w.extra["cross_n_kv"]
+            qs = np.zeros((w.n_items, ns), np.float32)
+            qc = np.zeros((w.n_items, ns), np.float32)
+            ks = np.zeros((w.n_items, cap, ns), np.float32)
+            vs = np.zeros((w.n_items, cap, ns), np.float32)
+            kc = np.zeros((w.n_items, n_cross, ns), np.float32)
+            vc = np.zeros((w.n_items, n_cross, ns), np.float32)
+            for i in range(w.n_items):
+                s = W.make_decoder_step(i)
+                qs[i], qc[i] = s["q_self"][0], s["q_cross"][0]
+                ks[i, : s["n_self"]], vs[i, : s["n_self"]] = s["k_self"], s["v_self"]
+                kc[i], vc[i] = s["k_cross"], s["v_cross"]
+            self.shape_self = AttnShape(1, cap, w.n_head, w.n_head, w.d, ns, ns, ns, True, None)
+            self.shape_cross = AttnShape(1, n_cross, w.n_head, w.n_head, w.d, ns, ns, ns, False, None)
+            nkv = t.from_numpy(self.lengths.astype(np.int32)).cuda()
+            for c in range(self.copies):
+                self.sets.append({
+                    "qs": self._dev(qs), "qc": self._dev(qc), "ks": self._dev(ks), "vs": self._dev(vs),
+                    "kc": self._dev(kc), "vc": self._dev(vc), "nkv": nkv,
+                    "os": t.empty((w.n_items, ns), dtype=t.float32, device="cuda"),
+                    "oc": t.empty((w.n_items, ns), dtype=t.float32, device="cuda"),
+                })
+            self.host = {"qs": qs, "qc": qc, "ks": ks, "vs": vs, "kc": kc, "vc": vc}
+        elif n == 5:
+            cap, ns, kvw = w.n_kv_cap, w.n_head * w.d, w.n_head_kv * w.d
+            q = np.zeros((w.n_items, ns), np.float32)
+            kt = np.zeros((w.n_items, w.n_head_kv, w.d, cap), np.float32)
+            v = np.zeros((w.n_items, cap, kvw), np.float32)
+            for i in range(w.n_items):
+                qi, kl, vi, n_kv = W.make_llm_decode(i)
+                q[i] = qi[0]
+                kt[i] = W.to_kt(kl, cap)
+                v[i, :n_kv] = vi
+            self.shape = AttnShape(1, cap, w.n_head, w.n_head_kv, w.d, ns, kvw, ns, True, cap)
+            nkv = t.from_numpy(self.lengths.astype(np.int32)).cuda()
+            for c in range(self.copies):
+                self.sets.append({"q": self._dev(q), "k": self._dev(kt), "v": self._dev(v), "nkv": nkv,
+                                  "out": t.empty((w.n_items, ns), dtype=t.float32, device="cuda")})
+            self.bstrides = (ns, kt[0].size, v[0].size, ns)
+            self.host = {"q": q, "k": kt, "v": v}
+
+    # ---- one step
+    def step(self, i: int):
+        s = self.sets[i % len(self.sets)]
+        w, ctx = self.spec, self.ctx
+        if self.number in (1, 2, 4):
+            qb, kb, vb, ob = self.bstrides
+            ctx.attention_batch_dev(s["q"], s["k"], s["v"], self.shape, s["out"], w.n_items, qb, kb, vb, ob)
+        elif self.number == 3:
+            ns = w.n_head * w.d
+            cap, n_cross = w.n_kv_cap, w.extra["cross_n_kv"]
+            ctx.attention_batch_dev(s["qs"], s["ks"], s["vs"], self.shape_self, s["os"], w.n_items, ns, cap * ns,
+                                    cap * ns, ns, s["nkv"])
+            ctx.attention_batch_dev(s["qc"], s["kc"], s["vc"], self.shape_cross, s["oc"], w.n_items, ns,
+                                    n_cross * ns, n_cross * ns, ns)
+        else:
+            qb, kb, vb, ob = self.bstrides
+            ctx.attention_batch_dev(s["q"], s["k"], s["v"], self.shape, s["out"], w.n_items, qb, kb, vb, ob, s["nkv"])
+
+    def free(self):
+        self.sets = []
+        self.host = None
+
+
+def time_workload(wl: Workload, steps: int, warmup: int) -> dict:
+    torch = wl.torch
+    for i in range(warmup):
+        wl.step(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record(stream)
+        wl.step(warmup + i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kms = [a.elapsed_time(b) for a, b in ev]
+    return {"wall_s": wall, "ms_per_step": 1e3 * wall / steps, "kernel_ms_mean": float(np.mean(kms)),
+            "kernel_ms_min": float(np.min(kms)), "kernel_ms_median": float(np.median(kms))}
+
+
+def cpu_baseline(number: int, threads: int) -> dict:
+    """The oracle (C restatement of ops.attentionEx + Pool) on a bounded sample of the workload."""
+    import oracle
+    from zwhisper_amd import workloads as W
+    from zwhisper_amd.ops import AttnShape
+
+    w = W.WORKLOADS[number]
+    if number in (3, 5):
+        threads = min(threads, 4)  # the decode pool, pool_dec (src/transcribe.zig:106, src/llm.zig:151)
+    o = oracle.Oracle(threads)
+    calls = []  # (q, k, v, shape) of the sample
+    if number in (1, 2):
+        n_items = 1 if number == 1 else 2
+        for item in range(n_items):
+            q, kl, v = W.make_dense(number, item)
+            # encoder.zig:167 passes row-major K; attentionEx transposes it itself
+            k = kl.reshape(w.n_kv_cap, -1)
+            ns = w.n_head * w.d
+            calls.append((q, k, v, AttnShape(w.n_q, w.n_kv_cap, w.n_head, w.n_head, w.d, ns, ns, ns, False, None)))
+        sample = f"{n_items} of {w.n_items} window(s)"
+        work = W.algorithmic_work(number) * n_items / w.n_items
+    elif number == 4:
+        q, kl, v = W.make_dense(4, 0)
+        kt = W.to_kt(kl, w.n_kv_cap)
+        ns, kvw = w.n_head * w.d, w.n_head_kv * w.d
+        # llm.prompt feeds batches of 256 rows with kt_stride = n_ctx (src/llm.zig:258-266, :191-202)
+        for b0 in range(0, w.n_q, 256):
+            calls.append((q[b0:b0 + 256], kt, v[: b0 + 256],
+                          AttnShape(256, b0 + 256, w.n_head, w.n_head_kv, w.d, ns, kvw, ns, True, w.n_kv_cap)))
+        sample = "the whole prefill as 8 calls of 256 rows"
+        work = W.algorithmic_work(4)
+    elif number == 3:
+        ns = w.n_head * w.d
+        n_items = 8
+        lengths = W.kv_lengths(3)
+        for item in range(n_items):
+            s = W.make_decoder_step(item)
+            calls.append((s["q_self"], s["k_self"], s["v_self"],
+                          AttnShape(1, s["n_self"], w.n_head, w.n_head, w.d, ns, ns, ns, True, None)))
+            calls.append((s["q_cross"], s["k_cross"], s["v_cross"],
+                          AttnShape(1, 1500, w.n_head, w.n_head, w.d, ns, ns, ns, False, None)))
+        sample = f"{n_items} of {w.n_items} windows (self + cross each)"
+        work = float(sum(2 * int(n) * ns * 4 + 2 * 1500 * ns * 4 + 4 * ns * 4 for n in lengths[:n_items]))
+    else:
+        ns, kvw = w.n_head * w.d, w.n_head_kv * w.d
+        n_items = 8
+        lengths = W.kv_lengths(5)
+        for item in range(n_items):
+            q, kl, v, n_kv = W.make_llm_decode(item)
+            kt = W.to_kt(kl, w.n_kv_cap)
+            calls.append((q, kt, v, AttnShape(1, n_kv, w.n_head, w.n_head_kv, w.d, ns, kvw, ns, True, w.n_kv_cap)))
+        sample = f"{n_items} of {w.n_items} sequences"
+        work = float(sum(2 * int(n) * kvw * 4 + 2 * ns * 4 for n in lengths[:n_items]))
+    prepared = []
+    for q, k, v, sh in calls:
+        out = np.zeros(sh.out_len(), dtype=np.float32)
+        scratch = np.empty(oracle.scratch_floats(sh), dtype=np.float32)
+        prepared.append((np.ascontiguousarray(q).reshape(-1), np.ascontiguousarray(k).reshape(-1),
+                         np.ascontiguousarray(v).reshape(-1), sh, out, scratch))
+
+    def run_all():
+        for q, k, v, sh, out, scratch in prepared:
+            o.attention_ex(q, k, v, sh, out=out, scratch=scratch)
+
+    run_all()  # warm-up, as src/bench.zig:69
+    best = float("inf")
+    for _ in range(5):  # best of 5, as src/bench.zig:70-75
+        t0 = time.perf_counter()
+        run_all()
+        best = min(best, time.perf_counter() - t0)
+    o.close()
+    bound = W.WORKLOADS[number].bound
+    value = work / best / (1e12 if bound == "mfma" else 1e9)
+    return {"value": value, "unit": "TFLOP/s" if bound == "mfma" else "GB/s", "cores": o.threads,
+            "kind": "port", "sample": f"{sample}; oracle/attn_oracle.c, best of 5 after one warm-up",
+            "seconds": best}
+
+
+def traffic_for(workload_name: str):
+    """HBM bytes per launch from the committed rocprofv3 counter summary, if one exists."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+        return data.get(workload_name)
+    except (OSError, ValueError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", type=int, default=2, choices=[1, 2, 3, 4, 5], help="headline workload")
+    ap.add_argument("--only", action="store_true", help="measure the headline workload only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE {world}).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    import zwhisper_amd as z
+    from zwhisper_amd import workloads as W
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    torch.cuda.set_device(0)
+    ctx = z.Context(0)
+    numbers = [args.workload] + ([] if args.only else [n for n in (1, 2, 3, 4, 5) if n != args.workload])
+    results = {}
+    for n in numbers:
+        spec = W.WORKLOADS[n]
+        copies = 2 if spec.bound == "hbm" else 1
+        wl = Workload(n, torch, ctx, copies)
+        r = time_workload(wl, args.steps, args.warmup)
+        per_step = wl.work
+        if spec.bound == "mfma":
+            achieved = per_step / (r["kernel_ms_mean"] * 1e-3)
+            roof = {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_MFMA_F32 / 1e12, "unit": "TFLOP/s",
+                    "frac": achieved / PEAK_MFMA_F32}
+            value = per_step / (r["ms_per_step"] * 1e-3) / 1e12
+            unit = "TFLOP/s"
+        else:
+            achieved = per_step / (r["kernel_ms_mean"] * 1e-3)
+            roof = {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                    "frac": achieved / PEAK_HBM}
+            value = per_step / (r["ms_per_step"] * 1e-3) / 1e9
+            unit = "GB/s"
+        roof["traffic"] = traffic_for(spec.name)
+        res = {"workload": spec.name, "description": spec.description, "value": value, "unit": unit,
+               "ms_per_step": r["ms_per_step"], "kernel_ms_mean": r["kernel_ms_mean"],
+               "kernel_ms_min": r["kernel_ms_min"], "algorithmic_work_per_step": per_step, "roofline": roof}
+        if not args.no_cpu:
+            res["cpu_baseline"] = cpu_baseline(n, host_threads())
+        results[n] = res
+        print(f"[bench] {spec.name}: {value:.2f} {unit} ({r['ms_per_step']:.4f} ms/step, kernel "
+              f"{r['kernel_ms_mean']:.4f} ms, {100 * roof['frac']:.1f}% of {spec.bound} peak)"
+              + (f", cpu {res['cpu_baseline']['value']:.3f} {res['cpu_baseline']['unit']}" if not args.no_cpu else ""),
+              file=sys.stderr, flush=True)
+        wl.free()
+        del wl
+        torch.cuda.empty_cache()
+    ctx.close()
+
+    head = results[args.workload]
+    spec = W.WORKLOADS[args.workload]
+    line = {
+        "metric": "encoder/prefill attn TFLOP/s + decode-attn HBM GB/s on 1 MI355X, % roofline",
+        "value": head["value"],
+        "unit": head["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": head["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded N(0,1), SplitMix64 + Box-Muller)",
+        "config": {"workload": spec.name, "items": spec.n_items, "n_q": spec.n_q, "n_kv": spec.n_kv_cap,
+                   "n_head": spec.n_head, "n_head_kv": spec.n_head_kv, "head_dim": spec.d, "causal": spec.causal,
+                   "k_layout": "transposed" if spec.kt else "row-major", "parallelism": "single GPU"},
+        "roofline": head["roofline"],
+        "cpu_baseline": head.get("cpu_baseline"),
+        "workloads": {r["workload"]: {k: v for k, v in r.items() if k not in ("workload",)}
+                      for n, r in results.items() if n != args.workload},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

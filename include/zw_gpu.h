@@ -98,7 +98,9 @@ void zwg_close(zwg_ctx *ctx);
 /* Why the last call on ctx failed; with ctx == NULL, the last failure on this thread. */
 const char *zwg_last_error(const zwg_ctx *ctx);
 
-/* Run on a caller's hipStream_t (NULL: the context's own stream) / the stream in use. */
+/* Queue the context's work on a caller's hipStream_t (NULL is HIP's null stream) / the stream
+ * in use.  A context starts on a stream of its own; zwg_get_stream right after zwg_open
+ * returns it, to switch back later. */
 int zwg_set_stream(zwg_ctx *ctx, void *hip_stream);
 void *zwg_get_stream(const zwg_ctx *ctx);
 /* Wait for all work queued on the context's stream. */

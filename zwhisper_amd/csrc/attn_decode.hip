@@ -35,6 +35,12 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(AttnArgs a)
     constexpr int T = kDecodeTile;
     constexpr int L = D / 4;            // lanes per key row (row-major loads)
     constexpr int P = kDecodeThreads / L; // key rows per pass
+    constexpr int NP = T / P;           // passes over a tile's key rows
+    // loads in flight per thread: 16, or 8 when many rows multiply the operands held with them
+    constexpr int MAXB = R > 2 ? 8 : 16;
+    constexpr int PB = NP < MAXB ? NP : MAXB; // key/value row loads per batch
+    constexpr int DK = D / 4;           // dims per dim group (transposed K)
+    constexpr int KB = DK < MAXB ? DK : MAXB; // transposed-K loads per batch
     constexpr int RED = KT ? 4 * R * T : 4 * R * D;
     static_assert(4 * R * D <= RED, "reduction buffer too small");
 
@@ -110,18 +116,24 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(AttnArgs a)
                 for (int i = 0; i < 4; ++i) acc[r][i] = 0.f;
             if (4 * kq < kn) {
                 // k0 + 4kq < n_kv <= kt_stride and kt_stride % 4 == 0: the 16-byte load is in bounds
-                const float *kp = kbase + (int64_t)(dg * (D / 4)) * a.kt_stride + k0 + 4 * kq;
-#pragma unroll 8
-                for (int p = 0; p < D / 4; ++p) {
-                    const float4 kk = *reinterpret_cast<const float4 *>(kp + (int64_t)p * a.kt_stride);
+                const float *kp = kbase + (int64_t)(dg * DK) * a.kt_stride + k0 + 4 * kq;
+#pragma unroll 1
+                for (int p0 = 0; p0 < DK; p0 += KB) {
+                    // issue the whole batch of loads before using any of them
+                    float4 kk[KB];
 #pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        const float qv = q_s[r][dg * (D / 4) + p];
-                        acc[r][0] += qv * kk.x;
-                        acc[r][1] += qv * kk.y;
-                        acc[r][2] += qv * kk.z;
-                        acc[r][3] += qv * kk.w;
-                    }
+                    for (int i = 0; i < KB; ++i)
+                        kk[i] = *reinterpret_cast<const float4 *>(kp + (int64_t)(p0 + i) * a.kt_stride);
+#pragma unroll
+                    for (int i = 0; i < KB; ++i)
+#pragma unroll
+                        for (int r = 0; r < R; ++r) {
+                            const float qv = q_s[r][dg * DK + p0 + i];
+                            acc[r][0] += qv * kk[i].x;
+                            acc[r][1] += qv * kk[i].y;
+                            acc[r][2] += qv * kk[i].z;
+                            acc[r][3] += qv * kk[i].w;
+                        }
                 }
             }
 #pragma unroll
@@ -136,22 +148,30 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(AttnArgs a)
                             red[(3 * R + r) * T + j];
             }
         } else {
-#pragma unroll 4
-            for (int pass = 0; pass < T / P; ++pass) {
-                const int j = kslot + pass * P;
-                float4 kk = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (j < kn) kk = *reinterpret_cast<const float4 *>(kbase + (int64_t)(k0 + j) * a.kv_stride + 4 * c);
-                float part[R];
+#pragma unroll 1
+            for (int b0 = 0; b0 < NP; b0 += PB) {
+                float4 kk[PB];
 #pragma unroll
-                for (int r = 0; r < R; ++r)
-                    part[r] = qr[r][0] * kk.x + qr[r][1] * kk.y + qr[r][2] * kk.z + qr[r][3] * kk.w;
+                for (int i = 0; i < PB; ++i) {
+                    const int j = kslot + (b0 + i) * P;
+                    kk[i] = j < kn ? *reinterpret_cast<const float4 *>(kbase + (int64_t)(k0 + j) * a.kv_stride + 4 * c)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
 #pragma unroll
-                for (int off = L / 2; off >= 1; off >>= 1)
+                for (int i = 0; i < PB; ++i) {
+                    const int j = kslot + (b0 + i) * P;
+                    float part[R];
 #pragma unroll
-                    for (int r = 0; r < R; ++r) part[r] += __shfl_xor(part[r], off);
-                if (c == 0) {
+                    for (int r = 0; r < R; ++r)
+                        part[r] = qr[r][0] * kk[i].x + qr[r][1] * kk[i].y + qr[r][2] * kk[i].z + qr[r][3] * kk[i].w;
 #pragma unroll
-                    for (int r = 0; r < R; ++r) s_s[r][j] = part[r];
+                    for (int off = L / 2; off >= 1; off >>= 1)
+#pragma unroll
+                        for (int r = 0; r < R; ++r) part[r] += __shfl_xor(part[r], off);
+                    if (c == 0) {
+#pragma unroll
+                        for (int r = 0; r < R; ++r) s_s[r][j] = part[r];
+                    }
                 }
             }
         }
@@ -195,18 +215,25 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(AttnArgs a)
 #pragma unroll
             for (int i = 0; i < 4; ++i) o[r][i] *= al;
         }
-#pragma unroll 4
-        for (int pass = 0; pass < T / P; ++pass) {
-            const int j = kslot + pass * P;
-            if (j < kn) {
-                const float4 vv = *reinterpret_cast<const float4 *>(vbase + (int64_t)(k0 + j) * a.kv_stride);
+#pragma unroll 1
+        for (int b0 = 0; b0 < NP; b0 += PB) {
+            float4 vv[PB];
+#pragma unroll
+            for (int i = 0; i < PB; ++i) {
+                const int j = kslot + (b0 + i) * P;
+                vv[i] = j < kn ? *reinterpret_cast<const float4 *>(vbase + (int64_t)(k0 + j) * a.kv_stride)
+                               : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int i = 0; i < PB; ++i) {
+                const int j = kslot + (b0 + i) * P;
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     const float p = s_s[r][j];
-                    o[r][0] += p * vv.x;
-                    o[r][1] += p * vv.y;
-                    o[r][2] += p * vv.z;
-                    o[r][3] += p * vv.w;
+                    o[r][0] += p * vv[i].x;
+                    o[r][1] += p * vv[i].y;
+                    o[r][2] += p * vv[i].z;
+                    o[r][3] += p * vv[i].w;
                 }
             }
         }
@@ -253,7 +280,7 @@ hipError_t launch_decode(const AttnArgs &a, int d, int rows, hipStream_t stream,
     dim3 block(kDecodeThreads);
     if (grid_blocks) *grid_blocks = (int)(grid.x * grid.y * grid.z);
     const bool kt = a.kt_stride != 0;
-    const int R = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : 8;
+    const int R = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : rows <= 6 ? 6 : 8;
     if (rows > kDecodeMaxRows) return hipErrorInvalidValue;
 #define ZWG_DEC(DD, RR)                                                                                          \
     if (kt)                                                                                                      \
@@ -265,6 +292,7 @@ hipError_t launch_decode(const AttnArgs &a, int d, int rows, hipStream_t stream,
     case 1: ZWG_DEC(DD, 1); break;                                                                               \
     case 2: ZWG_DEC(DD, 2); break;                                                                               \
     case 4: ZWG_DEC(DD, 4); break;                                                                               \
+    case 6: ZWG_DEC(DD, 6); break;                                                                               \
     default: ZWG_DEC(DD, 8); break;                                                                              \
     }
     switch (d) {

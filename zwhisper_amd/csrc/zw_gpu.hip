@@ -302,7 +302,7 @@ void zwg_close(zwg_ctx *ctx) {
 
 int zwg_set_stream(zwg_ctx *ctx, void *hip_stream) {
     if (!ctx) return fail(nullptr, "null context");
-    ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own_stream;
+    ctx->stream = static_cast<hipStream_t>(hip_stream);
     return ZWG_OK;
 }
 
