@@ -51,34 +51,44 @@ HIP_FLAGS = [
 def _run(cmd: list[str]) -> None:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        sys.stderr.write(" ".join(cmd) + "\n" + r.stdout + r.stderr)
+        err = (r.stdout + r.stderr).splitlines()
+        sys.stderr.write(" ".join(cmd) + "\n" + "\n".join(err[:60]) + "\n")
         raise RuntimeError(f"build step failed: {cmd[-1]}")
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(BUILD, exist_ok=True)
+def build(verbose: bool = False, defines: list[str] | None = None, out: str | None = None,
+          build_dir: str | None = None) -> str:
+    """Compile the library (and the C++ test program when building the default library).
+
+    defines: extra -D options for the tunables of the kernels and planner; out/build_dir: where
+    to put the library and objects (default: zwhisper_amd/libzwgpu.so, zwhisper_amd/_build/).
+    """
+    bdir = build_dir or BUILD
+    lib = out or LIB
+    os.makedirs(bdir, exist_ok=True)
+    extra = [f"-D{d}" for d in (defines or [])]
     cc = hipcc()
     jobs = []
     objs = []
     for src in SOURCES:
-        obj = os.path.join(BUILD, src.replace(".hip", ".o"))
+        obj = os.path.join(bdir, src.replace(".hip", ".o"))
         objs.append(obj)
-        jobs.append([cc, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        jobs.append([cc, *HIP_FLAGS, *extra, "-c", os.path.join(CSRC, src), "-o", obj])
     for src in HOST_SOURCES:
-        obj = os.path.join(BUILD, src.replace(".cpp", ".o"))
+        obj = os.path.join(bdir, src.replace(".cpp", ".o"))
         objs.append(obj)
-        jobs.append([cc, *HIP_FLAGS, "-x", "c++", "-c", os.path.join(HOST, src), "-o", obj])
+        jobs.append([cc, *HIP_FLAGS, *extra, "-x", "c++", "-c", os.path.join(HOST, src), "-o", obj])
     with ThreadPoolExecutor(max_workers=min(4, len(jobs))) as ex:
         list(ex.map(_run, jobs))
-    tmp = LIB + ".tmp"
+    tmp = lib + ".tmp"
     _run([cc, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
-    os.replace(tmp, LIB)
-    if os.path.exists(CPP_TEST_SRC):
+    os.replace(tmp, lib)
+    if lib == LIB and os.path.exists(CPP_TEST_SRC):
         _run([cc, "-O2", "-std=c++17", f"-I{INCLUDE}", f"-I{HOST}", CPP_TEST_SRC, "-o", CPP_TEST_BIN,
               f"-L{PKG}", "-lzwgpu", f"-Wl,-rpath,{PKG}", "-Wl,-rpath,$ORIGIN/.."])
     if verbose:
-        print(f"built {LIB}")
-    return LIB
+        print(f"built {lib}")
+    return lib
 
 
 if __name__ == "__main__":

@@ -2,17 +2,24 @@
 //
 // The reference runs single-token decode through the same (head, q-block) task as prefill
 // (AttnJob.run, src/ops.zig:517-541, called at n_q = 1 from src/decoder.zig:184, :191 and
-// src/llm.zig:191-202), which re-reads KT and V once per query head.  Here one workgroup takes
-// one (item, KV head, key chunk) and carries every query row that shares that KV head
-// (heads of the GQA group x queries, at most kDecodeMaxRows), so each K/V byte is read from
-// HBM once.  The chunk is walked in 256-key tiles with an online softmax; the partial
-// (max, sum, sum of p*v) of each row and chunk goes to the workspace and combine_kernel
-// merges the chunks, or the block writes the output itself when a row has one chunk.
+// src/llm.zig:191-202), which re-reads KT and V once per query head.  Here a work unit is one
+// (item, KV head) and carries every query row that shares that KV head (heads of the GQA group
+// x queries, at most kDecodeMaxRows), so each K/V byte is read from HBM once.  A unit's keys
+// are split into chunks; each chunk writes a partial (max, sum, sum of p*v) per row for
+// combine_kernel, or the normalised output itself when its unit has a single chunk.
 //
-// Scores: transposed K ([d][stride] per KV head) is read with lanes along keys (16-byte
-// loads of 4 keys, wave reads 1 KB contiguous per dim); row-major K ([key][stride]) with
-// D/4 lanes per key row (one 16-byte load each) and a cross-lane sum.  V is row-major in
-// every caller: D/4 lanes per key row, each lane accumulating 4 dims of every row.
+// Two kernels, by key layout:
+//
+// decode_kt_kernel -- transposed K ([d][kt_stride] per KV head, the LLM cache, src/llm.zig:27).
+//   One wavefront per chunk, no workgroup barrier.  Each lane owns 4 consecutive keys of a
+//   256-key step and forms their full dot products in-lane (16-byte loads, the wave reads 1 KB
+//   contiguous per dim); the softmax is online per row; the step's probabilities go through a
+//   wave-private LDS row to the V pass, where lanes run along the head dims.
+//
+// decode_rm_kernel -- row-major K ([key][kv_stride], the Whisper decoder caches,
+//   src/decoder.zig:39-42).  One 256-thread workgroup per chunk, walked in 256-key tiles:
+//   D/4 lanes per key row with a butterfly sum for the scores, the tile's softmax in LDS, then
+//   D/4 lanes per V row; loads are issued in batches so a thread has several in flight.
 #include "attn_kernels.hpp"
 
 namespace zwg {
@@ -30,19 +37,201 @@ static __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-template <int D, int R, bool KT>
-__global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(AttnArgs a) {
+#ifndef ZWG_DECODE_BATCH
+#define ZWG_DECODE_BATCH 8
+#endif
+
+template <int D, int R>
+__global__ __launch_bounds__(64) void decode_kt_kernel(AttnArgs a) {
+    constexpr int T = kDecodeTile; // keys per step of the transposed-K path (64 lanes x 4)
+    static_assert(T == 256, "the transposed-K step is 64 lanes x 4 keys");
+    constexpr int L = D / 4;       // lanes per key row (row-major K and V)
+    constexpr int G4 = 64 / L;     // key rows per wave instruction
+    constexpr int NB = ZWG_DECODE_BATCH; // loads in flight per lane and per tensor
+
+    __shared__ __align__(16) float q_s[R][D];
+    __shared__ __align__(16) float p_s[R][T];
+
+    const int lane = threadIdx.x;
+    // one wave per (item, chunk, KV head), KV head fastest
+    const int hk = blockIdx.x % a.n_head_kv;
+    const int chunk = (blockIdx.x / a.n_head_kv) % a.max_chunks;
+    const int item = blockIdx.x / (a.n_head_kv * a.max_chunks);
+
+    const int n_q = a.n_q;
+    const int G = a.group;
+    const int rows = n_q * G;
+    const int n_kv = item_kv(a, item);
+    // the last query sees every key, so the unit's key range is [0, n_kv)
+    const int n_chunks = max(1, (n_kv + a.chunk_len - 1) / a.chunk_len);
+    if (chunk >= n_chunks) return;
+    const int k_begin = chunk * a.chunk_len;
+    const int k_end = min(n_kv, k_begin + a.chunk_len);
+    const int diag = n_kv - n_q; // query i sees keys j <= diag + i
+
+    // row r = query (r / G) of head hk*G + r % G; q pre-scaled into log2 units
+    for (int idx = lane; idx < R * D; idx += 64) {
+        const int r = idx / D;
+        const int p = idx - r * D;
+        float val = 0.f;
+        if (r < rows) {
+            const int qi = r / G;
+            const int head = hk * G + (r - qi * G);
+            val = a.q[item * a.q_bstride + (int64_t)qi * a.q_stride + head * D + p] * a.scale_log2;
+        }
+        q_s[r][p] = val;
+    }
+    __syncthreads();
+
+    // exclusive key limit of each row: the chunk end, and the causal diagonal
+    int lim[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) lim[r] = r < rows ? min(k_end, a.causal ? diag + r / G + 1 : n_kv) : 0;
+
+    float m[R], l[R], o[R][4];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        m[r] = -INFINITY;
+        l[r] = 0.f;
+        o[r][0] = o[r][1] = o[r][2] = o[r][3] = 0.f;
+    }
+
+    const float *kbase = a.k + item * a.k_bstride + (int64_t)hk * D * a.kt_stride;
+    const float *vbase = a.v + item * a.v_bstride + hk * D;
+    const int c = lane % L;  // this lane's dims in the V pass: 4c .. 4c+3
+    const int grp = lane / L; // this lane's key row within an instruction
+
+    {
+        constexpr int KB = NB;
+        constexpr int KEYS_PER_GRP = T / G4; // V pass: each lane group walks its own key range
+#pragma unroll 1
+        for (int k0 = k_begin; k0 < k_end; k0 += T) {
+            float acc[R][4];
+#pragma unroll
+            for (int r = 0; r < R; ++r) acc[r][0] = acc[r][1] = acc[r][2] = acc[r][3] = 0.f;
+            if (k0 + 4 * lane < k_end) {
+                // k0 + 4*lane < n_kv <= kt_stride and kt_stride % 4 == 0: the 16-byte load is in bounds
+                const float *kp = kbase + k0 + 4 * lane;
+#pragma unroll 1
+                for (int p0 = 0; p0 < D; p0 += KB) {
+                    float4 kk[KB];
+#pragma unroll
+                    for (int i = 0; i < KB; ++i)
+                        kk[i] = *reinterpret_cast<const float4 *>(kp + (int64_t)(p0 + i) * a.kt_stride);
+#pragma unroll
+                    for (int i = 0; i < KB; ++i)
+#pragma unroll
+                        for (int r = 0; r < R; ++r) {
+                            const float qv = q_s[r][p0 + i];
+                            acc[r][0] += qv * kk[i].x;
+                            acc[r][1] += qv * kk[i].y;
+                            acc[r][2] += qv * kk[i].z;
+                            acc[r][3] += qv * kk[i].w;
+                        }
+                }
+            }
+            float alpha[R];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                float s[4];
+                float mx = -INFINITY;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    s[i] = k0 + 4 * lane + i < lim[r] ? acc[r][i] : -INFINITY;
+                    mx = fmaxf(mx, s[i]);
+                }
+                mx = wave_max(mx);
+                const float m_new = fmaxf(m[r], mx);
+                const float m_use = m_new == -INFINITY ? 0.f : m_new;
+                alpha[r] = exp2_fast(m[r] - m_use);
+                float4 p;
+                p.x = exp2_fast(s[0] - m_use);
+                p.y = exp2_fast(s[1] - m_use);
+                p.z = exp2_fast(s[2] - m_use);
+                p.w = exp2_fast(s[3] - m_use);
+                l[r] = l[r] * alpha[r] + (p.x + p.y + p.z + p.w); // this lane's keys only
+                m[r] = m_new;
+                *reinterpret_cast<float4 *>(&p_s[r][4 * lane]) = p;
+            }
+            __syncthreads(); // single-wave block: orders the p_s writes before the reads below
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                o[r][0] *= alpha[r];
+                o[r][1] *= alpha[r];
+                o[r][2] *= alpha[r];
+                o[r][3] *= alpha[r];
+            }
+            // lane group grp walks keys [grp*KEYS_PER_GRP, (grp+1)*KEYS_PER_GRP) of the step
+            const int j_lo = grp * KEYS_PER_GRP;
+            const int kn = min(T, k_end - k0);
+#pragma unroll 1
+            for (int j0 = 0; j0 < KEYS_PER_GRP; j0 += NB) {
+                float4 vv[NB];
+#pragma unroll
+                for (int i = 0; i < NB; ++i) {
+                    const int j = j_lo + j0 + i;
+                    vv[i] = j < kn ? *reinterpret_cast<const float4 *>(vbase + (int64_t)(k0 + j) * a.kv_stride + 4 * c)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+                }
+#pragma unroll
+                for (int i4 = 0; i4 < NB; i4 += 4) {
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        const float4 p = *reinterpret_cast<const float4 *>(&p_s[r][j_lo + j0 + i4]);
+                        const float pp[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            o[r][0] += pp[u] * vv[i4 + u].x;
+                            o[r][1] += pp[u] * vv[i4 + u].y;
+                            o[r][2] += pp[u] * vv[i4 + u].z;
+                            o[r][3] += pp[u] * vv[i4 + u].w;
+                        }
+                    }
+                }
+            }
+            __syncthreads(); // before the next step overwrites p_s
+        }
+        // l: each lane summed its own keys; o: each lane group its own keys
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) l[r] += __shfl_xor(l[r], off);
+#pragma unroll
+            for (int off = L; off < 64; off <<= 1)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[r][i] += __shfl_xor(o[r][i], off);
+        }
+    }
+
+    // lanes 0..L-1 hold rows' o for dims 4c..4c+3 (every lane group holds the same sums)
+    if (lane >= L) return;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (r >= rows) break;
+        const int qi = r / G;
+        const int head = hk * G + (r - qi * G);
+        if (n_chunks == 1) {
+            const float inv = l[r] > 0.f ? 1.f / l[r] : 0.f;
+            float *op = a.out + item * a.out_bstride + (int64_t)qi * a.out_stride + head * D + 4 * c;
+            *reinterpret_cast<float4 *>(op) = make_float4(o[r][0] * inv, o[r][1] * inv, o[r][2] * inv, o[r][3] * inv);
+        } else {
+            const int64_t slot = row_index(a, item, head, qi) * a.max_chunks + chunk;
+            *reinterpret_cast<float4 *>(a.part_o + slot * D + 4 * c) = make_float4(o[r][0], o[r][1], o[r][2], o[r][3]);
+            if (c == 0) *reinterpret_cast<float2 *>(a.part_ml + 2 * slot) = make_float2(m[r], l[r]);
+        }
+    }
+}
+
+template <int D, int R>
+__global__ __launch_bounds__(kDecodeThreads) void decode_rm_kernel(AttnArgs a) {
     constexpr int T = kDecodeTile;
-    constexpr int L = D / 4;            // lanes per key row (row-major loads)
+    constexpr int L = D / 4;              // lanes per key row
     constexpr int P = kDecodeThreads / L; // key rows per pass
-    constexpr int NP = T / P;           // passes over a tile's key rows
-    // loads in flight per thread: 16, or 8 when many rows multiply the operands held with them
-    constexpr int MAXB = R > 2 ? 8 : 16;
+    constexpr int NP = T / P;             // passes over a tile's key rows
+    // loads in flight per thread: 16, or 4 when many rows multiply the operands held with them
+    constexpr int MAXB = R > 2 ? 4 : 16;
     constexpr int PB = NP < MAXB ? NP : MAXB; // key/value row loads per batch
-    constexpr int DK = D / 4;           // dims per dim group (transposed K)
-    constexpr int KB = DK < MAXB ? DK : MAXB; // transposed-K loads per batch
-    constexpr int RED = KT ? 4 * R * T : 4 * R * D;
-    static_assert(4 * R * D <= RED, "reduction buffer too small");
+    constexpr int RED = 4 * R * D;
 
     __shared__ __align__(16) float q_s[R][D];
     __shared__ __align__(16) float s_s[R][T];
@@ -52,9 +241,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(AttnArgs a)
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int chunk = blockIdx.x;
-    const int hk = blockIdx.y;
-    const int item = blockIdx.z;
+    // one workgroup per (item, chunk, KV head), KV head fastest
+    const int hk = blockIdx.x % a.n_head_kv;
+    const int chunk = (blockIdx.x / a.n_head_kv) % a.max_chunks;
+    const int item = blockIdx.x / (a.n_head_kv * a.max_chunks);
 
     const int n_q = a.n_q;
     const int G = a.group;
@@ -88,66 +278,23 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(AttnArgs a)
     const int c = tid % L;     // this thread's 4 dims: 4c .. 4c+3
     const int kslot = tid / L; // this thread's key row within a pass
     float qr[R][4];
-    if (!KT) {
 #pragma unroll
-        for (int r = 0; r < R; ++r)
+    for (int r = 0; r < R; ++r)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) qr[r][i] = q_s[r][4 * c + i];
-    }
+        for (int i = 0; i < 4; ++i) qr[r][i] = q_s[r][4 * c + i];
     float o[R][4];
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[r][i] = 0.f;
 
-    const float *kbase = a.k + item * a.k_bstride + (KT ? (int64_t)hk * D * a.kt_stride : (int64_t)hk * D);
+    const float *kbase = a.k + item * a.k_bstride + (int64_t)hk * D;
     const float *vbase = a.v + item * a.v_bstride + hk * D + 4 * c;
 
     for (int k0 = k_begin; k0 < k_end; k0 += T) {
         const int kn = min(T, k_end - k0);
         // ---- scores of this tile into s_s (log2 units)
-        if (KT) {
-            const int kq = tid & 63;
-            const int dg = tid >> 6;
-            float acc[R][4];
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) acc[r][i] = 0.f;
-            if (4 * kq < kn) {
-                // k0 + 4kq < n_kv <= kt_stride and kt_stride % 4 == 0: the 16-byte load is in bounds
-                const float *kp = kbase + (int64_t)(dg * DK) * a.kt_stride + k0 + 4 * kq;
-#pragma unroll 1
-                for (int p0 = 0; p0 < DK; p0 += KB) {
-                    // issue the whole batch of loads before using any of them
-                    float4 kk[KB];
-#pragma unroll
-                    for (int i = 0; i < KB; ++i)
-                        kk[i] = *reinterpret_cast<const float4 *>(kp + (int64_t)(p0 + i) * a.kt_stride);
-#pragma unroll
-                    for (int i = 0; i < KB; ++i)
-#pragma unroll
-                        for (int r = 0; r < R; ++r) {
-                            const float qv = q_s[r][dg * DK + p0 + i];
-                            acc[r][0] += qv * kk[i].x;
-                            acc[r][1] += qv * kk[i].y;
-                            acc[r][2] += qv * kk[i].z;
-                            acc[r][3] += qv * kk[i].w;
-                        }
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < R; ++r)
-                *reinterpret_cast<float4 *>(&red[(dg * R + r) * T + 4 * kq]) =
-                    make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
-            __syncthreads();
-            for (int idx = tid; idx < R * T; idx += kDecodeThreads) {
-                const int r = idx / T;
-                const int j = idx - r * T;
-                s_s[r][j] = red[(0 * R + r) * T + j] + red[(1 * R + r) * T + j] + red[(2 * R + r) * T + j] +
-                            red[(3 * R + r) * T + j];
-            }
-        } else {
+        {
 #pragma unroll 1
             for (int b0 = 0; b0 < NP; b0 += PB) {
                 float4 kk[PB];
@@ -276,17 +423,18 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_attn_kernel(AttnArgs a)
 }
 
 hipError_t launch_decode(const AttnArgs &a, int d, int rows, hipStream_t stream, int *grid_blocks) {
-    dim3 grid(a.max_chunks, a.n_head_kv, a.n_batch);
-    dim3 block(kDecodeThreads);
-    if (grid_blocks) *grid_blocks = (int)(grid.x * grid.y * grid.z);
+    const int64_t blocks = (int64_t)a.max_chunks * a.n_head_kv * a.n_batch;
+    if (blocks > 0x7fffffffll) return hipErrorInvalidValue;
+    dim3 grid((unsigned)blocks);
+    if (grid_blocks) *grid_blocks = (int)blocks;
     const bool kt = a.kt_stride != 0;
     const int R = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : rows <= 6 ? 6 : 8;
     if (rows > kDecodeMaxRows) return hipErrorInvalidValue;
 #define ZWG_DEC(DD, RR)                                                                                          \
     if (kt)                                                                                                      \
-        decode_attn_kernel<DD, RR, true><<<grid, block, 0, stream>>>(a);                                         \
+        decode_kt_kernel<DD, RR><<<grid, dim3(64), 0, stream>>>(a);                                               \
     else                                                                                                         \
-        decode_attn_kernel<DD, RR, false><<<grid, block, 0, stream>>>(a);
+        decode_rm_kernel<DD, RR><<<grid, dim3(kDecodeThreads), 0, stream>>>(a);
 #define ZWG_DEC_R(DD)                                                                                            \
     switch (R) {                                                                                                 \
     case 1: ZWG_DEC(DD, 1); break;                                                                               \

@@ -45,10 +45,16 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
     const int col = lane & 31;
     const int half = lane >> 5;
 
-    const int chunk = blockIdx.x;
-    const int qb = blockIdx.y;
-    const int item = blockIdx.z / a.n_head;
-    const int head = blockIdx.z - item * a.n_head;
+    // logical block = ((item * n_head + head) * n_qblocks + qb) * max_chunks + chunk, so the
+    // q-blocks and splits of one head (which share its K/V) are neighbours on one XCD
+    const int n_qblocks = (a.n_q + BM - 1) / BM;
+    const int64_t lb = xcd_logical_block(blockIdx.x, (int64_t)gridDim.x);
+    const int chunk = (int)(lb % a.max_chunks);
+    const int64_t lq = lb / a.max_chunks;
+    const int qb = (int)(lq % n_qblocks);
+    const int ih = (int)(lq / n_qblocks);
+    const int item = ih / a.n_head;
+    const int head = ih - item * a.n_head;
     const int hk = head / a.group;
 
     const int n_q = a.n_q;
@@ -238,14 +244,17 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
     }
 }
 
-// Merge the split-KV partials of each row: out = sum_c 2^(m_c - M) o_c / sum_c 2^(m_c - M) l_c.
-// One wave per row; lane covers dims lane, lane + 64 (D = 128).
-template <int D>
+// Merge the split-KV partials of each row:
+//   out = sum_c 2^(m_c - M) o_c / sum_c 2^(m_c - M) l_c,   M = max_c m_c,
+// one thread per (row, 4 dims).  MAXC > 0: the call has at most MAXC splits per row.
+template <int D, int MAXC>
 __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    constexpr int G4 = D / 4;
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t n_rows = (int64_t)a.n_batch * a.n_head * a.n_q;
+    const int64_t row = t / G4;
     if (row >= n_rows) return;
+    const int g = (int)(t - row * G4);
     const int query = (int)(row % a.n_q);
     const int64_t ih = row / a.n_q;
     const int head = (int)(ih % a.n_head);
@@ -255,31 +264,61 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
     const int kv_hi = a.causal ? max(0, n_kv - a.n_q + q_end) : n_kv;
     const int n_chunks = max(1, (kv_hi + a.chunk_len - 1) / a.chunk_len);
 
-    const float *ml = a.part_ml + row * a.max_chunks * 2;
-    const float *po = a.part_o + row * a.max_chunks * D;
-    float M = -INFINITY;
-    for (int c = 0; c < n_chunks; ++c) M = fmaxf(M, ml[2 * c]);
-    float L = 0.f;
-    float acc0 = 0.f, acc1 = 0.f;
-    if (M != -INFINITY) {
-        for (int c = 0; c < n_chunks; ++c) {
-            const float m = ml[2 * c];
-            const float w = m == -INFINITY ? 0.f : exp2_fast(m - M);
-            L += w * ml[2 * c + 1];
-            if (lane < D) acc0 += w * po[c * D + lane];
-            if (D > 64) acc1 += w * po[c * D + 64 + lane];
+    const float2 *ml = reinterpret_cast<const float2 *>(a.part_ml) + row * a.max_chunks;
+    const float4 *po = reinterpret_cast<const float4 *>(a.part_o + row * a.max_chunks * D) + g;
+    float M = -INFINITY, L = 0.f;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (MAXC > 0) {
+        // every partial of the row loaded in one round, then merged from registers
+        float2 mlr[MAXC > 0 ? MAXC : 1];
+        float4 vr[MAXC > 0 ? MAXC : 1];
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c) {
+            mlr[c] = c < n_chunks ? ml[c] : make_float2(-INFINITY, 0.f);
+            vr[c] = c < n_chunks ? po[(int64_t)c * G4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c) M = fmaxf(M, mlr[c].x);
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int c = 0; c < MAXC; ++c) {
+                const float w = exp2_fast(mlr[c].x - M); // 0 for a split that saw no key of this row
+                L += w * mlr[c].y;
+                acc.x += w * vr[c].x;
+                acc.y += w * vr[c].y;
+                acc.z += w * vr[c].z;
+                acc.w += w * vr[c].w;
+            }
+        }
+    } else {
+        // two passes whose loads do not depend on each other, so they are all in flight at once
+#pragma unroll 8
+        for (int c = 0; c < n_chunks; ++c) M = fmaxf(M, ml[c].x);
+        if (M != -INFINITY) {
+#pragma unroll 8
+            for (int c = 0; c < n_chunks; ++c) {
+                const float2 m_l = ml[c];
+                const float4 v = po[(int64_t)c * G4];
+                const float w = exp2_fast(m_l.x - M);
+                L += w * m_l.y;
+                acc.x += w * v.x;
+                acc.y += w * v.y;
+                acc.z += w * v.z;
+                acc.w += w * v.w;
+            }
         }
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
-    float *op = a.out + item * a.out_bstride + (int64_t)query * a.out_stride + head * D;
-    if (lane < D) op[lane] = acc0 * inv;
-    if (D > 64) op[64 + lane] = acc1 * inv;
+    float *op = a.out + item * a.out_bstride + (int64_t)query * a.out_stride + head * D + 4 * g;
+    *reinterpret_cast<float4 *>(op) = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
 }
 
 hipError_t launch_flash(const AttnArgs &a, int d, hipStream_t stream, int *grid_blocks) {
     const int n_qblocks = (a.n_q + kFlashBM - 1) / kFlashBM;
     const int max_chunks = a.max_chunks;
-    dim3 grid(max_chunks, n_qblocks, a.n_batch * a.n_head);
+    const int64_t blocks = (int64_t)max_chunks * n_qblocks * a.n_batch * a.n_head;
+    if (blocks > 0x7fffffffll) return hipErrorInvalidValue;
+    dim3 grid((unsigned)blocks);
     dim3 block(256);
     if (grid_blocks) *grid_blocks = (int)(grid.x * grid.y * grid.z);
     const bool kt = a.kt_stride != 0;
@@ -300,14 +339,22 @@ hipError_t launch_flash(const AttnArgs &a, int d, hipStream_t stream, int *grid_
 
 hipError_t launch_combine(const AttnArgs &a, int d, hipStream_t stream) {
     const int64_t n_rows = (int64_t)a.n_batch * a.n_head * a.n_q;
-    dim3 grid((unsigned)((n_rows + 3) / 4));
+    dim3 grid((unsigned)((n_rows * (d / 4) + 255) / 256));
     dim3 block(256);
+#define ZWG_COMBINE(DD)                                                                                          \
+    if (a.max_chunks <= 4)                                                                                       \
+        combine_kernel<DD, 4><<<grid, block, 0, stream>>>(a);                                                    \
+    else if (a.max_chunks <= 16)                                                                                 \
+        combine_kernel<DD, 16><<<grid, block, 0, stream>>>(a);                                                   \
+    else                                                                                                         \
+        combine_kernel<DD, 0><<<grid, block, 0, stream>>>(a);
     switch (d) {
-    case 32: combine_kernel<32><<<grid, block, 0, stream>>>(a); break;
-    case 64: combine_kernel<64><<<grid, block, 0, stream>>>(a); break;
-    case 128: combine_kernel<128><<<grid, block, 0, stream>>>(a); break;
+    case 32: ZWG_COMBINE(32) break;
+    case 64: ZWG_COMBINE(64) break;
+    case 128: ZWG_COMBINE(128) break;
     default: return hipErrorInvalidValue;
     }
+#undef ZWG_COMBINE
     return hipGetLastError();
 }
 

@@ -40,6 +40,24 @@ __device__ inline int item_kv(const AttnArgs &a, int item) {
     return a.n_kv_item ? min(max(a.n_kv_item[item], 0), a.n_kv) : a.n_kv;
 }
 
+// MI355X dispatches consecutive workgroups round-robin over its 8 XCDs, each with its own L2.
+// Renumber so that workgroups the kernel numbers consecutively run on the same XCD: hardware
+// ids x, x+8, x+16, ... (all on XCD x) become one contiguous range of logical ids.
+#ifndef ZWG_XCD_REMAP
+#define ZWG_XCD_REMAP 1
+#endif
+constexpr int kNumXCD = 8;
+__device__ __forceinline__ int64_t xcd_logical_block(int64_t hw, int64_t n) {
+#if ZWG_XCD_REMAP
+    const int64_t xcd = hw % kNumXCD, local = hw / kNumXCD;
+    const int64_t q = n / kNumXCD, r = n % kNumXCD;
+    return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+#else
+    (void)n;
+    return hw;
+#endif
+}
+
 // Flash (dense, MFMA) kernel geometry.
 constexpr int kFlashWaves = 4;
 constexpr int kFlashRowsPerWave = 32;
@@ -47,8 +65,11 @@ constexpr int kFlashBM = kFlashWaves * kFlashRowsPerWave; // query rows per work
 constexpr int kFlashBN = 32;                              // keys per MFMA tile
 
 // Decode (split-K streaming) kernel geometry.
+#ifndef ZWG_DECODE_TILE
+#define ZWG_DECODE_TILE 256
+#endif
 constexpr int kDecodeThreads = 256;
-constexpr int kDecodeTile = 256; // keys per inner tile
+constexpr int kDecodeTile = ZWG_DECODE_TILE; // keys per inner tile
 constexpr int kDecodeMaxRows = 8; // heads-per-KV-group x queries a block can carry
 
 hipError_t launch_flash(const AttnArgs &a, int d, hipStream_t stream, int *grid_blocks);

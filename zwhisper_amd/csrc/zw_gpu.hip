@@ -28,6 +28,23 @@ namespace {
 constexpr uint64_t kDefaultWorkspace = 256ull << 20;
 constexpr int kNumCUs = 256;
 
+// Planner tunables (compile-time).
+#ifndef ZWG_DECODE_BLOCKS_PER_CU
+#define ZWG_DECODE_BLOCKS_PER_CU 8 // decode grid size aimed at, per CU
+#endif
+#ifndef ZWG_DECODE_NOSPLIT_UNITS_PER_CU
+#define ZWG_DECODE_NOSPLIT_UNITS_PER_CU 64 // no key split once units alone reach this many per CU
+#endif
+#ifndef ZWG_DECODE_NOSPLIT_TILES
+#define ZWG_DECODE_NOSPLIT_TILES 0 // ... or when a unit has at most this many 256-key tiles
+#endif
+#ifndef ZWG_FLASH_MIN_CHUNK_TILES
+#define ZWG_FLASH_MIN_CHUNK_TILES 8 // smallest dense key split, in 32-key tiles
+#endif
+#ifndef ZWG_FLASH_CHUNKS_PER_SLOT
+#define ZWG_FLASH_CHUNKS_PER_SLOT 2
+#endif
+
 thread_local std::string t_err;
 
 int fail(zwg_ctx *ctx, const std::string &msg) {
@@ -106,7 +123,12 @@ Plan make_plan(const zwg_attn_shape &s, const zwg_batch &b, uint64_t ws_cap) {
         const uint64_t T = zwg::kDecodeTile;
         const uint64_t units = b.n_batch * s.n_head_kv;
         const uint64_t tiles = std::max<uint64_t>(1, ceil_div(s.n_kv, T));
-        const uint64_t want_chunks = std::min<uint64_t>(tiles, std::max<uint64_t>(1, ceil_div(8 * kNumCUs, units)));
+        uint64_t want_chunks =
+            std::min<uint64_t>(tiles, std::max<uint64_t>(1, ceil_div(ZWG_DECODE_BLOCKS_PER_CU * kNumCUs, units)));
+        // no split when the units already fill the machine, or are short enough that a merge
+        // pass would cost more than the extra parallelism gains
+        if (units >= (uint64_t)ZWG_DECODE_NOSPLIT_UNITS_PER_CU * kNumCUs || tiles <= ZWG_DECODE_NOSPLIT_TILES)
+            want_chunks = 1;
         uint64_t chunk_tiles = ceil_div(tiles, want_chunks);
         uint64_t chunks = ceil_div(tiles, chunk_tiles);
         while (chunks > 1 && n_rows_total * chunks * row_bytes > ws_cap) {
@@ -135,7 +157,7 @@ Plan make_plan(const zwg_attn_shape &s, const zwg_batch &b, uint64_t ws_cap) {
         uint64_t chunk_tiles = kv_tiles;
         if (units < 4 * slots || s.causal) {
             // aim for two chunks per resident slot, at least 8 tiles (256 keys) each
-            chunk_tiles = std::max<uint64_t>(8, ceil_div(tiles, 2 * slots));
+            chunk_tiles = std::max<uint64_t>(ZWG_FLASH_MIN_CHUNK_TILES, ceil_div(tiles, ZWG_FLASH_CHUNKS_PER_SLOT * slots));
             chunk_tiles = std::min(chunk_tiles, kv_tiles);
         }
         uint64_t chunks = ceil_div(kv_tiles, chunk_tiles);
