@@ -110,6 +110,24 @@ def _ptr(a: np.ndarray):
     return a.ctypes.data_as(_fp)
 
 
+def _check_lengths(q, k, v, out, sh) -> None:
+    """The C code trusts its buffers: refuse arrays shorter than the shape reads or writes."""
+    kvd = sh.n_head_kv * sh.d
+    need_q = (sh.n_q - 1) * sh.q_stride + sh.n_head * sh.d if sh.n_q else 0
+    need_o = (sh.n_q - 1) * sh.out_stride + sh.n_head * sh.d if sh.n_q else 0
+    if sh.n_kv == 0:
+        need_k = need_v = 0
+    elif sh.kt_stride:
+        # the reference reads round_up(n_kv, V) columns of every transposed row
+        need_k = (kvd - 1) * sh.kt_stride + (sh.n_kv + V - 1) // V * V
+        need_v = (sh.n_kv - 1) * sh.kv_stride + kvd
+    else:
+        need_k = need_v = (sh.n_kv - 1) * sh.kv_stride + kvd
+    for name, arr, need in (("q", q, need_q), ("k", k, need_k), ("v", v, need_v), ("out", out, need_o)):
+        if arr.size < need:
+            raise ValueError(f"{name} holds {arr.size} floats, the shape needs {need}")
+
+
 def to_ora_shape(sh) -> OraShape:
     return OraShape(sh.n_q, sh.n_kv, sh.n_head, sh.n_head_kv, sh.d, sh.q_stride, sh.kv_stride, sh.out_stride,
                     sh.kt_stride or 0, 1 if sh.causal else 0, 0)
@@ -155,6 +173,7 @@ class Oracle:
         n_out = (sh.n_q - 1) * sh.out_stride + sh.n_head * sh.d if sh.n_q else 0
         if out is None:
             out = np.zeros(max(n_out, 1), dtype=np.float32)
+        _check_lengths(q, k, v, out, sh)
         if scratch is None:
             scratch = np.empty(max(scratch_floats(sh), 1), dtype=np.float32)
         shape = to_ora_shape(sh)
@@ -171,6 +190,8 @@ class Oracle:
         v = np.ascontiguousarray(v, dtype=np.float32).reshape(-1)
         if out is None:
             out = np.zeros(max(n_q * n_state, 1), dtype=np.float32)
+        if q.size < n_q * n_state or k.size < n_kv * n_state or v.size < n_kv * n_state or out.size < n_q * n_state:
+            raise ValueError("a buffer is shorter than n_q/n_kv x n_state")
         scratch = np.empty(max(int(self._L.ora_attention_scratch(n_q, n_kv, n_head, n_state)), 1), dtype=np.float32)
         rc = self._L.ora_attention(self._pool, _ptr(q), _ptr(k), _ptr(v), n_q, n_kv, n_state, n_head,
                                    1 if causal else 0, _ptr(scratch), scratch.size, _ptr(out))

@@ -218,7 +218,8 @@ def attentionEx(pool, q, k, v, sh: AttnShape, scratch, out) -> None:
     del pool, scratch
     if not isinstance(out, np.ndarray) or out.dtype != np.float32 or not out.flags["C_CONTIGUOUS"]:
         raise ZwgError("out must be a contiguous float32 numpy array")
-    default_context().attention_ex_host(_as_f32(q, "q"), _as_f32(k, "k"), _as_f32(v, "v"), sh, out.reshape(-1))
+    q, k, v = _as_f32(q, "q"), _as_f32(k, "k"), _as_f32(v, "v")
+    default_context().attention_ex_host(q, k, v, sh, out.reshape(-1))
 
 
 def attention(pool, q, k, v, n_q: int, n_kv: int, n_state: int, n_head: int, causal: bool, scratch, out) -> None:
