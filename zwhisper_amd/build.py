@@ -42,6 +42,9 @@ HIP_FLAGS = [
     "-fPIC",
     "-Wall",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: keeps the compiler from parking them in AGPRs and copying
+    # them back and forth around every MFMA chain
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     f"-I{INCLUDE}",
     f"-I{CSRC}",
     f"-I{HOST}",

@@ -229,7 +229,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_rm_kernel(AttnArgs a) {
     constexpr int P = kDecodeThreads / L; // key rows per pass
     constexpr int NP = T / P;             // passes over a tile's key rows
     // loads in flight per thread: 16, or 4 when many rows multiply the operands held with them
-    constexpr int MAXB = R > 2 ? 4 : 16;
+#ifndef ZWG_DECODE_RM_BATCH
+#define ZWG_DECODE_RM_BATCH 8
+#endif
+    constexpr int MAXB = R > 2 ? 4 : ZWG_DECODE_RM_BATCH;
     constexpr int PB = NP < MAXB ? NP : MAXB; // key/value row loads per batch
     constexpr int RED = 4 * R * D;
 
@@ -257,6 +260,32 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_rm_kernel(AttnArgs a) {
     const int k_end = min(n_kv, k_begin + a.chunk_len);
     const int diag = n_kv - n_q;
 
+    const int c = tid % L;     // this thread's 4 dims: 4c .. 4c+3
+    const int kslot = tid / L; // this thread's key row within a pass
+    const float *kbase = a.k + item * a.k_bstride + (int64_t)hk * D + 4 * c;
+    const float *vbase = a.v + item * a.v_bstride + hk * D + 4 * c;
+    // batches of key / value rows held in registers; the first K batch of the first tile is
+    // issued before q is staged, the first V batch of a tile before its softmax, and the next
+    // tile's first K batch before this tile's P.V, so those latencies overlap other work
+    float4 kk[PB], vv[PB];
+    auto load_k = [&](int k0, int b0, int kn) {
+#pragma unroll
+        for (int i = 0; i < PB; ++i) {
+            const int j = kslot + (b0 + i) * P;
+            kk[i] = j < kn ? *reinterpret_cast<const float4 *>(kbase + (int64_t)(k0 + j) * a.kv_stride)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto load_v = [&](int k0, int b0, int kn) {
+#pragma unroll
+        for (int i = 0; i < PB; ++i) {
+            const int j = kslot + (b0 + i) * P;
+            vv[i] = j < kn ? *reinterpret_cast<const float4 *>(vbase + (int64_t)(k0 + j) * a.kv_stride)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    if (k_begin < k_end) load_k(k_begin, 0, min(T, k_end - k_begin));
+
     // row r = query (r / G) of head hk*G + r % G
     for (int idx = tid; idx < R * D; idx += kDecodeThreads) {
         const int r = idx / D;
@@ -275,8 +304,6 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_rm_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    const int c = tid % L;     // this thread's 4 dims: 4c .. 4c+3
-    const int kslot = tid / L; // this thread's key row within a pass
     float qr[R][4];
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -288,40 +315,30 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_rm_kernel(AttnArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) o[r][i] = 0.f;
 
-    const float *kbase = a.k + item * a.k_bstride + (int64_t)hk * D;
-    const float *vbase = a.v + item * a.v_bstride + hk * D + 4 * c;
-
     for (int k0 = k_begin; k0 < k_end; k0 += T) {
         const int kn = min(T, k_end - k0);
         // ---- scores of this tile into s_s (log2 units)
-        {
 #pragma unroll 1
-            for (int b0 = 0; b0 < NP; b0 += PB) {
-                float4 kk[PB];
+        for (int b0 = 0; b0 < NP; b0 += PB) {
+            if (b0 > 0) load_k(k0, b0, kn);
 #pragma unroll
-                for (int i = 0; i < PB; ++i) {
-                    const int j = kslot + (b0 + i) * P;
-                    kk[i] = j < kn ? *reinterpret_cast<const float4 *>(kbase + (int64_t)(k0 + j) * a.kv_stride + 4 * c)
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
-                }
+            for (int i = 0; i < PB; ++i) {
+                const int j = kslot + (b0 + i) * P;
+                float part[R];
 #pragma unroll
-                for (int i = 0; i < PB; ++i) {
-                    const int j = kslot + (b0 + i) * P;
-                    float part[R];
+                for (int r = 0; r < R; ++r)
+                    part[r] = qr[r][0] * kk[i].x + qr[r][1] * kk[i].y + qr[r][2] * kk[i].z + qr[r][3] * kk[i].w;
 #pragma unroll
-                    for (int r = 0; r < R; ++r)
-                        part[r] = qr[r][0] * kk[i].x + qr[r][1] * kk[i].y + qr[r][2] * kk[i].z + qr[r][3] * kk[i].w;
+                for (int off = L / 2; off >= 1; off >>= 1)
 #pragma unroll
-                    for (int off = L / 2; off >= 1; off >>= 1)
+                    for (int r = 0; r < R; ++r) part[r] += __shfl_xor(part[r], off);
+                if (c == 0) {
 #pragma unroll
-                        for (int r = 0; r < R; ++r) part[r] += __shfl_xor(part[r], off);
-                    if (c == 0) {
-#pragma unroll
-                        for (int r = 0; r < R; ++r) s_s[r][j] = part[r];
-                    }
+                    for (int r = 0; r < R; ++r) s_s[r][j] = part[r];
                 }
             }
         }
+        load_v(k0, 0, kn);
         __syncthreads();
         // ---- mask, online softmax; wave w owns rows w, w + 4
         for (int r = wave; r < R; r += 4) {
@@ -364,13 +381,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_rm_kernel(AttnArgs a) {
         }
 #pragma unroll 1
         for (int b0 = 0; b0 < NP; b0 += PB) {
-            float4 vv[PB];
-#pragma unroll
-            for (int i = 0; i < PB; ++i) {
-                const int j = kslot + (b0 + i) * P;
-                vv[i] = j < kn ? *reinterpret_cast<const float4 *>(vbase + (int64_t)(k0 + j) * a.kv_stride)
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
+            if (b0 > 0)
+                load_v(k0, b0, kn);
+            else if (k0 + T < k_end)
+                load_k(k0 + T, 0, min(T, k_end - k0 - T));
 #pragma unroll
             for (int i = 0; i < PB; ++i) {
                 const int j = kslot + (b0 + i) * P;

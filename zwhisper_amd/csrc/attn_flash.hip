@@ -1,5 +1,6 @@
 // Dense attention on gfx950 fp32 MFMA: one workgroup = 4 waves x 32 query rows of one head,
-// streaming 32-key tiles of K and V through LDS, online softmax in registers.
+// streaming 32-key tiles of K and V through LDS, online softmax in registers, the tile loop
+// software-pipelined so one tile's softmax overlaps the next tile's score MFMAs.
 //
 // Replaces the per-(head, 64-row q-block) task of the reference (AttnJob.run,
 // src/ops.zig:517-541: S = Q.KT by broadcast FMA, scale, causal limit, softmaxRow, O = S.V)
@@ -24,6 +25,13 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 static __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+#ifndef ZWG_SCHED_INTERLEAVE
+#define ZWG_SCHED_INTERLEAVE 0
+#endif
+#ifndef ZWG_RESCALE_SLACK
+#define ZWG_RESCALE_SLACK 8.0f
+#endif
 
 template <int D, bool KT>
 __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
@@ -104,8 +112,12 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
     float m_run = -INFINITY;
     float l_run = 0.f;
 
+    // Tile staging.  K runs two tiles ahead of the tile being finished and V one tile ahead,
+    // so that in iteration t the MFMAs of S(t+1) (from K(t+1)) can overlap the softmax of
+    // tile t, and the LDS buffers read in an iteration (K(t+1), V(t)) are never the ones
+    // written in it (K(t+2), V(t+1)): one barrier per tile suffices.
     f32x4 kr[LD], vr[LD];
-    auto load_tile = [&](int k0) {
+    auto load_k = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < LD; ++i) {
             const int f = tid + 256 * i;
@@ -119,12 +131,18 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
                 kr[i] = gk < n_kv ? *reinterpret_cast<const f32x4 *>(kp + (int64_t)gk * a.kv_stride + 4 * (f % (D / 4)))
                                   : (f32x4){0};
             }
+        }
+    };
+    auto load_v = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < LD; ++i) {
+            const int f = tid + 256 * i;
             const int gv = k0 + f / (D / 4);
             vr[i] = gv < n_kv ? *reinterpret_cast<const f32x4 *>(vp + (int64_t)gv * a.kv_stride + 4 * (f % (D / 4)))
                               : (f32x4){0};
         }
     };
-    auto store_tile = [&](int buf) {
+    auto store_k = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < LD; ++i) {
             const int f = tid + 256 * i;
@@ -137,81 +155,153 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
                 const int key = f / (D / 4);
                 *reinterpret_cast<f32x4 *>(&Ks[buf][key * KS + 4 * (f % (D / 4))]) = kr[i];
             }
+        }
+    };
+    auto store_v = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < LD; ++i) {
+            const int f = tid + 256 * i;
             const int key = f / (D / 4);
             const int dim = 4 * (f % (D / 4));
 #pragma unroll
             for (int j = 0; j < 4; ++j) Vt[buf][(dim + j) * VS + key] = vr[i][j];
         }
     };
+    // S^T tile = K . Q^T (32 keys x 32 queries) from the K buffer
+    auto qk = [&](int buf) {
+        f32x16 sc = (f32x16){0};
+        const float *krow = &Ks[buf][col * KS + half * HD];
+#pragma unroll
+        for (int j = 0; j < HD; j += 4) {
+            const f32x4 kk = *reinterpret_cast<const f32x4 *>(krow + j);
+            sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[0], qreg[j + 0], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[1], qreg[j + 1], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[2], qreg[j + 2], sc, 0, 0, 0);
+            sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[3], qreg[j + 3], sc, 0, 0, 0);
+        }
+        return sc;
+    };
+    // mask keys past the chunk end or past this query's causal limit, then move the running
+    // max.  It only moves when a tile's max exceeds it by more than ZWG_RESCALE_SLACK (log2
+    // units): until then p = 2^(s - m_run) stays below 2^slack while o and l keep sharing one
+    // reference point, so the final o / l is unchanged and the rescale of o runs on the first
+    // tile and almost never after.  The lane holds 16 of its query's 32 keys, the partner lane
+    // (l ^ 32) the other 16.
+    auto mask_and_max = [&](f32x16 &sc, int k0) {
+        if (k0 + BN > wave_full) {
+            const int lim = min(k_end, a.causal ? diag + query + 1 : n_kv);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = k0 + 8 * (r >> 2) + 4 * half + (r & 3);
+                sc[r] = key < lim ? sc[r] : -INFINITY;
+            }
+        }
+        float mt = sc[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mt = fmaxf(mt, sc[r]);
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        if (__any(mt > m_run + ZWG_RESCALE_SLACK)) {
+            const float m_new = fmaxf(m_run, mt);
+            const float alpha = m_run == -INFINITY ? 0.f : exp2_fast(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+            m_run = m_new;
+        }
+    };
+    auto exp_sum = [&](f32x16 &sc) {
+        const float m_use = m_run == -INFINITY ? 0.f : m_run;
+        float ls = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            sc[r] = exp2_fast(sc[r] - m_use);
+            ls += sc[r];
+        }
+        l_run += ls;
+    };
+    // qk() of the next tile fused with exp_sum() of this one, in a fixed issue order: after
+    // each score MFMA comes one step of the exponentials, so the VALU work executes while the
+    // MFMA pipe is busy with the (dependent) MFMA chain.  The K operand is read one group ahead.
+    auto qk_exp = [&](int buf, f32x16 &p) {
+        constexpr int EVERY = HD / 16; // MFMA steps per exponential
+        const float m_use = m_run == -INFINITY ? 0.f : m_run;
+        float ls = 0.f;
+        f32x16 sc = (f32x16){0};
+        const float *krow = &Ks[buf][col * KS + half * HD];
+        f32x4 kk = *reinterpret_cast<const f32x4 *>(krow);
+#pragma unroll
+        for (int j = 0; j < HD; j += 4) {
+            const f32x4 kn = j + 4 < HD ? *reinterpret_cast<const f32x4 *>(krow + j + 4) : kk;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                sc = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[u], qreg[j + u], sc, 0, 0, 0);
+                if ((j + u) % EVERY == 0) {
+                    const int r = (j + u) / EVERY;
+                    p[r] = exp2_fast(p[r] - m_use);
+                    ls += p[r];
+                }
+#if ZWG_SCHED_INTERLEAVE
+                __builtin_amdgcn_sched_barrier(0);
+#endif
+            }
+            kk = kn;
+        }
+        l_run += ls;
+        return sc;
+    };
+    // O^T += V^T . P^T from the V buffer
+    auto pv = [&](const f32x16 &p, int buf) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+            const float *vrow = &Vt[buf][(db * 32 + col) * VS + 4 * half];
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 vv = *reinterpret_cast<const f32x4 *>(vrow + 8 * g);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[0], p[4 * g + 0], o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[1], p[4 * g + 1], o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[2], p[4 * g + 2], o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[3], p[4 * g + 3], o[db], 0, 0, 0);
+            }
+        }
+    };
+    auto wave_needs = [&](int k0) { return wave_active && k0 < wave_hi; };
 
     const int n_tiles = k_end > k_begin ? (k_end - k_begin + BN - 1) / BN : 0;
+    f32x16 s_cur = (f32x16){0};
     if (n_tiles > 0) {
-        load_tile(k_begin);
-        store_tile(0);
+        load_k(k_begin);
+        load_v(k_begin);
+        store_k(0);
+        store_v(0);
+        if (n_tiles > 1) load_k(k_begin + BN);
     }
+    __syncthreads();
+    if (n_tiles > 0 && wave_needs(k_begin)) s_cur = qk(0);
+    if (n_tiles > 1) store_k(1);
     __syncthreads();
 
     for (int t = 0; t < n_tiles; ++t) {
-        const int buf = t & 1;
         const int k0 = k_begin + t * BN;
-        if (t + 1 < n_tiles) load_tile(k0 + BN);
-
-        if (wave_active && k0 < wave_hi) {
-            // S^T tile = K . Q^T  (32 keys x 32 queries)
-            f32x16 s = (f32x16){0};
-            const float *krow = &Ks[buf][col * KS + half * HD];
-#pragma unroll
-            for (int j = 0; j < HD; j += 4) {
-                const f32x4 kk = *reinterpret_cast<const f32x4 *>(krow + j);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[0], qreg[j + 0], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[1], qreg[j + 1], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[2], qreg[j + 2], s, 0, 0, 0);
-                s = __builtin_amdgcn_mfma_f32_32x32x2f32(kk[3], qreg[j + 3], s, 0, 0, 0);
-            }
-            // mask keys past the chunk end or past this query's causal limit
-            if (k0 + BN > wave_full) {
-                const int lim = min(k_end, a.causal ? diag + query + 1 : n_kv);
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int key = k0 + 8 * (r >> 2) + 4 * half + (r & 3);
-                    s[r] = key < lim ? s[r] : -INFINITY;
-                }
-            }
-            // online softmax over keys: this lane holds 16 of the query's 32 keys, the
-            // partner lane (l ^ 32) the other 16
-            float mt = s[0];
-#pragma unroll
-            for (int r = 1; r < 16; ++r) mt = fmaxf(mt, s[r]);
-            mt = fmaxf(mt, __shfl_xor(mt, 32));
-            const float m_new = fmaxf(m_run, mt);
-            const float m_use = m_new == -INFINITY ? 0.f : m_new;
-            const float alpha = exp2_fast(m_run - m_use);
-            float ls = 0.f;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                s[r] = exp2_fast(s[r] - m_use);
-                ls += s[r];
-            }
-            l_run = l_run * alpha + ls;
-            m_run = m_new;
-#pragma unroll
-            for (int db = 0; db < NDB; ++db) o[db] *= alpha;
-            // O^T += V^T . P^T
-#pragma unroll
-            for (int db = 0; db < NDB; ++db) {
-                const float *vrow = &Vt[buf][(db * 32 + col) * VS + 4 * half];
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const f32x4 vv = *reinterpret_cast<const f32x4 *>(vrow + 8 * g);
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[0], s[4 * g + 0], o[db], 0, 0, 0);
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[1], s[4 * g + 1], o[db], 0, 0, 0);
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[2], s[4 * g + 2], o[db], 0, 0, 0);
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv[3], s[4 * g + 3], o[db], 0, 0, 0);
-                }
-            }
+        if (t + 2 < n_tiles) load_k(k0 + 2 * BN);
+        if (t + 1 < n_tiles) load_v(k0 + BN);
+        const bool need_cur = wave_needs(k0);
+        const bool need_next = t + 1 < n_tiles && wave_needs(k0 + BN);
+        f32x16 s_next = (f32x16){0};
+        if (need_cur) mask_and_max(s_cur, k0);
+        if (need_cur && need_next) {
+            // the MFMAs of the next tile's scores and this tile's exponentials are independent:
+            // issued in one block, the VALU work runs while the MFMA pipe is busy
+            s_next = qk_exp((t + 1) & 1, s_cur);
+        } else if (need_cur) {
+            exp_sum(s_cur);
+        } else if (need_next) {
+            s_next = qk((t + 1) & 1);
         }
-        if (t + 1 < n_tiles) store_tile(buf ^ 1);
+        if (need_cur) pv(s_cur, t & 1);
+        if (t + 2 < n_tiles) store_k(t & 1);
+        if (t + 1 < n_tiles) store_v((t + 1) & 1);
         __syncthreads();
+        s_cur = s_next;
     }
 
     const float l_tot = l_run + __shfl_xor(l_run, 32);

@@ -42,7 +42,7 @@ constexpr int kNumCUs = 256;
 #define ZWG_FLASH_MIN_CHUNK_TILES 8 // smallest dense key split, in 32-key tiles
 #endif
 #ifndef ZWG_FLASH_CHUNKS_PER_SLOT
-#define ZWG_FLASH_CHUNKS_PER_SLOT 2
+#define ZWG_FLASH_CHUNKS_PER_SLOT 1
 #endif
 
 thread_local std::string t_err;
