@@ -116,6 +116,17 @@ def test_plan_picks_decode_for_few_rows_per_kv_head():
     assert z.plan(S(1500, 1500, 6, 6, 64, False, kt=1504)).kernel == 1
 
 
+def unit_split(kv_hi, tile, chunk_len, max_chunks):
+    """The kernels' key split of one work unit (attn_kernels.hpp, unit_split): (chunks, keys each)."""
+    w = -(-kv_hi // tile)
+    if w <= 0:
+        return 1, tile
+    tau = max(1, chunk_len // tile)
+    nc = min(max((w + tau // 2) // tau, 1), max_chunks)
+    lt = -(-w // nc)
+    return -(-w // lt), lt * tile
+
+
 @pytest.mark.parametrize("sh,nb", [
     (S(1500, 1500, 6, 6, 64, False, kt=1504), 1), (S(1500, 1500, 8, 8, 64, False, kt=1504), 16),
     (S(2048, 2048, 14, 2, 64, True, kt=2048), 1), (S(1, 4096, 12, 2, 128, True, kt=4096), 64),
@@ -125,7 +136,13 @@ def test_plan_invariants(sh, nb):
     p = z.plan(sh, nb)
     tile = 256 if p.kernel == 2 else 32
     assert p.chunk_len % tile == 0 and p.chunk_len > 0
-    assert (p.max_chunks - 1) * p.chunk_len < max(sh.n_kv, 1) <= p.max_chunks * p.chunk_len or sh.n_kv == 0
+    # every unit's keys are covered by at most max_chunks non-empty chunks
+    his = ([sh.n_kv - sh.n_q + min(sh.n_q, (qb + 1) * 128) if sh.causal else sh.n_kv
+            for qb in range(-(-sh.n_q // 128))] if p.kernel == 1 else list(range(0, sh.n_kv + 1, 7)) + [sh.n_kv])
+    for hi in his:
+        n, keys = unit_split(hi, tile, p.chunk_len, p.max_chunks)
+        assert 1 <= n <= p.max_chunks
+        assert keys % tile == 0 and (n - 1) * keys < max(hi, 1) <= n * keys or hi == 0
     rows = nb * sh.n_head * sh.n_q
     assert p.workspace_bytes == (rows * p.max_chunks * (sh.d + 2) * 4 if p.max_chunks > 1 else 0)
     if p.kernel == 2:

@@ -63,10 +63,11 @@ __global__ __launch_bounds__(64) void decode_kt_kernel(AttnArgs a) {
     const int rows = n_q * G;
     const int n_kv = item_kv(a, item);
     // the last query sees every key, so the unit's key range is [0, n_kv)
-    const int n_chunks = max(1, (n_kv + a.chunk_len - 1) / a.chunk_len);
+    int chunk_keys;
+    const int n_chunks = unit_split(n_kv, T, a.chunk_len, a.max_chunks, &chunk_keys);
     if (chunk >= n_chunks) return;
-    const int k_begin = chunk * a.chunk_len;
-    const int k_end = min(n_kv, k_begin + a.chunk_len);
+    const int k_begin = chunk * chunk_keys;
+    const int k_end = min(n_kv, k_begin + chunk_keys);
     const int diag = n_kv - n_q; // query i sees keys j <= diag + i
 
     // row r = query (r / G) of head hk*G + r % G; q pre-scaled into log2 units
@@ -254,10 +255,11 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_rm_kernel(AttnArgs a) {
     const int rows = n_q * G;
     const int n_kv = item_kv(a, item);
     // the last query sees every key, so the unit's key range is [0, n_kv)
-    const int n_chunks = max(1, (n_kv + a.chunk_len - 1) / a.chunk_len);
+    int chunk_keys;
+    const int n_chunks = unit_split(n_kv, T, a.chunk_len, a.max_chunks, &chunk_keys);
     if (chunk >= n_chunks) return;
-    const int k_begin = chunk * a.chunk_len;
-    const int k_end = min(n_kv, k_begin + a.chunk_len);
+    const int k_begin = chunk * chunk_keys;
+    const int k_end = min(n_kv, k_begin + chunk_keys);
     const int diag = n_kv - n_q;
 
     const int c = tid % L;     // this thread's 4 dims: 4c .. 4c+3
@@ -422,7 +424,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_rm_kernel(AttnArgs a) {
                           red[(3 * R + r) * D + p];
         const int qi = r / G;
         const int head = hk * G + (r - qi * G);
-        if (a.max_chunks == 1) {
+        if (n_chunks == 1) {
             const float l = l_s[r];
             a.out[item * a.out_bstride + (int64_t)qi * a.out_stride + head * D + p] = l > 0.f ? acc / l : 0.f;
         } else {

@@ -56,11 +56,26 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
     // logical block = ((item * n_head + head) * n_qblocks + qb) * max_chunks + chunk, so the
     // q-blocks and splits of one head (which share its K/V) are neighbours on one XCD
     const int n_qblocks = (a.n_q + BM - 1) / BM;
-    const int64_t lb = xcd_logical_block(blockIdx.x, (int64_t)gridDim.x);
-    const int chunk = (int)(lb % a.max_chunks);
-    const int64_t lq = lb / a.max_chunks;
-    const int qb = (int)(lq % n_qblocks);
-    const int ih = (int)(lq / n_qblocks);
+    const int64_t lb = blockIdx.x;
+    // workgroup -> (item*head, q-block, chunk):
+    //  default      ((item * n_head + head) * n_qblocks + qb) * max_chunks + chunk
+    //  heavy_first  ((n_qblocks - 1 - qb) * max_chunks + chunk) * n_batch*n_head + item*head:
+    //               the longest (causal) q-blocks start first and shorter work fills the slots
+    //               they free; heads vary fastest, so neighbouring workgroups -- which the
+    //               hardware deals round-robin over the 8 XCDs -- carry equal work
+    const int64_t n_ih = (int64_t)a.n_batch * a.n_head;
+    int chunk, qb, ih;
+    if (a.heavy_first) {
+        ih = (int)(lb % n_ih);
+        const int64_t t = lb / n_ih;
+        chunk = (int)(t % a.max_chunks);
+        qb = n_qblocks - 1 - (int)(t / a.max_chunks);
+    } else {
+        chunk = (int)(lb % a.max_chunks);
+        const int64_t lq = lb / a.max_chunks;
+        qb = (int)(lq % n_qblocks);
+        ih = (int)(lq / n_qblocks);
+    }
     const int item = ih / a.n_head;
     const int head = ih - item * a.n_head;
     const int hk = head / a.group;
@@ -70,10 +85,11 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
     const int q_first = qb * BM;
     const int q_end_blk = min(q_first + BM, n_q);
     const int kv_hi = a.causal ? max(0, n_kv - n_q + q_end_blk) : n_kv;
-    const int n_chunks = max(1, (kv_hi + a.chunk_len - 1) / a.chunk_len);
+    int chunk_keys;
+    const int n_chunks = unit_split(kv_hi, BN, a.chunk_len, a.max_chunks, &chunk_keys);
     if (chunk >= n_chunks) return;
-    const int k_begin = chunk * a.chunk_len;
-    const int k_end = min(kv_hi, k_begin + a.chunk_len);
+    const int k_begin = chunk * chunk_keys;
+    const int k_end = min(kv_hi, k_begin + chunk_keys);
 
     const float *qp = a.q + item * a.q_bstride + head * D;
     const float *kp = a.k + item * a.k_bstride + (KT ? (int64_t)hk * D * a.kt_stride : (int64_t)hk * D);
@@ -307,7 +323,7 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
     const float l_tot = l_run + __shfl_xor(l_run, 32);
     if (!q_valid) return;
     // lane holds dims db*32 + 8*g + 4*half + {0..3} in registers 4g..4g+3 of o[db]
-    if (a.max_chunks == 1) {
+    if (n_chunks == 1) { // an unsplit unit writes its rows itself; the merge pass skips them
         const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
         float *op = a.out + item * a.out_bstride + (int64_t)query * a.out_stride + head * D;
 #pragma unroll
@@ -352,7 +368,9 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
     const int n_kv = item_kv(a, item);
     const int q_end = min((query / a.rows_per_unit + 1) * a.rows_per_unit, a.n_q);
     const int kv_hi = a.causal ? max(0, n_kv - a.n_q + q_end) : n_kv;
-    const int n_chunks = max(1, (kv_hi + a.chunk_len - 1) / a.chunk_len);
+    int chunk_keys;
+    const int n_chunks = unit_split(kv_hi, a.split_tile, a.chunk_len, a.max_chunks, &chunk_keys);
+    if (n_chunks == 1) return; // written by the attention kernel
 
     const float2 *ml = reinterpret_cast<const float2 *>(a.part_ml) + row * a.max_chunks;
     const float4 *po = reinterpret_cast<const float4 *>(a.part_o + row * a.max_chunks * D) + g;

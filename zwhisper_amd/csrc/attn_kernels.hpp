@@ -21,9 +21,11 @@ struct AttnArgs {
     int32_t n_batch;
     int32_t causal;
     float scale_log2; // f32(1/sqrt(d)) * log2(e): scores go straight into exp2
-    // split-KV
-    int32_t chunk_len;  // keys per split, a multiple of the kernel's key tile
+    // split-KV (see unit_split)
+    int32_t split_tile; // keys per tile of the split (the kernel's key tile)
+    int32_t chunk_len;  // keys per split aimed at, a multiple of split_tile
     int32_t max_chunks; // partial slots per row; 1 = the kernel writes `out` itself
+    int32_t heavy_first; // dense kernel: dispatch the longest (causal) q-blocks first
     int32_t rows_per_unit; // query rows sharing one key range (flash: BM; decode: n_q)
     float *part_o;      // [row][max_chunks][d]   unnormalised sum of p*v
     float *part_ml;     // [row][max_chunks][2]   (running max in log2 units, sum of p)
@@ -34,28 +36,28 @@ __host__ __device__ inline int64_t row_index(const AttnArgs &a, int item, int he
     return ((int64_t)item * a.n_head + head) * a.n_q + query;
 }
 
+// Key split of one work unit whose rows see keys [0, kv_hi): its W = ceil(kv_hi / tile) tiles are
+// dealt into chunks of equal length (the last may be shorter), about tau = chunk_len / tile
+// tiles each, at most max_chunks.  Returns the number of chunks (>= 1) and sets *chunk_keys to
+// the chunk length in keys.  The kernels, the merge pass and the planner all split this way.
+__host__ __device__ inline int unit_split(int kv_hi, int tile, int chunk_len, int max_chunks, int *chunk_keys) {
+    const int w = (kv_hi + tile - 1) / tile;
+    if (w <= 0) {
+        *chunk_keys = tile;
+        return 1;
+    }
+    const int tau = chunk_len / tile > 1 ? chunk_len / tile : 1;
+    int nc = (w + tau / 2) / tau; // round(w / tau)
+    nc = nc < 1 ? 1 : nc > max_chunks ? max_chunks : nc;
+    const int lt = (w + nc - 1) / nc;
+    *chunk_keys = lt * tile;
+    return (w + lt - 1) / lt;
+}
+
 // Keys of batch item `item`: its own count when the call has per-item counts, clamped to the
 // capacity n_kv the buffers were sized for.
 __device__ inline int item_kv(const AttnArgs &a, int item) {
     return a.n_kv_item ? min(max(a.n_kv_item[item], 0), a.n_kv) : a.n_kv;
-}
-
-// MI355X dispatches consecutive workgroups round-robin over its 8 XCDs, each with its own L2.
-// Renumber so that workgroups the kernel numbers consecutively run on the same XCD: hardware
-// ids x, x+8, x+16, ... (all on XCD x) become one contiguous range of logical ids.
-#ifndef ZWG_XCD_REMAP
-#define ZWG_XCD_REMAP 1
-#endif
-constexpr int kNumXCD = 8;
-__device__ __forceinline__ int64_t xcd_logical_block(int64_t hw, int64_t n) {
-#if ZWG_XCD_REMAP
-    const int64_t xcd = hw % kNumXCD, local = hw / kNumXCD;
-    const int64_t q = n / kNumXCD, r = n % kNumXCD;
-    return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
-#else
-    (void)n;
-    return hw;
-#endif
 }
 
 // Flash (dense, MFMA) kernel geometry.

@@ -27,6 +27,10 @@ namespace {
 
 constexpr uint64_t kDefaultWorkspace = 256ull << 20;
 constexpr int kNumCUs = 256;
+// Largest key split count: keeps chunk indices and partial-slot offsets small.
+constexpr uint64_t kMaxChunks = 4096;
+// Calls with more work units than this fill the machine without splitting keys.
+constexpr uint64_t kMaxSplitUnitsHint = 1ull << 22;
 
 // Planner tunables (compile-time).
 #ifndef ZWG_DECODE_BLOCKS_PER_CU
@@ -38,11 +42,11 @@ constexpr int kNumCUs = 256;
 #ifndef ZWG_DECODE_NOSPLIT_TILES
 #define ZWG_DECODE_NOSPLIT_TILES 0 // ... or when a unit has at most this many 256-key tiles
 #endif
-#ifndef ZWG_FLASH_MIN_CHUNK_TILES
-#define ZWG_FLASH_MIN_CHUNK_TILES 8 // smallest dense key split, in 32-key tiles
+#ifndef ZWG_FLASH_BLOCKS_PER_CU
+#define ZWG_FLASH_BLOCKS_PER_CU 2 // dense grid aimed at when keys are split, per CU
 #endif
-#ifndef ZWG_FLASH_CHUNKS_PER_SLOT
-#define ZWG_FLASH_CHUNKS_PER_SLOT 1
+#ifndef ZWG_FLASH_CAUSAL_BLOCKS_PER_CU
+#define ZWG_FLASH_CAUSAL_BLOCKS_PER_CU 6 // ... for causal calls, dispatched longest-first
 #endif
 
 thread_local std::string t_err;
@@ -100,76 +104,77 @@ std::string check_batch(const zwg_attn_shape &s, const zwg_batch &b) {
 struct Plan {
     int kernel = 0; // 1 flash, 2 decode
     int rows_per_unit = 0;
+    int split_tile = 0;
     int chunk_len = 0;
     int max_chunks = 1;
+    int heavy_first = 0;
     uint64_t grid_blocks = 0;
     uint64_t ws_bytes = 0;
 };
 
 uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
-// Work units and key splits.  Decode: one unit per (item, KV head), keys split so the grid
-// has ~8 workgroups per CU.  Dense: one unit per (item, head, 128-row q-block); keys are
-// split only when the units alone cannot fill the machine (short or few sequences, causal
-// triangles), in chunks large enough to keep the partial traffic small.
+// Chunks of about tau tiles that a unit of w tiles is split into (unit_split's count before
+// the last chunk is trimmed): an upper bound on the chunks of any unit of at most w tiles.
+uint64_t split_bound(uint64_t w, uint64_t tau) { return std::max<uint64_t>(1, (w + tau / 2) / tau); }
+
+// Work units and key splits (unit_split deals a unit's key tiles into equal chunks of about
+// tau tiles).  Decode: one unit per (item, KV head); keys split so the grid has ~8 workgroups
+// per CU.  Dense: one unit per (item, head, 128-row q-block); when the units alone cannot fill
+// the machine, keys are split so the workgroups are about equal in work, two per CU.  Causal
+// calls (q-blocks of very unequal length) are always split, into about six workgroups per CU
+// dispatched longest q-block first, so slots freed by short work keep the machine busy.
 Plan make_plan(const zwg_attn_shape &s, const zwg_batch &b, uint64_t ws_cap) {
     Plan p;
     const uint64_t group = s.n_head / s.n_head_kv;
     const uint64_t n_rows_total = b.n_batch * s.n_head * s.n_q;
     const uint64_t row_bytes = (s.d + 2) * sizeof(float);
+    uint64_t tile = 0, tau = 1, w_max = 1, units = 0;
     if (s.n_q * group <= (uint64_t)zwg::kDecodeMaxRows) {
         p.kernel = 2;
         p.rows_per_unit = (int)s.n_q;
-        const uint64_t T = zwg::kDecodeTile;
-        const uint64_t units = b.n_batch * s.n_head_kv;
-        const uint64_t tiles = std::max<uint64_t>(1, ceil_div(s.n_kv, T));
+        tile = zwg::kDecodeTile;
+        units = b.n_batch * s.n_head_kv;
+        w_max = std::max<uint64_t>(1, ceil_div(s.n_kv, tile));
         uint64_t want_chunks =
-            std::min<uint64_t>(tiles, std::max<uint64_t>(1, ceil_div(ZWG_DECODE_BLOCKS_PER_CU * kNumCUs, units)));
+            std::min<uint64_t>(w_max, std::max<uint64_t>(1, ceil_div(ZWG_DECODE_BLOCKS_PER_CU * kNumCUs, units)));
         // no split when the units already fill the machine, or are short enough that a merge
         // pass would cost more than the extra parallelism gains
-        if (units >= (uint64_t)ZWG_DECODE_NOSPLIT_UNITS_PER_CU * kNumCUs || tiles <= ZWG_DECODE_NOSPLIT_TILES)
+        if (units >= (uint64_t)ZWG_DECODE_NOSPLIT_UNITS_PER_CU * kNumCUs || w_max <= ZWG_DECODE_NOSPLIT_TILES)
             want_chunks = 1;
-        uint64_t chunk_tiles = ceil_div(tiles, want_chunks);
-        uint64_t chunks = ceil_div(tiles, chunk_tiles);
-        while (chunks > 1 && n_rows_total * chunks * row_bytes > ws_cap) {
-            ++chunk_tiles;
-            chunks = ceil_div(tiles, chunk_tiles);
-        }
-        p.chunk_len = (int)(chunk_tiles * T);
-        p.max_chunks = (int)chunks;
-        p.grid_blocks = chunks * s.n_head_kv * b.n_batch;
+        tau = ceil_div(w_max, want_chunks);
     } else {
         p.kernel = 1;
-        const uint64_t BM = zwg::kFlashBM, BN = zwg::kFlashBN;
+        const uint64_t BM = zwg::kFlashBM;
+        tile = zwg::kFlashBN;
         p.rows_per_unit = (int)BM;
         const uint64_t n_qb = ceil_div(s.n_q, BM);
-        // key tiles the whole call visits (causal blocks stop at their diagonal)
+        units = n_qb * s.n_head * b.n_batch;
+        // key tiles of every q-block (causal blocks stop at their diagonal)
         uint64_t tiles = 0;
         for (uint64_t qb = 0; qb < n_qb; ++qb) {
             const uint64_t q_end = std::min(s.n_q, (qb + 1) * BM);
             const uint64_t hi = s.causal ? s.n_kv - s.n_q + q_end : s.n_kv;
-            tiles += ceil_div(hi, BN);
+            tiles += ceil_div(hi, tile);
         }
         tiles *= s.n_head * b.n_batch;
-        const uint64_t slots = 2 * kNumCUs; // workgroups resident at once
-        const uint64_t units = n_qb * s.n_head * b.n_batch;
-        const uint64_t kv_tiles = std::max<uint64_t>(1, ceil_div(s.n_kv, BN));
-        uint64_t chunk_tiles = kv_tiles;
-        if (units < 4 * slots || s.causal) {
-            // aim for two chunks per resident slot, at least 8 tiles (256 keys) each
-            chunk_tiles = std::max<uint64_t>(ZWG_FLASH_MIN_CHUNK_TILES, ceil_div(tiles, ZWG_FLASH_CHUNKS_PER_SLOT * slots));
-            chunk_tiles = std::min(chunk_tiles, kv_tiles);
-        }
-        uint64_t chunks = ceil_div(kv_tiles, chunk_tiles);
-        while (chunks > 1 && n_rows_total * chunks * row_bytes > ws_cap) {
-            ++chunk_tiles;
-            chunks = ceil_div(kv_tiles, chunk_tiles);
-        }
-        p.chunk_len = (int)(chunk_tiles * BN);
-        p.max_chunks = (int)chunks;
-        p.grid_blocks = chunks * n_qb * s.n_head * b.n_batch;
+        w_max = std::max<uint64_t>(1, ceil_div(s.n_kv, tile));
+        const uint64_t target = (uint64_t)(s.causal ? ZWG_FLASH_CAUSAL_BLOCKS_PER_CU : ZWG_FLASH_BLOCKS_PER_CU) * kNumCUs;
+        tau = w_max;
+        if (s.causal || units < target) tau = std::min(w_max, std::max<uint64_t>(1, ceil_div(tiles, target)));
     }
+    if (units > kMaxSplitUnitsHint) tau = w_max;
+    uint64_t chunks = split_bound(w_max, tau);
+    while (chunks > 1 && (n_rows_total * chunks * row_bytes > ws_cap || chunks > kMaxChunks)) {
+        ++tau;
+        chunks = split_bound(w_max, tau);
+    }
+    p.chunk_len = (int)(tau * tile);
+    p.max_chunks = (int)chunks;
+    p.split_tile = (int)tile;
+    p.grid_blocks = p.kernel == 2 ? chunks * s.n_head_kv * b.n_batch : chunks * units;
     p.ws_bytes = p.max_chunks > 1 ? n_rows_total * p.max_chunks * row_bytes : 0;
+    p.heavy_first = p.kernel == 1 && s.causal;
     return p;
 }
 
@@ -209,8 +214,10 @@ int run(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_
     // f32(1/sqrt(d)) as the reference computes it (src/ops.zig:531), then to log2 units
     const float scl = 1.0f / std::sqrt((float)s.d);
     a.scale_log2 = scl * 1.4426950408889634f;
+    a.split_tile = p.split_tile;
     a.chunk_len = p.chunk_len;
     a.max_chunks = p.max_chunks;
+    a.heavy_first = p.heavy_first;
     a.rows_per_unit = p.rows_per_unit;
     a.part_ml = ctx->workspace;
     a.part_o = ctx->workspace + (p.max_chunks > 1 ? 2 * b.n_batch * s.n_head * s.n_q * (uint64_t)p.max_chunks : 0);
