@@ -26,6 +26,16 @@ namespace zwg {
 
 static __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Raw buffer loads: 32-bit byte offsets from a descriptor's base, split into a per-lane part
+// (VGPR) and a wave-uniform part (SGPR), range-checked by the hardware against `bytes` (a load
+// past it returns 0).
+static __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const float *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), 0, (int)bytes, 0x00020000);
+}
+static __device__ __forceinline__ f32x4 load_f32x4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+
 static __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
@@ -223,19 +233,23 @@ __global__ __launch_bounds__(64) void decode_kt_kernel(AttnArgs a) {
     }
 }
 
+// Loads go in batches of ZWG_DECODE_RM_BATCH rows per thread: measured on MI355X, deeper
+// per-thread queues stream a cache more slowly, not faster.
 template <int D, int R>
 __global__ __launch_bounds__(kDecodeThreads) void decode_rm_kernel(AttnArgs a) {
+    constexpr int NT = kDecodeThreads;
     constexpr int T = kDecodeTile;
-    constexpr int L = D / 4;              // lanes per key row
-    constexpr int P = kDecodeThreads / L; // key rows per pass
-    constexpr int NP = T / P;             // passes over a tile's key rows
-    // loads in flight per thread: 16, or 4 when many rows multiply the operands held with them
+    constexpr int NW = NT / 64;
+    constexpr int L = D / 4;   // lanes per key row
+    constexpr int P = NT / L;  // key rows per pass
+    constexpr int NP = T / P;  // passes over a tile's key rows
 #ifndef ZWG_DECODE_RM_BATCH
 #define ZWG_DECODE_RM_BATCH 8
 #endif
+    // loads per thread and batch: 8, or 4 when many rows multiply the operands held with them
     constexpr int MAXB = R > 2 ? 4 : ZWG_DECODE_RM_BATCH;
     constexpr int PB = NP < MAXB ? NP : MAXB; // key/value row loads per batch
-    constexpr int RED = 4 * R * D;
+    constexpr int RED = NW * R * D;
 
     __shared__ __align__(16) float q_s[R][D];
     __shared__ __align__(16) float s_s[R][T];
@@ -264,32 +278,30 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_rm_kernel(AttnArgs a) {
 
     const int c = tid % L;     // this thread's 4 dims: 4c .. 4c+3
     const int kslot = tid / L; // this thread's key row within a pass
-    const float *kbase = a.k + item * a.k_bstride + (int64_t)hk * D + 4 * c;
-    const float *vbase = a.v + item * a.v_bstride + hk * D + 4 * c;
+    // K and V rows through buffer descriptors bounded at the item's last valid row: a row at or
+    // past n_kv reads as 0 with no branch (rows in [kn, n_kv) of a split are masked by vlim and
+    // get p = 0); per-lane byte offsets sit in VGPRs, per-row ones in SGPRs.
+    const uint32_t row_bytes = (uint32_t)a.kv_stride * 4u;
+    const uint32_t kv_bytes = n_kv > 0 ? (uint32_t)(n_kv - 1) * row_bytes + 4u * D : 0u;
+    const __amdgpu_buffer_rsrc_t krs = make_rsrc(a.k + item * a.k_bstride + (int64_t)hk * D, kv_bytes);
+    const __amdgpu_buffer_rsrc_t vrs = make_rsrc(a.v + item * a.v_bstride + hk * D, kv_bytes);
+    const uint32_t lane_off = (uint32_t)kslot * row_bytes + 16u * c;
     // batches of key / value rows held in registers; the first K batch of the first tile is
     // issued before q is staged, the first V batch of a tile before its softmax, and the next
     // tile's first K batch before this tile's P.V, so those latencies overlap other work
-    float4 kk[PB], vv[PB];
-    auto load_k = [&](int k0, int b0, int kn) {
+    f32x4 kk[PB], vv[PB];
+    auto load_k = [&](int k0, int b0) {
 #pragma unroll
-        for (int i = 0; i < PB; ++i) {
-            const int j = kslot + (b0 + i) * P;
-            kk[i] = j < kn ? *reinterpret_cast<const float4 *>(kbase + (int64_t)(k0 + j) * a.kv_stride)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+        for (int i = 0; i < PB; ++i) kk[i] = load_f32x4(krs, lane_off, (uint32_t)(k0 + (b0 + i) * P) * row_bytes);
     };
-    auto load_v = [&](int k0, int b0, int kn) {
+    auto load_v = [&](int k0, int b0) {
 #pragma unroll
-        for (int i = 0; i < PB; ++i) {
-            const int j = kslot + (b0 + i) * P;
-            vv[i] = j < kn ? *reinterpret_cast<const float4 *>(vbase + (int64_t)(k0 + j) * a.kv_stride)
-                           : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+        for (int i = 0; i < PB; ++i) vv[i] = load_f32x4(vrs, lane_off, (uint32_t)(k0 + (b0 + i) * P) * row_bytes);
     };
-    if (k_begin < k_end) load_k(k_begin, 0, min(T, k_end - k_begin));
+    if (k_begin < k_end) load_k(k_begin, 0);
 
     // row r = query (r / G) of head hk*G + r % G
-    for (int idx = tid; idx < R * D; idx += kDecodeThreads) {
+    for (int idx = tid; idx < R * D; idx += NT) {
         const int r = idx / D;
         const int p = idx - r * D;
         float val = 0.f;
@@ -322,14 +334,14 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_rm_kernel(AttnArgs a) {
         // ---- scores of this tile into s_s (log2 units)
 #pragma unroll 1
         for (int b0 = 0; b0 < NP; b0 += PB) {
-            if (b0 > 0) load_k(k0, b0, kn);
+            if (b0 > 0) load_k(k0, b0);
 #pragma unroll
             for (int i = 0; i < PB; ++i) {
                 const int j = kslot + (b0 + i) * P;
                 float part[R];
 #pragma unroll
                 for (int r = 0; r < R; ++r)
-                    part[r] = qr[r][0] * kk[i].x + qr[r][1] * kk[i].y + qr[r][2] * kk[i].z + qr[r][3] * kk[i].w;
+                    part[r] = qr[r][0] * kk[i][0] + qr[r][1] * kk[i][1] + qr[r][2] * kk[i][2] + qr[r][3] * kk[i][3];
 #pragma unroll
                 for (int off = L / 2; off >= 1; off >>= 1)
 #pragma unroll
@@ -340,10 +352,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_rm_kernel(AttnArgs a) {
                 }
             }
         }
-        load_v(k0, 0, kn);
+        load_v(k0, 0);
         __syncthreads();
-        // ---- mask, online softmax; wave w owns rows w, w + 4
-        for (int r = wave; r < R; r += 4) {
+        // ---- mask, online softmax; wave w owns rows w, w + NW, ...
+        for (int r = wave; r < R; r += NW) {
             int vlim = 0;
             if (r < rows) vlim = min(kn, (a.causal ? diag + r / G + 1 : n_kv) - k0);
             float v[T / 64];
@@ -384,26 +396,26 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_rm_kernel(AttnArgs a) {
 #pragma unroll 1
         for (int b0 = 0; b0 < NP; b0 += PB) {
             if (b0 > 0)
-                load_v(k0, b0, kn);
+                load_v(k0, b0);
             else if (k0 + T < k_end)
-                load_k(k0 + T, 0, min(T, k_end - k0 - T));
+                load_k(k0 + T, 0);
 #pragma unroll
             for (int i = 0; i < PB; ++i) {
                 const int j = kslot + (b0 + i) * P;
 #pragma unroll
                 for (int r = 0; r < R; ++r) {
                     const float p = s_s[r][j];
-                    o[r][0] += p * vv[i].x;
-                    o[r][1] += p * vv[i].y;
-                    o[r][2] += p * vv[i].z;
-                    o[r][3] += p * vv[i].w;
+                    o[r][0] += p * vv[i][0];
+                    o[r][1] += p * vv[i][1];
+                    o[r][2] += p * vv[i][2];
+                    o[r][3] += p * vv[i][3];
                 }
             }
         }
         __syncthreads();
     }
 
-    // ---- sum o over the key rows: lanes L apart within a wave, then the 4 waves through LDS
+    // ---- sum o over the key rows: lanes L apart within a wave, then the NW waves through LDS
 #pragma unroll
     for (int off = L; off < 64; off <<= 1)
 #pragma unroll
@@ -416,12 +428,13 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_rm_kernel(AttnArgs a) {
             *reinterpret_cast<float4 *>(&red[(wave * R + r) * D + 4 * c]) = make_float4(o[r][0], o[r][1], o[r][2], o[r][3]);
     }
     __syncthreads();
-    for (int idx = tid; idx < R * D; idx += kDecodeThreads) {
+    for (int idx = tid; idx < R * D; idx += NT) {
         const int r = idx / D;
         const int p = idx - r * D;
         if (r >= rows) continue;
-        const float acc = red[(0 * R + r) * D + p] + red[(1 * R + r) * D + p] + red[(2 * R + r) * D + p] +
-                          red[(3 * R + r) * D + p];
+        float acc = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) acc += red[(w * R + r) * D + p];
         const int qi = r / G;
         const int head = hk * G + (r - qi * G);
         if (n_chunks == 1) {

@@ -22,7 +22,6 @@
 namespace zwg {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 static __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -56,9 +55,11 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
     // logical block = ((item * n_head + head) * n_qblocks + qb) * max_chunks + chunk, so the
     // q-blocks and splits of one head (which share its K/V) are neighbours on one XCD
     const int n_qblocks = (a.n_q + BM - 1) / BM;
-    const int64_t lb = blockIdx.x;
+    const int64_t lb = a.xcd_group ? xcd_logical_block(blockIdx.x, (int64_t)gridDim.x) : (int64_t)blockIdx.x;
     // workgroup -> (item*head, q-block, chunk):
-    //  default      ((item * n_head + head) * n_qblocks + qb) * max_chunks + chunk
+    //  default      ((item * n_head + head) * n_qblocks + qb) * max_chunks + chunk; with
+    //               xcd_group the q-blocks of a head, which read the same K and V, share an
+    //               XCD and its L2, so K/V leave HBM about once per head
     //  heavy_first  ((n_qblocks - 1 - qb) * max_chunks + chunk) * n_batch*n_head + item*head:
     //               the longest (causal) q-blocks start first and shorter work fills the slots
     //               they free; heads vary fastest, so neighbouring workgroups -- which the

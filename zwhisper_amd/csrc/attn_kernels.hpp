@@ -26,6 +26,7 @@ struct AttnArgs {
     int32_t chunk_len;  // keys per split aimed at, a multiple of split_tile
     int32_t max_chunks; // partial slots per row; 1 = the kernel writes `out` itself
     int32_t heavy_first; // dense kernel: dispatch the longest (causal) q-blocks first
+    int32_t xcd_group;   // dense kernel: run each head's q-blocks on one XCD (xcd_logical_block)
     int32_t rows_per_unit; // query rows sharing one key range (flash: BM; decode: n_q)
     float *part_o;      // [row][max_chunks][d]   unnormalised sum of p*v
     float *part_ml;     // [row][max_chunks][2]   (running max in log2 units, sum of p)
@@ -58,6 +59,18 @@ __host__ __device__ inline int unit_split(int kv_hi, int tile, int chunk_len, in
 // capacity n_kv the buffers were sized for.
 __device__ inline int item_kv(const AttnArgs &a, int item) {
     return a.n_kv_item ? min(max(a.n_kv_item[item], 0), a.n_kv) : a.n_kv;
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// MI355X deals consecutive workgroups round-robin over its 8 XCDs, each with its own L2.
+// xcd_logical_block renumbers them so that consecutive logical ids run on the same XCD:
+// hardware ids x, x+8, x+16, ... (all on XCD x) become one contiguous range of logical ids.
+constexpr int kNumXCD = 8;
+__device__ __forceinline__ int64_t xcd_logical_block(int64_t hw, int64_t n) {
+    const int64_t xcd = hw % kNumXCD, local = hw / kNumXCD;
+    const int64_t q = n / kNumXCD, r = n % kNumXCD;
+    return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
 }
 
 // Flash (dense, MFMA) kernel geometry.
