@@ -16,6 +16,11 @@ the kernel time used for the roofline.  Decode workloads rotate between two copi
 inputs so no step finds its K/V in the 256 MB last-level cache left by the previous one.
 The CPU baseline is the C restatement of the reference's multithreaded attention (oracle/),
 timed on this host's cores on a bounded sample of the same workload.
+
+Unless --only, the line also carries the device cache updates of three of the workloads (the K/V
+rows of a step written into the HBM-resident caches, with rotary positions for Qwen2), as
+"small_dec_kv_append_x32", "qwen15_kv_append_x64" and "qwen05_prefill_kv_append", each with an
+HBM roofline and oracle/kv.py's update timed beside it.
 """
 from __future__ import annotations
 
@@ -149,6 +154,129 @@ class Workload:
     def free(self):
         self.sets = []
         self.host = None
+
+
+class AppendWorkload:
+    """A cache update of one step (zwg_kv_append / _batch): the new K/V rows (and q) of a step
+    written into the device-resident caches, with rotary positions for the Qwen2 shapes.
+
+    Algorithmic bytes: the k, v (and q) rows read, the cache rows written, q written back, and
+    the cos/sin table rows read.  The sources and caches (1-20 MB) stay in the 256 MB last-level
+    cache between steps, as they would in a decode loop; at one token per sequence the update is
+    bound by launch and memory latency, not bandwidth.
+    """
+
+    def __init__(self, name: str, torch, ctx):
+        import zwhisper_amd as z
+        from zwhisper_amd import workloads as W
+
+        self.name = name
+        self.torch = torch
+        rng = np.random.default_rng(0x5A57)
+        f32 = np.float32
+        if name == "qwen15_kv_append_x64":
+            w = W.WORKLOADS[5]
+            self.description = "Qwen2.5-1.5B decode-step cache update: 64 sequences x 1 token, rotary q/k, K^T scatter"
+            n, h, hkv, d, n_ctx = w.n_items, w.n_head, w.n_head_kv, w.d, w.n_kv_cap
+            self.kv = z.KVCache(ctx, 1, n, n_ctx, hkv, d, z.KV_KT, rope_base=1.0e6)
+            self.pos = (W.kv_lengths(5) - 1).astype(np.int32)
+            self.batch = True
+        elif name == "qwen05_prefill_kv_append":
+            w = W.WORKLOADS[4]
+            self.description = "Qwen2.5-0.5B prefill cache update: 2048 tokens, rotary q/k, K^T scatter"
+            n, h, hkv, d, n_ctx = w.n_q, w.n_head, w.n_head_kv, w.d, w.n_kv_cap
+            self.kv = z.KVCache(ctx, 1, 1, n_ctx, hkv, d, z.KV_KT, rope_base=1.0e6)
+            self.pos = np.arange(n, dtype=np.int32)
+            self.batch = False
+        else:
+            w = W.WORKLOADS[3]
+            self.description = "Whisper small.en decoder-step cache update: 32 windows x 1 token, row-major"
+            n, h, hkv, d, n_ctx = w.n_items, w.n_head, w.n_head_kv, w.d, w.n_kv_cap
+            self.kv = z.KVCache(ctx, 1, n, n_ctx, hkv, d, z.KV_ROW)
+            self.pos = (W.kv_lengths(3) - 1).astype(np.int32)
+            self.batch = True
+        self.n, self.h, self.hkv, self.d, self.n_ctx = n, h, hkv, d, n_ctx
+        self.rope = name != "small_dec_kv_append_x32"
+        kvw, ne = hkv * d, h * d
+        self.host = {"k": rng.standard_normal((n, kvw)).astype(f32), "v": rng.standard_normal((n, kvw)).astype(f32),
+                     "q": rng.standard_normal((n, ne)).astype(f32)}
+        self.dev = {k: torch.from_numpy(a).cuda() for k, a in self.host.items()}
+        self.pos_dev = torch.from_numpy(self.pos).cuda()
+        rows = 2 * n * kvw * 4 * 2  # k, v read and written
+        if self.rope:
+            rows += 2 * n * ne * 4 + 2 * n * (d // 2) * 4  # q read + written, cos/sin rows
+        self.work = float(rows)
+
+    def step(self, i: int):
+        d = self.dev
+        q = d["q"] if self.rope else None
+        if self.batch:
+            self.kv.append_batch(0, 0, self.pos_dev, d["k"], d["v"], q, self.h, self.h * self.d)
+        else:
+            self.kv.append(0, 0, 0, d["k"], d["v"], q, self.h, self.h * self.d)
+
+    def device_time(self, steps: int) -> float:
+        """Mean device time of one update, in ms: `steps` updates captured back to back in a HIP
+        graph and replayed, so host launch overhead (larger than these kernels in this Python
+        harness) does not count.  The replay rotates q again each step; the timing does not
+        depend on the values."""
+        torch = self.torch
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self.step(0)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(steps):
+                self.step(i)
+        g.replay()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        best = float("inf")
+        for _ in range(3):
+            ev[0].record(stream)
+            g.replay()
+            ev[1].record(stream)
+            torch.cuda.synchronize()
+            best = min(best, ev[0].elapsed_time(ev[1]) / steps)
+        del g
+        return best
+
+    def cpu_baseline(self) -> dict:
+        """oracle/kv.py's vectorised update (the reference's loops of src/llm.zig:182-190 and
+        src/decoder.zig:182-183, in numpy), best of 5, on this host."""
+        from oracle import kv as okv
+
+        kvw = self.hkv * self.d
+        kt = np.zeros(kvw * self.n_ctx, np.float32)
+        cv = np.zeros(self.n_ctx * kvw, np.float32)
+        cos, sin = okv.rope_tables(self.n_ctx, self.d, 1.0e6) if self.rope else (None, None)
+
+        def run():
+            if self.rope:
+                # one sequence's cache stands in for each of the batch's, as each token writes its own
+                okv.llm_append_vec(self.host["q"].copy(), self.host["k"], self.host["v"], self.pos, self.h, self.hkv,
+                                   self.d, kt, cv, self.n_ctx, cos, sin)
+            else:  # row-major self caches: k and v rows at their positions (src/decoder.zig:182-183)
+                kt.reshape(self.n_ctx, kvw)[self.pos] = self.host["k"]
+                cv.reshape(self.n_ctx, kvw)[self.pos] = self.host["v"]
+
+        run()
+        best = float("inf")
+        for _ in range(5):
+            t0 = time.perf_counter()
+            run()
+            best = min(best, time.perf_counter() - t0)
+        return {"value": self.work / best / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": "the whole update; oracle/kv.py llm_append_vec (numpy, one thread), best of 5",
+                "seconds": best}
+
+    def free(self):
+        self.kv.close()
+        self.dev = None
 
 
 def time_workload(wl: Workload, steps: int, warmup: int) -> dict:
@@ -332,6 +460,27 @@ def main() -> int:
         wl.free()
         del wl
         torch.cuda.empty_cache()
+    if not args.only:
+        for name in ("small_dec_kv_append_x32", "qwen15_kv_append_x64", "qwen05_prefill_kv_append"):
+            wl = AppendWorkload(name, torch, ctx)
+            r = time_workload(wl, args.steps, args.warmup)
+            dev_ms = wl.device_time(max(args.steps, 20))
+            achieved = wl.work / (dev_ms * 1e-3)
+            res = {"workload": name, "description": wl.description,
+                   "value": wl.work / (r["ms_per_step"] * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": r["ms_per_step"],
+                   "kernel_ms_mean": dev_ms, "kernel_ms_note": "device time per update, from a HIP graph of "
+                   "back-to-back updates; ms_per_step includes this Python harness's launch overhead",
+                   "algorithmic_work_per_step": wl.work,
+                   "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                                "frac": achieved / PEAK_HBM, "traffic": None}}
+            if not args.no_cpu:
+                res["cpu_baseline"] = wl.cpu_baseline()
+            results[name] = res
+            print(f"[bench] {name}: {res['value']:.2f} GB/s ({r['ms_per_step']:.4f} ms/step, device "
+                  f"{dev_ms:.4f} ms, {100 * res['roofline']['frac']:.1f}% of hbm peak)"
+                  + (f", cpu {res['cpu_baseline']['value']:.3f} GB/s" if not args.no_cpu else ""),
+                  file=sys.stderr, flush=True)
+            wl.free()
     ctx.close()
 
     head = results[args.workload]

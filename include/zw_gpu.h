@@ -136,6 +136,76 @@ int zwg_plan(const zwg_attn_shape *shape, const zwg_batch *batch, uint64_t works
 /* Shape check alone (same rules as the calls), host-only.  0 ok, 2 with a message. */
 int zwg_check_shape(const zwg_attn_shape *shape, char *msg, size_t msg_len);
 
+/*
+ * Device-resident KV caches.  The reference's callers own host caches and fill them on the
+ * CPU: the Whisper decoder writes each token's K/V projections into row-major caches
+ * (src/decoder.zig:39-42, :182-183) and a window's cross K/V once (src/decoder.zig:151-159);
+ * Qwen2 rotates q and k (NeoX rotary positions, src/llm.zig:182-183, :221-238, tables
+ * :128-137), scatters k into a transposed cache and copies v (src/llm.zig:185-190).
+ * A zwg_kv keeps those caches in HBM, one per (layer, sequence), and appends to them on the
+ * device; attention then reads them in place through zwg_attention_dev / _batch_dev with the
+ * pointers and strides of zwg_kv_get_info.  These calls replace the cache writes around
+ * ops.attentionEx; the attention entry points above are unchanged.
+ */
+typedef struct zwg_kv zwg_kv;
+
+#define ZWG_KV_ROW 0u /* k, v: [n_ctx][n_head_kv*d] (Whisper decoder self and cross caches) */
+#define ZWG_KV_KT 1u  /* k: [n_head_kv][d][n_ctx] transposed, v: [n_ctx][n_head_kv*d] (Qwen2) */
+
+typedef struct zwg_kv_desc {
+    uint64_t n_layer;
+    uint64_t n_seq;     /* independent sequences: decoder windows, LLM sequences */
+    uint64_t n_ctx;     /* positions per sequence (a multiple of 4 for ZWG_KV_KT) */
+    uint64_t n_head_kv;
+    uint64_t d;         /* 32, 64 or 128 */
+    uint32_t layout;    /* ZWG_KV_ROW or ZWG_KV_KT */
+    uint32_t reserved;  /* must be 0 */
+    double rope_base;   /* > 0: NeoX rotary positions with this base (qwen2.rope.freq_base,
+                           src/llm.zig:101) applied to appended keys and to q; 0: none */
+} zwg_kv_desc;
+
+/* Where the caches are, for the attention calls.  Layer l, sequence s: k + l*layer_stride +
+ * s*seq_stride (likewise v); a batch of consecutive sequences is a zwg_batch with
+ * k_bstride = v_bstride = seq_stride. */
+typedef struct zwg_kv_info {
+    float *k;
+    float *v;
+    uint64_t layer_stride; /* floats */
+    uint64_t seq_stride;   /* floats */
+    uint64_t kv_stride;    /* the attention shape's kv_stride: n_head_kv * d */
+    uint64_t kt_stride;    /* the attention shape's kt_stride: n_ctx for ZWG_KV_KT, 0 for ZWG_KV_ROW */
+} zwg_kv_info;
+
+/* Flag of zwg_kv_append: k_rows, v_rows (and q) are host memory.  The call stages them through
+ * the context, hands the rotated q back, and returns when the cache holds the rows. */
+#define ZWG_ROWS_ON_HOST 1u
+
+/* Allocate the caches of `desc` on ctx's device (zeroed; rotary tables built on the host in
+ * f64 and rounded to f32, as src/llm.zig:128-137).  *out is NULL on failure. */
+int zwg_kv_create(zwg_ctx *ctx, const zwg_kv_desc *desc, zwg_kv **out);
+void zwg_kv_destroy(zwg_kv *kv);
+int zwg_kv_get_info(const zwg_kv *kv, zwg_kv_info *out);
+
+/*
+ * Append n rows to (layer, seq) at positions pos .. pos+n-1 (pos + n <= n_ctx).  k_rows, v_rows:
+ * [n][n_head_kv*d], the new keys and values before rotation.  With rope_base > 0 the keys are
+ * rotated at their positions, and q (if not NULL: [n][q_stride], n_head heads of d, rotated in
+ * place) too -- src/llm.zig:182-190 as one kernel.  Device pointers (16-byte aligned; q_stride a
+ * multiple of 4) and asynchronous on the context's stream, unless flags has ZWG_ROWS_ON_HOST.
+ */
+int zwg_kv_append(zwg_kv *kv, uint64_t layer, uint64_t seq, uint64_t pos, uint64_t n, const float *k_rows,
+                  const float *v_rows, float *q, uint64_t n_head, uint64_t q_stride, uint32_t flags);
+
+/* One new row for each of the sequences seq0 .. seq0+n_seq-1 (a batched decode step), at the
+ * positions in the device int32 array pos_dev[n_seq]; row i of k_rows, v_rows and q belongs to
+ * sequence seq0 + i.  A position outside [0, n_ctx) is skipped.  Device pointers, asynchronous. */
+int zwg_kv_append_batch(zwg_kv *kv, uint64_t layer, uint64_t seq0, uint64_t n_seq, const int32_t *pos_dev,
+                        const float *k_rows, const float *v_rows, float *q, uint64_t n_head, uint64_t q_stride);
+
+/* Copy one (layer, seq) cache to host memory (k_host, v_host: n_ctx*n_head_kv*d floats each,
+ * either may be NULL), in the cache's own layout.  Synchronous. */
+int zwg_kv_read(zwg_kv *kv, uint64_t layer, uint64_t seq, float *k_host, float *v_host);
+
 int zwg_version(void); /* ZWG_VERSION */
 
 #ifdef __cplusplus

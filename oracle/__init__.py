@@ -9,8 +9,10 @@ Contents:
   ops.attentionEx / attention / pvBlock / expVec / softmaxRow / Pool (oracle/attn_oracle.c,
   which cites src/ops.zig and src/gemm.zig line by line).
 * ``naive``: the f64 closed form (oracle/naive.py).
+* ``kv``: the reference's cache writes -- rotary tables and NeoX rotation, the transposed key
+  scatter, row appends (oracle/kv.py, citing src/llm.zig and src/decoder.zig).
 
-Parity pinning of each function lives in tests/test_oracle.py.
+Parity pinning of each function lives in tests/test_oracle.py and tests/test_kv_oracle.py.
 """
 from __future__ import annotations
 

@@ -1,13 +1,15 @@
 """zwhisper_amd: zwhisper's attention hot path (src/ops.zig:464-605) on AMD MI355X (gfx950).
 
 The compute is libzwgpu.so (HIP, built by ``python -m zwhisper_amd.build``) behind the C ABI in
-include/zw_gpu.h; ``zwhisper_amd.ops`` mirrors the reference's ``ops`` interface on top of it.
+include/zw_gpu.h; ``zwhisper_amd.ops`` mirrors the reference's ``ops`` interface on top of it, and
+``KVCache`` keeps the decoder and LLM caches in HBM (the cache writes of src/decoder.zig:182-183
+and src/llm.zig:182-190).
 """
-from ._lib import ZwgError
-from .ops import (AttnShape, Context, V, attention, attentionEx, attentionScratch, attentionScratchEx,
+from ._lib import KV_KT, KV_ROW, ZwgError
+from .ops import (AttnShape, Context, KVCache, V, attention, attentionEx, attentionScratch, attentionScratchEx,
                   attentionScratchKT, check_shape, default_context, plan, q_block)
 
 __all__ = [
-    "AttnShape", "Context", "V", "ZwgError", "attention", "attentionEx", "attentionScratch", "attentionScratchEx",
-    "attentionScratchKT", "check_shape", "default_context", "plan", "q_block",
+    "AttnShape", "Context", "KVCache", "KV_KT", "KV_ROW", "V", "ZwgError", "attention", "attentionEx",
+    "attentionScratch", "attentionScratchEx", "attentionScratchKT", "check_shape", "default_context", "plan", "q_block",
 ]

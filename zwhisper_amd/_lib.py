@@ -66,6 +66,35 @@ class PlanC(ctypes.Structure):
     ]
 
 
+class KVDescC(ctypes.Structure):
+    _fields_ = [
+        ("n_layer", _u64),
+        ("n_seq", _u64),
+        ("n_ctx", _u64),
+        ("n_head_kv", _u64),
+        ("d", _u64),
+        ("layout", ctypes.c_uint32),
+        ("reserved", ctypes.c_uint32),
+        ("rope_base", ctypes.c_double),
+    ]
+
+
+class KVInfoC(ctypes.Structure):
+    _fields_ = [
+        ("k", ctypes.c_void_p),
+        ("v", ctypes.c_void_p),
+        ("layer_stride", _u64),
+        ("seq_stride", _u64),
+        ("kv_stride", _u64),
+        ("kt_stride", _u64),
+    ]
+
+
+KV_ROW = 0
+KV_KT = 1
+ROWS_ON_HOST = 1
+
+
 def declared_symbols() -> list[str]:
     """Every function the C header declares."""
     with open(HEADER) as f:
@@ -109,6 +138,18 @@ def lib() -> ctypes.CDLL:
     L.zwg_plan.argtypes = [ctypes.POINTER(ShapeC), ctypes.POINTER(BatchC), _u64, ctypes.POINTER(PlanC)]
     L.zwg_check_shape.restype = c_int
     L.zwg_check_shape.argtypes = [ctypes.POINTER(ShapeC), ctypes.c_char_p, ctypes.c_size_t]
+    L.zwg_kv_create.restype = c_int
+    L.zwg_kv_create.argtypes = [vp, ctypes.POINTER(KVDescC), ctypes.POINTER(vp)]
+    L.zwg_kv_destroy.restype = None
+    L.zwg_kv_destroy.argtypes = [vp]
+    L.zwg_kv_get_info.restype = c_int
+    L.zwg_kv_get_info.argtypes = [vp, ctypes.POINTER(KVInfoC)]
+    L.zwg_kv_append.restype = c_int
+    L.zwg_kv_append.argtypes = [vp, _u64, _u64, _u64, _u64, _fp, _fp, _fp, _u64, _u64, ctypes.c_uint32]
+    L.zwg_kv_append_batch.restype = c_int
+    L.zwg_kv_append_batch.argtypes = [vp, _u64, _u64, _u64, vp, _fp, _fp, _fp, _u64, _u64]
+    L.zwg_kv_read.restype = c_int
+    L.zwg_kv_read.argtypes = [vp, _u64, _u64, _fp, _fp]
     _lib = L
     return L
 

@@ -1,0 +1,32 @@
+// The library context behind the opaque zwg_ctx of include/zw_gpu.h, and the error / staging
+// helpers the C ABI translation units share (zw_gpu.hip, kv_cache.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "zw_gpu.h"
+
+struct zwg_ctx {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    float *workspace = nullptr;
+    uint64_t workspace_bytes = 0;
+    // device staging for the host-pointer calls: q, k, v, out
+    float *stage[4] = {nullptr, nullptr, nullptr, nullptr};
+    uint64_t stage_bytes[4] = {0, 0, 0, 0};
+    std::string err;
+};
+
+namespace zwg_host {
+
+// Record `msg` as the last error (of ctx, and of this thread) and return ZWG_ERROR.
+int fail(zwg_ctx *ctx, const std::string &msg);
+int fail_hip(zwg_ctx *ctx, const char *what, hipError_t e);
+// Grow staging buffer i of ctx to at least `bytes` (synchronises the stream when it grows).
+int ensure_stage(zwg_ctx *ctx, int i, uint64_t bytes);
+
+} // namespace zwg_host

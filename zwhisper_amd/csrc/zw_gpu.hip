@@ -10,18 +10,43 @@
 #include <string>
 
 #include "attn_kernels.hpp"
+#include "zw_ctx.hpp"
 
-struct zwg_ctx {
-    int device = 0;
-    hipStream_t own_stream = nullptr;
-    hipStream_t stream = nullptr;
-    float *workspace = nullptr;
-    uint64_t workspace_bytes = 0;
-    // device staging for the host-pointer calls: q, k, v, out
-    float *stage[4] = {nullptr, nullptr, nullptr, nullptr};
-    uint64_t stage_bytes[4] = {0, 0, 0, 0};
-    std::string err;
-};
+namespace zwg_host {
+
+thread_local std::string t_err;
+
+int fail(zwg_ctx *ctx, const std::string &msg) {
+    t_err = msg;
+    if (ctx) ctx->err = msg;
+    return ZWG_ERROR;
+}
+
+int fail_hip(zwg_ctx *ctx, const char *what, hipError_t e) {
+    return fail(ctx, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int ensure_stage(zwg_ctx *ctx, int i, uint64_t bytes) {
+    bytes = std::max<uint64_t>(bytes, 256);
+    if (ctx->stage_bytes[i] >= bytes) return ZWG_OK;
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return fail_hip(ctx, "hipStreamSynchronize", e);
+    if (ctx->stage[i]) {
+        (void)hipFree(ctx->stage[i]);
+        ctx->stage[i] = nullptr;
+        ctx->stage_bytes[i] = 0;
+    }
+    void *p = nullptr;
+    e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return fail_hip(ctx, "hipMalloc (staging)", e);
+    ctx->stage[i] = static_cast<float *>(p);
+    ctx->stage_bytes[i] = bytes;
+    return ZWG_OK;
+}
+
+} // namespace zwg_host
+
+using namespace zwg_host;
 
 namespace {
 
@@ -48,18 +73,6 @@ constexpr uint64_t kMaxSplitUnitsHint = 1ull << 22;
 #ifndef ZWG_FLASH_CAUSAL_BLOCKS_PER_CU
 #define ZWG_FLASH_CAUSAL_BLOCKS_PER_CU 6 // ... for causal calls, dispatched longest-first
 #endif
-
-thread_local std::string t_err;
-
-int fail(zwg_ctx *ctx, const std::string &msg) {
-    t_err = msg;
-    if (ctx) ctx->err = msg;
-    return ZWG_ERROR;
-}
-
-int fail_hip(zwg_ctx *ctx, const char *what, hipError_t e) {
-    return fail(ctx, std::string(what) + ": " + hipGetErrorString(e));
-}
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -240,24 +253,6 @@ int run(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_
         e = zwg::launch_combine(a, (int)s.d, ctx->stream);
         if (e != hipSuccess) return fail_hip(ctx, "combine kernel launch", e);
     }
-    return ZWG_OK;
-}
-
-int ensure_stage(zwg_ctx *ctx, int i, uint64_t bytes) {
-    bytes = std::max<uint64_t>(bytes, 256);
-    if (ctx->stage_bytes[i] >= bytes) return ZWG_OK;
-    hipError_t e = hipStreamSynchronize(ctx->stream);
-    if (e != hipSuccess) return fail_hip(ctx, "hipStreamSynchronize", e);
-    if (ctx->stage[i]) {
-        (void)hipFree(ctx->stage[i]);
-        ctx->stage[i] = nullptr;
-        ctx->stage_bytes[i] = 0;
-    }
-    void *p = nullptr;
-    e = hipMalloc(&p, bytes);
-    if (e != hipSuccess) return fail_hip(ctx, "hipMalloc (staging)", e);
-    ctx->stage[i] = static_cast<float *>(p);
-    ctx->stage_bytes[i] = bytes;
     return ZWG_OK;
 }
 

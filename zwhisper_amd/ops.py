@@ -166,6 +166,8 @@ class Context:
 
         if t is None:
             return 0
+        if isinstance(t, int):  # a raw device address (e.g. a KVCache's cache pointers)
+            return t
         if not isinstance(t, torch.Tensor) or not t.is_cuda or t.dtype != torch.float32:
             raise ZwgError(f"{name} must be a CUDA float32 tensor")
         return t.data_ptr()
@@ -192,6 +194,87 @@ class Context:
         self._check(self._L.zwg_attention_batch_dev(self._h, self._dev_ptr(q, "q"), self._dev_ptr(k, "k"),
                                                     self._dev_ptr(v, "v"), ctypes.byref(c), ctypes.byref(b),
                                                     self._dev_ptr(out, "out")))
+
+
+class KVCache:
+    """Device-resident KV caches of one context (zwg_kv_*): per (layer, sequence), in the Whisper
+    decoder's row-major layout (layout=KV_ROW) or Qwen2's transposed-key layout (layout=KV_KT),
+    with NeoX rotary positions applied on append when rope_base > 0."""
+
+    def __init__(self, ctx: Context, n_layer: int, n_seq: int, n_ctx: int, n_head_kv: int, d: int,
+                 layout: int = _lib.KV_ROW, rope_base: float = 0.0):
+        self.ctx = ctx
+        self._L = ctx._L
+        self.desc = _lib.KVDescC(n_layer, n_seq, n_ctx, n_head_kv, d, layout, 0, rope_base)
+        h = ctypes.c_void_p()
+        rc = self._L.zwg_kv_create(ctx.handle, ctypes.byref(self.desc), ctypes.byref(h))
+        if rc != _lib.ZWG_OK:
+            raise ZwgError(_lib.last_error(ctx.handle))
+        self._h = h
+        self.n_layer, self.n_seq, self.n_ctx, self.n_head_kv, self.d = n_layer, n_seq, n_ctx, n_head_kv, d
+        self.layout = layout
+        self.kvw = n_head_kv * d
+        self.info = _lib.KVInfoC()
+        ctx._check(self._L.zwg_kv_get_info(self._h, ctypes.byref(self.info)))
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self._L.zwg_kv_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def ptrs(self, layer: int, seq: int = 0) -> tuple[int, int]:
+        """Device addresses of (layer, seq)'s K and V caches."""
+        off = 4 * (layer * self.info.layer_stride + seq * self.info.seq_stride)
+        return self.info.k + off, self.info.v + off
+
+    def append(self, layer: int, seq: int, pos: int, k_rows, v_rows, q=None, n_head: int = 0, q_stride: int = 0) -> None:
+        """Append rows at pos.. of (layer, seq): CUDA float32 tensors (asynchronous, torch's current
+        stream) or float32 numpy arrays (staged, synchronous; q is rotated in place either way)."""
+        if isinstance(k_rows, np.ndarray):
+            for name, a in (("k_rows", k_rows), ("v_rows", v_rows), ("q", q)):
+                if a is not None and (a.dtype != np.float32 or not a.flags["C_CONTIGUOUS"]):
+                    raise ZwgError(f"{name} must be a contiguous float32 array")
+            n = k_rows.size // self.kvw
+            self.ctx._check(self._L.zwg_kv_append(self._h, layer, seq, pos, n, k_rows.ctypes.data, v_rows.ctypes.data,
+                                                  q.ctypes.data if q is not None else None, n_head, q_stride,
+                                                  _lib.ROWS_ON_HOST))
+            return
+        self.ctx._bind_torch_stream()
+        n = k_rows.numel() // self.kvw
+        self.ctx._check(self._L.zwg_kv_append(self._h, layer, seq, pos, n, Context._dev_ptr(k_rows, "k_rows"),
+                                              Context._dev_ptr(v_rows, "v_rows"), Context._dev_ptr(q, "q"), n_head,
+                                              q_stride, 0))
+
+    def append_batch(self, layer: int, seq0: int, pos_dev, k_rows, v_rows, q=None, n_head: int = 0,
+                     q_stride: int = 0) -> None:
+        """One row per sequence seq0.. at the positions in pos_dev (CUDA int32 tensor)."""
+        import torch
+
+        if not pos_dev.is_cuda or pos_dev.dtype != torch.int32:
+            raise ZwgError("pos_dev must be a CUDA int32 tensor")
+        self.ctx._bind_torch_stream()
+        self.ctx._check(self._L.zwg_kv_append_batch(self._h, layer, seq0, pos_dev.numel(), pos_dev.data_ptr(),
+                                                    Context._dev_ptr(k_rows, "k_rows"), Context._dev_ptr(v_rows, "v_rows"),
+                                                    Context._dev_ptr(q, "q"), n_head, q_stride))
+
+    def read(self, layer: int, seq: int = 0) -> tuple[np.ndarray, np.ndarray]:
+        """(K, V) of (layer, seq) on the host, in the cache's layout (synchronous)."""
+        k = np.empty(self.n_ctx * self.kvw, np.float32)
+        v = np.empty(self.n_ctx * self.kvw, np.float32)
+        self.ctx._check(self._L.zwg_kv_read(self._h, layer, seq, k.ctypes.data, v.ctypes.data))
+        return k, v
 
 
 _tls = threading.local()
