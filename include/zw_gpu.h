@@ -206,6 +206,25 @@ int zwg_kv_append_batch(zwg_kv *kv, uint64_t layer, uint64_t seq0, uint64_t n_se
  * either may be NULL), in the cache's own layout.  Synchronous. */
 int zwg_kv_read(zwg_kv *kv, uint64_t layer, uint64_t seq, float *k_host, float *v_host);
 
+/*
+ * Linear layers: the drop-in for ops.linear (src/ops.zig:283-306) with f16 weights, the encoder's
+ * Q/K/V/O projections and MLP (src/encoder.zig:164-174), BERT's (src/bert.zig:223-232) and the
+ * scene model's (src/scene.zig:369-378).  out[i][o] = sum_p x[i][p] * w[o][p] (+ bias[o]), with
+ * x f32 [m][k], w [n][k] of type w_type, bias f32 [n] or NULL, out f32 [m][n].
+ * Computed on f16 MFMA with each x split into two f16 terms (f32-level accuracy; |x| must be
+ * within f16's range, 65504, or its output row turns inf).  k a multiple of 8; pointers 16-byte
+ * aligned.
+ */
+#define ZWG_W_F16 1u /* IEEE binary16 weights, as src/encoder.zig loads them */
+
+/* Host pointers, synchronous: the drop-in for ops.linear.  Stages x, w, bias and out through
+ * the context. */
+int zwg_linear(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void *w, uint32_t w_type,
+               const float *bias, uint64_t n, float *out);
+/* Device pointers, asynchronous on the context's stream. */
+int zwg_linear_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void *w, uint32_t w_type,
+                   const float *bias, uint64_t n, float *out);
+
 int zwg_version(void); /* ZWG_VERSION */
 
 #ifdef __cplusplus

@@ -6,8 +6,9 @@ library under zwhisper_amd/ — never imports, links or calls anything here.
 
 Contents:
 * ``Oracle``: ctypes front end to liboracle_v{3,4}.so, the C restatement of the reference's
-  ops.attentionEx / attention / pvBlock / expVec / softmaxRow / Pool (oracle/attn_oracle.c,
-  which cites src/ops.zig and src/gemm.zig line by line).
+  ops.attentionEx / attention / pvBlock / expVec / softmaxRow / Pool, and ops.linear with f16
+  weights (gemm.ntBlock) (oracle/attn_oracle.c, which cites src/ops.zig and src/gemm.zig line by
+  line).
 * ``naive``: the f64 closed form (oracle/naive.py).
 * ``kv``: the reference's cache writes -- rotary tables and NeoX rotation, the transposed key
   scatter, row appends (oracle/kv.py, citing src/llm.zig and src/decoder.zig).
@@ -103,6 +104,9 @@ def lib():
         L.ora_pv_block.argtypes = [_fp, _c_size, _fp, _c_size, _fp, _c_size, _c_size, _c_size, _c_size]
         L.ora_vector_width.restype = ctypes.c_int
         L.ora_q_block.restype = ctypes.c_int
+        L.ora_linear_f16.restype = None
+        L.ora_linear_f16.argtypes = [ctypes.c_void_p, _fp, _c_size, _c_size, ctypes.c_void_p, ctypes.c_void_p, _c_size,
+                                     _fp]
         _lib = L
     return _lib
 
@@ -183,6 +187,19 @@ class Oracle:
                                       scratch.size, _ptr(out))
         if rc != 0:
             raise ValueError(f"oracle rejected shape {sh}")
+        return out
+
+    def linear_f16(self, x, m: int, k: int, w, b, n: int, out=None) -> np.ndarray:
+        """ops.linear with f16 weights (src/ops.zig:283-306): x f32 [m][k], w float16 [n][k], b f32 [n] or None."""
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+        w = np.ascontiguousarray(w, dtype=np.float16).reshape(-1)
+        if x.size < m * k or w.size < n * k:
+            raise ValueError("x or w shorter than m*k / n*k")
+        bb = None if b is None else np.ascontiguousarray(b, dtype=np.float32).reshape(-1)
+        if out is None:
+            out = np.zeros(max(m * n, 1), dtype=np.float32)
+        self._L.ora_linear_f16(self._pool, _ptr(x), m, k, w.ctypes.data, None if bb is None else bb.ctypes.data, n,
+                               _ptr(out))
         return out
 
     def attention(self, q, k, v, n_q, n_kv, n_state, n_head, causal, out=None) -> np.ndarray:

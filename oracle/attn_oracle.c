@@ -19,6 +19,10 @@
  *   Pool ................... src/ops.zig:31-146    (ora_pool_*)
  *   small_op_macs .......... src/ops.zig:280
  *   q_block = 64 ........... src/ops.zig:473
+ *   ops.linear (f16 w) ..... src/ops.zig:283-306, LinearJob :247-275  (ora_linear_f16)
+ *   gemm.ntBlock ........... src/gemm.zig:117-137  (nt_block_f16)
+ *   gemm.micro4x4/1x4/dot1.. src/gemm.zig:40-115   (micro4x4_f16, micro1x4_f16, dot1_f16)
+ *   gemm.mc, nc ............ src/gemm.zig:27-28
  *
  * V, the vector width, is 16 (the reference's value on AVX-512 hosts, src/gemm.zig:15-24):
  * it fixes the K padding (n_kv_pad), the column count of S and the split between
@@ -470,3 +474,136 @@ void ora_pv_block(const float *p, size_t ldp, const float *v, size_t ldv, float 
 
 int ora_vector_width(void) { return V; }
 int ora_q_block(void) { return Q_BLOCK; }
+
+/* ---------------------------------------------------------------------------------------
+ * ops.linear with f16 weights (src/ops.zig:283-306; src/gemm.zig:27-137).
+ * out[i][o] = sum_p x[i][p] * w[o][p] (+ b[o]); w is IEEE binary16, widened per vector
+ * (src/gemm.zig:34-38).
+ * ------------------------------------------------------------------------------------- */
+
+#define GEMM_MC 64  /* src/gemm.zig:27 */
+#define GEMM_NC 128 /* src/gemm.zig:28 */
+
+/* IEEE binary16 -> f32, exact (every f16 value is an f32 value). */
+static inline float h2f(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1fu, man = h & 0x3ffu;
+    if (e == 0) { /* zero or subnormal: man * 2^-24 */
+        const float f = (float)man * 0x1p-24f;
+        return sign ? -f : f;
+    }
+    const uint32_t bits = e == 31 ? sign | 0x7f800000u | (man << 13) : sign | ((e + 112u) << 23) | (man << 13);
+    float f;
+    memcpy(&f, &bits, sizeof f);
+    return f;
+}
+
+static inline vf vload_h(const uint16_t *p) {
+    float t[V];
+    for (int i = 0; i < V; ++i) t[i] = h2f(p[i]);
+    return vload(t);
+}
+
+/* 4x4 micro-kernel (src/gemm.zig:40-75): c[i][j] = dot(a_i, b_j) over k. */
+static inline void micro4x4_f16(const float *a, size_t lda, const uint16_t *b, size_t ldb, size_t k, float *c,
+                                size_t ldc) {
+    vf acc[4][4];
+    for (int i = 0; i < 4; ++i)
+        for (int j = 0; j < 4; ++j) acc[i][j] = (vf){0};
+    size_t p = 0;
+    for (; p + V <= k; p += V) {
+        vf va[4], vb[4];
+        for (int i = 0; i < 4; ++i) va[i] = vload(a + i * lda + p);
+        for (int j = 0; j < 4; ++j) vb[j] = vload_h(b + j * ldb + p);
+        for (int i = 0; i < 4; ++i)
+            for (int j = 0; j < 4; ++j) acc[i][j] = va[i] * vb[j] + acc[i][j];
+    }
+    float s[4][4];
+    for (int i = 0; i < 4; ++i)
+        for (int j = 0; j < 4; ++j) s[i][j] = hsum(acc[i][j]);
+    for (; p < k; ++p)
+        for (int i = 0; i < 4; ++i)
+            for (int j = 0; j < 4; ++j) s[i][j] += a[i * lda + p] * h2f(b[j * ldb + p]);
+    for (int i = 0; i < 4; ++i)
+        for (int j = 0; j < 4; ++j) c[i * ldc + j] = s[i][j];
+}
+
+/* 1x4 rows (src/gemm.zig:78-101). */
+static inline void micro1x4_f16(const float *a, const uint16_t *b, size_t ldb, size_t k, float *c) {
+    vf acc[4] = {{0}, {0}, {0}, {0}};
+    size_t p = 0;
+    for (; p + V <= k; p += V) {
+        const vf va = vload(a + p);
+        for (int j = 0; j < 4; ++j) acc[j] = va * vload_h(b + j * ldb + p) + acc[j];
+    }
+    float s[4];
+    for (int j = 0; j < 4; ++j) s[j] = hsum(acc[j]);
+    for (; p < k; ++p)
+        for (int j = 0; j < 4; ++j) s[j] += a[p] * h2f(b[j * ldb + p]);
+    for (int j = 0; j < 4; ++j) c[j] = s[j];
+}
+
+/* One row against one weight row (src/gemm.zig:106-113). */
+static inline float dot1_f16(const float *a, const uint16_t *b, size_t k) {
+    vf acc = (vf){0};
+    size_t p = 0;
+    for (; p + V <= k; p += V) acc = vload(a + p) * vload_h(b + p) + acc;
+    float s = hsum(acc);
+    for (; p < k; ++p) s += a[p] * h2f(b[p]);
+    return s;
+}
+
+/* Rows [m0,m1) of a against weight rows [n0,n1) (src/gemm.zig:117-137). */
+static void nt_block_f16(const float *a, size_t lda, const uint16_t *b, size_t ldb, float *c, size_t ldc, size_t m0,
+                         size_t m1, size_t n0, size_t n1, size_t k) {
+    size_t j = n0;
+    for (; j + 4 <= n1; j += 4) {
+        const uint16_t *bj = b + j * ldb;
+        size_t i = m0;
+        for (; i + 4 <= m1; i += 4) micro4x4_f16(a + i * lda, lda, bj, ldb, k, c + i * ldc + j, ldc);
+        for (; i < m1; ++i) micro1x4_f16(a + i * lda, bj, ldb, k, c + i * ldc + j);
+    }
+    for (; j < n1; ++j)
+        for (size_t i = m0; i < m1; ++i) c[i * ldc + j] = dot1_f16(a + i * lda, b + j * ldb, k);
+}
+
+typedef struct linear_job {
+    const float *x;
+    const uint16_t *w;
+    const float *b;
+    float *out;
+    size_t m, n, k, mb, nb, n_mblocks;
+} linear_job;
+
+/* LinearJob.run (src/ops.zig:260-274): one (m-block, n-block) task, then its bias. */
+static void linear_task(void *raw, size_t task) {
+    const linear_job *j = raw;
+    const size_t mi = task % j->n_mblocks, ni = task / j->n_mblocks;
+    const size_t m0 = mi * j->mb, m1 = m0 + j->mb < j->m ? m0 + j->mb : j->m;
+    const size_t n0 = ni * j->nb, n1 = n0 + j->nb < j->n ? n0 + j->nb : j->n;
+    nt_block_f16(j->x, j->k, j->w, j->k, j->out, j->n, m0, m1, n0, n1, j->k);
+    if (j->b)
+        for (size_t i = m0; i < m1; ++i)
+            for (size_t o = n0; o < n1; ++o) j->out[i * j->n + o] += j->b[o];
+}
+
+/* ops.linear (src/ops.zig:283-306): serial below small_op_macs, else m-blocks of mc rows and
+ * n-blocks halved until there are at least 3 tasks per thread. */
+void ora_linear_f16(ora_pool *pool, const float *x, size_t m, size_t k, const uint16_t *w, const float *b, size_t n,
+                    float *out) {
+    if (m * n * k < SMALL_OP_MACS) {
+        nt_block_f16(x, k, w, k, out, n, 0, m, 0, n, k);
+        if (b)
+            for (size_t i = 0; i < m; ++i)
+                for (size_t o = 0; o < n; ++o) out[i * n + o] += b[o];
+        return;
+    }
+    const size_t mb = m >= GEMM_MC ? GEMM_MC : m;
+    size_t nb = GEMM_NC;
+    const size_t n_mblocks = (m + mb - 1) / mb;
+    const size_t want = ora_pool_size(pool) * 3;
+    while (n_mblocks * ((n + nb - 1) / nb) < want && nb > 4) nb /= 2;
+    linear_job job = {.x = x, .w = w, .b = b, .out = out, .m = m, .n = n, .k = k, .mb = mb, .nb = nb,
+                      .n_mblocks = n_mblocks};
+    pool_parallel_for(pool, n_mblocks * ((n + nb - 1) / nb), &job, linear_task);
+}

@@ -1,0 +1,135 @@
+"""GPU parity of the linear layer (zwg_linear / zwg_linear_dev, f16 weights) against the f64
+closed form and the oracle's ops.linear (src/ops.zig:283-306).
+
+Bar: max abs error <= 2e-5 * sqrt(k) on outputs of unit scale (x ~ N(0, 1), w ~ N(0, 1/k)), the
+size of the reference's own f32 accumulation error, and never worse than the oracle by more
+than that.  Known answers: with identity or one-hot weights every output is exactly the two-term
+split's value, f32(w*hi + w*lo) with hi = f16(x), lo = f16(x - hi) -- which keeps 22 of f32's 24
+significand bits of x.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch
+
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU on this machine")
+    return torch
+
+
+@pytest.fixture(scope="module")
+def ctx(torch):
+    import zwhisper_amd as z
+
+    c = z.Context(0)
+    yield c
+    c.close()
+
+
+def inputs(seed, m, k, n, bias=True):
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w = (rng.standard_normal((n, k)) / np.sqrt(k)).astype(np.float16)
+    b = rng.standard_normal(n).astype(np.float32) if bias else None
+    return x, w, b
+
+
+def run_dev(torch, ctx, x, w, b, m, k, n):
+    out = torch.full((m, n), float("nan"), device="cuda")
+    ctx.linear_dev(torch.from_numpy(x).cuda(), m, k, torch.from_numpy(w).cuda(),
+                   None if b is None else torch.from_numpy(b).cuda(), n, out)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def ref64(x, w, b):
+    r = x.astype(np.float64) @ w.astype(np.float64).T
+    return r if b is None else r + b.astype(np.float64)[None, :]
+
+
+@pytest.mark.parametrize("m,k,n", [
+    (1500, 384, 384),    # tiny.en Q/K/V/O (src/encoder.zig:164-168)
+    (1500, 384, 1536),   # tiny.en MLP up (:172)
+    (1500, 1536, 384),   # tiny.en MLP down (:174)
+    (1500, 512, 512),    # base.en projections
+    (3000, 240, 384),    # conv1 as a linear over im2col rows, k = 80 mels x 3 (:139)
+    (7, 8, 5), (1, 64, 1), (65, 72, 130), (129, 520, 257),  # tails in m, n and k
+])
+def test_linear_matches_reference(torch, ctx, m, k, n):
+    x, w, b = inputs(m * 7 + n, m, k, n)
+    got = run_dev(torch, ctx, x, w, b, m, k, n)
+    ref = ref64(x, w, b)
+    err = float(np.abs(got - ref).max())
+    bar = 2e-5 * np.sqrt(k)
+    print(f"linear {m}x{k}x{n}: max abs {err:.2e} (bar {bar:.1e})", flush=True)
+    assert np.all(np.isfinite(got)) and err <= bar
+    if m * n * k <= 50_000_000:
+        with oracle.Oracle(4) as o:
+            ora = o.linear_f16(x, m, k, w, b, n).reshape(m, n)
+        assert float(np.abs(got - ora).max()) <= err + bar
+
+
+def split_product(x, wv):
+    """What one weight times x gives through the two-term split: f32(wv*hi + wv*lo), hi = f16(x),
+    lo = f16(x - hi) -- both products exact in f32, one rounding for the sum."""
+    hi = x.astype(np.float16).astype(np.float32)
+    lo = (x - hi).astype(np.float16).astype(np.float32)
+    w = np.float32(wv)
+    return (w * hi + w * lo).astype(np.float32)
+
+
+def test_identity_and_one_hot(torch, ctx):
+    """With one nonzero weight per output, the result is exactly the split's value."""
+    m, k = 300, 64
+    x = np.random.default_rng(1).standard_normal((m, k)).astype(np.float32)
+    x[0, :8] = [1e-4, -3e-5, 7e-8, 65000.0, -1.0, 0.0, 1.0 / 3.0, 2.0 ** -14]  # subnormal lo, large, exact
+    got = run_dev(torch, ctx, x, np.eye(k, dtype=np.float16), None, m, k, k)
+    assert np.array_equal(got, split_product(x, 1.0))
+    assert np.max(np.abs(got - x) / np.maximum(np.abs(x), 2.0 ** -4)) <= 2.0 ** -21
+    w = np.zeros((2, k), np.float16)
+    w[0, 3] = 1
+    w[1, 63] = -2
+    got = run_dev(torch, ctx, x, w, None, m, k, 2)
+    assert np.array_equal(got[:, 0], split_product(x[:, 3], 1.0))
+    assert np.array_equal(got[:, 1], split_product(x[:, 63], -2.0))
+
+
+def test_host_dropin(torch, ctx):
+    """zwhisper_amd.linear: ops.linear's call form on host arrays."""
+    import zwhisper_amd as z
+
+    m, k, n = 200, 128, 96
+    x, w, b = inputs(9, m, k, n)
+    out = np.zeros(m * n, np.float32)
+    z.linear(None, x.reshape(-1), m, k, w, b, n, out)
+    assert float(np.abs(out.reshape(m, n) - ref64(x, w, b)).max()) <= 2e-5 * np.sqrt(k)
+
+
+def test_large_input_turns_inf_not_wrong(torch, ctx):
+    """An input beyond f16's range makes its output row non-finite rather than silently wrong."""
+    m, k, n = 4, 16, 8
+    x, w, _ = inputs(3, m, k, n, bias=False)
+    x[2, 5] = 1e6
+    got = run_dev(torch, ctx, x, w, None, m, k, n)
+    assert not np.all(np.isfinite(got[2]))
+    assert np.all(np.isfinite(got[[0, 1, 3]]))
+
+
+def test_linear_errors(torch, ctx):
+    import zwhisper_amd as z
+
+    t = torch.zeros(64, device="cuda")
+    w = torch.zeros(64, dtype=torch.float16, device="cuda")
+    with pytest.raises(z.ZwgError, match="multiple of 8"):
+        ctx.linear_dev(t, 2, 12, w, None, 2, t)
+    with pytest.raises(z.ZwgError, match="float16"):
+        ctx.linear_dev(t, 2, 8, t, None, 2, t)

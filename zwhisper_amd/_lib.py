@@ -92,6 +92,7 @@ class KVInfoC(ctypes.Structure):
 
 KV_ROW = 0
 KV_KT = 1
+W_F16 = 1
 ROWS_ON_HOST = 1
 
 
@@ -150,6 +151,9 @@ def lib() -> ctypes.CDLL:
     L.zwg_kv_append_batch.argtypes = [vp, _u64, _u64, _u64, vp, _fp, _fp, _fp, _u64, _u64]
     L.zwg_kv_read.restype = c_int
     L.zwg_kv_read.argtypes = [vp, _u64, _u64, _fp, _fp]
+    for name in ("zwg_linear", "zwg_linear_dev"):
+        getattr(L, name).restype = c_int
+        getattr(L, name).argtypes = [vp, _fp, _u64, _u64, vp, ctypes.c_uint32, _fp, _u64, _fp]
     _lib = L
     return L
 

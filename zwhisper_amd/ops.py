@@ -172,6 +172,18 @@ class Context:
             raise ZwgError(f"{name} must be a CUDA float32 tensor")
         return t.data_ptr()
 
+    def linear_dev(self, x, m: int, k: int, w, bias, n: int, out) -> None:
+        """out[m][n] = x[m][k] . w[n][k]^T (+ bias): CUDA tensors, x/bias/out float32, w float16."""
+        import torch
+
+        if not isinstance(w, torch.Tensor) or not w.is_cuda or w.dtype != torch.float16:
+            raise ZwgError("w must be a CUDA float16 tensor")
+        if x.numel() < m * k or w.numel() < n * k or out.numel() < m * n or (bias is not None and bias.numel() < n):
+            raise ZwgError("a tensor is shorter than m, n and k need")
+        self._bind_torch_stream()
+        self._check(self._L.zwg_linear_dev(self._h, self._dev_ptr(x, "x"), m, k, w.data_ptr(), _lib.W_F16,
+                                           self._dev_ptr(bias, "bias"), n, self._dev_ptr(out, "out")))
+
     def attention_dev(self, q, k, v, sh: AttnShape, out) -> None:
         self._bind_torch_stream()
         c = sh.to_c()
@@ -303,6 +315,24 @@ def attentionEx(pool, q, k, v, sh: AttnShape, scratch, out) -> None:
         raise ZwgError("out must be a contiguous float32 numpy array")
     q, k, v = _as_f32(q, "q"), _as_f32(k, "k"), _as_f32(v, "v")
     default_context().attention_ex_host(q, k, v, sh, out.reshape(-1))
+
+
+def linear(pool, x, m: int, k: int, w, b, n: int, out) -> None:
+    """ops.linear (src/ops.zig:283-306) with f16 weights: out[i][o] = sum_p x[i][p] * w[o][p] (+ b[o]).
+    x f32 [m][k], w float16 [n][k], b f32 [n] or None, out f32 [m][n]; host arrays, synchronous."""
+    del pool  # the GPU context replaces the thread pool
+    x = _as_f32(x, "x")
+    w = np.asarray(w)
+    if w.dtype != np.float16 or not w.flags["C_CONTIGUOUS"]:
+        raise ZwgError("w must be a contiguous float16 array")
+    bb = None if b is None else _as_f32(b, "b")
+    if not isinstance(out, np.ndarray) or out.dtype != np.float32 or not out.flags["C_CONTIGUOUS"]:
+        raise ZwgError("out must be a contiguous float32 array")
+    if x.size < m * k or w.size < n * k or out.size < m * n or (bb is not None and bb.size < n):
+        raise ZwgError("a buffer is shorter than m, n and k need")
+    ctx = default_context()
+    ctx._check(ctx._L.zwg_linear(ctx.handle, x.ctypes.data, m, k, w.ctypes.data, _lib.W_F16,
+                                 None if bb is None else bb.ctypes.data, n, out.ctypes.data))
 
 
 def attention(pool, q, k, v, n_q: int, n_kv: int, n_state: int, n_head: int, causal: bool, scratch, out) -> None:
