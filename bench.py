@@ -20,7 +20,9 @@ timed on this host's cores on a bounded sample of the same workload.
 Unless --only, the line also carries the device cache updates of three of the workloads (the K/V
 rows of a step written into the HBM-resident caches, with rotary positions for Qwen2), as
 "small_dec_kv_append_x32", "qwen15_kv_append_x64" and "qwen05_prefill_kv_append", each with an
-HBM roofline and oracle/kv.py's update timed beside it.
+HBM roofline and oracle/kv.py's update timed beside it, and the six linear layers of a base.en
+encoder layer over the 16 windows ("base_enc_linear_x16", f16 weights on f16 MFMA) with the
+oracle's ops.linear timed beside it.
 """
 from __future__ import annotations
 
@@ -36,6 +38,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_MFMA_F32 = 157.3e12  # FLOP/s, MI355X dense fp32 matrix
+PEAK_MFMA_F16 = 2500e12  # FLOP/s, MI355X dense fp16 matrix
 PEAK_HBM = 8.0e12  # B/s, MI355X HBM3E
 
 
@@ -279,6 +282,68 @@ class AppendWorkload:
         self.dev = None
 
 
+class LinearWorkload:
+    """The six linear layers of one Whisper base.en encoder layer over 16 windows x 1500 frames
+    (src/encoder.zig:164-174): q, k, v and out projections (512 -> 512), MLP up (512 -> 2048) and
+    down (2048 -> 512), f16 weights, f32 activations and bias, through zwg_linear_dev.
+
+    Algorithmic work: 2 m n k flops per layer, m = 24000 rows.  The kernels run on f16 MFMA with
+    each f32 activation split into two f16 terms, so their ceiling is half the f16 peak.
+    """
+
+    name = "base_enc_linear_x16"
+    description = ("Whisper base.en encoder layer projections, 16 windows x 1500 frames: q/k/v/o 512->512, "
+                   "MLP 512->2048->512, f16 weights")
+
+    def __init__(self, torch, ctx, windows: int = 16):
+        self.torch = torch
+        self.ctx = ctx
+        self.m = windows * 1500
+        d, f = 512, 2048
+        self.layers = [(d, d)] * 4 + [(d, f), (f, d)]  # (k, n)
+        g = torch.Generator(device="cuda").manual_seed(0x11EA)
+        self.x = {kk: torch.randn(self.m, kk, device="cuda", generator=g) for kk in (d, f)}
+        self.out = {nn: torch.empty(self.m, nn, device="cuda") for nn in (d, f)}
+        self.w = [(torch.randn(n, k, device="cuda", generator=g) / np.sqrt(k)).half() for k, n in self.layers]
+        self.b = [torch.randn(n, device="cuda", generator=g) for _, n in self.layers]
+        self.work = float(sum(2 * self.m * n * k for k, n in self.layers))
+
+    def step(self, i: int):
+        for (k, n), w, b in zip(self.layers, self.w, self.b):
+            self.ctx.linear_dev(self.x[k], self.m, k, w, b, n, self.out[n])
+
+    def cpu_baseline(self, threads: int) -> dict:
+        """The oracle's ops.linear with f16 weights (oracle/attn_oracle.c, the reference's ntBlock
+        over its Pool) on one of the 16 windows, best of 3 after a warm-up."""
+        import oracle
+
+        rows = 1500
+        xs = {kk: v[:rows].cpu().numpy() for kk, v in self.x.items()}
+        ws = [w.cpu().numpy() for w in self.w]
+        bs = [b.cpu().numpy() for b in self.b]
+        outs = {nn: np.zeros(rows * nn, np.float32) for nn in self.out}
+        o = oracle.Oracle(threads)
+
+        def run():
+            for (k, n), w, b in zip(self.layers, ws, bs):
+                o.linear_f16(xs[k], rows, k, w, b, n, out=outs[n])
+
+        run()
+        best = float("inf")
+        for _ in range(3):
+            t0 = time.perf_counter()
+            run()
+            best = min(best, time.perf_counter() - t0)
+        o.close()
+        work = self.work * rows / self.m
+        return {"value": work / best / 1e12, "unit": "TFLOP/s", "cores": o.threads, "kind": "port",
+                "sample": "1 of 16 windows (1500 rows), all six layers; oracle/attn_oracle.c ora_linear_f16, "
+                          "best of 3 after one warm-up", "seconds": best}
+
+    def free(self):
+        self.x = self.out = self.w = self.b = None
+
+
 def time_workload(wl: Workload, steps: int, warmup: int) -> dict:
     torch = wl.torch
     for i in range(warmup):
@@ -481,6 +546,25 @@ def main() -> int:
                   + (f", cpu {res['cpu_baseline']['value']:.3f} GB/s" if not args.no_cpu else ""),
                   file=sys.stderr, flush=True)
             wl.free()
+        wl = LinearWorkload(torch, ctx)
+        r = time_workload(wl, args.steps, args.warmup)
+        achieved = wl.work / (r["kernel_ms_mean"] * 1e-3)
+        res = {"workload": wl.name, "description": wl.description,
+               "value": wl.work / (r["ms_per_step"] * 1e-3) / 1e12, "unit": "TFLOP/s",
+               "ms_per_step": r["ms_per_step"], "kernel_ms_mean": r["kernel_ms_mean"],
+               "kernel_ms_min": r["kernel_ms_min"], "algorithmic_work_per_step": wl.work,
+               "dtype": "f32 activations x f16 weights, f32 accumulation (f16 MFMA, x split into two f16 terms)",
+               "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_MFMA_F16 / 1e12,
+                            "unit": "TFLOP/s", "frac": achieved / PEAK_MFMA_F16, "traffic": traffic_for(wl.name),
+                            "note": "two f16 MFMAs per f32 x f16 product: the kernels' ceiling is frac 0.5"}}
+        if not args.no_cpu:
+            res["cpu_baseline"] = wl.cpu_baseline(host_threads())
+        results[wl.name] = res
+        print(f"[bench] {wl.name}: {res['value']:.2f} TFLOP/s ({r['ms_per_step']:.4f} ms/step, kernels "
+              f"{r['kernel_ms_mean']:.4f} ms, {100 * res['roofline']['frac']:.1f}% of f16 mfma peak)"
+              + (f", cpu {res['cpu_baseline']['value']:.3f} TFLOP/s" if not args.no_cpu else ""),
+              file=sys.stderr, flush=True)
+        wl.free()
     ctx.close()
 
     head = results[args.workload]
