@@ -7,8 +7,8 @@ library under zwhisper_amd/ — never imports, links or calls anything here.
 Contents:
 * ``Oracle``: ctypes front end to liboracle_v{3,4}.so, the C restatement of the reference's
   ops.attentionEx / attention / pvBlock / expVec / softmaxRow / Pool, and ops.linear with f16
-  weights (gemm.ntBlock) (oracle/attn_oracle.c, which cites src/ops.zig and src/gemm.zig line by
-  line).
+  weights (gemm.ntBlock) or int8 block weights (gemm.Q8, Q8.quantize, ntBlockQ)
+  (oracle/attn_oracle.c, which cites src/ops.zig and src/gemm.zig line by line).
 * ``naive``: the f64 closed form (oracle/naive.py).
 * ``kv``: the reference's cache writes -- rotary tables and NeoX rotation, the transposed key
   scatter, row appends (oracle/kv.py, citing src/llm.zig and src/decoder.zig).
@@ -107,8 +107,36 @@ def lib():
         L.ora_linear_f16.restype = None
         L.ora_linear_f16.argtypes = [ctypes.c_void_p, _fp, _c_size, _c_size, ctypes.c_void_p, ctypes.c_void_p, _c_size,
                                      _fp]
+        L.ora_linear_q8.restype = None
+        L.ora_linear_q8.argtypes = [ctypes.c_void_p, _fp, _c_size, _c_size, ctypes.c_void_p, _fp, ctypes.c_void_p,
+                                    _c_size, _fp]
+        L.ora_q8_quantize.restype = None
+        L.ora_q8_quantize.argtypes = [_fp, _c_size, _c_size, ctypes.c_void_p, _fp]
         _lib = L
     return _lib
+
+
+Q8_BLOCK = 32
+
+
+def q8_quantize(w, n: int, k: int):
+    """gemm.Q8.quantize (src/gemm.zig:209-230) of an [n][k] f16 or f32 matrix: (q int8 [n][k],
+    scales f32 [n][k / 32])."""
+    if k % Q8_BLOCK:
+        raise ValueError("k must be a multiple of 32")
+    w = np.ascontiguousarray(np.asarray(w).reshape(-1)[: n * k], dtype=np.float32)
+    q = np.zeros(n * k, np.int8)
+    sc = np.zeros(n * (k // Q8_BLOCK), np.float32)
+    lib().ora_q8_quantize(_ptr(w), n, k, q.ctypes.data, _ptr(sc))
+    return q.reshape(n, k), sc.reshape(n, k // Q8_BLOCK)
+
+
+def q8_dequantize(q, scales) -> np.ndarray:
+    """Q8.row (src/gemm.zig:255-263) for every row: f32(q) * scale, [n][k]."""
+    q = np.asarray(q, dtype=np.int8)
+    n, k = q.shape
+    return (q.reshape(n, k // Q8_BLOCK, Q8_BLOCK).astype(np.float32)
+            * np.asarray(scales, np.float32).reshape(n, -1, 1)).reshape(n, k)
 
 
 def _ptr(a: np.ndarray):
@@ -200,6 +228,23 @@ class Oracle:
             out = np.zeros(max(m * n, 1), dtype=np.float32)
         self._L.ora_linear_f16(self._pool, _ptr(x), m, k, w.ctypes.data, None if bb is None else bb.ctypes.data, n,
                                _ptr(out))
+        return out
+
+    def linear_q8(self, x, m: int, k: int, q, scales, b, n: int, out=None) -> np.ndarray:
+        """ops.linear with gemm.Q8 weights (src/ops.zig:283-306, src/gemm.zig:336-351): q int8
+        [n][k], scales f32 [n][k / 32], k a multiple of 32."""
+        if k % Q8_BLOCK:
+            raise ValueError("k must be a multiple of 32")
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+        q = np.ascontiguousarray(q, dtype=np.int8).reshape(-1)
+        sc = np.ascontiguousarray(scales, dtype=np.float32).reshape(-1)
+        if x.size < m * k or q.size < n * k or sc.size < n * (k // Q8_BLOCK):
+            raise ValueError("x, q or scales shorter than the shape needs")
+        bb = None if b is None else np.ascontiguousarray(b, dtype=np.float32).reshape(-1)
+        if out is None:
+            out = np.zeros(max(m * n, 1), dtype=np.float32)
+        self._L.ora_linear_q8(self._pool, _ptr(x), m, k, q.ctypes.data, _ptr(sc),
+                              None if bb is None else bb.ctypes.data, n, _ptr(out))
         return out
 
     def attention(self, q, k, v, n_q, n_kv, n_state, n_head, causal, out=None) -> np.ndarray:

@@ -22,6 +22,9 @@
  *   ops.linear (f16 w) ..... src/ops.zig:283-306, LinearJob :247-275  (ora_linear_f16)
  *   gemm.ntBlock ........... src/gemm.zig:117-137  (nt_block_f16)
  *   gemm.micro4x4/1x4/dot1.. src/gemm.zig:40-115   (micro4x4_f16, micro1x4_f16, dot1_f16)
+ *   ops.linear (Q8 w) ...... src/ops.zig:283-306, gemm.ntBlockQ :336-351 (ora_linear_q8)
+ *   gemm.Q8.quantize ....... src/gemm.zig:209-230  (ora_q8_quantize)
+ *   gemm.dotQ / micro4x4Q .. src/gemm.zig:274-333  (dot_q8, micro4x4_q8)
  *   gemm.mc, nc ............ src/gemm.zig:27-28
  *
  * V, the vector width, is 16 (the reference's value on AVX-512 hosts, src/gemm.zig:15-24):
@@ -569,11 +572,16 @@ static void nt_block_f16(const float *a, size_t lda, const uint16_t *b, size_t l
 
 typedef struct linear_job {
     const float *x;
-    const uint16_t *w;
+    const uint16_t *w;   /* f16 weights, or NULL for int8 blocks */
+    const int8_t *q;     /* int8 blocks [n][k] */
+    const float *scales; /* [n][k / 32] */
     const float *b;
     float *out;
     size_t m, n, k, mb, nb, n_mblocks;
 } linear_job;
+
+static void nt_block_q8(const float *a, size_t lda, const int8_t *q, const float *scales, size_t k, float *c,
+                        size_t ldc, size_t m0, size_t m1, size_t n0, size_t n1);
 
 /* LinearJob.run (src/ops.zig:260-274): one (m-block, n-block) task, then its bias. */
 static void linear_task(void *raw, size_t task) {
@@ -581,7 +589,10 @@ static void linear_task(void *raw, size_t task) {
     const size_t mi = task % j->n_mblocks, ni = task / j->n_mblocks;
     const size_t m0 = mi * j->mb, m1 = m0 + j->mb < j->m ? m0 + j->mb : j->m;
     const size_t n0 = ni * j->nb, n1 = n0 + j->nb < j->n ? n0 + j->nb : j->n;
-    nt_block_f16(j->x, j->k, j->w, j->k, j->out, j->n, m0, m1, n0, n1, j->k);
+    if (j->w)
+        nt_block_f16(j->x, j->k, j->w, j->k, j->out, j->n, m0, m1, n0, n1, j->k);
+    else
+        nt_block_q8(j->x, j->k, j->q, j->scales, j->k, j->out, j->n, m0, m1, n0, n1);
     if (j->b)
         for (size_t i = m0; i < m1; ++i)
             for (size_t o = n0; o < n1; ++o) j->out[i * j->n + o] += j->b[o];
@@ -589,13 +600,14 @@ static void linear_task(void *raw, size_t task) {
 
 /* ops.linear (src/ops.zig:283-306): serial below small_op_macs, else m-blocks of mc rows and
  * n-blocks halved until there are at least 3 tasks per thread. */
-void ora_linear_f16(ora_pool *pool, const float *x, size_t m, size_t k, const uint16_t *w, const float *b, size_t n,
-                    float *out) {
+static void linear_any(ora_pool *pool, const float *x, size_t m, size_t k, const uint16_t *w, const int8_t *q,
+                       const float *scales, const float *b, size_t n, float *out) {
+    linear_job job = {.x = x, .w = w, .q = q, .scales = scales, .b = b, .out = out, .m = m, .n = n, .k = k};
     if (m * n * k < SMALL_OP_MACS) {
-        nt_block_f16(x, k, w, k, out, n, 0, m, 0, n, k);
-        if (b)
-            for (size_t i = 0; i < m; ++i)
-                for (size_t o = 0; o < n; ++o) out[i * n + o] += b[o];
+        job.mb = m ? m : 1;
+        job.nb = n;
+        job.n_mblocks = 1;
+        linear_task(&job, 0);
         return;
     }
     const size_t mb = m >= GEMM_MC ? GEMM_MC : m;
@@ -603,7 +615,112 @@ void ora_linear_f16(ora_pool *pool, const float *x, size_t m, size_t k, const ui
     const size_t n_mblocks = (m + mb - 1) / mb;
     const size_t want = ora_pool_size(pool) * 3;
     while (n_mblocks * ((n + nb - 1) / nb) < want && nb > 4) nb /= 2;
-    linear_job job = {.x = x, .w = w, .b = b, .out = out, .m = m, .n = n, .k = k, .mb = mb, .nb = nb,
-                      .n_mblocks = n_mblocks};
+    job.mb = mb;
+    job.nb = nb;
+    job.n_mblocks = n_mblocks;
     pool_parallel_for(pool, n_mblocks * ((n + nb - 1) / nb), &job, linear_task);
+}
+
+void ora_linear_f16(ora_pool *pool, const float *x, size_t m, size_t k, const uint16_t *w, const float *b, size_t n,
+                    float *out) {
+    linear_any(pool, x, m, k, w, NULL, NULL, b, n, out);
+}
+
+/* ---------------------------------------------------------------------------------------
+ * Int8 block weights (gemm.Q8, src/gemm.zig:188-351): q int8 [n][k], scales f32 [n][k / 32],
+ * every block of 32 weights of a row scaled by one f32 (absmax / 127).
+ * ------------------------------------------------------------------------------------- */
+
+#define Q8_BLOCK 32 /* src/gemm.zig:194 */
+
+/* Q8.quantize (src/gemm.zig:209-230) of an f32 [n][k] matrix (f16 weights widen exactly):
+ * scale = amax / 127, q = clamp(round(v * (127 / amax)), -127, 127), rounding half away from
+ * zero (Zig's @round). */
+void ora_q8_quantize(const float *w, size_t n, size_t k, int8_t *q, float *scales) {
+    const size_t nb = k / Q8_BLOCK;
+    for (size_t i = 0; i < n; ++i)
+        for (size_t b = 0; b < nb; ++b) {
+            const float *src = w + i * k + b * Q8_BLOCK;
+            float amax = 0;
+            for (int t = 0; t < Q8_BLOCK; ++t) amax = fmaxf(amax, fabsf(src[t]));
+            const float scale = amax / 127.0f;
+            const float inv = amax > 0 ? 127.0f / amax : 0;
+            scales[i * nb + b] = scale;
+            for (int t = 0; t < Q8_BLOCK; ++t) {
+                const float r = roundf(src[t] * inv);
+                q[i * k + b * Q8_BLOCK + t] = (int8_t)fminf(fmaxf(r, -127.0f), 127.0f);
+            }
+        }
+}
+
+static inline vf vload_q(const int8_t *p) {
+    float t[V];
+    for (int i = 0; i < V; ++i) t[i] = (float)p[i];
+    return vload(t);
+}
+
+/* dotQ (src/gemm.zig:280-293): per block t = sum of a*q over V-wide FMA chains, then
+ * acc = t * scale + acc; one horizontal sum at the end. */
+static inline float dot_q8(const float *a, const int8_t *q, const float *sc, size_t nb) {
+    vf acc = (vf){0};
+    for (size_t b = 0; b < nb; ++b) {
+        vf t = (vf){0};
+        for (size_t c = 0; c < Q8_BLOCK / V; ++c) {
+            const size_t off = b * Q8_BLOCK + c * V;
+            t = vload(a + off) * vload_q(q + off) + t;
+        }
+        acc = t * vsplat(sc[b]) + acc;
+    }
+    return hsum(acc);
+}
+
+/* micro4x4Q (src/gemm.zig:296-333): 4 rows of a against 4 int8 rows, blocks as dotQ. */
+static inline void micro4x4_q8(const float *a, size_t lda, const int8_t *q, const float *scales, size_t k, size_t j,
+                               float *c, size_t ldc) {
+    const size_t nb = k / Q8_BLOCK;
+    vf acc[4][4];
+    for (int i = 0; i < 4; ++i)
+        for (int jj = 0; jj < 4; ++jj) acc[i][jj] = (vf){0};
+    for (size_t b = 0; b < nb; ++b) {
+        vf t[4][4];
+        for (int i = 0; i < 4; ++i)
+            for (int jj = 0; jj < 4; ++jj) t[i][jj] = (vf){0};
+        for (size_t ch = 0; ch < Q8_BLOCK / V; ++ch) {
+            const size_t off = b * Q8_BLOCK + ch * V;
+            vf va[4], vq[4];
+            for (int i = 0; i < 4; ++i) va[i] = vload(a + i * lda + off);
+            for (int jj = 0; jj < 4; ++jj) vq[jj] = vload_q(q + (j + jj) * k + off);
+            for (int i = 0; i < 4; ++i)
+                for (int jj = 0; jj < 4; ++jj) t[i][jj] = va[i] * vq[jj] + t[i][jj];
+        }
+        for (int jj = 0; jj < 4; ++jj) {
+            const vf sv = vsplat(scales[(j + jj) * nb + b]);
+            for (int i = 0; i < 4; ++i) acc[i][jj] = t[i][jj] * sv + acc[i][jj];
+        }
+    }
+    for (int i = 0; i < 4; ++i)
+        for (int jj = 0; jj < 4; ++jj) c[i * ldc + jj] = hsum(acc[i][jj]);
+}
+
+/* ntBlockQ (src/gemm.zig:336-351): 4x4 tiles, then the row tail by dotQ per weight row, then the
+ * column tail by dotQ. */
+static void nt_block_q8(const float *a, size_t lda, const int8_t *q, const float *scales, size_t k, float *c,
+                        size_t ldc, size_t m0, size_t m1, size_t n0, size_t n1) {
+    const size_t nb = k / Q8_BLOCK;
+    size_t j = n0;
+    for (; j + 4 <= n1; j += 4) {
+        size_t i = m0;
+        for (; i + 4 <= m1; i += 4) micro4x4_q8(a + i * lda, lda, q, scales, k, j, c + i * ldc + j, ldc);
+        for (; i < m1; ++i)
+            for (size_t jj = 0; jj < 4; ++jj)
+                c[i * ldc + j + jj] = dot_q8(a + i * lda, q + (j + jj) * k, scales + (j + jj) * nb, nb);
+    }
+    for (; j < n1; ++j)
+        for (size_t i = m0; i < m1; ++i) c[i * ldc + j] = dot_q8(a + i * lda, q + j * k, scales + j * nb, nb);
+}
+
+/* ops.linear with Q8 weights; k must be a multiple of 32 (Q8.quantize's assertion). */
+void ora_linear_q8(ora_pool *pool, const float *x, size_t m, size_t k, const int8_t *q, const float *scales,
+                   const float *b, size_t n, float *out) {
+    linear_any(pool, x, m, k, NULL, q, scales, b, n, out);
 }
