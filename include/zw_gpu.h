@@ -225,6 +225,27 @@ int zwg_linear(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void 
 int zwg_linear_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void *w, uint32_t w_type,
                    const float *bias, uint64_t n, float *out);
 
+/*
+ * Linear layers over int8 block weights: the drop-in for ops.linear with a gemm.Q8
+ * (src/ops.zig:283-306, src/gemm.zig:188-351 -- ntBlockQ :330-351, micro4x4Q :289-327,
+ * dotQ :274-286), the Whisper decoder's projections, MLP and logits (src/decoder.zig:181-205)
+ * and cross K/V (:151-159), and Qwen2's q/k/v/o, gate/up/down and output (src/llm.zig:179-216).
+ * q: int8 [n][k], scales: f32 [n][k / 32] (the Q8 struct's two arrays, as Q8.quantize and
+ * Q8.fromQ8_0 build them, src/gemm.zig:209-248):
+ *     out[i][o] = sum_b scales[o][b] * sum_{p in 32-block b} x[i][p] * q[o][p]  (+ bias[o])
+ * k a multiple of 32 (the Q8 assertion, src/gemm.zig:210); x, q and out 16-byte aligned, scales
+ * 4-byte aligned; |x| within f16's range (x is split into two f16 terms for the f16 MFMA, int8
+ * weights are exact in f16).  m <= 64 (token steps) streams the weights once from HBM.
+ */
+#define ZWG_W_Q8 2u /* int8 block weights + f32 block scales (zwg_linear_q8*) */
+
+/* Host pointers, synchronous. */
+int zwg_linear_q8(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const int8_t *q, const float *scales,
+                  const float *bias, uint64_t n, float *out);
+/* Device pointers, asynchronous on the context's stream. */
+int zwg_linear_q8_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const int8_t *q, const float *scales,
+                      const float *bias, uint64_t n, float *out);
+
 int zwg_version(void); /* ZWG_VERSION */
 
 #ifdef __cplusplus

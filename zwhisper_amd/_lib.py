@@ -93,6 +93,7 @@ class KVInfoC(ctypes.Structure):
 KV_ROW = 0
 KV_KT = 1
 W_F16 = 1
+W_Q8 = 2
 ROWS_ON_HOST = 1
 
 
@@ -154,6 +155,9 @@ def lib() -> ctypes.CDLL:
     for name in ("zwg_linear", "zwg_linear_dev"):
         getattr(L, name).restype = c_int
         getattr(L, name).argtypes = [vp, _fp, _u64, _u64, vp, ctypes.c_uint32, _fp, _u64, _fp]
+    for name in ("zwg_linear_q8", "zwg_linear_q8_dev"):
+        getattr(L, name).restype = c_int
+        getattr(L, name).argtypes = [vp, _fp, _u64, _u64, vp, _fp, _fp, _u64, _fp]
     _lib = L
     return L
 

@@ -1,17 +1,23 @@
 // Linear layers around attention on gfx950 MFMA (include/zw_gpu.h, zwg_linear*).
 //
-// Replaces ops.linear (src/ops.zig:283-306) with f16 weights: out[i][o] = sum_p x[i][p] * w[o][p]
-// (+ b[o]), x f32 [m][k], w f16 [n][k] (logically [n][k], as the reference keeps them), over the
-// register-blocked broadcast-FMA kernels of src/gemm.zig:117-137 (ntBlock / micro4x4 / dot1).
-// Callers: the encoder's Q/K/V/O projections and MLP (src/encoder.zig:164-174), BERT
-// (src/bert.zig:223-232), the scene model (src/scene.zig:369-378).  The kernel, its precision
-// and its tiling are described in linear_kernel.hpp.
+// Replaces ops.linear (src/ops.zig:283-306): out[i][o] = sum_p x[i][p] * w[o][p] (+ b[o]), x f32
+// [m][k], w logically [n][k] as the reference keeps it, over the register-blocked broadcast-FMA
+// kernels of src/gemm.zig.
+//   * f16 weights (ntBlock / micro4x4 / dot1, src/gemm.zig:117-137): the encoder's Q/K/V/O
+//     projections and MLP (src/encoder.zig:164-174), BERT (src/bert.zig:223-232), the scene
+//     model (src/scene.zig:369-378).
+//   * int8 block weights (gemm.Q8, ntBlockQ / micro4x4Q / dotQ, src/gemm.zig:188-351): the
+//     Whisper decoder's projections, MLP and logits (src/decoder.zig:181-205) and cross K/V
+//     (:151-159), Qwen2's q/k/v/o, gate/up/down and output (src/llm.zig:179-216).
+// The kernels, their precision and tiling are described in linear_kernel.hpp and
+// linear_q8_kernel.hpp.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <string>
 
 #include "linear_kernel.hpp"
+#include "linear_q8_kernel.hpp"
 #include "zw_ctx.hpp"
 #include "zw_gpu.h"
 
@@ -24,35 +30,94 @@ int64_t tiles(uint64_t m, uint64_t n, int bm, int bn) { return (int64_t)((m + bm
 
 // Tile choice (swept on the device over the encoder, decoder and Qwen2 projection shapes): the
 // 128 x 256 tile when it gives two workgroups per CU (256 CUs), else 64 x 256 when that fills
-// the CUs once, else 64 x 64 for the small single-window shapes, which are latency bound.
-hipError_t launch_linear(const LinearArgs &a, hipStream_t stream) {
-    if (tiles(a.m, a.n, 128, 256) >= 512) return zwg_lin::launch_linear_tile<128, 256>(a, stream);
-    if (tiles(a.m, a.n, 64, 256) >= 256) return zwg_lin::launch_linear_tile<64, 256>(a, stream);
-    return zwg_lin::launch_linear_tile<64, 64>(a, stream);
+// the CUs once, else 64 x 64 for the small single-window shapes, which are latency bound.  Int8
+// weights take 128 x 128 in place of 128 x 256: the block sums need 16 more VGPRs per tile row,
+// which would leave the larger tile one wave per SIMD.
+template <bool Q8>
+hipError_t launch_tiled(const LinearArgs &a, hipStream_t stream) {
+    if constexpr (Q8) {
+        if (tiles(a.m, a.n, 128, 128) >= 512) return zwg_lin::launch_linear_tile<128, 128, true>(a, stream);
+    } else {
+        if (tiles(a.m, a.n, 128, 256) >= 512) return zwg_lin::launch_linear_tile<128, 256, false>(a, stream);
+    }
+    if (tiles(a.m, a.n, 64, 256) >= 256) return zwg_lin::launch_linear_tile<64, 256, Q8>(a, stream);
+    return zwg_lin::launch_linear_tile<64, 64, Q8>(a, stream);
 }
 
 std::string check_linear(uint64_t m, uint64_t k, uint32_t w_type, uint64_t n) {
-    if (w_type != ZWG_W_F16) return "w_type must be ZWG_W_F16";
+    if (w_type != ZWG_W_F16 && w_type != ZWG_W_Q8) return "w_type must be ZWG_W_F16 or ZWG_W_Q8";
     if (k == 0 || k % 8) return "k must be a positive multiple of 8";
+    if (w_type == ZWG_W_Q8 && k % 32) return "k must be a multiple of 32 for int8 block weights";
     if (m > 0x7fffffffull || n > 0x7fffffffull || k > 0x7fffffffull) return "m, n and k must be below 2^31";
     if ((n + 63) / 64 > 65535) return "n too large (above 65535 x 64)";
     if (k > (1ull << 20)) return "k above 2^20";  // keeps a workgroup's buffer range below 2^31 bytes
     return "";
 }
 
+// Q8 with m <= 64: the weight-streaming kernel.  Four waves of S slabs of 32 weight rows per
+// workgroup (S = 2 when that alone makes >= 256 workgroups, else 1); k is split over more
+// workgroups, at chunk granularity, until there are about 512 of them, as long as the partial
+// sums fit the workspace.
+int run_q8_stream(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const int8_t *q, const float *scales,
+                  const float *bias, uint64_t n, float *out) {
+    zwg_lin::Q8Args a{};
+    a.x = x;
+    a.q = q;
+    a.scales = scales;
+    a.bias = bias;
+    a.out = out;
+    a.m = (int32_t)m;
+    a.n = (int32_t)n;
+    a.k = (int32_t)k;
+    a.nb = (int32_t)(k / zwg_lin::kQ8Block);
+    const int S = (n + 255) / 256 >= 256 ? 2 : 1;
+    const int64_t gx = (int64_t)((n + 128 * S - 1) / (128 * S));
+    const int n_chunks = (int)((k + zwg_lin::kQ8Chunk - 1) / zwg_lin::kQ8Chunk);
+    int n_split = 1;
+    if (gx < 512) n_split = (int)std::min<int64_t>(n_chunks, (512 + gx - 1) / gx);
+    while (n_split > 1 && (uint64_t)n_split * m * n * 4 > ctx->workspace_bytes) --n_split;
+    a.chunks_per_split = (n_chunks + n_split - 1) / n_split;
+    n_split = (n_chunks + a.chunks_per_split - 1) / a.chunks_per_split; // no empty splits
+    a.n_split = n_split;
+    a.part = n_split > 1 ? ctx->workspace : nullptr;
+    dim3 grid((unsigned)gx, (unsigned)n_split);
+    const bool two = m > 32;
+    if (S == 2) {
+        if (two) zwg_lin::linear_q8_stream_kernel<2, 2><<<grid, zwg_lin::kQ8Threads, 0, ctx->stream>>>(a);
+        else zwg_lin::linear_q8_stream_kernel<1, 2><<<grid, zwg_lin::kQ8Threads, 0, ctx->stream>>>(a);
+    } else {
+        if (two) zwg_lin::linear_q8_stream_kernel<2, 1><<<grid, zwg_lin::kQ8Threads, 0, ctx->stream>>>(a);
+        else zwg_lin::linear_q8_stream_kernel<1, 1><<<grid, zwg_lin::kQ8Threads, 0, ctx->stream>>>(a);
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail_hip(ctx, "linear (int8 stream) kernel launch", e);
+    if (n_split > 1) {
+        const int64_t mn = (int64_t)(m * n);
+        zwg_lin::linear_split_sum_kernel<<<(unsigned)((mn + 255) / 256), 256, 0, ctx->stream>>>(
+            ctx->workspace, bias, out, mn, (int32_t)n, n_split);
+        e = hipGetLastError();
+        if (e != hipSuccess) return fail_hip(ctx, "linear split-sum kernel launch", e);
+    }
+    return ZWG_OK;
+}
+
 int run_linear(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void *w, uint32_t w_type,
-               const float *bias, uint64_t n, float *out) {
+               const float *scales, const float *bias, uint64_t n, float *out) {
     const std::string msg = check_linear(m, k, w_type, n);
     if (!msg.empty()) return fail(ctx, msg);
     if (m == 0 || n == 0) return ZWG_OK;
-    if (!x || !w || !out) return fail(ctx, "null x, w or out");
+    if (!x || !w || !out || (w_type == ZWG_W_Q8 && !scales)) return fail(ctx, "null x, w, scales or out");
     const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
     if (!al16(x) || !al16(w) || !al16(out)) return fail(ctx, "x, w and out must be 16-byte aligned");
+    if (scales && (reinterpret_cast<uintptr_t>(scales) & 3u)) return fail(ctx, "scales must be 4-byte aligned");
     hipError_t e = hipSetDevice(ctx->device);
     if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
+    if (w_type == ZWG_W_Q8 && m <= 64)
+        return run_q8_stream(ctx, x, m, k, static_cast<const int8_t *>(w), scales, bias, n, out);
     LinearArgs a{};
     a.x = x;
-    a.w = static_cast<const _Float16 *>(w);
+    a.w = w;
+    a.scales = scales;
     a.bias = bias;
     a.out = out;
     a.ldx = (int64_t)k;
@@ -61,8 +126,40 @@ int run_linear(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void 
     a.m = (int32_t)m;
     a.n = (int32_t)n;
     a.k = (int32_t)k;
-    e = launch_linear(a, ctx->stream);
+    a.nb = (int32_t)(k / 32);
+    e = w_type == ZWG_W_Q8 ? launch_tiled<true>(a, ctx->stream) : launch_tiled<false>(a, ctx->stream);
     if (e != hipSuccess) return fail_hip(ctx, "linear kernel launch", e);
+    return ZWG_OK;
+}
+
+// Host-pointer form: stages x (slot 0), the weights (slot 1), the scales and bias (slot 2) and
+// out (slot 3) through the context, then waits.
+int run_linear_host(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void *w, uint32_t w_type,
+                    const float *scales, const float *bias, uint64_t n, float *out) {
+    const std::string msg = check_linear(m, k, w_type, n);
+    if (!msg.empty()) return fail(ctx, msg);
+    if (m == 0 || n == 0) return ZWG_OK;
+    if (!x || !w || !out || (w_type == ZWG_W_Q8 && !scales)) return fail(ctx, "null x, w, scales or out");
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
+    const uint64_t xb = m * k * 4, wb = n * k * (w_type == ZWG_W_Q8 ? 1 : 2);
+    const uint64_t sb = w_type == ZWG_W_Q8 ? n * (k / 32) * 4 : 0;
+    const uint64_t sb_al = (sb + 15) / 16 * 16, bb = bias ? n * 4 : 0, ob = m * n * 4;
+    if (ensure_stage(ctx, 0, xb) || ensure_stage(ctx, 1, wb) || ensure_stage(ctx, 2, sb_al + bb + 16) ||
+        ensure_stage(ctx, 3, ob))
+        return ZWG_ERROR;
+    float *d_scales = sb ? ctx->stage[2] : nullptr;
+    float *d_bias = bias ? reinterpret_cast<float *>(reinterpret_cast<char *>(ctx->stage[2]) + sb_al) : nullptr;
+    e = hipMemcpyAsync(ctx->stage[0], x, xb, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(ctx->stage[1], w, wb, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess && sb) e = hipMemcpyAsync(d_scales, scales, sb, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess && bias) e = hipMemcpyAsync(d_bias, bias, bb, hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess) return fail_hip(ctx, "hipMemcpyAsync (linear upload)", e);
+    int rc = run_linear(ctx, ctx->stage[0], m, k, ctx->stage[1], w_type, d_scales, d_bias, n, ctx->stage[3]);
+    if (rc != ZWG_OK) return rc;
+    e = hipMemcpyAsync(out, ctx->stage[3], ob, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return fail_hip(ctx, "linear download", e);
     return ZWG_OK;
 }
 
@@ -73,34 +170,27 @@ extern "C" {
 int zwg_linear_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void *w, uint32_t w_type,
                    const float *bias, uint64_t n, float *out) {
     if (!ctx) return fail(nullptr, "null context");
-    return run_linear(ctx, x, m, k, w, w_type, bias, n, out);
+    if (w_type != ZWG_W_F16) return fail(ctx, "zwg_linear_dev takes ZWG_W_F16 weights (zwg_linear_q8_dev: int8)");
+    return run_linear(ctx, x, m, k, w, w_type, nullptr, bias, n, out);
 }
 
 int zwg_linear(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void *w, uint32_t w_type,
                const float *bias, uint64_t n, float *out) {
     if (!ctx) return fail(nullptr, "null context");
-    const std::string msg = check_linear(m, k, w_type, n);
-    if (!msg.empty()) return fail(ctx, msg);
-    if (m == 0 || n == 0) return ZWG_OK;
-    if (!x || !w || !out) return fail(ctx, "null x, w or out");
-    hipError_t e = hipSetDevice(ctx->device);
-    if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
-    // staging: x in slot 0, w in slot 1, bias then out in slots 2 and 3
-    const uint64_t xb = m * k * 4, wb = n * k * 2, bb = bias ? n * 4 : 0, ob = m * n * 4;
-    if (ensure_stage(ctx, 0, xb) || ensure_stage(ctx, 1, wb) || ensure_stage(ctx, 2, bb + 16) ||
-        ensure_stage(ctx, 3, ob))
-        return ZWG_ERROR;
-    e = hipMemcpyAsync(ctx->stage[0], x, xb, hipMemcpyHostToDevice, ctx->stream);
-    if (e == hipSuccess) e = hipMemcpyAsync(ctx->stage[1], w, wb, hipMemcpyHostToDevice, ctx->stream);
-    if (e == hipSuccess && bias) e = hipMemcpyAsync(ctx->stage[2], bias, bb, hipMemcpyHostToDevice, ctx->stream);
-    if (e != hipSuccess) return fail_hip(ctx, "hipMemcpyAsync (linear upload)", e);
-    int rc = run_linear(ctx, ctx->stage[0], m, k, ctx->stage[1], w_type, bias ? ctx->stage[2] : nullptr, n,
-                        ctx->stage[3]);
-    if (rc != ZWG_OK) return rc;
-    e = hipMemcpyAsync(out, ctx->stage[3], ob, hipMemcpyDeviceToHost, ctx->stream);
-    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-    if (e != hipSuccess) return fail_hip(ctx, "linear download", e);
-    return ZWG_OK;
+    if (w_type != ZWG_W_F16) return fail(ctx, "zwg_linear takes ZWG_W_F16 weights (zwg_linear_q8: int8)");
+    return run_linear_host(ctx, x, m, k, w, w_type, nullptr, bias, n, out);
+}
+
+int zwg_linear_q8_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const int8_t *q, const float *scales,
+                      const float *bias, uint64_t n, float *out) {
+    if (!ctx) return fail(nullptr, "null context");
+    return run_linear(ctx, x, m, k, q, ZWG_W_Q8, scales, bias, n, out);
+}
+
+int zwg_linear_q8(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const int8_t *q, const float *scales,
+                  const float *bias, uint64_t n, float *out) {
+    if (!ctx) return fail(nullptr, "null context");
+    return run_linear_host(ctx, x, m, k, q, ZWG_W_Q8, scales, bias, n, out);
 }
 
 } // extern "C"

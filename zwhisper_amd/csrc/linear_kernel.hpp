@@ -1,5 +1,6 @@
 // The linear-layer kernel on gfx950 MFMA: out[i][o] = sum_p x[i][p] * w[o][p] (+ b[o]), x f32,
-// w f16, out f32 (ops.linear with f16 weights, src/ops.zig:283-306, src/gemm.zig:117-137).
+// w f16 or int8 blocks, out f32 (ops.linear with f16 weights, src/ops.zig:283-306,
+// src/gemm.zig:117-137; with gemm.Q8 weights, src/gemm.zig:188-351).
 //
 // Precision.  An f16 weight is exact in f16, and each f32 activation is split into two f16
 // terms, x = hi + lo with hi = f16(x) and lo = f16(x - hi): they keep 22 of x's 24 significand
@@ -20,6 +21,12 @@
 // no padding, so two workgroups of the 128 x 256 tile fit a CU's LDS.  MFMA operand layout
 // (measured on the device): lane l, half s of A is A[l % 32][8 (l / 32) + s], of B is
 // B[8 (l / 32) + s][l % 32]; result register r of lane l is C[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
+//
+// Int8 block weights (Q8 = true; gemm.Q8, src/gemm.zig:188-351).  A stage of BK = 32 is exactly
+// one Q8 block, so the weight tile is widened from int8 to f16 (exact) on its way into LDS, the
+// stage's MFMAs accumulate into a zeroed block sum, and the block sum is scaled by the weight
+// row's f32 scale into the accumulator (one scale per lane and 32-column tile: the result column
+// is the weight row).  The scales of the next stage are loaded with its tiles.
 //
 // Bounds.  Loads go through buffer descriptors whose range ends at the workgroup's last row of
 // x (or w): rows past m (or n) read as 0 in hardware, and a K column past k gets an offset
@@ -43,13 +50,33 @@ constexpr int BK = 32;                 // K per LDS stage: one 64-byte LDS row
 constexpr uint32_t kOutOfRange = 0x80000000u; // a buffer offset past every range the host allows
 
 struct LinearArgs {
-    const float *x;    // [m][ldx]
-    const _Float16 *w; // [n][ldw]
-    const float *bias; // [n] or nullptr
-    float *out;        // [m][ldo]
+    const float *x;      // [m][ldx]
+    const void *w;       // [n][ldw]: f16, or int8 for Q8 weights
+    const float *scales; // Q8 weights: [n][nb] f32 block scales
+    const float *bias;   // [n] or nullptr
+    float *out;          // [m][ldo]
     int64_t ldx, ldw, ldo;
-    int32_t m, n, k;
+    int32_t m, n, k, nb;
 };
+
+// Eight int8 (two dwords) to eight exact f16: the biased byte b + 128 is placed under the
+// exponent bits of 1024.0 (0x64), which gives 1024 + b + 128, and 1152 is taken off in f16.
+__device__ __forceinline__ half8 int8x8_to_half8(uint32_t w0, uint32_t w1) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+    half8 r;
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+        const uint32_t u = (d ? w1 : w0) ^ 0x80808080u;
+        const h2 a = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) - bias;
+        const h2 b = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) - bias;
+        r[4 * d + 0] = a[0];
+        r[4 * d + 1] = a[1];
+        r[4 * d + 2] = b[0];
+        r[4 * d + 3] = b[1];
+    }
+    return r;
+}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
@@ -58,13 +85,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_
 // half index of (row, 8-half chunk) in a swizzled LDS tile
 __device__ __forceinline__ int lds_at(int row, int chunk) { return row * BK + ((chunk ^ ((row ^ (row >> 2)) & 3)) << 3); }
 
-template <int BM, int BN>
-__global__ __launch_bounds__(kThreads) void linear_f16_kernel(LinearArgs a) {
+template <int BM, int BN, bool Q8>
+__global__ __launch_bounds__(kThreads) void linear_mfma_kernel(LinearArgs a) {
     constexpr int WM = BM / 2, WN = BN / 2;   // per wave
     constexpr int TM = WM / 32, TN = WN / 32; // 32 x 32 MFMA tiles per wave
     constexpr int XL = BM * BK / 4 / kThreads; // float4 loads of x per thread per stage
-    constexpr int WL = BN * BK / 8 / kThreads; // 8-half loads of w per thread per stage
-    static_assert(XL >= 1 && WL >= 1 && TM >= 1 && TN >= 1, "tile too small for the workgroup");
+    // 16-byte loads of w per stage: 8 halves (f16) or 16 int8 (Q8) each
+    constexpr int W_LOADS = Q8 ? BN * BK / 16 : BN * BK / 8;
+    constexpr int WL = (W_LOADS + kThreads - 1) / kThreads;
+    static_assert(XL >= 1 && TM >= 1 && TN >= 1, "tile too small for the workgroup");
+    static_assert(W_LOADS % 64 == 0, "w loads must cover whole waves");
 
     __shared__ __align__(16) _Float16 xh[2][BM * BK];
     __shared__ __align__(16) _Float16 xl[2][BM * BK];
@@ -75,14 +105,20 @@ __global__ __launch_bounds__(kThreads) void linear_f16_kernel(LinearArgs a) {
     const int wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+    const int r32 = lane & 31, ch = lane >> 5;
 
     const int rows_x = min(BM, a.m - m0), rows_w = min(BN, a.n - n0);
+    const int wbytes = Q8 ? 1 : 2;
     const __amdgpu_buffer_rsrc_t xr_src = rsrc(a.x + (int64_t)m0 * a.ldx, (uint32_t)(rows_x * a.ldx * 4));
-    const __amdgpu_buffer_rsrc_t wr_src = rsrc(a.w + (int64_t)n0 * a.ldw, (uint32_t)(rows_w * a.ldw * 2));
+    const __amdgpu_buffer_rsrc_t wr_src = rsrc(static_cast<const char *>(a.w) + (int64_t)n0 * a.ldw * wbytes,
+                                               (uint32_t)(rows_w * a.ldw * wbytes));
+    const __amdgpu_buffer_rsrc_t sc_src =
+        rsrc(Q8 ? a.scales + (int64_t)n0 * a.nb : a.x, Q8 ? (uint32_t)(rows_w * a.nb * 4) : 0u);
 
     f32x4 xr[XL];
-    half8 wr[WL];
-    // stage loads: x element (row, 4 k) and w element (row, 8 k)
+    f32x4 wr[WL]; // raw 16-byte weight loads
+    float sc_next[Q8 ? TN : 1];
+    // stage loads: x element (row, 4 k) and w element (row, 8 halves or 16 int8 along k)
     auto load = [&](int k0) {
 #pragma unroll
         for (int i = 0; i < XL; ++i) {
@@ -94,9 +130,20 @@ __global__ __launch_bounds__(kThreads) void linear_f16_kernel(LinearArgs a) {
 #pragma unroll
         for (int i = 0; i < WL; ++i) {
             const int f = tid + kThreads * i;
-            const int row = f / (BK / 8), gk = k0 + 8 * (f % (BK / 8));
-            const uint32_t off = gk < a.k ? (uint32_t)(row * a.ldw + gk) * 2u : kOutOfRange;
-            wr[i] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(wr_src, (int)off, 0, 0));
+            if (W_LOADS % kThreads != 0 && f >= W_LOADS) break; // whole waves drop out
+            constexpr int PER_ROW = Q8 ? BK / 16 : BK / 8;
+            const int row = f / PER_ROW, gk = k0 + (BK / PER_ROW) * (f % PER_ROW);
+            const uint32_t off = gk < a.k ? (uint32_t)(row * a.ldw + gk) * (uint32_t)wbytes : kOutOfRange;
+            wr[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wr_src, (int)off, 0, 0));
+        }
+        if constexpr (Q8) {
+            // this lane's weight rows of the next stage: one block scale each (k0 / 32 is the block)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int row = wn * WN + j * 32 + r32;
+                const uint32_t off = k0 < a.k ? (uint32_t)(row * a.nb + k0 / BK) * 4u : kOutOfRange;
+                sc_next[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sc_src, (int)off, 0, 0));
+            }
         }
     };
     auto store = [&](int buf) {
@@ -117,8 +164,17 @@ __global__ __launch_bounds__(kThreads) void linear_f16_kernel(LinearArgs a) {
 #pragma unroll
         for (int i = 0; i < WL; ++i) {
             const int f = tid + kThreads * i;
-            const int row = f / (BK / 8), c = f % (BK / 8);
-            *reinterpret_cast<half8 *>(&ws[buf][lds_at(row, c)]) = wr[i];
+            if (W_LOADS % kThreads != 0 && f >= W_LOADS) break;
+            if constexpr (Q8) {
+                // 16 int8 of k 16 (f % 2) .. +16 of row f / 2: two f16 chunks
+                const int row = f >> 1, c = 2 * (f & 1);
+                const uint32_t *u = reinterpret_cast<const uint32_t *>(&wr[i]);
+                *reinterpret_cast<half8 *>(&ws[buf][lds_at(row, c)]) = int8x8_to_half8(u[0], u[1]);
+                *reinterpret_cast<half8 *>(&ws[buf][lds_at(row, c + 1)]) = int8x8_to_half8(u[2], u[3]);
+            } else {
+                const int row = f / (BK / 8), c = f % (BK / 8);
+                *reinterpret_cast<half8 *>(&ws[buf][lds_at(row, c)]) = __builtin_bit_cast(half8, wr[i]);
+            }
         }
     };
 
@@ -128,41 +184,78 @@ __global__ __launch_bounds__(kThreads) void linear_f16_kernel(LinearArgs a) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = (f32x16){0};
 
-    const int r32 = lane & 31, ch = lane >> 5;
+    float sc[Q8 ? TN : 1];
     auto compute = [&](int buf) {
+        if constexpr (!Q8) {
 #pragma unroll
-        for (int kk = 0; kk < BK / 16; ++kk) {
-            half8 ah[TM], al[TM], b[TN];
+            for (int kk = 0; kk < BK / 16; ++kk) {
+                half8 ah[TM], al[TM], b[TN];
 #pragma unroll
-            for (int i = 0; i < TM; ++i) {
-                const int at = lds_at(wm * WM + i * 32 + r32, 2 * kk + ch);
-                ah[i] = *reinterpret_cast<const half8 *>(&xh[buf][at]);
-                al[i] = *reinterpret_cast<const half8 *>(&xl[buf][at]);
+                for (int i = 0; i < TM; ++i) {
+                    const int at = lds_at(wm * WM + i * 32 + r32, 2 * kk + ch);
+                    ah[i] = *reinterpret_cast<const half8 *>(&xh[buf][at]);
+                    al[i] = *reinterpret_cast<const half8 *>(&xl[buf][at]);
+                }
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    b[j] = *reinterpret_cast<const half8 *>(&ws[buf][lds_at(wn * WN + j * 32 + r32, 2 * kk + ch)]);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], b[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], b[j], acc[i][j], 0, 0, 0);
             }
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-                b[j] = *reinterpret_cast<const half8 *>(&ws[buf][lds_at(wn * WN + j * 32 + r32, 2 * kk + ch)]);
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i], b[j], acc[i][j], 0, 0, 0);
+        } else {
+            // the stage is one Q8 block: its sum over 32 k, then scaled into acc
+            half8 ah[TM][2], al[TM][2];
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < TN; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i], b[j], acc[i][j], 0, 0, 0);
+                for (int kk = 0; kk < 2; ++kk) {
+                    const int at = lds_at(wm * WM + i * 32 + r32, 2 * kk + ch);
+                    ah[i][kk] = *reinterpret_cast<const half8 *>(&xh[buf][at]);
+                    al[i][kk] = *reinterpret_cast<const half8 *>(&xl[buf][at]);
+                }
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                half8 b[2];
+#pragma unroll
+                for (int kk = 0; kk < 2; ++kk)
+                    b[kk] = *reinterpret_cast<const half8 *>(&ws[buf][lds_at(wn * WN + j * 32 + r32, 2 * kk + ch)]);
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    f32x16 t = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][0], b[0], (f32x16){0}, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][0], b[0], t, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][1], b[1], t, 0, 0, 0);
+                    t = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][1], b[1], t, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][j][r] = __builtin_fmaf(t[r], sc[j], acc[i][j][r]);
+                }
+            }
         }
     };
 
     const int n_k = (a.k + BK - 1) / BK;
     load(0);
     store(0);
+    if constexpr (Q8) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) sc[j] = sc_next[j];
+    }
     __syncthreads();
     for (int t = 0; t + 1 < n_k; ++t) {
         load((t + 1) * BK);
         compute(t & 1);
         store((t + 1) & 1);
+        if constexpr (Q8) {
+#pragma unroll
+            for (int j = 0; j < TN; ++j) sc[j] = sc_next[j];
+        }
         __syncthreads();
     }
     compute((n_k - 1) & 1);
@@ -183,10 +276,10 @@ __global__ __launch_bounds__(kThreads) void linear_f16_kernel(LinearArgs a) {
     }
 }
 
-template <int BM, int BN>
+template <int BM, int BN, bool Q8>
 inline hipError_t launch_linear_tile(const LinearArgs &a, hipStream_t stream) {
     dim3 grid((unsigned)((a.m + BM - 1) / BM), (unsigned)((a.n + BN - 1) / BN));
-    linear_f16_kernel<BM, BN><<<grid, kThreads, 0, stream>>>(a);
+    linear_mfma_kernel<BM, BN, Q8><<<grid, kThreads, 0, stream>>>(a);
     return hipGetLastError();
 }
 

@@ -184,6 +184,22 @@ class Context:
         self._check(self._L.zwg_linear_dev(self._h, self._dev_ptr(x, "x"), m, k, w.data_ptr(), _lib.W_F16,
                                            self._dev_ptr(bias, "bias"), n, self._dev_ptr(out, "out")))
 
+    def linear_q8_dev(self, x, m: int, k: int, w: "Q8", bias, n: int, out) -> None:
+        """out[m][n] = x[m][k] . dequant(w)^T (+ bias) over int8 block weights: CUDA tensors, w.q int8
+        [n][k] and w.scales float32 [n][k / 32] (see Q8.to_device), x/bias/out float32."""
+        import torch
+
+        if not isinstance(w, Q8) or not isinstance(w.q, torch.Tensor) or not w.q.is_cuda or w.q.dtype != torch.int8:
+            raise ZwgError("w must be a Q8 holding CUDA tensors (Q8.to_device)")
+        if w.n != n or w.k != k:
+            raise ZwgError(f"w is [{w.n}][{w.k}], the call asks for [{n}][{k}]")
+        if x.numel() < m * k or out.numel() < m * n or (bias is not None and bias.numel() < n):
+            raise ZwgError("a tensor is shorter than m, n and k need")
+        self._bind_torch_stream()
+        self._check(self._L.zwg_linear_q8_dev(self._h, self._dev_ptr(x, "x"), m, k, w.q.data_ptr(),
+                                              self._dev_ptr(w.scales, "scales"), self._dev_ptr(bias, "bias"), n,
+                                              self._dev_ptr(out, "out")))
+
     def attention_dev(self, q, k, v, sh: AttnShape, out) -> None:
         self._bind_torch_stream()
         c = sh.to_c()
@@ -317,11 +333,72 @@ def attentionEx(pool, q, k, v, sh: AttnShape, scratch, out) -> None:
     default_context().attention_ex_host(q, k, v, sh, out.reshape(-1))
 
 
+Q8_BLOCK = 32  # src/gemm.zig:194
+
+
+class Q8:
+    """gemm.Q8 (src/gemm.zig:196-266): int8 weights q [n][k] and f32 scales [n][k / 32], one per block
+    of 32 weights of a row (absmax / 127).  Holds numpy arrays (host) or CUDA tensors (to_device)."""
+
+    def __init__(self, q, scales, n: int, k: int):
+        if k % Q8_BLOCK:
+            raise ZwgError("k must be a multiple of 32")
+        self.q, self.scales, self.n, self.k = q, scales, int(n), int(k)
+
+    def blocks(self) -> int:
+        return self.k // Q8_BLOCK
+
+    @classmethod
+    def quantize(cls, w, n: int, k: int) -> "Q8":
+        """Q8.quantize (src/gemm.zig:209-230) of an [n][k] f16 or f32 matrix: scale = amax / 127 in f32,
+        q = clamp(round(v * (127 / amax)), -127, 127) with ties away from zero (Zig's @round)."""
+        if k % Q8_BLOCK:
+            raise ZwgError("k must be a multiple of 32")
+        w = np.asarray(w).reshape(-1)[: n * k].astype(np.float32).reshape(n, k // Q8_BLOCK, Q8_BLOCK)
+        amax = np.abs(w).max(axis=2)
+        scale = (amax / np.float32(127.0)).astype(np.float32)
+        with np.errstate(divide="ignore"):
+            inv = np.where(amax > 0, np.float32(127.0) / amax, np.float32(0)).astype(np.float32)
+        r = (w * inv[:, :, None]).astype(np.float32).astype(np.float64)
+        r = np.sign(r) * np.floor(np.abs(r) + 0.5)  # exact in f64 for any f32 product
+        q = np.clip(r, -127, 127).astype(np.int8).reshape(n, k)
+        return cls(q, scale.reshape(n, k // Q8_BLOCK), n, k)
+
+    @classmethod
+    def from_q8_0(cls, data: bytes, n: int, k: int) -> "Q8":
+        """Q8.fromQ8_0 (src/gemm.zig:232-248): GGUF q8_0 blocks (f16 scale, then 32 int8) to the same
+        int8 and f32 scales."""
+        if k % Q8_BLOCK:
+            raise ZwgError("k must be a multiple of 32")
+        nb = k // Q8_BLOCK
+        blk = np.frombuffer(data, dtype=np.uint8, count=n * nb * 34).reshape(n * nb, 34)
+        scales = blk[:, :2].copy().view(np.float16).astype(np.float32).reshape(n, nb)
+        q = blk[:, 2:].copy().view(np.int8).reshape(n, k)
+        return cls(q, scales, n, k)
+
+    def row(self, i: int) -> np.ndarray:
+        """Q8.row (src/gemm.zig:255-263): row i dequantized, f32(q) * scale."""
+        q = np.asarray(self.q).reshape(self.n, self.k)[i].astype(np.float32).reshape(-1, Q8_BLOCK)
+        return (q * np.asarray(self.scales, np.float32).reshape(self.n, -1)[i][:, None]).reshape(-1)
+
+    def to_device(self, device: int = 0) -> "Q8":
+        """The same weights as CUDA tensors (int8 q, float32 scales), for Context.linear_q8_dev."""
+        import torch
+
+        q = torch.as_tensor(np.ascontiguousarray(np.asarray(self.q, np.int8).reshape(self.n, self.k)))
+        s = torch.as_tensor(np.ascontiguousarray(np.asarray(self.scales, np.float32).reshape(self.n, -1)))
+        return Q8(q.to(f"cuda:{device}"), s.to(f"cuda:{device}"), self.n, self.k)
+
+
 def linear(pool, x, m: int, k: int, w, b, n: int, out) -> None:
-    """ops.linear (src/ops.zig:283-306) with f16 weights: out[i][o] = sum_p x[i][p] * w[o][p] (+ b[o]).
-    x f32 [m][k], w float16 [n][k], b f32 [n] or None, out f32 [m][n]; host arrays, synchronous."""
+    """ops.linear (src/ops.zig:283-306): out[i][o] = sum_p x[i][p] * w[o][p] (+ b[o]).  w is a float16
+    [n][k] array or a Q8 (int8 block weights), as the reference's `anytype`; x f32 [m][k], b f32 [n] or
+    None, out f32 [m][n]; host arrays, synchronous."""
     del pool  # the GPU context replaces the thread pool
     x = _as_f32(x, "x")
+    if isinstance(w, Q8):
+        _linear_q8_host(x, m, k, w, b, n, out)
+        return
     w = np.asarray(w)
     if w.dtype != np.float16 or not w.flags["C_CONTIGUOUS"]:
         raise ZwgError("w must be a contiguous float16 array")
@@ -333,6 +410,24 @@ def linear(pool, x, m: int, k: int, w, b, n: int, out) -> None:
     ctx = default_context()
     ctx._check(ctx._L.zwg_linear(ctx.handle, x.ctypes.data, m, k, w.ctypes.data, _lib.W_F16,
                                  None if bb is None else bb.ctypes.data, n, out.ctypes.data))
+
+
+def _linear_q8_host(x, m: int, k: int, w: Q8, b, n: int, out) -> None:
+    q = np.asarray(w.q)
+    sc = np.asarray(w.scales)
+    if q.dtype != np.int8 or sc.dtype != np.float32 or not q.flags["C_CONTIGUOUS"] or not sc.flags["C_CONTIGUOUS"]:
+        raise ZwgError("w must hold contiguous int8 q and float32 scales (host arrays)")
+    if w.n != n or w.k != k:
+        raise ZwgError(f"w is [{w.n}][{w.k}], the call asks for [{n}][{k}]")
+    bb = None if b is None else _as_f32(b, "b")
+    if not isinstance(out, np.ndarray) or out.dtype != np.float32 or not out.flags["C_CONTIGUOUS"]:
+        raise ZwgError("out must be a contiguous float32 array")
+    if x.size < m * k or q.size < n * k or sc.size < n * (k // Q8_BLOCK) or out.size < m * n or (
+            bb is not None and bb.size < n):
+        raise ZwgError("a buffer is shorter than m, n and k need")
+    ctx = default_context()
+    ctx._check(ctx._L.zwg_linear_q8(ctx.handle, x.ctypes.data, m, k, q.ctypes.data, sc.ctypes.data,
+                                    None if bb is None else bb.ctypes.data, n, out.ctypes.data))
 
 
 def attention(pool, q, k, v, n_q: int, n_kv: int, n_state: int, n_head: int, causal: bool, scratch, out) -> None:
