@@ -22,7 +22,9 @@ rows of a step written into the HBM-resident caches, with rotary positions for Q
 "small_dec_kv_append_x32", "qwen15_kv_append_x64" and "qwen05_prefill_kv_append", each with an
 HBM roofline and oracle/kv.py's update timed beside it, and the six linear layers of a base.en
 encoder layer over the 16 windows ("base_enc_linear_x16", f16 weights on f16 MFMA) with the
-oracle's ops.linear timed beside it.
+oracle's ops.linear timed beside it, and three decode steps' linear layers over int8 block
+weights (HBM-bound; "qwen15_logits_q8_x64", "qwen15_decode_q8_linear_x64",
+"small_dec_q8_linear_x32") with the oracle's ops.linear over Q8 timed beside them.
 """
 from __future__ import annotations
 
@@ -344,6 +346,120 @@ class LinearWorkload:
         self.x = self.out = self.w = self.b = None
 
 
+class Q8LinearWorkload:
+    """A decode step's linear layers over int8 block weights (gemm.Q8, src/gemm.zig:188-351), m rows
+    (sequences or windows decoded in lockstep) per layer, with the weights resident in HBM in the
+    packed device layout (zwg_q8w_create, done once as the reference builds its Q8 at load) and
+    each layer run by zwg_linear_q8w_dev.
+
+    Algorithmic bytes per step: for every layer its int8 weights (n k), f32 block scales (n k / 32 * 4),
+    bias (n * 4, when it has one), the x rows read (m k * 4) and the out rows written (m n * 4): the
+    weights are read once per step, which is what makes these layers HBM-bound at m <= 64.  `copies`
+    sets of weights rotate so that no step finds its weights in the 256 MB last-level cache.
+    A step is one replay of a HIP graph that holds the step's launches (captured once per weight
+    set), as a serving loop would run it: the step's many small launches are then not paced by this
+    Python harness.
+    """
+
+    def __init__(self, name: str, description: str, torch, ctx, m: int, layers, copies: int = 1,
+                 cpu_layers: int = 0):
+        import zwhisper_amd as z
+
+        self.name, self.description = name, description
+        self.torch, self.ctx, self.m = torch, ctx, m
+        self.layers = layers  # (k, n, has_bias)
+        g = torch.Generator(device="cuda").manual_seed(0x0808)
+        dims = sorted({k for k, _, _ in layers} | {n for _, n, _ in layers})
+        self.x = {d: torch.randn(m, d, device="cuda", generator=g) for d in dims}
+        self.out = {d: torch.empty(m, d, device="cuda") for d in dims}
+        self.sets = []
+        self.raw = []  # unpacked copies of the first layers, for the CPU baseline
+        for c in range(copies):
+            ws = []
+            for li, (k, n, hb) in enumerate(layers):
+                q = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda", generator=g)
+                sc = torch.rand(n, k // 32, device="cuda", generator=g) * (2.0 / 127 / np.sqrt(k))
+                b = torch.randn(n, device="cuda", generator=g) if hb else None
+                ws.append((z.Q8(q, sc, n, k).resident(ctx), b))
+                if c == 0 and li < cpu_layers:
+                    self.raw.append((q.cpu().numpy(), sc.cpu().numpy(), None if b is None else b.cpu().numpy()))
+                del q, sc
+            self.sets.append(ws)
+        torch.cuda.synchronize()
+        self.work = float(sum(n * k + n * k // 32 * 4 + (n * 4 if hb else 0) + m * k * 4 + m * n * 4
+                              for k, n, hb in layers))
+        # one graph per weight set, captured after an eager warm-up
+        for ws in self.sets:
+            self._run(ws)
+        torch.cuda.synchronize()
+        self.graphs = []
+        for ws in self.sets:
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                self._run(ws)
+            self.graphs.append(gr)
+        torch.cuda.synchronize()
+
+    def _run(self, ws):
+        for (k, n, _), (w, b) in zip(self.layers, ws):
+            self.ctx.linear_q8w_dev(self.x[k], self.m, w, b, self.out[n])
+
+    def step(self, i: int):
+        self.graphs[i % len(self.graphs)].replay()
+
+    def cpu_baseline(self, threads: int) -> dict:
+        """The oracle's ops.linear over Q8 (oracle/attn_oracle.c: ntBlockQ over the reference's Pool),
+        on the first layers, best of 3 after a warm-up."""
+        import oracle
+
+        sample = self.layers[:len(self.raw)]
+        xs = {d: v.cpu().numpy() for d, v in self.x.items()}
+        outs = {d: np.zeros(self.m * d, np.float32) for d in self.out}
+        o = oracle.Oracle(threads)
+
+        def run():
+            for (k, n, _), (q, sc, b) in zip(sample, self.raw):
+                o.linear_q8(xs[k], self.m, k, q, sc, b, n, out=outs[n])
+
+        run()
+        best = float("inf")
+        for _ in range(3):
+            t0 = time.perf_counter()
+            run()
+            best = min(best, time.perf_counter() - t0)
+        o.close()
+        work = float(sum(n * k + n * k // 32 * 4 + (n * 4 if hb else 0) + self.m * k * 4 + self.m * n * 4
+                         for k, n, hb in sample))
+        return {"value": work / best / 1e9, "unit": "GB/s", "cores": o.threads, "kind": "port",
+                "sample": f"{len(sample)} of {len(self.layers)} layers at the full {self.m} rows; "
+                          "oracle/attn_oracle.c ora_linear_q8, best of 3 after one warm-up", "seconds": best}
+
+    def free(self):
+        self.graphs = None
+        for ws in self.sets or []:
+            for w, _ in ws:
+                w.close()
+        self.x = self.out = self.sets = self.raw = None
+
+
+def q8_workloads(torch, ctx):
+    """Constructors of the three int8 decode-step measurements."""
+    qwen_layer = [(1536, 1536, True), (1536, 256, True), (1536, 256, True), (1536, 1536, False),
+                  (1536, 8960, False), (1536, 8960, False), (8960, 1536, False)]  # src/llm.zig:179-207
+    whisper_layer = [(768, 768, True), (768, 768, False), (768, 768, True), (768, 768, True),
+                     (768, 768, True), (768, 768, True), (768, 3072, True), (3072, 768, True)]  # src/decoder.zig:181-201
+    yield lambda: Q8LinearWorkload(
+        "qwen15_logits_q8_x64", "Qwen2.5-1.5B output projection over the 151936-token vocabulary, 64 sequences "
+        "(src/llm.zig:214-216), int8 block weights", torch, ctx, 64, [(1536, 151936, False)], copies=2, cpu_layers=1)
+    yield lambda: Q8LinearWorkload(
+        "qwen15_decode_q8_linear_x64", "Qwen2.5-1.5B decode step, 64 sequences: q/k/v/o, gate/up/down of all "
+        "28 layers (196 linear calls), int8 block weights", torch, ctx, 64, qwen_layer * 28, cpu_layers=7)
+    yield lambda: Q8LinearWorkload(
+        "small_dec_q8_linear_x32", "Whisper small.en decoder step, 32 windows: q/k/v/o, cross q/o, MLP of all "
+        "12 layers and the 51864-token logits (97 linear calls), int8 block weights", torch, ctx, 32,
+        whisper_layer * 12 + [(768, 51864, False)], copies=2, cpu_layers=8)
+
+
 def time_workload(wl: Workload, steps: int, warmup: int) -> dict:
     torch = wl.torch
     for i in range(warmup):
@@ -565,6 +681,28 @@ def main() -> int:
               + (f", cpu {res['cpu_baseline']['value']:.3f} TFLOP/s" if not args.no_cpu else ""),
               file=sys.stderr, flush=True)
         wl.free()
+        for make in q8_workloads(torch, ctx):
+            wl = make()
+            r = time_workload(wl, args.steps, args.warmup)
+            achieved = wl.work / (r["kernel_ms_mean"] * 1e-3)
+            res = {"workload": wl.name, "description": wl.description,
+                   "value": wl.work / (r["ms_per_step"] * 1e-3) / 1e9, "unit": "GB/s",
+                   "ms_per_step": r["ms_per_step"], "kernel_ms_mean": r["kernel_ms_mean"],
+                   "kernel_ms_min": r["kernel_ms_min"], "algorithmic_work_per_step": wl.work,
+                   "dtype": "f32 activations x int8 block weights, f32 accumulation (f16 MFMA, x split into two "
+                            "f16 terms, block sums scaled in f32)",
+                   "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                                "frac": achieved / PEAK_HBM, "traffic": traffic_for(wl.name)}}
+            if not args.no_cpu:
+                res["cpu_baseline"] = wl.cpu_baseline(host_threads())
+            results[wl.name] = res
+            print(f"[bench] {wl.name}: {res['value']:.2f} GB/s ({r['ms_per_step']:.4f} ms/step, kernels "
+                  f"{r['kernel_ms_mean']:.4f} ms, {100 * res['roofline']['frac']:.1f}% of hbm peak)"
+                  + (f", cpu {res['cpu_baseline']['value']:.3f} GB/s" if not args.no_cpu else ""),
+                  file=sys.stderr, flush=True)
+            wl.free()
+            del wl
+            torch.cuda.empty_cache()
     ctx.close()
 
     head = results[args.workload]

@@ -246,6 +246,28 @@ int zwg_linear_q8(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const in
 int zwg_linear_q8_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const int8_t *q, const float *scales,
                       const float *bias, uint64_t n, float *out);
 
+/*
+ * Device-resident int8 block weights.  The reference builds each gemm.Q8 once at load
+ * (Q8.quantize / Q8.fromQ8_0, src/gemm.zig:209-248; src/decoder.zig:203-215 getQ, src/llm.zig
+ * loaders) and every forward then calls ops.linear with it.  zwg_q8w_create is that load step for
+ * the GPU: it copies the Q8's two arrays into HBM once, repacked so that the token-step kernel
+ * reads every weight byte in contiguous 1 KB wave-loads (tiles of 32 rows x 32 k in lane order,
+ * scales grouped per 32 rows; zero padding to 32 rows and 256 k).  zwg_linear_q8w_dev computes
+ * exactly what zwg_linear_q8_dev computes with the unpacked arrays.  Destroy the weights before
+ * closing their context.
+ */
+typedef struct zwg_q8w zwg_q8w;
+#define ZWG_Q8W_FROM_HOST 1u /* q and scales are host memory (else device memory) */
+
+/* q int8 [n][k], scales f32 [n][k / 32]; k a multiple of 32.  Returns when the packed copy is
+ * done for host sources; device sources are packed asynchronously on ctx's stream. */
+int zwg_q8w_create(zwg_ctx *ctx, const int8_t *q, const float *scales, uint64_t n, uint64_t k, uint32_t flags,
+                   zwg_q8w **out);
+void zwg_q8w_destroy(zwg_q8w *w);
+int zwg_q8w_shape(const zwg_q8w *w, uint64_t *n, uint64_t *k);
+/* out[m][n] = x[m][k] . W^T (+ bias): device pointers, asynchronous on ctx's stream. */
+int zwg_linear_q8w_dev(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, const float *bias, float *out);
+
 int zwg_version(void); /* ZWG_VERSION */
 
 #ifdef __cplusplus

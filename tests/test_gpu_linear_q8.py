@@ -179,3 +179,37 @@ def test_linear_q8_errors(torch, ctx):
     w2 = z.Q8(torch.zeros((4, 64), dtype=torch.int8, device="cuda"), torch.zeros((4, 2), device="cuda"), 4, 64)
     with pytest.raises(z.ZwgError, match="asks for"):
         ctx.linear_q8_dev(t, 2, 64, w2, None, 5, t)
+
+
+@pytest.mark.parametrize("m,k,n", CASES)
+def test_resident_packed_matches_raw(torch, ctx, m, k, n):
+    """Weights uploaded once in the packed device layout (zwg_q8w) give the raw-layout call's
+    results bit for bit: same kernels' arithmetic, only the weight loads differ."""
+    x, w, b = inputs(m * 11 + n + k, m, k, n)
+    raw = run_dev(torch, ctx, x, w, b, m, k, n)
+    xd = torch.from_numpy(x).cuda()
+    bd = torch.from_numpy(b).cuda()
+    for src in (w, w.to_device()):  # packed from host arrays and from device tensors
+        with src.resident(ctx) as rw:
+            out = torch.full((m, n), float("nan"), device="cuda")
+            ctx.linear_q8w_dev(xd, m, rw, bd, out)
+            torch.cuda.synchronize()
+            assert np.array_equal(out.cpu().numpy(), raw)
+
+
+def test_resident_logits(torch, ctx):
+    """The Qwen2.5-1.5B vocabulary projection from resident packed weights, against f64."""
+    import zwhisper_amd as z
+
+    m, k, n = 64, 1536, 151936
+    rng = np.random.default_rng(3)
+    x = torch.from_numpy(rng.standard_normal((m, k)).astype(np.float32)).cuda()
+    q = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=torch.Generator().manual_seed(4)).cuda()
+    sc = (torch.rand(n, k // 32, generator=torch.Generator().manual_seed(5)) * (2.0 / 127 / np.sqrt(k))).cuda()
+    with z.Q8(q, sc, n, k).resident(ctx) as rw:
+        out = torch.full((m, n), float("nan"), device="cuda")
+        ctx.linear_q8w_dev(x, m, rw, None, out)
+        torch.cuda.synchronize()
+    deq = (q.double().view(n, k // 32, 32) * sc.double().view(n, k // 32, 1)).view(n, k)
+    err = float((out.double() - x.double() @ deq.T).abs().max())
+    assert bool(torch.isfinite(out).all()) and err <= 2e-5 * np.sqrt(k)

@@ -7,10 +7,10 @@ and src/llm.zig:182-190).
 """
 from ._lib import KV_KT, KV_ROW, ZwgError
 from .ops import (AttnShape, Context, KVCache, V, attention, attentionEx, attentionScratch, attentionScratchEx,
-                  attentionScratchKT, check_shape, default_context, linear, plan, q_block, Q8)
+                  attentionScratchKT, check_shape, default_context, linear, plan, q_block, Q8, Q8Resident)
 
 __all__ = [
     "AttnShape", "Context", "KVCache", "KV_KT", "KV_ROW", "V", "ZwgError", "attention", "attentionEx",
     "attentionScratch", "attentionScratchEx", "attentionScratchKT", "check_shape", "default_context", "linear", "plan",
-    "Q8", "q_block",
+    "Q8", "Q8Resident", "q_block",
 ]

@@ -94,6 +94,7 @@ KV_ROW = 0
 KV_KT = 1
 W_F16 = 1
 W_Q8 = 2
+Q8W_FROM_HOST = 1
 ROWS_ON_HOST = 1
 
 
@@ -155,6 +156,14 @@ def lib() -> ctypes.CDLL:
     for name in ("zwg_linear", "zwg_linear_dev"):
         getattr(L, name).restype = c_int
         getattr(L, name).argtypes = [vp, _fp, _u64, _u64, vp, ctypes.c_uint32, _fp, _u64, _fp]
+    L.zwg_q8w_create.restype = c_int
+    L.zwg_q8w_create.argtypes = [vp, vp, _fp, _u64, _u64, ctypes.c_uint32, ctypes.POINTER(vp)]
+    L.zwg_q8w_destroy.restype = None
+    L.zwg_q8w_destroy.argtypes = [vp]
+    L.zwg_q8w_shape.restype = c_int
+    L.zwg_q8w_shape.argtypes = [vp, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]
+    L.zwg_linear_q8w_dev.restype = c_int
+    L.zwg_linear_q8w_dev.argtypes = [vp, _fp, _u64, vp, _fp, _fp]
     for name in ("zwg_linear_q8", "zwg_linear_q8_dev"):
         getattr(L, name).restype = c_int
         getattr(L, name).argtypes = [vp, _fp, _u64, _u64, vp, _fp, _fp, _u64, _fp]

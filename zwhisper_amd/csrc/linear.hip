@@ -33,15 +33,15 @@ int64_t tiles(uint64_t m, uint64_t n, int bm, int bn) { return (int64_t)((m + bm
 // the CUs once, else 64 x 64 for the small single-window shapes, which are latency bound.  Int8
 // weights take 128 x 128 in place of 128 x 256: the block sums need 16 more VGPRs per tile row,
 // which would leave the larger tile one wave per SIMD.
-template <bool Q8>
+template <int WMODE>
 hipError_t launch_tiled(const LinearArgs &a, hipStream_t stream) {
-    if constexpr (Q8) {
-        if (tiles(a.m, a.n, 128, 128) >= 512) return zwg_lin::launch_linear_tile<128, 128, true>(a, stream);
+    if constexpr (WMODE != zwg_lin::kWF16) {
+        if (tiles(a.m, a.n, 128, 128) >= 512) return zwg_lin::launch_linear_tile<128, 128, WMODE>(a, stream);
     } else {
-        if (tiles(a.m, a.n, 128, 256) >= 512) return zwg_lin::launch_linear_tile<128, 256, false>(a, stream);
+        if (tiles(a.m, a.n, 128, 256) >= 512) return zwg_lin::launch_linear_tile<128, 256, WMODE>(a, stream);
     }
-    if (tiles(a.m, a.n, 64, 256) >= 256) return zwg_lin::launch_linear_tile<64, 256, Q8>(a, stream);
-    return zwg_lin::launch_linear_tile<64, 64, Q8>(a, stream);
+    if (tiles(a.m, a.n, 64, 256) >= 256) return zwg_lin::launch_linear_tile<64, 256, WMODE>(a, stream);
+    return zwg_lin::launch_linear_tile<64, 64, WMODE>(a, stream);
 }
 
 std::string check_linear(uint64_t m, uint64_t k, uint32_t w_type, uint64_t n) {
@@ -54,10 +54,55 @@ std::string check_linear(uint64_t m, uint64_t k, uint32_t w_type, uint64_t n) {
     return "";
 }
 
-// Q8 with m <= 64: the weight-streaming kernel.  Four waves of S slabs of 32 weight rows per
-// workgroup (S = 2 when that alone makes >= 256 workgroups, else 1); k is split over more
-// workgroups, at chunk granularity, until there are about 512 of them, as long as the partial
-// sums fit the workspace.
+// Q8 with m <= 64: x split into hi/lo halves by linear_q8_xprep_kernel into the workspace, then
+// the weight-streaming kernel.  Four waves of S slabs of 32 weight rows per workgroup (S = 2 when
+// that alone makes >= 256 workgroups, else 1); k is split over more workgroups, at chunk
+// granularity, until there are about 512 of them, as long as the partial sums fit the workspace.
+template <int MT>
+int run_q8_stream_mt(zwg_ctx *ctx, const zwg_lin::Q8Args &base, const zwg_lin::Q8Packed *packed) {
+    zwg_lin::Q8Args a = base;
+    const uint64_t m = (uint64_t)a.m, n = (uint64_t)a.n;
+    // the raw-layout kernel takes two slabs per wave on wide matrices; the pipelined packed kernel
+    // holds two stages of weights in registers and takes one
+    const int S = (!packed && (n + 255) / 256 >= 256) ? 2 : 1;
+    const int64_t gx = (int64_t)((n + 128 * S - 1) / (128 * S));
+    const int n_chunks = (a.k + zwg_lin::kQ8Chunk - 1) / zwg_lin::kQ8Chunk;
+    const uint64_t xcvt_bytes = (uint64_t)n_chunks * zwg_lin::q8_chunk_halves<MT>() * 2;
+    const uint64_t part_off = (xcvt_bytes + 255) / 256 * 256;
+    if (part_off > ctx->workspace_bytes) return fail(ctx, "workspace too small for this linear call");
+    int n_split = 1;
+    if (gx < 512) n_split = (int)std::min<int64_t>(n_chunks, (512 + gx - 1) / gx);
+    while (n_split > 1 && part_off + (uint64_t)n_split * m * n * 4 > ctx->workspace_bytes) --n_split;
+    a.chunks_per_split = (n_chunks + n_split - 1) / n_split;
+    n_split = (n_chunks + a.chunks_per_split - 1) / a.chunks_per_split; // no empty splits
+    a.n_split = n_split;
+    _Float16 *xcvt = reinterpret_cast<_Float16 *>(ctx->workspace);
+    a.part = n_split > 1 ? reinterpret_cast<float *>(reinterpret_cast<char *>(ctx->workspace) + part_off) : nullptr;
+
+    const int64_t prep_threads = (int64_t)n_chunks * MT * 32 * (zwg_lin::kQ8Chunk / 4);
+    zwg_lin::linear_q8_xprep_kernel<MT><<<(unsigned)((prep_threads + 255) / 256), 256, 0, ctx->stream>>>(
+        a.x, xcvt, a.m, a.k, n_chunks);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail_hip(ctx, "linear (int8) x preparation launch", e);
+    dim3 grid((unsigned)gx, (unsigned)n_split);
+    if (packed) {
+        zwg_lin::linear_q8p_stream_kernel<MT, 1><<<grid, zwg_lin::kQ8Threads, 0, ctx->stream>>>(a, *packed, xcvt);
+    } else {
+        if (S == 2) zwg_lin::linear_q8_stream_kernel<MT, 2><<<grid, zwg_lin::kQ8Threads, 0, ctx->stream>>>(a, xcvt);
+        else zwg_lin::linear_q8_stream_kernel<MT, 1><<<grid, zwg_lin::kQ8Threads, 0, ctx->stream>>>(a, xcvt);
+    }
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail_hip(ctx, "linear (int8 stream) kernel launch", e);
+    if (n_split > 1) {
+        const int64_t mn = (int64_t)(m * n);
+        zwg_lin::linear_split_sum_kernel<<<(unsigned)((mn + 255) / 256), 256, 0, ctx->stream>>>(
+            a.part, a.bias, a.out, mn, (int32_t)n, n_split);
+        e = hipGetLastError();
+        if (e != hipSuccess) return fail_hip(ctx, "linear split-sum kernel launch", e);
+    }
+    return ZWG_OK;
+}
+
 int run_q8_stream(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const int8_t *q, const float *scales,
                   const float *bias, uint64_t n, float *out) {
     zwg_lin::Q8Args a{};
@@ -70,35 +115,7 @@ int run_q8_stream(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const in
     a.n = (int32_t)n;
     a.k = (int32_t)k;
     a.nb = (int32_t)(k / zwg_lin::kQ8Block);
-    const int S = (n + 255) / 256 >= 256 ? 2 : 1;
-    const int64_t gx = (int64_t)((n + 128 * S - 1) / (128 * S));
-    const int n_chunks = (int)((k + zwg_lin::kQ8Chunk - 1) / zwg_lin::kQ8Chunk);
-    int n_split = 1;
-    if (gx < 512) n_split = (int)std::min<int64_t>(n_chunks, (512 + gx - 1) / gx);
-    while (n_split > 1 && (uint64_t)n_split * m * n * 4 > ctx->workspace_bytes) --n_split;
-    a.chunks_per_split = (n_chunks + n_split - 1) / n_split;
-    n_split = (n_chunks + a.chunks_per_split - 1) / a.chunks_per_split; // no empty splits
-    a.n_split = n_split;
-    a.part = n_split > 1 ? ctx->workspace : nullptr;
-    dim3 grid((unsigned)gx, (unsigned)n_split);
-    const bool two = m > 32;
-    if (S == 2) {
-        if (two) zwg_lin::linear_q8_stream_kernel<2, 2><<<grid, zwg_lin::kQ8Threads, 0, ctx->stream>>>(a);
-        else zwg_lin::linear_q8_stream_kernel<1, 2><<<grid, zwg_lin::kQ8Threads, 0, ctx->stream>>>(a);
-    } else {
-        if (two) zwg_lin::linear_q8_stream_kernel<2, 1><<<grid, zwg_lin::kQ8Threads, 0, ctx->stream>>>(a);
-        else zwg_lin::linear_q8_stream_kernel<1, 1><<<grid, zwg_lin::kQ8Threads, 0, ctx->stream>>>(a);
-    }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return fail_hip(ctx, "linear (int8 stream) kernel launch", e);
-    if (n_split > 1) {
-        const int64_t mn = (int64_t)(m * n);
-        zwg_lin::linear_split_sum_kernel<<<(unsigned)((mn + 255) / 256), 256, 0, ctx->stream>>>(
-            ctx->workspace, bias, out, mn, (int32_t)n, n_split);
-        e = hipGetLastError();
-        if (e != hipSuccess) return fail_hip(ctx, "linear split-sum kernel launch", e);
-    }
-    return ZWG_OK;
+    return m > 32 ? run_q8_stream_mt<2>(ctx, a, nullptr) : run_q8_stream_mt<1>(ctx, a, nullptr);
 }
 
 int run_linear(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void *w, uint32_t w_type,
@@ -127,7 +144,7 @@ int run_linear(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void 
     a.n = (int32_t)n;
     a.k = (int32_t)k;
     a.nb = (int32_t)(k / 32);
-    e = w_type == ZWG_W_Q8 ? launch_tiled<true>(a, ctx->stream) : launch_tiled<false>(a, ctx->stream);
+    e = w_type == ZWG_W_Q8 ? launch_tiled<zwg_lin::kWQ8>(a, ctx->stream) : launch_tiled<zwg_lin::kWF16>(a, ctx->stream);
     if (e != hipSuccess) return fail_hip(ctx, "linear kernel launch", e);
     return ZWG_OK;
 }
@@ -165,7 +182,141 @@ int run_linear_host(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const 
 
 } // namespace
 
+// Device-resident int8 block weights in the packed layout of linear_q8_kernel.hpp (Q8Packed).
+struct zwg_q8w {
+    zwg_ctx *ctx = nullptr;
+    uint64_t n = 0, k = 0;
+    int32_t n_slabs = 0, n_chunks = 0;
+    uint8_t *q = nullptr;
+    float *scales = nullptr;
+};
+
+namespace {
+
+int run_linear_q8w(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, const float *bias, float *out) {
+    if (!w) return fail(ctx, "null weights");
+    const std::string msg = check_linear(m, w->k, ZWG_W_Q8, w->n);
+    if (!msg.empty()) return fail(ctx, msg);
+    if (m == 0) return ZWG_OK;
+    if (!x || !out) return fail(ctx, "null x or out");
+    const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (!al16(x) || !al16(out)) return fail(ctx, "x and out must be 16-byte aligned");
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
+    const zwg_lin::Q8Packed p{w->q, w->scales, w->n_slabs, w->n_chunks};
+    if (m <= 64) {
+        zwg_lin::Q8Args a{};
+        a.x = x;
+        a.bias = bias;
+        a.out = out;
+        a.m = (int32_t)m;
+        a.n = (int32_t)w->n;
+        a.k = (int32_t)w->k;
+        a.nb = (int32_t)(w->k / zwg_lin::kQ8Block);
+        return m > 32 ? run_q8_stream_mt<2>(ctx, a, &p) : run_q8_stream_mt<1>(ctx, a, &p);
+    }
+    LinearArgs a{};
+    a.x = x;
+    a.w = w->q;
+    a.scales = w->scales;
+    a.p_chunks = w->n_chunks;
+    a.bias = bias;
+    a.out = out;
+    a.ldx = (int64_t)w->k;
+    a.ldo = (int64_t)w->n;
+    a.m = (int32_t)m;
+    a.n = (int32_t)w->n;
+    a.k = (int32_t)w->k;
+    a.nb = (int32_t)(w->k / 32);
+    e = launch_tiled<zwg_lin::kWQ8P>(a, ctx->stream);
+    if (e != hipSuccess) return fail_hip(ctx, "linear kernel launch", e);
+    return ZWG_OK;
+}
+
+} // namespace
+
 extern "C" {
+
+int zwg_q8w_create(zwg_ctx *ctx, const int8_t *q, const float *scales, uint64_t n, uint64_t k, uint32_t flags,
+                   zwg_q8w **out) {
+    if (out) *out = nullptr;
+    if (!ctx || !out) return fail(ctx, "null context or out");
+    const std::string msg = check_linear(1, k, ZWG_W_Q8, n);
+    if (!msg.empty()) return fail(ctx, msg);
+    if (n == 0 || !q || !scales) return fail(ctx, "empty matrix or null q / scales");
+    if (flags & ~ZWG_Q8W_FROM_HOST) return fail(ctx, "unknown flags");
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
+    auto *w = new zwg_q8w();
+    w->ctx = ctx;
+    w->n = n;
+    w->k = k;
+    w->n_slabs = (int32_t)((n + 31) / 32);
+    w->n_chunks = (int32_t)((k + zwg_lin::kQ8Chunk - 1) / zwg_lin::kQ8Chunk);
+    const int64_t qb = zwg_lin::q8p_q_bytes(w->n_slabs, w->n_chunks);
+    const int64_t sb = zwg_lin::q8p_scale_bytes(w->n_slabs, w->n_chunks);
+    void *pq = nullptr, *ps = nullptr;
+    e = hipMalloc(&pq, (size_t)qb);
+    if (e == hipSuccess) e = hipMalloc(&ps, (size_t)sb);
+    if (e != hipSuccess) {
+        if (pq) (void)hipFree(pq);
+        delete w;
+        return fail_hip(ctx, "hipMalloc (int8 weights)", e);
+    }
+    w->q = static_cast<uint8_t *>(pq);
+    w->scales = static_cast<float *>(ps);
+    const int8_t *src_q = q;
+    const float *src_s = scales;
+    void *tq = nullptr, *ts = nullptr;
+    if (flags & ZWG_Q8W_FROM_HOST) { // stage the raw arrays, pack on the device, free the staging
+        e = hipMalloc(&tq, (size_t)(n * k));
+        if (e == hipSuccess) e = hipMalloc(&ts, (size_t)(n * (k / 32) * 4));
+        if (e == hipSuccess) e = hipMemcpyAsync(tq, q, n * k, hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess) e = hipMemcpyAsync(ts, scales, n * (k / 32) * 4, hipMemcpyHostToDevice, ctx->stream);
+        src_q = static_cast<const int8_t *>(tq);
+        src_s = static_cast<const float *>(ts);
+    } else if ((reinterpret_cast<uintptr_t>(q) & 15u) || (reinterpret_cast<uintptr_t>(scales) & 3u)) {
+        e = hipErrorInvalidValue;
+    }
+    if (e == hipSuccess) {
+        zwg_lin::linear_q8_pack_kernel<<<2048, 256, 0, ctx->stream>>>(src_q, src_s, (int32_t)n, (int32_t)k, w->q,
+                                                                     w->scales, w->n_slabs, w->n_chunks);
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess && (flags & ZWG_Q8W_FROM_HOST)) e = hipStreamSynchronize(ctx->stream);
+    if (tq) (void)hipFree(tq);
+    if (ts) (void)hipFree(ts);
+    if (e != hipSuccess) {
+        (void)hipFree(w->q);
+        (void)hipFree(w->scales);
+        delete w;
+        return fail_hip(ctx, "int8 weight packing (q 16-byte and scales 4-byte aligned?)", e);
+    }
+    *out = w;
+    return ZWG_OK;
+}
+
+void zwg_q8w_destroy(zwg_q8w *w) {
+    if (!w) return;
+    (void)hipSetDevice(w->ctx->device);
+    (void)hipStreamSynchronize(w->ctx->stream);
+    (void)hipFree(w->q);
+    (void)hipFree(w->scales);
+    delete w;
+}
+
+int zwg_q8w_shape(const zwg_q8w *w, uint64_t *n, uint64_t *k) {
+    if (!w) return fail(nullptr, "null weights");
+    if (n) *n = w->n;
+    if (k) *k = w->k;
+    return ZWG_OK;
+}
+
+int zwg_linear_q8w_dev(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, const float *bias, float *out) {
+    if (!ctx) return fail(nullptr, "null context");
+    return run_linear_q8w(ctx, x, m, w, bias, out);
+}
+
 
 int zwg_linear_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void *w, uint32_t w_type,
                    const float *bias, uint64_t n, float *out) {

@@ -49,10 +49,16 @@ constexpr int kThreads = 256;
 constexpr int BK = 32;                 // K per LDS stage: one 64-byte LDS row
 constexpr uint32_t kOutOfRange = 0x80000000u; // a buffer offset past every range the host allows
 
+// Weight formats of the tiled kernel.
+constexpr int kWF16 = 0;   // f16 [n][ldw]
+constexpr int kWQ8 = 1;    // int8 [n][ldw] + f32 scales [n][nb]
+constexpr int kWQ8P = 2;   // int8 + scales packed per slab of 32 rows (linear_q8_kernel.hpp, Q8Packed)
+
 struct LinearArgs {
     const float *x;      // [m][ldx]
-    const void *w;       // [n][ldw]: f16, or int8 for Q8 weights
-    const float *scales; // Q8 weights: [n][nb] f32 block scales
+    const void *w;       // f16 [n][ldw], int8 [n][ldw], or packed int8 tiles
+    const float *scales; // Q8 weights: [n][nb] f32 block scales, or packed scales
+    int32_t p_chunks;    // packed weights: chunks of 256 k per slab
     const float *bias;   // [n] or nullptr
     float *out;          // [m][ldo]
     int64_t ldx, ldw, ldo;
@@ -85,8 +91,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_
 // half index of (row, 8-half chunk) in a swizzled LDS tile
 __device__ __forceinline__ int lds_at(int row, int chunk) { return row * BK + ((chunk ^ ((row ^ (row >> 2)) & 3)) << 3); }
 
-template <int BM, int BN, bool Q8>
+template <int BM, int BN, int WMODE>
 __global__ __launch_bounds__(kThreads) void linear_mfma_kernel(LinearArgs a) {
+    constexpr bool Q8 = WMODE != kWF16;
     constexpr int WM = BM / 2, WN = BN / 2;   // per wave
     constexpr int TM = WM / 32, TN = WN / 32; // 32 x 32 MFMA tiles per wave
     constexpr int XL = BM * BK / 4 / kThreads; // float4 loads of x per thread per stage
@@ -110,10 +117,17 @@ __global__ __launch_bounds__(kThreads) void linear_mfma_kernel(LinearArgs a) {
     const int rows_x = min(BM, a.m - m0), rows_w = min(BN, a.n - n0);
     const int wbytes = Q8 ? 1 : 2;
     const __amdgpu_buffer_rsrc_t xr_src = rsrc(a.x + (int64_t)m0 * a.ldx, (uint32_t)(rows_x * a.ldx * 4));
-    const __amdgpu_buffer_rsrc_t wr_src = rsrc(static_cast<const char *>(a.w) + (int64_t)n0 * a.ldw * wbytes,
-                                               (uint32_t)(rows_w * a.ldw * wbytes));
-    const __amdgpu_buffer_rsrc_t sc_src =
-        rsrc(Q8 ? a.scales + (int64_t)n0 * a.nb : a.x, Q8 ? (uint32_t)(rows_w * a.nb * 4) : 0u);
+    __amdgpu_buffer_rsrc_t wr_src, sc_src;
+    if constexpr (WMODE == kWQ8P) {
+        // packed: this tile's slabs n0 / 32 .. ; slabs past the matrix read as 0
+        const int64_t slab_q = (int64_t)a.p_chunks * 8 * 1024, slab_s = (int64_t)a.p_chunks * 32 * 8 * 4;
+        const int live = (rows_w + 31) / 32;
+        wr_src = rsrc(static_cast<const char *>(a.w) + (int64_t)(n0 / 32) * slab_q, (uint32_t)(live * slab_q));
+        sc_src = rsrc(reinterpret_cast<const char *>(a.scales) + (int64_t)(n0 / 32) * slab_s, (uint32_t)(live * slab_s));
+    } else {
+        wr_src = rsrc(static_cast<const char *>(a.w) + (int64_t)n0 * a.ldw * wbytes, (uint32_t)(rows_w * a.ldw * wbytes));
+        sc_src = rsrc(Q8 ? a.scales + (int64_t)n0 * a.nb : a.x, Q8 ? (uint32_t)(rows_w * a.nb * 4) : 0u);
+    }
 
     f32x4 xr[XL];
     f32x4 wr[WL]; // raw 16-byte weight loads
@@ -131,9 +145,15 @@ __global__ __launch_bounds__(kThreads) void linear_mfma_kernel(LinearArgs a) {
         for (int i = 0; i < WL; ++i) {
             const int f = tid + kThreads * i;
             if (W_LOADS % kThreads != 0 && f >= W_LOADS) break; // whole waves drop out
-            constexpr int PER_ROW = Q8 ? BK / 16 : BK / 8;
-            const int row = f / PER_ROW, gk = k0 + (BK / PER_ROW) * (f % PER_ROW);
-            const uint32_t off = gk < a.k ? (uint32_t)(row * a.ldw + gk) * (uint32_t)wbytes : kOutOfRange;
+            uint32_t off;
+            if constexpr (WMODE == kWQ8P) {
+                // (slab f / 64, lane f % 64) of block k0 / 32: 16 int8 of row 32 slab + lane % 32
+                off = (uint32_t)(((f >> 6) * a.p_chunks * 8 + k0 / BK) * 64 + (f & 63)) * 16u;
+            } else {
+                constexpr int PER_ROW = Q8 ? BK / 16 : BK / 8;
+                const int row = f / PER_ROW, gk = k0 + (BK / PER_ROW) * (f % PER_ROW);
+                off = gk < a.k ? (uint32_t)(row * a.ldw + gk) * (uint32_t)wbytes : kOutOfRange;
+            }
             wr[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(wr_src, (int)off, 0, 0));
         }
         if constexpr (Q8) {
@@ -141,7 +161,11 @@ __global__ __launch_bounds__(kThreads) void linear_mfma_kernel(LinearArgs a) {
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
                 const int row = wn * WN + j * 32 + r32;
-                const uint32_t off = k0 < a.k ? (uint32_t)(row * a.nb + k0 / BK) * 4u : kOutOfRange;
+                uint32_t off;
+                if constexpr (WMODE == kWQ8P)
+                    off = (uint32_t)((((row >> 5) * a.p_chunks + k0 / 256) * 32 + (row & 31)) * 8 + (k0 / BK) % 8) * 4u;
+                else
+                    off = k0 < a.k ? (uint32_t)(row * a.nb + k0 / BK) * 4u : kOutOfRange;
                 sc_next[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sc_src, (int)off, 0, 0));
             }
         }
@@ -166,8 +190,10 @@ __global__ __launch_bounds__(kThreads) void linear_mfma_kernel(LinearArgs a) {
             const int f = tid + kThreads * i;
             if (W_LOADS % kThreads != 0 && f >= W_LOADS) break;
             if constexpr (Q8) {
-                // 16 int8 of k 16 (f % 2) .. +16 of row f / 2: two f16 chunks
-                const int row = f >> 1, c = 2 * (f & 1);
+                // 16 int8 of k 16 h .. +16 of one row: two f16 chunks.  Raw: row f / 2, h = f % 2;
+                // packed: slab f / 64, lane f % 64 -> row 32 slab + lane % 32, h = lane / 32
+                const int row = WMODE == kWQ8P ? ((f >> 6) << 5) + (f & 31) : f >> 1;
+                const int c = WMODE == kWQ8P ? 2 * ((f >> 5) & 1) : 2 * (f & 1);
                 const uint32_t *u = reinterpret_cast<const uint32_t *>(&wr[i]);
                 *reinterpret_cast<half8 *>(&ws[buf][lds_at(row, c)]) = int8x8_to_half8(u[0], u[1]);
                 *reinterpret_cast<half8 *>(&ws[buf][lds_at(row, c + 1)]) = int8x8_to_half8(u[2], u[3]);
@@ -276,10 +302,10 @@ __global__ __launch_bounds__(kThreads) void linear_mfma_kernel(LinearArgs a) {
     }
 }
 
-template <int BM, int BN, bool Q8>
+template <int BM, int BN, int WMODE>
 inline hipError_t launch_linear_tile(const LinearArgs &a, hipStream_t stream) {
     dim3 grid((unsigned)((a.m + BM - 1) / BM), (unsigned)((a.n + BN - 1) / BN));
-    linear_mfma_kernel<BM, BN, Q8><<<grid, kThreads, 0, stream>>>(a);
+    linear_mfma_kernel<BM, BN, WMODE><<<grid, kThreads, 0, stream>>>(a);
     return hipGetLastError();
 }
 

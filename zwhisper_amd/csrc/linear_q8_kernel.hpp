@@ -16,9 +16,11 @@
 // * linear_q8_stream_kernel<MT, S>: m <= 64 (decoder and LLM token steps, logits).  The weights
 //   are the stream: every int8 byte is read from HBM once, 16 bytes per lane per load (one Q8
 //   block of 32 weight rows per wave-load).  A workgroup of 4 waves owns 4*S slabs of 32 weight
-//   rows and walks k in chunks of 256 (8 blocks).  Each chunk of x ([32*MT][256] f32) is split
-//   into hi/lo halves once per workgroup and parked in LDS in the exact order the MFMA A operand
-//   wants it, so a wave's operand read is 1 KB contiguous (conflict-free ds_read_b128).
+//   rows and walks k in chunks of 256 (8 blocks).  x is split into hi/lo halves once per call by
+//   linear_q8_xprep_kernel, in the exact order the MFMA A operand wants it; each workgroup copies
+//   a chunk of it into LDS with direct global-to-LDS loads (no VGPRs, no VALU), issued before the
+//   chunk's weight loads so the wait for x never waits on the weights.  An operand read is then
+//   1 KB contiguous per wave (conflict-free ds_read_b128).
 //   v_mfma_f32_32x32x16_f16 with A = x rows, B = weight rows: lane l's 16 weight bytes
 //   q[row l%32][kb + 16 (l/32) .. +16] feed the block's two k-steps (bytes 0-7, then 8-15), and
 //   the result column l%32 is the weight row, so the block's scale is one f32 per lane.
@@ -48,6 +50,12 @@ constexpr int kQ8Threads = 256;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt in bits 3:0 and 15:14,
+// expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+__host__ __device__ constexpr int q8_vmcnt(int n) {
+    return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8);
+}
+
 struct Q8Args {
     const float *x;      // [m][k]
     const int8_t *q;     // [n][k]
@@ -59,19 +67,52 @@ struct Q8Args {
     int32_t chunks_per_split, n_split;
 };
 
-// Stream kernel LDS layout of one chunk of x: [block][m-tile][hi/lo][k-step][lane][8 halves].
-// Lane l, k-step s of (block b, m-tile i) holds x[32 i + l % 32][kb + 16 (l / 32) + 8 s + 0..7].
+// Layout of x's hi/lo halves, per chunk of 256 k: [block][m-tile][hi/lo][k-step][lane][8 halves],
+// 32 KB per m-tile.  Lane l, k-step s of (block b, m-tile i) holds x[32 i + l % 32][kb + 16 (l / 32)
+// + 8 s + 0..7], kb = 32 b.  One [hi/lo][k-step] piece of a (block, m-tile) is 1 KB: 64 lanes x 16 B.
+template <int MT>
+__host__ __device__ constexpr int q8_chunk_halves() {
+    return kQ8ChunkBlocks * MT * 2 * 2 * 64 * 8;
+}
 template <int MT>
 __device__ __forceinline__ int q8_xs_at(int b, int i, int hl, int s, int lane) {
     return ((((b * MT + i) * 2 + hl) * 2 + s) * 64 + lane) * 8;
 }
 
+// x f32 [m][k] -> xcvt f16 [n_chunks][chunk layout above]; rows >= m and columns >= k are 0.
+// One thread per 4 consecutive k of one row.
+template <int MT>
+__global__ __launch_bounds__(256) void linear_q8_xprep_kernel(const float *x, _Float16 *xcvt, int32_t m, int32_t k,
+                                                             int32_t n_chunks) {
+    const int64_t f = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t per_chunk = MT * 32 * (kQ8Chunk / 4);
+    if (f >= per_chunk * n_chunks) return;
+    const int c = (int)(f / per_chunk), rem = (int)(f % per_chunk);
+    const int row = rem / (kQ8Chunk / 4), kk = 4 * (rem % (kQ8Chunk / 4));
+    const int gk = c * kQ8Chunk + kk;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (row < m && gk < k) v = *reinterpret_cast<const f32x4 *>(x + (int64_t)row * k + gk);
+    const int b = kk >> 5, kb = kk & 31;
+    const int gg = kb >> 4, s = (kb >> 3) & 1, j = kb & 7;
+    const int i = row >> 5, l = (row & 31) + 32 * gg;
+    half4 hi, lo;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        hi[e] = (_Float16)v[e];
+        lo[e] = (_Float16)(v[e] - (float)hi[e]);
+    }
+    _Float16 *base = xcvt + (int64_t)c * q8_chunk_halves<MT>();
+    *reinterpret_cast<half4 *>(base + q8_xs_at<MT>(b, i, 0, s, l) + j) = hi;
+    *reinterpret_cast<half4 *>(base + q8_xs_at<MT>(b, i, 1, s, l) + j) = lo;
+}
+
 template <int MT, int S>
-__global__ __launch_bounds__(kQ8Threads) void linear_q8_stream_kernel(Q8Args a) {
+__global__ __launch_bounds__(kQ8Threads) void linear_q8_stream_kernel(Q8Args a, const _Float16 *xcvt) {
     constexpr int NB = kQ8ChunkBlocks;
-    constexpr int XL = MT * 32 * kQ8Chunk / 4 / kQ8Threads; // float4 loads of x per thread per chunk
-    constexpr int ROWS = 4 * S * 32;                         // weight rows per workgroup
-    __shared__ __align__(16) _Float16 xs[MT * NB * 2 * 2 * 64 * 8];
+    constexpr int ROWS = 4 * S * 32;                   // weight rows per workgroup
+    constexpr int PIECES = q8_chunk_halves<MT>() / 512; // 1 KB pieces of an x chunk
+    constexpr int XL = PIECES / 4;                      // pieces each wave copies
+    __shared__ __align__(16) _Float16 xs[q8_chunk_halves<MT>()];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r32 = lane & 31, g = lane >> 5;
@@ -82,11 +123,18 @@ __global__ __launch_bounds__(kQ8Threads) void linear_q8_stream_kernel(Q8Args a) 
     const int c_begin = split * a.chunks_per_split;
     const int c_end = min(c_begin + a.chunks_per_split, n_chunks);
 
-    // x: rows past m read as 0 (range ends at row m); q / scales: rows past n read as 0.
-    const __amdgpu_buffer_rsrc_t x_src = rsrc(a.x, (uint32_t)((int64_t)a.m * a.k * 4));
+    // q / scales: rows past n read as 0.  x_src: the call's prepared x chunks.
+    const __amdgpu_buffer_rsrc_t x_src = rsrc(xcvt, (uint32_t)n_chunks * (uint32_t)PIECES * 1024u);
     const int rows_w = min(ROWS, a.n - n0);
     const __amdgpu_buffer_rsrc_t q_src = rsrc(a.q + (int64_t)n0 * a.k, (uint32_t)((int64_t)rows_w * a.k));
     const __amdgpu_buffer_rsrc_t s_src = rsrc(a.scales + (int64_t)n0 * a.nb, (uint32_t)((int64_t)rows_w * a.nb * 4));
+    uint32_t qbase[S], sbase[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int row = wrow0 + s * 32 + r32;
+        qbase[s] = (uint32_t)(row * a.k + 16 * g);
+        sbase[s] = (uint32_t)(row * a.nb) * 4u;
+    }
 
     f32x16 acc[MT][S];
 #pragma unroll
@@ -96,35 +144,18 @@ __global__ __launch_bounds__(kQ8Threads) void linear_q8_stream_kernel(Q8Args a) 
 
     for (int c = c_begin; c < c_end; ++c) {
         const int k0 = c * kQ8Chunk;
-        // x chunk: float4 f covers row f / 64, k = k0 + 4 (f % 64)
-        f32x4 xr[XL];
-#pragma unroll
-        for (int u = 0; u < XL; ++u) {
-            const int f = tid + kQ8Threads * u;
-            const int row = f / (kQ8Chunk / 4), gk = k0 + 4 * (f % (kQ8Chunk / 4));
-            const uint32_t off = gk < a.k ? (uint32_t)(row * a.k + gk) * 4u : kOutOfRange;
-            xr[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(x_src, (int)off, 0, 0));
-        }
         __syncthreads(); // the previous chunk's operand reads are done
+        // x chunk into LDS: wave w copies pieces w, w + 4, ...; lane l's 16 bytes land at l * 16
 #pragma unroll
         for (int u = 0; u < XL; ++u) {
-            const int f = tid + kQ8Threads * u;
-            const int row = f / (kQ8Chunk / 4), kk = 4 * (f % (kQ8Chunk / 4));
-            const int b = kk >> 5, kb = kk & 31;
-            const int gg = kb >> 4, s = (kb >> 3) & 1, j = kb & 7;
-            const int i = row >> 5, l = (row & 31) + 32 * gg;
-            half4 hi, lo;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                hi[e] = (_Float16)xr[u][e];
-                lo[e] = (_Float16)(xr[u][e] - (float)hi[e]);
-            }
-            *reinterpret_cast<half4 *>(&xs[q8_xs_at<MT>(b, i, 0, s, l) + j]) = hi;
-            *reinterpret_cast<half4 *>(&xs[q8_xs_at<MT>(b, i, 1, s, l) + j]) = lo;
+            const int piece = wave + 4 * u;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(x_src, (__attribute__((address_space(3))) void *)(xs + piece * 512), 16,
+                                                 (uint32_t)((c * PIECES + piece) * 1024 + lane * 16), 0, 0, 0);
         }
-        __syncthreads();
-
-        // this wave's weights for the chunk: slab s, block b -> 16 bytes per lane, and its scale
+        __builtin_amdgcn_sched_barrier(0);
+        // This wave's weights for the chunk (slab s, block b: 16 bytes per lane) and the blocks'
+        // scales.  A block past k gets scale 0 (its offset is out of range), so whatever the
+        // weight load returned there adds exactly nothing.
         u32x4 wq[S][NB];
         float sc[S][NB];
 #pragma unroll
@@ -132,16 +163,21 @@ __global__ __launch_bounds__(kQ8Threads) void linear_q8_stream_kernel(Q8Args a) 
             const int kb = k0 + b * kQ8Block;
 #pragma unroll
             for (int s = 0; s < S; ++s) {
-                const int row = wrow0 + s * 32 + r32;
-                const uint32_t qoff = kb < a.k ? (uint32_t)(row * a.k + kb + 16 * g) : kOutOfRange;
-                const uint32_t soff = kb < a.k ? (uint32_t)(row * a.nb + kb / kQ8Block) * 4u : kOutOfRange;
-                wq[s][b] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(q_src, (int)qoff, 0, 0));
+                wq[s][b] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(q_src, (int)(qbase[s] + (uint32_t)kb), 0, 0));
+                const uint32_t soff = kb < a.k ? sbase[s] + (uint32_t)(kb / kQ8Block) * 4u : kOutOfRange;
                 sc[s][b] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(s_src, (int)soff, 0, 0));
             }
         }
+        // wait for this wave's x pieces only (loads complete in order; the 2 S NB weight and
+        // scale loads were issued after them), then for every wave's
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(q8_vmcnt(2 * S * NB));
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-            if (k0 + b * kQ8Block >= a.k) break; // uniform: the last chunk may be short
             half8 ah[MT][2], al[MT][2];
 #pragma unroll
             for (int i = 0; i < MT; ++i)
@@ -172,6 +208,200 @@ __global__ __launch_bounds__(kQ8Threads) void linear_q8_stream_kernel(Q8Args a) 
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         const int col = n0 + wrow0 + s * 32 + r32;
+        if (col >= a.n) continue;
+        const float bj = (a.n_split == 1 && a.bias) ? a.bias[col] : 0.f;
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+                if (row < a.m) dst[(int64_t)row * a.n + col] = acc[i][s][r] + bj;
+            }
+    }
+}
+
+// Packed device weights (zwg_q8w): the same int8 and scales, laid out for the stream kernel so
+// that every wave-load is contiguous.  n is padded to whole slabs of 32 rows, k to whole chunks
+// of 256 (8 blocks); padding is zero (scale 0).
+//   q:      [slab][block][lane][16 bytes], lane l of (slab s, block b) holding
+//           q[32 s + l % 32][32 b + 16 (l / 32) .. +16]: one 1 KB tile per (slab, block).
+//   scales: [slab][chunk][32 rows][8 blocks] f32: a lane's 8 block scales of a chunk are 32
+//           contiguous bytes, and the 32 rows of a slab 1 KB.
+struct Q8Packed {
+    const uint8_t *q;
+    const float *scales;
+    int32_t n_slabs, n_chunks;
+};
+
+__host__ __device__ inline int64_t q8p_q_bytes(int64_t n_slabs, int64_t n_chunks) {
+    return n_slabs * n_chunks * kQ8ChunkBlocks * 1024;
+}
+__host__ __device__ inline int64_t q8p_scale_bytes(int64_t n_slabs, int64_t n_chunks) {
+    return n_slabs * n_chunks * 32 * kQ8ChunkBlocks * 4;
+}
+
+// Pack q [n][k] (int8) and scales [n][k / 32] into the layout above: one thread per 16-byte
+// piece of a q tile (and, for the first 8 lanes of a slab's chunk, nothing else); scales by a
+// second grid-stride pass in the same kernel.
+__global__ __launch_bounds__(256) void linear_q8_pack_kernel(const int8_t *q, const float *scales, int32_t n,
+                                                            int32_t k, uint8_t *pq, float *ps, int32_t n_slabs,
+                                                            int32_t n_chunks) {
+    const int32_t nb = k / kQ8Block, nbp = n_chunks * kQ8ChunkBlocks;
+    const int64_t pieces = (int64_t)n_slabs * nbp * 64;
+    const int64_t sc_elems = (int64_t)n_slabs * n_chunks * 32 * kQ8ChunkBlocks;
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t f = (int64_t)blockIdx.x * 256 + threadIdx.x; f < pieces; f += stride) {
+        const int lane = (int)(f & 63);
+        const int64_t tile = f >> 6;
+        const int b = (int)(tile % nbp);
+        const int64_t slab = tile / nbp;
+        const int64_t row = slab * 32 + (lane & 31);
+        const int kk = b * kQ8Block + 16 * (lane >> 5);
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (row < n && kk < k) v = *reinterpret_cast<const u32x4 *>(q + row * k + kk);
+        *reinterpret_cast<u32x4 *>(pq + f * 16) = v;
+    }
+    for (int64_t f = (int64_t)blockIdx.x * 256 + threadIdx.x; f < sc_elems; f += stride) {
+        const int b8 = (int)(f & 7);
+        const int r = (int)((f >> 3) & 31);
+        const int64_t sc_chunk = f >> 8; // slab * n_chunks + chunk
+        const int c = (int)(sc_chunk % n_chunks);
+        const int64_t slab = sc_chunk / n_chunks;
+        const int64_t row = slab * 32 + r;
+        const int b = c * kQ8ChunkBlocks + b8;
+        ps[f] = (row < n && b < nb) ? scales[row * nb + b] : 0.f;
+    }
+}
+
+// The stream kernel over packed weights, software-pipelined.  k is walked in stages of 4 blocks
+// (128 k).  x stages sit in LDS double-buffered and each wave keeps two register sets of weights
+// and scales, so the loads of stage t + 1 (x by LDS DMA, then weights, then scales) are in flight
+// while stage t's MFMAs run: at the top of stage t the wave waits only for its own x pieces of
+// stage t (loads complete in order, and stage t's weights were issued after them), and the
+// barrier that follows also tells every wave that stage t - 1's LDS buffer is free again.
+// Padding blocks (k is padded to 256) have scale 0 and x 0; a stage wholly past k is not run.
+constexpr int kQ8StageBlocks = 4;
+
+template <int MT, int S>
+__global__ __launch_bounds__(kQ8Threads) void linear_q8p_stream_kernel(Q8Args a, Q8Packed w, const _Float16 *xcvt) {
+    constexpr int NB = kQ8StageBlocks;
+    constexpr int SLABS = 4 * S;                  // slabs of 32 weight rows per workgroup
+    constexpr int PIECES = NB * MT * 4;           // 1 KB pieces of an x stage
+    constexpr int XL = PIECES / 4;                // pieces each wave copies
+    constexpr int STAGE_HALVES = PIECES * 512;
+    __shared__ __align__(16) _Float16 xs[2][STAGE_HALVES];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // uniform: the LDS DMA base is per wave
+    const int r32 = lane & 31, g = lane >> 5;
+    const int slab0 = blockIdx.x * SLABS + wave * S; // this wave's first slab
+    const int split = blockIdx.y;
+    const int n_stages = (a.k + NB * kQ8Block - 1) / (NB * kQ8Block);
+    const int t_begin = split * a.chunks_per_split * 2;
+    const int t_end = min(t_begin + a.chunks_per_split * 2, n_stages);
+
+    const __amdgpu_buffer_rsrc_t x_src = rsrc(xcvt, (uint32_t)w.n_chunks * 2u * (uint32_t)PIECES * 1024u);
+    // slabs past the matrix (the last workgroup's) read as 0
+    const int live = __builtin_amdgcn_readfirstlane(max(0, min(S, w.n_slabs - slab0)));
+    const int64_t slab_q = (int64_t)w.n_chunks * kQ8ChunkBlocks * 1024;
+    const int64_t slab_s = (int64_t)w.n_chunks * 32 * kQ8ChunkBlocks * 4;
+    const __amdgpu_buffer_rsrc_t q_src = rsrc(w.q + (int64_t)slab0 * slab_q, (uint32_t)(live * slab_q));
+    const __amdgpu_buffer_rsrc_t s_src =
+        rsrc(reinterpret_cast<const char *>(w.scales) + (int64_t)slab0 * slab_s, (uint32_t)(live * slab_s));
+
+    // stage t: x pieces into LDS buffer `buf`, then this wave's weights and scales into (wq, sc).
+    // Past the last stage (t >= t_end) the same loads go out with out-of-range offsets: they return
+    // zeros without touching memory, and every path through the loop then has the same loads in
+    // flight, so the compiler's in-order wait counts stay exact.
+    auto issue = [&](int t, int buf, u32x4 (&wq)[S][NB], f32x4 (&sc)[S]) {
+        const bool live_t = t < t_end;
+#pragma unroll
+        for (int u = 0; u < XL; ++u) {
+            const int piece = wave + 4 * u;
+            const uint32_t off = live_t ? (uint32_t)((t * PIECES + piece) * 1024 + lane * 16) : kOutOfRange;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                x_src, (__attribute__((address_space(3))) void *)(&xs[buf][piece * 512]), 16, off, 0, 0, 0);
+        }
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+                const uint32_t off = live_t ? (uint32_t)(s * slab_q + ((int64_t)(t * NB + b) * 64 + lane) * 16)
+                                            : kOutOfRange;
+                wq[s][b] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(q_src, (int)off, 0, 0));
+            }
+            // scales of blocks 4 (t % 2) .. +4 of chunk t / 2, this lane's row
+            const uint32_t off =
+                live_t ? (uint32_t)(s * slab_s + (((t >> 1) * 32 + r32) * kQ8ChunkBlocks + 4 * (t & 1)) * 4)
+                       : kOutOfRange;
+            sc[s] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(s_src, (int)off, 0, 0));
+        }
+    };
+
+    f32x16 acc[MT][S];
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int s = 0; s < S; ++s) acc[i][s] = (f32x16){0};
+
+    auto compute = [&](int buf, const u32x4 (&wq)[S][NB], const f32x4 (&sc)[S]) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            half8 ah[MT][2], al[MT][2];
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    ah[i][s] = *reinterpret_cast<const half8 *>(&xs[buf][q8_xs_at<MT>(b, i, 0, s, lane)]);
+                    al[i][s] = *reinterpret_cast<const half8 *>(&xs[buf][q8_xs_at<MT>(b, i, 1, s, lane)]);
+                }
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const half8 w0 = int8x8_to_half8(wq[s][b][0], wq[s][b][1]);
+                const half8 w1 = int8x8_to_half8(wq[s][b][2], wq[s][b][3]);
+                const float scb = sc[s][b];
+#pragma unroll
+                for (int i = 0; i < MT; ++i) {
+                    f32x16 tt = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][0], w0, (f32x16){0}, 0, 0, 0);
+                    tt = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][0], w0, tt, 0, 0, 0);
+                    tt = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[i][1], w1, tt, 0, 0, 0);
+                    tt = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[i][1], w1, tt, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) acc[i][s][r] = __builtin_fmaf(tt[r], scb, acc[i][s][r]);
+                }
+            }
+        }
+    };
+
+    // Two register sets (A for even stages, B for odd) so every index is static.
+    u32x4 wqA[S][NB], wqB[S][NB];
+    f32x4 scA[S], scB[S];
+    constexpr int LOADS = S * (NB + 1); // weight and scale loads of one stage, issued after its x
+    issue(t_begin, 0, wqA, scA);
+    for (int t = t_begin; t < t_end; t += 2) {
+        // stage t (set A, buffer 0)
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(q8_vmcnt(LOADS));
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        issue(t + 1, 1, wqB, scB);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(0, wqA, scA);
+        // stage t + 1 (set B, buffer 1); a no-op past the end (its loads returned zeros)
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(q8_vmcnt(LOADS));
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        issue(t + 2, 0, wqA, scA);
+        __builtin_amdgcn_sched_barrier(0);
+        if (t + 1 < t_end) compute(1, wqB, scB);
+    }
+    __builtin_amdgcn_s_waitcnt(q8_vmcnt(0)); // the last, out-of-range prefetch
+
+    float *dst = a.n_split > 1 ? a.part + (int64_t)split * a.m * a.n : a.out;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int col = (slab0 + s) * 32 + r32;
         if (col >= a.n) continue;
         const float bj = (a.n_split == 1 && a.bias) ? a.bias[col] : 0.f;
 #pragma unroll

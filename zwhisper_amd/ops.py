@@ -200,6 +200,16 @@ class Context:
                                               self._dev_ptr(w.scales, "scales"), self._dev_ptr(bias, "bias"), n,
                                               self._dev_ptr(out, "out")))
 
+    def linear_q8w_dev(self, x, m: int, w: "Q8Resident", bias, out) -> None:
+        """out[m][w.n] = x[m][w.k] . W^T (+ bias) over resident packed int8 weights: CUDA float32 tensors."""
+        if not isinstance(w, Q8Resident):
+            raise ZwgError("w must be a Q8Resident (Q8.resident)")
+        if x.numel() < m * w.k or out.numel() < m * w.n or (bias is not None and bias.numel() < w.n):
+            raise ZwgError("a tensor is shorter than m, n and k need")
+        self._bind_torch_stream()
+        self._check(self._L.zwg_linear_q8w_dev(self._h, self._dev_ptr(x, "x"), m, w.handle,
+                                               self._dev_ptr(bias, "bias"), self._dev_ptr(out, "out")))
+
     def attention_dev(self, q, k, v, sh: AttnShape, out) -> None:
         self._bind_torch_stream()
         c = sh.to_c()
@@ -381,6 +391,11 @@ class Q8:
         q = np.asarray(self.q).reshape(self.n, self.k)[i].astype(np.float32).reshape(-1, Q8_BLOCK)
         return (q * np.asarray(self.scales, np.float32).reshape(self.n, -1)[i][:, None]).reshape(-1)
 
+    def resident(self, ctx: "Context") -> "Q8Resident":
+        """These weights uploaded once into HBM in the packed device layout (zwg_q8w_create): the
+        GPU form of building the Q8 at load.  From host arrays or CUDA tensors."""
+        return Q8Resident(ctx, self)
+
     def to_device(self, device: int = 0) -> "Q8":
         """The same weights as CUDA tensors (int8 q, float32 scales), for Context.linear_q8_dev."""
         import torch
@@ -388,6 +403,60 @@ class Q8:
         q = torch.as_tensor(np.ascontiguousarray(np.asarray(self.q, np.int8).reshape(self.n, self.k)))
         s = torch.as_tensor(np.ascontiguousarray(np.asarray(self.scales, np.float32).reshape(self.n, -1)))
         return Q8(q.to(f"cuda:{device}"), s.to(f"cuda:{device}"), self.n, self.k)
+
+
+class Q8Resident:
+    """Int8 block weights resident in HBM in the packed device layout (zwg_q8w).  Use with
+    Context.linear_q8w_dev; close() (or the context manager) frees them, before the context."""
+
+    def __init__(self, ctx: "Context", w: Q8):
+        import ctypes
+
+        self.ctx, self.n, self.k = ctx, w.n, w.k
+        h = ctypes.c_void_p()
+        if isinstance(w.q, np.ndarray):
+            q = np.ascontiguousarray(w.q, dtype=np.int8)
+            sc = np.ascontiguousarray(w.scales, dtype=np.float32)
+            if q.size < w.n * w.k or sc.size < w.n * (w.k // Q8_BLOCK):
+                raise ZwgError("q or scales shorter than [n][k] needs")
+            rc = ctx._L.zwg_q8w_create(ctx.handle, q.ctypes.data, sc.ctypes.data, w.n, w.k, _lib.Q8W_FROM_HOST,
+                                       ctypes.byref(h))
+        else:
+            import torch
+
+            if not (isinstance(w.q, torch.Tensor) and w.q.is_cuda and w.q.dtype == torch.int8
+                    and w.q.is_contiguous() and w.scales.is_contiguous()):
+                raise ZwgError("w must hold contiguous host arrays or CUDA int8 / float32 tensors")
+            if w.q.numel() < w.n * w.k or w.scales.numel() < w.n * (w.k // Q8_BLOCK):
+                raise ZwgError("q or scales shorter than [n][k] needs")
+            ctx._bind_torch_stream()
+            rc = ctx._L.zwg_q8w_create(ctx.handle, w.q.data_ptr(), Context._dev_ptr(w.scales, "scales"), w.n, w.k, 0,
+                                       ctypes.byref(h))
+        ctx._check(rc)
+        self._h = h.value
+
+    @property
+    def handle(self):
+        if not self._h:
+            raise ZwgError("weights are closed")
+        return self._h
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            self.ctx._L.zwg_q8w_destroy(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def linear(pool, x, m: int, k: int, w, b, n: int, out) -> None:
