@@ -24,7 +24,8 @@ HBM roofline and oracle/kv.py's update timed beside it, and the six linear layer
 encoder layer over the 16 windows ("base_enc_linear_x16", f16 weights on f16 MFMA) with the
 oracle's ops.linear timed beside it, and three decode steps' linear layers over int8 block
 weights (HBM-bound; "qwen15_logits_q8_x64", "qwen15_decode_q8_linear_x64",
-"small_dec_q8_linear_x32") with the oracle's ops.linear over Q8 timed beside them.
+"small_dec_q8_linear_x32") with the oracle's ops.linear over Q8 timed beside them, and one whole
+base.en encoder layer over the 16 windows ("base_enc_layer_x16") with the oracle's layer beside it.
 """
 from __future__ import annotations
 
@@ -344,6 +345,77 @@ class LinearWorkload:
 
     def free(self):
         self.x = self.out = self.w = self.b = None
+
+
+class EncoderLayerWorkload:
+    """One Whisper base.en encoder layer over 16 windows x 1500 frames on the device
+    (zwg_encoder_layer_dev: the loop body of src/encoder.zig:164-175): two layer norms, the q/k/v/o
+    and MLP projections with f16 weights (GELU and the residual adds fused into their stores) and
+    the 16 windows' self-attention (8 heads x 64).
+
+    Algorithmic work: the projections' 2 m n k (24 m n_state^2 over all six) plus attention's 4 d H per
+    (q, k) pair.  Roofline: the time both would take at their own MFMA peaks (f16 MFMA for the
+    projections at two MFMAs per f32 x f16 product, fp32 MFMA for attention); the layer norms and
+    the attention's row-major K read add no flops.
+    """
+
+    name = "base_enc_layer_x16"
+    description = ("Whisper base.en encoder layer, 16 windows x 1500 frames: layer norms, q/k/v/o and MLP "
+                   "(f16 weights, GELU and residuals fused), self-attention 8x64")
+
+    def __init__(self, torch, ctx, windows: int = 16):
+        import zwhisper_amd as z
+
+        self.torch, self.ctx, self.windows = torch, ctx, windows
+        self.n_ctx, self.ns, self.n_head = 1500, 512, 8
+        ns = self.ns
+        g = torch.Generator(device="cuda").manual_seed(0xE1)
+
+        def f16(n, k):
+            return (torch.randn(n, k, device="cuda", generator=g) / np.sqrt(k)).half()
+
+        def vec(n):
+            return torch.randn(n, device="cuda", generator=g) * 0.1
+
+        self.w = {"attn_ln_w": 1 + vec(ns), "attn_ln_b": vec(ns), "q_w": f16(ns, ns), "q_b": vec(ns),
+                  "k_w": f16(ns, ns), "v_w": f16(ns, ns), "v_b": vec(ns), "o_w": f16(ns, ns), "o_b": vec(ns),
+                  "mlp_ln_w": 1 + vec(ns), "mlp_ln_b": vec(ns), "mlp0_w": f16(4 * ns, ns), "mlp0_b": vec(4 * ns),
+                  "mlp1_w": f16(ns, 4 * ns), "mlp1_b": vec(ns)}
+        rows = windows * self.n_ctx
+        self.x0 = torch.randn(windows, self.n_ctx, ns, device="cuda", generator=g)
+        self.x = self.x0.clone()
+        self.scratch = torch.empty(z.ops.encoder_layer_scratch(rows, ns), device="cuda")
+        self.lin_flops = 24.0 * rows * ns * ns
+        self.attn_flops = 4.0 * self.n_ctx * self.n_ctx * ns * windows
+        self.work = self.lin_flops + self.attn_flops
+        self.ideal_s = self.lin_flops * 2 / PEAK_MFMA_F16 + self.attn_flops / PEAK_MFMA_F32
+
+    def step(self, i: int):
+        # the layer updates x in place, so successive steps apply it to its own output, as the
+        # encoder's stack of layers does; every linear reads normalised rows, so magnitudes stay put
+        self.ctx.encoder_layer_dev(self.x, self.windows, self.n_ctx, self.ns, self.n_head, self.w, self.scratch)
+
+    def cpu_baseline(self, threads: int) -> dict:
+        """The oracle's encoder layer (ops.layerNorm, ops.linear over f16, ops.attention, ops.gelu,
+        ops.add restated in oracle/attn_oracle.c) on one of the 16 windows, best of 3 after a warm-up."""
+        import oracle
+
+        w = {k: v.cpu().numpy() for k, v in self.w.items()}
+        x = self.x0[0].cpu().numpy()
+        o = oracle.Oracle(threads)
+        o.encoder_layer(x, self.n_ctx, self.ns, self.n_head, w)
+        best = float("inf")
+        for _ in range(3):
+            t0 = time.perf_counter()
+            o.encoder_layer(x, self.n_ctx, self.ns, self.n_head, w)
+            best = min(best, time.perf_counter() - t0)
+        o.close()
+        return {"value": self.work / self.windows / best / 1e12, "unit": "TFLOP/s", "cores": o.threads,
+                "kind": "port", "sample": "1 of 16 windows; oracle Oracle.encoder_layer (attn_oracle.c), best of 3 "
+                                          "after one warm-up", "seconds": best}
+
+    def free(self):
+        self.w = self.x = self.x0 = self.scratch = None
 
 
 class Q8LinearWorkload:
@@ -678,6 +750,27 @@ def main() -> int:
         results[wl.name] = res
         print(f"[bench] {wl.name}: {res['value']:.2f} TFLOP/s ({r['ms_per_step']:.4f} ms/step, kernels "
               f"{r['kernel_ms_mean']:.4f} ms, {100 * res['roofline']['frac']:.1f}% of f16 mfma peak)"
+              + (f", cpu {res['cpu_baseline']['value']:.3f} TFLOP/s" if not args.no_cpu else ""),
+              file=sys.stderr, flush=True)
+        wl.free()
+        wl = EncoderLayerWorkload(torch, ctx)
+        r = time_workload(wl, args.steps, args.warmup)
+        achieved = wl.work / (r["kernel_ms_mean"] * 1e-3)
+        peak = wl.work / wl.ideal_s
+        res = {"workload": wl.name, "description": wl.description,
+               "value": wl.work / (r["ms_per_step"] * 1e-3) / 1e12, "unit": "TFLOP/s",
+               "ms_per_step": r["ms_per_step"], "kernel_ms_mean": r["kernel_ms_mean"],
+               "kernel_ms_min": r["kernel_ms_min"], "algorithmic_work_per_step": wl.work,
+               "dtype": "f32 (projections: f32 x f16 on f16 MFMA with x split into two f16 terms; attention: fp32 MFMA)",
+               "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
+                            "frac": achieved / peak, "traffic": None,
+                            "note": "peak = the layer's flops over the time they take at their own peaks: "
+                                    "projections at half the f16 MFMA peak, attention at the fp32 MFMA peak"}}
+        if not args.no_cpu:
+            res["cpu_baseline"] = wl.cpu_baseline(host_threads())
+        results[wl.name] = res
+        print(f"[bench] {wl.name}: {res['value']:.2f} TFLOP/s ({r['ms_per_step']:.4f} ms/step, kernels "
+              f"{r['kernel_ms_mean']:.4f} ms, {100 * res['roofline']['frac']:.1f}% of the layer's mfma roofline)"
               + (f", cpu {res['cpu_baseline']['value']:.3f} TFLOP/s" if not args.no_cpu else ""),
               file=sys.stderr, flush=True)
         wl.free()

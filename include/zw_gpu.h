@@ -268,6 +268,63 @@ int zwg_q8w_shape(const zwg_q8w *w, uint64_t *n, uint64_t *k);
 /* out[m][n] = x[m][k] . W^T (+ bias): device pointers, asynchronous on ctx's stream. */
 int zwg_linear_q8w_dev(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, const float *bias, float *out);
 
+/*
+ * Linear-layer epilogues: the value v = x . W^T + b of out[i][o] is stored as v (NONE), as gelu(v)
+ * (GELU: ops.linear then ops.gelu, src/encoder.zig:172-173, src/decoder.zig:198-199), or added to
+ * what out holds (ADD: ops.linear then ops.add, the residual of src/encoder.zig:169, :174).
+ */
+#define ZWG_EPI_NONE 0u
+#define ZWG_EPI_GELU 1u
+#define ZWG_EPI_ADD 2u
+
+/* f16 weights with an epilogue and an output row stride (out_stride >= n; 0 = n),
+ * device pointers, asynchronous. */
+int zwg_linear_epi_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void *w, uint32_t w_type,
+                       const float *bias, uint64_t n, float *out, uint64_t out_stride, uint32_t epilogue);
+/* Resident int8 weights with an epilogue, device pointers, asynchronous. */
+int zwg_linear_q8w_epi_dev(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, const float *bias, float *out,
+                           uint32_t epilogue);
+
+/*
+ * Row-wise and elementwise ops around the projections, device pointers, asynchronous:
+ * ops.layerNormEps (src/ops.zig:388-395; ops.layerNorm is eps = 1e-5, BERT uses 1e-12):
+ * out[i] = (x[i] - mean) / sqrt(var + eps) * w + b per row of x [m][n]; ops.gelu (src/ops.zig:
+ * 310-340), ggml's tanh form, in place; ops.add: x += y.  n and count multiples of 4, buffers
+ * 16-byte aligned.
+ */
+int zwg_layer_norm_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t n, const float *w, const float *b, float eps,
+                       float *out);
+int zwg_gelu_dev(zwg_ctx *ctx, float *x, uint64_t count);
+int zwg_add_dev(zwg_ctx *ctx, float *x, const float *y, uint64_t count);
+
+/*
+ * One Whisper encoder layer (the loop body of Encoder.encode, src/encoder.zig:164-175) over
+ * n_windows windows at once: x [n_windows][n_ctx][n_state] is updated in place, as the
+ * reference updates e.x.  Weights are the layer's tensors as src/encoder.zig loads them: f16
+ * matrices [out][in], f32 norms and biases (k has no bias).  scratch: device memory of
+ * zwg_encoder_layer_scratch(n_windows * n_ctx, n_state) floats (the reference's x_ln, q, k, v,
+ * attn and hidden buffers, src/encoder.zig:98-106).  Device pointers, asynchronous.
+ */
+typedef struct zwg_enc_layer {
+    const float *attn_ln_w, *attn_ln_b; /* [n_state] */
+    const void *q_w;                    /* f16 [n_state][n_state] */
+    const float *q_b;
+    const void *k_w; /* no bias */
+    const void *v_w;
+    const float *v_b;
+    const void *o_w;
+    const float *o_b;
+    const float *mlp_ln_w, *mlp_ln_b;
+    const void *mlp0_w; /* f16 [4 n_state][n_state] */
+    const float *mlp0_b;
+    const void *mlp1_w; /* f16 [n_state][4 n_state] */
+    const float *mlp1_b;
+} zwg_enc_layer;
+
+uint64_t zwg_encoder_layer_scratch(uint64_t n_rows, uint64_t n_state);
+int zwg_encoder_layer_dev(zwg_ctx *ctx, float *x, uint64_t n_windows, uint64_t n_ctx, uint64_t n_state,
+                          uint64_t n_head, const zwg_enc_layer *w, float *scratch);
+
 int zwg_version(void); /* ZWG_VERSION */
 
 #ifdef __cplusplus

@@ -110,6 +110,10 @@ def lib():
         L.ora_linear_q8.restype = None
         L.ora_linear_q8.argtypes = [ctypes.c_void_p, _fp, _c_size, _c_size, ctypes.c_void_p, _fp, ctypes.c_void_p,
                                     _c_size, _fp]
+        L.ora_layer_norm.restype = None
+        L.ora_layer_norm.argtypes = [ctypes.c_void_p, _fp, _c_size, _c_size, _fp, _fp, ctypes.c_float, _fp]
+        L.ora_gelu.restype = None
+        L.ora_gelu.argtypes = [ctypes.c_void_p, _fp, _c_size]
         L.ora_q8_quantize.restype = None
         L.ora_q8_quantize.argtypes = [_fp, _c_size, _c_size, ctypes.c_void_p, _fp]
         _lib = L
@@ -246,6 +250,40 @@ class Oracle:
         self._L.ora_linear_q8(self._pool, _ptr(x), m, k, q.ctypes.data, _ptr(sc),
                               None if bb is None else bb.ctypes.data, n, _ptr(out))
         return out
+
+    def layer_norm(self, x, m: int, n: int, w, b, eps: float = 1e-5) -> np.ndarray:
+        """ops.layerNormEps (src/ops.zig:388-395) of x [m][n]; returns out [m][n]."""
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+        w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+        b = np.ascontiguousarray(b, dtype=np.float32).reshape(-1)
+        if x.size < m * n or w.size < n or b.size < n:
+            raise ValueError("x, w or b shorter than the shape needs")
+        out = np.empty(m * n, np.float32)
+        self._L.ora_layer_norm(self._pool, _ptr(x), m, n, _ptr(w), _ptr(b), eps, _ptr(out))
+        return out.reshape(m, n)
+
+    def gelu(self, x) -> np.ndarray:
+        """ops.gelu (src/ops.zig:335-340) on a copy of x."""
+        y = np.ascontiguousarray(x, dtype=np.float32).copy()
+        self._L.ora_gelu(self._pool, _ptr(y.reshape(-1)), y.size)
+        return y
+
+    def encoder_layer(self, x, n_ctx: int, n_state: int, n_head: int, w: dict) -> np.ndarray:
+        """One Whisper encoder layer (src/encoder.zig:164-175) on one window x [n_ctx][n_state] with f16
+        weights (w: attn_ln_w/b, q_w/q_b, k_w, v_w/v_b, o_w/o_b, mlp_ln_w/b, mlp0_w/b, mlp1_w/b); returns
+        the new x.  ops.add is the plain f32 sum."""
+        ns = n_state
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(n_ctx, ns).copy()
+        xl = self.layer_norm(x, n_ctx, ns, w["attn_ln_w"], w["attn_ln_b"])
+        q = self.linear_f16(xl, n_ctx, ns, w["q_w"], w["q_b"], ns)
+        k = self.linear_f16(xl, n_ctx, ns, w["k_w"], None, ns)
+        v = self.linear_f16(xl, n_ctx, ns, w["v_w"], w["v_b"], ns)
+        att = self.attention(q, k, v, n_ctx, n_ctx, ns, n_head, False)
+        x += self.linear_f16(att, n_ctx, ns, w["o_w"], w["o_b"], ns).reshape(n_ctx, ns)
+        xl = self.layer_norm(x, n_ctx, ns, w["mlp_ln_w"], w["mlp_ln_b"])
+        h = self.gelu(self.linear_f16(xl, n_ctx, ns, w["mlp0_w"], w["mlp0_b"], 4 * ns))
+        x += self.linear_f16(h, n_ctx, 4 * ns, w["mlp1_w"], w["mlp1_b"], ns).reshape(n_ctx, ns)
+        return x
 
     def attention(self, q, k, v, n_q, n_kv, n_state, n_head, causal, out=None) -> np.ndarray:
         """ops.attention (src/ops.zig:593-605)."""

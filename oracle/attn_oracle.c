@@ -26,6 +26,8 @@
  *   gemm.Q8.quantize ....... src/gemm.zig:209-230  (ora_q8_quantize)
  *   gemm.dotQ / micro4x4Q .. src/gemm.zig:274-333  (dot_q8, micro4x4_q8)
  *   gemm.mc, nc ............ src/gemm.zig:27-28
+ *   ops.layerNormEps ....... src/ops.zig:342-395, normRow :355-381 (ora_layer_norm)
+ *   ops.gelu ............... src/ops.zig:310-340, geluScalar/geluVec :312-327 (ora_gelu)
  *
  * V, the vector width, is 16 (the reference's value on AVX-512 hosts, src/gemm.zig:15-24):
  * it fixes the K padding (n_kv_pad), the column count of S and the split between
@@ -723,4 +725,99 @@ static void nt_block_q8(const float *a, size_t lda, const int8_t *q, const float
 void ora_linear_q8(ora_pool *pool, const float *x, size_t m, size_t k, const int8_t *q, const float *scales,
                    const float *b, size_t n, float *out) {
     linear_any(pool, x, m, k, NULL, q, scales, b, n, out);
+}
+
+/* ---------------------------------------------------------------------------------------
+ * Row-wise and elementwise ops of an encoder layer.  Zig's default float mode does not
+ * contract a*b+c, so these functions are built with contraction off and use fmaf exactly where
+ * the reference writes @mulAdd.
+ * ------------------------------------------------------------------------------------- */
+
+/* normRow (src/ops.zig:355-381) */
+__attribute__((optimize("fp-contract=off"))) static void norm_row(const float *row, size_t n, const float *w,
+                                                                   const float *b, float eps, float *o) {
+    vf sv = vsplat(0);
+    size_t i = 0;
+    for (; i + V <= n; i += V) sv += vload(row + i);
+    float sum = hsum(sv);
+    for (; i < n; ++i) sum += row[i];
+    const float mean = sum / (float)n;
+    const vf mv = vsplat(mean);
+    vf qv = vsplat(0);
+    i = 0;
+    for (; i + V <= n; i += V) {
+        const vf d = vload(row + i) - mv;
+        for (int e = 0; e < V; ++e) qv[e] = fmaf(d[e], d[e], qv[e]);
+    }
+    float sq = hsum(qv);
+    for (; i < n; ++i) {
+        const float d = row[i] - mean;
+        sq += d * d;
+    }
+    const float inv = 1.0f / sqrtf(sq / (float)n + eps);
+    const vf iv = vsplat(inv);
+    i = 0;
+    for (; i + V <= n; i += V) {
+        const vf d = (vload(row + i) - mv) * iv;
+        const vf wv = vload(w + i), bv = vload(b + i);
+        vf r;
+        for (int e = 0; e < V; ++e) r[e] = fmaf(d[e], wv[e], bv[e]);
+        vstore(o + i, r);
+    }
+    for (; i < n; ++i) o[i] = (row[i] - mean) * inv * w[i] + b[i];
+}
+
+typedef struct {
+    const float *x, *w, *b;
+    float *out;
+    size_t n, m, rows_per_task;
+    float eps;
+} norm_job;
+
+static void norm_task(void *raw, size_t task) {
+    const norm_job *j = raw;
+    const size_t r0 = task * j->rows_per_task;
+    const size_t r1 = r0 + j->rows_per_task < j->m ? r0 + j->rows_per_task : j->m;
+    for (size_t i = r0; i < r1; ++i) norm_row(j->x + i * j->n, j->n, j->w, j->b, j->eps, j->out + i * j->n);
+}
+
+/* layerNormEps (src/ops.zig:388-395): 64 rows per task */
+void ora_layer_norm(ora_pool *pool, const float *x, size_t m, size_t n, const float *w, const float *b, float eps,
+                    float *out) {
+    norm_job j = {x, w, b, out, n, m, 64, eps};
+    pool_parallel_for(pool, (m + 63) / 64, &j, norm_task);
+}
+
+/* geluScalar (src/ops.zig:312-315): std.math.tanh */
+__attribute__((optimize("fp-contract=off"))) static float gelu_scalar(float x) {
+    const float c = 0.7978845608028654f;
+    return 0.5f * x * (1.0f + tanhf(c * (x + 0.044715f * x * x * x)));
+}
+
+/* geluVec (src/ops.zig:317-327): tanh(u) = 1 - 2 / (1 + expVec(2u)) */
+__attribute__((optimize("fp-contract=off"))) static vf gelu_vec(vf x) {
+    const vf c = vsplat(0.7978845608028654f), k = vsplat(0.044715f), one = vsplat(1.0f), two = vsplat(2.0f),
+             half = vsplat(0.5f);
+    const vf u = c * (x + k * x * x * x);
+    const vf t = one - two / (one + exp_vec(two * u));
+    return half * x * (one + t);
+}
+
+typedef struct {
+    float *x;
+    size_t len, chunk;
+} gelu_job;
+
+static void gelu_task(void *raw, size_t task) {
+    const gelu_job *j = raw;
+    const size_t a = task * j->chunk, e = a + j->chunk < j->len ? a + j->chunk : j->len;
+    size_t i = a;
+    for (; i + V <= e; i += V) vstore(j->x + i, gelu_vec(vload(j->x + i)));
+    for (; i < e; ++i) j->x[i] = gelu_scalar(j->x[i]);
+}
+
+/* ops.gelu (src/ops.zig:335-340): in place, tasks of 32 Ki elements */
+void ora_gelu(ora_pool *pool, float *x, size_t len) {
+    gelu_job j = {x, len, 32 * 1024};
+    pool_parallel_for(pool, (len + j.chunk - 1) / j.chunk, &j, gelu_task);
 }

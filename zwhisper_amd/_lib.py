@@ -66,6 +66,12 @@ class PlanC(ctypes.Structure):
     ]
 
 
+class EncLayerC(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_void_p) for name in (
+        "attn_ln_w", "attn_ln_b", "q_w", "q_b", "k_w", "v_w", "v_b", "o_w", "o_b", "mlp_ln_w", "mlp_ln_b", "mlp0_w",
+        "mlp0_b", "mlp1_w", "mlp1_b")]
+
+
 class KVDescC(ctypes.Structure):
     _fields_ = [
         ("n_layer", _u64),
@@ -95,6 +101,9 @@ KV_KT = 1
 W_F16 = 1
 W_Q8 = 2
 Q8W_FROM_HOST = 1
+EPI_NONE = 0
+EPI_GELU = 1
+EPI_ADD = 2
 ROWS_ON_HOST = 1
 
 
@@ -164,6 +173,20 @@ def lib() -> ctypes.CDLL:
     L.zwg_q8w_shape.argtypes = [vp, ctypes.POINTER(_u64), ctypes.POINTER(_u64)]
     L.zwg_linear_q8w_dev.restype = c_int
     L.zwg_linear_q8w_dev.argtypes = [vp, _fp, _u64, vp, _fp, _fp]
+    L.zwg_linear_q8w_epi_dev.restype = c_int
+    L.zwg_linear_q8w_epi_dev.argtypes = [vp, _fp, _u64, vp, _fp, _fp, ctypes.c_uint32]
+    L.zwg_linear_epi_dev.restype = c_int
+    L.zwg_linear_epi_dev.argtypes = [vp, _fp, _u64, _u64, vp, ctypes.c_uint32, _fp, _u64, _fp, _u64, ctypes.c_uint32]
+    L.zwg_layer_norm_dev.restype = c_int
+    L.zwg_layer_norm_dev.argtypes = [vp, _fp, _u64, _u64, _fp, _fp, ctypes.c_float, _fp]
+    L.zwg_gelu_dev.restype = c_int
+    L.zwg_gelu_dev.argtypes = [vp, _fp, _u64]
+    L.zwg_add_dev.restype = c_int
+    L.zwg_add_dev.argtypes = [vp, _fp, _fp, _u64]
+    L.zwg_encoder_layer_scratch.restype = _u64
+    L.zwg_encoder_layer_scratch.argtypes = [_u64, _u64]
+    L.zwg_encoder_layer_dev.restype = c_int
+    L.zwg_encoder_layer_dev.argtypes = [vp, _fp, _u64, _u64, _u64, _u64, ctypes.POINTER(EncLayerC), _fp]
     for name in ("zwg_linear_q8", "zwg_linear_q8_dev"):
         getattr(L, name).restype = c_int
         getattr(L, name).argtypes = [vp, _fp, _u64, _u64, vp, _fp, _fp, _u64, _fp]

@@ -18,6 +18,7 @@
 
 #include "linear_kernel.hpp"
 #include "linear_q8_kernel.hpp"
+#include "elementwise.hpp"
 #include "zw_ctx.hpp"
 #include "zw_gpu.h"
 
@@ -96,7 +97,7 @@ int run_q8_stream_mt(zwg_ctx *ctx, const zwg_lin::Q8Args &base, const zwg_lin::Q
     if (n_split > 1) {
         const int64_t mn = (int64_t)(m * n);
         zwg_lin::linear_split_sum_kernel<<<(unsigned)((mn + 255) / 256), 256, 0, ctx->stream>>>(
-            a.part, a.bias, a.out, mn, (int32_t)n, n_split);
+            a.part, a.bias, a.out, mn, (int32_t)n, n_split, a.epi);
         e = hipGetLastError();
         if (e != hipSuccess) return fail_hip(ctx, "linear split-sum kernel launch", e);
     }
@@ -104,8 +105,9 @@ int run_q8_stream_mt(zwg_ctx *ctx, const zwg_lin::Q8Args &base, const zwg_lin::Q
 }
 
 int run_q8_stream(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const int8_t *q, const float *scales,
-                  const float *bias, uint64_t n, float *out) {
+                  const float *bias, uint64_t n, float *out, uint32_t epi) {
     zwg_lin::Q8Args a{};
+    a.epi = epi;
     a.x = x;
     a.q = q;
     a.scales = scales;
@@ -119,8 +121,11 @@ int run_q8_stream(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const in
 }
 
 int run_linear(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void *w, uint32_t w_type,
-               const float *scales, const float *bias, uint64_t n, float *out) {
+               const float *scales, const float *bias, uint64_t n, float *out, uint64_t ldo = 0, uint32_t epi = 0) {
+    if (ldo == 0) ldo = n;
     const std::string msg = check_linear(m, k, w_type, n);
+    if (ldo < n || ldo > 0x7fffffffull) return fail(ctx, "output row stride must be >= n");
+    if (epi > zwg_ew::kEpiAdd) return fail(ctx, "unknown epilogue");
     if (!msg.empty()) return fail(ctx, msg);
     if (m == 0 || n == 0) return ZWG_OK;
     if (!x || !w || !out || (w_type == ZWG_W_Q8 && !scales)) return fail(ctx, "null x, w, scales or out");
@@ -129,8 +134,10 @@ int run_linear(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void 
     if (scales && (reinterpret_cast<uintptr_t>(scales) & 3u)) return fail(ctx, "scales must be 4-byte aligned");
     hipError_t e = hipSetDevice(ctx->device);
     if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
-    if (w_type == ZWG_W_Q8 && m <= 64)
-        return run_q8_stream(ctx, x, m, k, static_cast<const int8_t *>(w), scales, bias, n, out);
+    if (w_type == ZWG_W_Q8 && m <= 64) {
+        if (ldo != n) return fail(ctx, "int8 token-step calls write dense rows (output stride n)");
+        return run_q8_stream(ctx, x, m, k, static_cast<const int8_t *>(w), scales, bias, n, out, epi);
+    }
     LinearArgs a{};
     a.x = x;
     a.w = w;
@@ -139,11 +146,12 @@ int run_linear(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void 
     a.out = out;
     a.ldx = (int64_t)k;
     a.ldw = (int64_t)k;
-    a.ldo = (int64_t)n;
+    a.ldo = (int64_t)ldo;
     a.m = (int32_t)m;
     a.n = (int32_t)n;
     a.k = (int32_t)k;
     a.nb = (int32_t)(k / 32);
+    a.epi = epi;
     e = w_type == ZWG_W_Q8 ? launch_tiled<zwg_lin::kWQ8>(a, ctx->stream) : launch_tiled<zwg_lin::kWF16>(a, ctx->stream);
     if (e != hipSuccess) return fail_hip(ctx, "linear kernel launch", e);
     return ZWG_OK;
@@ -193,8 +201,10 @@ struct zwg_q8w {
 
 namespace {
 
-int run_linear_q8w(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, const float *bias, float *out) {
+int run_linear_q8w(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, const float *bias, float *out,
+                   uint32_t epi) {
     if (!w) return fail(ctx, "null weights");
+    if (epi > zwg_ew::kEpiAdd) return fail(ctx, "unknown epilogue");
     const std::string msg = check_linear(m, w->k, ZWG_W_Q8, w->n);
     if (!msg.empty()) return fail(ctx, msg);
     if (m == 0) return ZWG_OK;
@@ -213,6 +223,7 @@ int run_linear_q8w(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, c
         a.n = (int32_t)w->n;
         a.k = (int32_t)w->k;
         a.nb = (int32_t)(w->k / zwg_lin::kQ8Block);
+        a.epi = epi;
         return m > 32 ? run_q8_stream_mt<2>(ctx, a, &p) : run_q8_stream_mt<1>(ctx, a, &p);
     }
     LinearArgs a{};
@@ -228,6 +239,7 @@ int run_linear_q8w(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, c
     a.n = (int32_t)w->n;
     a.k = (int32_t)w->k;
     a.nb = (int32_t)(w->k / 32);
+    a.epi = epi;
     e = launch_tiled<zwg_lin::kWQ8P>(a, ctx->stream);
     if (e != hipSuccess) return fail_hip(ctx, "linear kernel launch", e);
     return ZWG_OK;
@@ -314,7 +326,20 @@ int zwg_q8w_shape(const zwg_q8w *w, uint64_t *n, uint64_t *k) {
 
 int zwg_linear_q8w_dev(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, const float *bias, float *out) {
     if (!ctx) return fail(nullptr, "null context");
-    return run_linear_q8w(ctx, x, m, w, bias, out);
+    return run_linear_q8w(ctx, x, m, w, bias, out, zwg_ew::kEpiNone);
+}
+
+int zwg_linear_q8w_epi_dev(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, const float *bias, float *out,
+                           uint32_t epilogue) {
+    if (!ctx) return fail(nullptr, "null context");
+    return run_linear_q8w(ctx, x, m, w, bias, out, epilogue);
+}
+
+int zwg_linear_epi_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void *w, uint32_t w_type,
+                       const float *bias, uint64_t n, float *out, uint64_t out_stride, uint32_t epilogue) {
+    if (!ctx) return fail(nullptr, "null context");
+    if (w_type != ZWG_W_F16) return fail(ctx, "zwg_linear_epi_dev takes ZWG_W_F16 weights (zwg_linear_q8w_epi_dev: int8)");
+    return run_linear(ctx, x, m, k, w, w_type, nullptr, bias, n, out, out_stride, epilogue);
 }
 
 

@@ -38,6 +38,8 @@
 
 #include <stdint.h>
 
+#include "elementwise.hpp"
+
 namespace zwg_lin {
 
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
@@ -63,6 +65,7 @@ struct LinearArgs {
     float *out;          // [m][ldo]
     int64_t ldx, ldw, ldo;
     int32_t m, n, k, nb;
+    uint32_t epi; // zwg_ew::kEpi*: store v, gelu(v) or out + v, v = x . w + b
 };
 
 // Eight int8 (two dwords) to eight exact f16: the biased byte b + 128 is placed under the
@@ -297,7 +300,7 @@ __global__ __launch_bounds__(kThreads) void linear_mfma_kernel(LinearArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (row < a.m) a.out[(int64_t)row * a.ldo + col] = acc[i][j][r] + bj;
+                if (row < a.m) zwg_ew::epilogue_store(&a.out[(int64_t)row * a.ldo + col], acc[i][j][r] + bj, a.epi);
             }
     }
 }

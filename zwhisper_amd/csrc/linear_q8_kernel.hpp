@@ -65,6 +65,7 @@ struct Q8Args {
     float *part;         // [n_split][m][n] when n_split > 1
     int32_t m, n, k, nb;
     int32_t chunks_per_split, n_split;
+    uint32_t epi; // zwg_ew::kEpi*, applied where `out` is written (here, or by the split sum)
 };
 
 // Layout of x's hi/lo halves, per chunk of 256 k: [block][m-tile][hi/lo][k-step][lane][8 halves],
@@ -215,7 +216,10 @@ __global__ __launch_bounds__(kQ8Threads) void linear_q8_stream_kernel(Q8Args a, 
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
-                if (row < a.m) dst[(int64_t)row * a.n + col] = acc[i][s][r] + bj;
+                if (row < a.m) {
+                    if (a.n_split > 1) dst[(int64_t)row * a.n + col] = acc[i][s][r];
+                    else zwg_ew::epilogue_store(&dst[(int64_t)row * a.n + col], acc[i][s][r] + bj, a.epi);
+                }
             }
     }
 }
@@ -409,20 +413,23 @@ __global__ __launch_bounds__(kQ8Threads) void linear_q8p_stream_kernel(Q8Args a,
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
-                if (row < a.m) dst[(int64_t)row * a.n + col] = acc[i][s][r] + bj;
+                if (row < a.m) {
+                    if (a.n_split > 1) dst[(int64_t)row * a.n + col] = acc[i][s][r];
+                    else zwg_ew::epilogue_store(&dst[(int64_t)row * a.n + col], acc[i][s][r] + bj, a.epi);
+                }
             }
     }
 }
 
-// out[i][o] = sum over splits (in split order) of part[split][i][o], + bias[o].
+// out[i][o] = epilogue(sum over splits (in split order) of part[split][i][o], + bias[o]).
 __global__ __launch_bounds__(256) void linear_split_sum_kernel(const float *part, const float *bias, float *out,
-                                                              int64_t mn, int32_t n, int32_t n_split) {
+                                                              int64_t mn, int32_t n, int32_t n_split, uint32_t epi) {
     const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (e >= mn) return;
     float s = part[e];
     for (int p = 1; p < n_split; ++p) s += part[(int64_t)p * mn + e];
     if (bias) s += bias[e % n];
-    out[e] = s;
+    zwg_ew::epilogue_store(&out[e], s, epi);
 }
 
 } // namespace zwg_lin

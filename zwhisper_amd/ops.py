@@ -210,6 +210,69 @@ class Context:
         self._check(self._L.zwg_linear_q8w_dev(self._h, self._dev_ptr(x, "x"), m, w.handle,
                                                self._dev_ptr(bias, "bias"), self._dev_ptr(out, "out")))
 
+    def linear_epi_dev(self, x, m: int, k: int, w, bias, n: int, out, epilogue: int, out_stride: int = 0) -> None:
+        """linear_dev with an epilogue (_lib.EPI_NONE / EPI_GELU / EPI_ADD) and an output row stride."""
+        import torch
+
+        if not isinstance(w, torch.Tensor) or not w.is_cuda or w.dtype != torch.float16:
+            raise ZwgError("w must be a CUDA float16 tensor")
+        ld = out_stride or n
+        if x.numel() < m * k or w.numel() < n * k or (m and out.numel() < (m - 1) * ld + n) or (
+                bias is not None and bias.numel() < n):
+            raise ZwgError("a tensor is shorter than m, n and k need")
+        self._bind_torch_stream()
+        self._check(self._L.zwg_linear_epi_dev(self._h, self._dev_ptr(x, "x"), m, k, w.data_ptr(), _lib.W_F16,
+                                               self._dev_ptr(bias, "bias"), n, self._dev_ptr(out, "out"), out_stride,
+                                               epilogue))
+
+    def linear_q8w_epi_dev(self, x, m: int, w: "Q8Resident", bias, out, epilogue: int) -> None:
+        """linear_q8w_dev with an epilogue (_lib.EPI_NONE / EPI_GELU / EPI_ADD)."""
+        if not isinstance(w, Q8Resident):
+            raise ZwgError("w must be a Q8Resident (Q8.resident)")
+        if x.numel() < m * w.k or out.numel() < m * w.n or (bias is not None and bias.numel() < w.n):
+            raise ZwgError("a tensor is shorter than m, n and k need")
+        self._bind_torch_stream()
+        self._check(self._L.zwg_linear_q8w_epi_dev(self._h, self._dev_ptr(x, "x"), m, w.handle,
+                                                   self._dev_ptr(bias, "bias"), self._dev_ptr(out, "out"), epilogue))
+
+    def layer_norm_dev(self, x, m: int, n: int, w, b, eps: float, out) -> None:
+        """ops.layerNormEps (src/ops.zig:388-395) on CUDA float32 tensors."""
+        if x.numel() < m * n or out.numel() < m * n or w.numel() < n or b.numel() < n:
+            raise ZwgError("a tensor is shorter than m and n need")
+        self._bind_torch_stream()
+        self._check(self._L.zwg_layer_norm_dev(self._h, self._dev_ptr(x, "x"), m, n, self._dev_ptr(w, "w"),
+                                               self._dev_ptr(b, "b"), eps, self._dev_ptr(out, "out")))
+
+    def gelu_dev(self, x) -> None:
+        """ops.gelu (src/ops.zig:335-340) in place on a CUDA float32 tensor."""
+        self._bind_torch_stream()
+        self._check(self._L.zwg_gelu_dev(self._h, self._dev_ptr(x, "x"), x.numel()))
+
+    def add_dev(self, x, y) -> None:
+        """ops.add: x += y, CUDA float32 tensors of one size."""
+        if y.numel() != x.numel():
+            raise ZwgError("x and y differ in size")
+        self._bind_torch_stream()
+        self._check(self._L.zwg_add_dev(self._h, self._dev_ptr(x, "x"), self._dev_ptr(y, "y"), x.numel()))
+
+    def encoder_layer_dev(self, x, n_windows: int, n_ctx: int, n_state: int, n_head: int, w: dict, scratch) -> None:
+        """One Whisper encoder layer (src/encoder.zig:164-175) over n_windows windows, x [n_windows][n_ctx]
+        [n_state] updated in place.  w maps the zwg_enc_layer field names to CUDA tensors (f16 matrices,
+        f32 norms and biases); scratch holds encoder_layer_scratch(n_windows * n_ctx, n_state) floats."""
+        need = int(self._L.zwg_encoder_layer_scratch(n_windows * n_ctx, n_state))
+        if scratch.numel() < need or x.numel() < n_windows * n_ctx * n_state:
+            raise ZwgError(f"x or scratch too small (scratch needs {need} floats)")
+        ptrs = {}
+        for name, _ in _lib.EncLayerC._fields_:  # every field is required (k has no bias field)
+            t = w.get(name)
+            if t is None or not t.is_cuda or not t.is_contiguous():
+                raise ZwgError(f"encoder-layer tensor {name} must be a contiguous CUDA tensor")
+            ptrs[name] = t.data_ptr()
+        c = _lib.EncLayerC(**ptrs)
+        self._bind_torch_stream()
+        self._check(self._L.zwg_encoder_layer_dev(self._h, self._dev_ptr(x, "x"), n_windows, n_ctx, n_state, n_head,
+                                                  ctypes_byref(c), self._dev_ptr(scratch, "scratch")))
+
     def attention_dev(self, q, k, v, sh: AttnShape, out) -> None:
         self._bind_torch_stream()
         c = sh.to_c()
@@ -316,6 +379,17 @@ class KVCache:
 
 
 _tls = threading.local()
+
+
+def ctypes_byref(c):
+    import ctypes
+
+    return ctypes.byref(c)
+
+
+def encoder_layer_scratch(n_rows: int, n_state: int) -> int:
+    """Floats of scratch zwg_encoder_layer_dev needs for n_rows rows (windows x frames)."""
+    return int(_lib.lib().zwg_encoder_layer_scratch(n_rows, n_state))
 
 
 def default_context() -> Context:
