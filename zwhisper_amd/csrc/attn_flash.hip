@@ -366,6 +366,21 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
     const int64_t ih = row / a.n_q;
     const int head = (int)(ih % a.n_head);
     const int item = (int)(ih / a.n_head);
+    const float2 *ml = reinterpret_cast<const float2 *>(a.part_ml) + row * a.max_chunks;
+    const float4 *po = reinterpret_cast<const float4 *>(a.part_o + row * a.max_chunks * D) + g;
+    // Every slot of the row (c < max_chunks, all inside the workspace) is loaded before the
+    // item's key count arrives, so the partials' round trip overlaps that of the count; slots past
+    // the row's chunk count are discarded below by selection (they may hold anything).
+    float2 mlr[MAXC > 0 ? MAXC : 1];
+    float4 vr[MAXC > 0 ? MAXC : 1];
+    if (MAXC > 0) {
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c) { // slots past max_chunks reload the last one: no branches
+            const int cc = min(c, a.max_chunks - 1);
+            mlr[c] = ml[cc];
+            vr[c] = po[(int64_t)cc * G4];
+        }
+    }
     const int n_kv = item_kv(a, item);
     const int q_end = min((query / a.rows_per_unit + 1) * a.rows_per_unit, a.n_q);
     const int kv_hi = a.causal ? max(0, n_kv - a.n_q + q_end) : n_kv;
@@ -373,24 +388,17 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
     const int n_chunks = unit_split(kv_hi, a.split_tile, a.chunk_len, a.max_chunks, &chunk_keys);
     if (n_chunks == 1) return; // written by the attention kernel
 
-    const float2 *ml = reinterpret_cast<const float2 *>(a.part_ml) + row * a.max_chunks;
-    const float4 *po = reinterpret_cast<const float4 *>(a.part_o + row * a.max_chunks * D) + g;
     float M = -INFINITY, L = 0.f;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     if (MAXC > 0) {
-        // every partial of the row loaded in one round, then merged from registers
-        float2 mlr[MAXC > 0 ? MAXC : 1];
-        float4 vr[MAXC > 0 ? MAXC : 1];
+        // merged from registers: the row's first n_chunks slots only
 #pragma unroll
-        for (int c = 0; c < MAXC; ++c) {
-            mlr[c] = c < n_chunks ? ml[c] : make_float2(-INFINITY, 0.f);
-            vr[c] = c < n_chunks ? po[(int64_t)c * G4] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int c = 0; c < MAXC; ++c) M = fmaxf(M, mlr[c].x);
+        for (int c = 0; c < MAXC; ++c)
+            if (c < n_chunks) M = fmaxf(M, mlr[c].x);
         if (M != -INFINITY) {
 #pragma unroll
             for (int c = 0; c < MAXC; ++c) {
+                if (c >= n_chunks) continue;
                 const float w = exp2_fast(mlr[c].x - M); // 0 for a split that saw no key of this row
                 L += w * mlr[c].y;
                 acc.x += w * vr[c].x;

@@ -47,6 +47,9 @@ constexpr int kQ8Block = 32;                // src/gemm.zig:194
 constexpr int kQ8Chunk = 256;               // k per LDS chunk of the stream kernel
 constexpr int kQ8ChunkBlocks = kQ8Chunk / kQ8Block;
 constexpr int kQ8Threads = 256;
+// The packed weights and scales are read once per call: non-temporal loads (cache policy nt)
+// stream them past the caches, which keep the x stages every workgroup reuses.
+constexpr int kQ8CachePolicyNT = 2;
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
@@ -332,13 +335,14 @@ __global__ __launch_bounds__(kQ8Threads) void linear_q8p_stream_kernel(Q8Args a,
             for (int b = 0; b < NB; ++b) {
                 const uint32_t off = live_t ? (uint32_t)(s * slab_q + ((int64_t)(t * NB + b) * 64 + lane) * 16)
                                             : kOutOfRange;
-                wq[s][b] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(q_src, (int)off, 0, 0));
+                wq[s][b] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(q_src, (int)off, 0, kQ8CachePolicyNT));
             }
             // scales of blocks 4 (t % 2) .. +4 of chunk t / 2, this lane's row
             const uint32_t off =
                 live_t ? (uint32_t)(s * slab_s + (((t >> 1) * 32 + r32) * kQ8ChunkBlocks + 4 * (t & 1)) * 4)
                        : kOutOfRange;
-            sc[s] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(s_src, (int)off, 0, 0));
+            sc[s] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(s_src, (int)off, 0, kQ8CachePolicyNT));
         }
     };
 
