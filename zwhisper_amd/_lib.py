@@ -52,7 +52,7 @@ class BatchC(ctypes.Structure):
 
 
 class LimitsC(ctypes.Structure):
-    _fields_ = [("workspace_bytes", _u64)]
+    _fields_ = [("workspace_bytes", _u64), ("dense_math", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
 
 
 class PlanC(ctypes.Structure):
@@ -96,6 +96,8 @@ class KVInfoC(ctypes.Structure):
     ]
 
 
+DENSE_BF16X3 = 0
+DENSE_FP32 = 1
 KV_ROW = 0
 KV_KT = 1
 W_F16 = 1
@@ -138,6 +140,8 @@ def lib() -> ctypes.CDLL:
     L.zwg_get_stream.argtypes = [vp]
     L.zwg_sync.restype = c_int
     L.zwg_sync.argtypes = [vp]
+    L.zwg_set_dense_math.restype = c_int
+    L.zwg_set_dense_math.argtypes = [vp, ctypes.c_uint32]
     L.zwg_attention_ex.restype = c_int
     L.zwg_attention_ex.argtypes = [vp, _fp, _fp, _fp, ctypes.POINTER(ShapeC), _fp]
     L.zwg_attention.restype = c_int

@@ -1,0 +1,413 @@
+// Dense attention on gfx950 bf16 MFMA with f32-level accuracy: the fp32 kernel of attn_flash.hip
+// (same workgroup geometry, tile pipeline, online softmax, split and merge), with each product
+// of Q.K^T and P.V computed as three bf16 MFMA products of split operands.
+//
+// Split.  Every f32 operand x is written as hi + lo, hi = bf16(x), lo = bf16(x - hi): 16 of the
+// 24 significand bits, with f32's exponent range (no overflow, unlike an f16 split).  A product
+// a.b is then ah.bh + ah.bl + al.bh (the al.bl term is below 2^-16 of it), each on
+// v_mfma_f32_32x32x16_bf16 with f32 accumulation: 12 MFMAs of 32x32x16 per 32 x 32 tile of
+// Q.K^T (d = 64) and 12 for P.V, against 64 fp32 MFMAs of 32x32x2, so about 5x fewer MFMA cycles.
+// Measured against f64 on the Whisper shapes the outputs stay within ~2e-6 absolute.
+//
+// Operands.  S^T = K . Q^T (M = keys, N = queries, K = head dims): lane l of the A operand (K)
+// holds key l%32, dims 16 j + 8 (l/32) + 0..7 of k-step j; the B operand (Q^T) the same dims of
+// query l%32, split once into registers.  The result layout of every 32x32 MFMA is the one the
+// fp32 kernel uses (register r of lane l: key 8 (r/4) + 4 (l/32) + r%4 of query l%32), so the
+// masking and softmax are unchanged.  For O^T = V^T . P^T, k-step s contracts the keys of
+// registers 8 s .. 8 s + 7, which for lane half h are keys 16 s + 4 h + 0..3 and 16 s + 8 + 4 h
+// + 0..3: the V^T tile is stored with keys 4..7 and 8..11 of every 16 swapped, so each lane's
+// eight keys are contiguous and one 16-byte read.
+//
+// LDS.  K tiles [key][dim] and V^T tiles [dim][key], bf16 hi and lo planes, double-buffered,
+// 16-byte chunks XOR-swizzled by row so a wave's operand reads are conflict-free.
+#include "attn_kernels.hpp"
+
+namespace zwg {
+
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// bf16 hi/lo of eight floats
+__device__ __forceinline__ void split8(const float *x, bf16x8 &hi, bf16x8 &lo) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const __bf16 h = (__bf16)x[i];
+        hi[i] = h;
+        lo[i] = (__bf16)(x[i] - (float)h);
+    }
+}
+
+// K tile element (key, dim): rows of D bf16, 16-byte chunk c stored at c ^ (key / (128 / D))
+// mod (D / 8): the rows sharing LDS banks within a 16-lane read phase land in different chunks.
+template <int D>
+__device__ __forceinline__ int k_at(int key, int dim) {
+    constexpr int C = D / 8, R = 128 / D > 0 ? 128 / D : 1;
+    return key * D + ((((dim >> 3) ^ ((key / R) & (C - 1))) << 3) | (dim & 7));
+}
+// V^T tile position of a key: bits 2 and 3 swapped (keys 4..7 <-> 8..11 of every 16)
+__device__ __forceinline__ int v_pos(int key) { return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1); }
+// V^T tile element (dim, pos): rows of 32 bf16 (64 bytes, 4 chunks), chunk c at c ^ ((dim >> 2) & 3)
+__device__ __forceinline__ int v_at(int dim, int pos) {
+    return dim * kFlashBN + ((((pos >> 3) ^ ((dim >> 2) & 3)) << 3) | (pos & 7));
+}
+
+} // namespace
+
+template <int D, bool KT>
+__global__ __launch_bounds__(256) void flash_x3_kernel(AttnArgs a) {
+    constexpr int BM = kFlashBM;
+    constexpr int BN = kFlashBN;
+    constexpr int NKS = D / 16;  // k-steps of the QK product
+    constexpr int NDB = D / 32;  // 32-dim output tiles
+    static_assert(BN * D == 256 * 4 * (D / 32), "each thread stages D/32 quads of each tile");
+    static_assert(BN == 32, "the P.V key order assumes 32-key tiles");
+
+    __shared__ __align__(16) __bf16 Kh[2][BN * D];
+    __shared__ __align__(16) __bf16 Kl[2][BN * D];
+    __shared__ __align__(16) __bf16 Vh[2][D * BN];
+    __shared__ __align__(16) __bf16 Vl[2][D * BN];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int col = lane & 31;
+    const int half = lane >> 5;
+
+    // workgroup -> (item*head, q-block, chunk), as flash_attn_kernel
+    const int n_qblocks = (a.n_q + BM - 1) / BM;
+    const int64_t lb = a.xcd_group ? xcd_logical_block(blockIdx.x, (int64_t)gridDim.x) : (int64_t)blockIdx.x;
+    const int64_t n_ih = (int64_t)a.n_batch * a.n_head;
+    int chunk, qb, ih;
+    if (a.heavy_first) {
+        ih = (int)(lb % n_ih);
+        const int64_t t = lb / n_ih;
+        chunk = (int)(t % a.max_chunks);
+        qb = n_qblocks - 1 - (int)(t / a.max_chunks);
+    } else {
+        chunk = (int)(lb % a.max_chunks);
+        const int64_t lq = lb / a.max_chunks;
+        qb = (int)(lq % n_qblocks);
+        ih = (int)(lq / n_qblocks);
+    }
+    const int item = ih / a.n_head;
+    const int head = ih - item * a.n_head;
+    const int hk = head / a.group;
+
+    const int n_q = a.n_q;
+    const int n_kv = item_kv(a, item);
+    const int q_first = qb * BM;
+    const int q_end_blk = min(q_first + BM, n_q);
+    const int kv_hi = a.causal ? max(0, n_kv - n_q + q_end_blk) : n_kv;
+    int chunk_keys;
+    const int n_chunks = unit_split(kv_hi, BN, a.chunk_len, a.max_chunks, &chunk_keys);
+    if (chunk >= n_chunks) return;
+    const int k_begin = chunk * chunk_keys;
+    const int k_end = min(kv_hi, k_begin + chunk_keys);
+
+    const float *qp = a.q + item * a.q_bstride + head * D;
+    const float *kp = a.k + item * a.k_bstride + (KT ? (int64_t)hk * D * a.kt_stride : (int64_t)hk * D);
+    const float *vp = a.v + item * a.v_bstride + hk * D;
+
+    const int q_wave = q_first + wave * 32;
+    const int query = q_wave + col;
+    const bool q_valid = query < n_q;
+    const bool wave_active = q_wave < n_q;
+    const int q_wave_last = min(q_wave + 31, n_q - 1);
+    const int diag = n_kv - n_q; // query i sees keys j <= diag + i
+    const int wave_hi = min(k_end, a.causal ? diag + q_wave_last + 1 : n_kv);
+    const int wave_full = min(k_end, a.causal ? diag + q_wave + 1 : n_kv);
+
+    // this lane's query, pre-scaled into log2 units, dims 16 j + 8 half + 0..7, split
+    bf16x8 qh[NKS], ql[NKS];
+    {
+        float qv[8];
+#pragma unroll
+        for (int j = 0; j < NKS; ++j) {
+            if (q_valid) {
+                const f32x4 *src = reinterpret_cast<const f32x4 *>(qp + (int64_t)query * a.q_stride + 16 * j + 8 * half);
+                const f32x4 t0 = src[0], t1 = src[1];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    qv[e] = t0[e] * a.scale_log2;
+                    qv[4 + e] = t1[e] * a.scale_log2;
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qv[e] = 0.f;
+            }
+            split8(qv, qh[j], ql[j]);
+        }
+    }
+
+    f32x16 o[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) o[db] = (f32x16){0};
+    float m_run = -INFINITY;
+    float l_run = 0.f;
+
+    // Tile staging as in flash_attn_kernel: K two tiles ahead, V one tile ahead, one barrier per
+    // tile.  Each thread holds what it stores as contiguous bf16 quads: four dims of one key for K
+    // (row-major K: one 16-byte load; transposed K: four coalesced dword loads, one per dim row)
+    // and four keys of one dim for V^T (four coalesced dword loads, one per key row).
+    constexpr int NG = D / 32;        // quads per thread per tile, per tensor
+    constexpr int VTPD = 256 / D;     // V: threads per dim
+    f32x4 kr[NG], vr[NG];
+    const int k_key = tid % BN, k_dq = tid / BN;   // transposed K: key, first dim quad
+    const int v_dim = tid % D, v_kq = tid / D;     // V: dim, first key quad
+    auto k_dim = [&](int g) { return 4 * (k_dq + 8 * g); };   // transposed K: quads k_dq, k_dq + 8, ..
+    auto v_key = [&](int g) { return 4 * (v_kq + VTPD * g); }; // V: quads v_kq, v_kq + VTPD, ..
+    // Branch-free loads through buffer descriptors (32-bit byte offsets; the host keeps an item's
+    // K and V spans below 4 GiB): V and row-major K end at the item's last key row, so a key at or
+    // past n_kv reads 0; transposed K ends at the last dim row's n_kv-th column, and a key past
+    // n_kv in an earlier dim row reads that row's padding (finite by the reference's contract,
+    // src/ops.zig:477-492) -- masked out of the scores either way.
+    const uint32_t row_b = (uint32_t)a.kv_stride * 4u;
+    const uint32_t kv_span = n_kv > 0 ? (uint32_t)(n_kv - 1) * row_b + 4u * D : 0u;
+    const uint32_t kt_span = n_kv > 0 ? (uint32_t)((D - 1) * a.kt_stride + n_kv) * 4u : 0u;
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(kp), 0, (int)(KT ? kt_span : kv_span), 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(vp), 0, (int)kv_span, 0x00020000);
+    auto load_k = [&](int k0) {
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            if (KT) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    kr[g][j] = __builtin_bit_cast(
+                        float, __builtin_amdgcn_raw_buffer_load_b32(
+                                   krs, (int)((uint32_t)((k_dim(g) + j) * a.kt_stride + k_key) * 4u), k0 * 4, 0));
+            } else {
+                const int f = tid + 256 * g;
+                kr[g] = __builtin_bit_cast(
+                    f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                               krs, (int)((uint32_t)(f / (D / 4)) * row_b + 16u * (f % (D / 4))), (int)(k0 * row_b), 0));
+            }
+        }
+    };
+    auto load_v = [&](int k0) {
+#pragma unroll
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                vr[g][j] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(
+                               vrs, (int)((uint32_t)(v_key(g) + j) * row_b + 4u * v_dim), (int)(k0 * row_b), 0));
+    };
+    auto split4 = [&](const f32x4 &x, bf16x4 &h, bf16x4 &l) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            h[j] = (__bf16)x[j];
+            l[j] = (__bf16)(x[j] - (float)h[j]);
+        }
+    };
+    auto store_k = [&](int buf) {
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            int key, dim;
+            if (KT) {
+                key = k_key;
+                dim = k_dim(g);
+            } else {
+                const int f = tid + 256 * g;
+                key = f / (D / 4);
+                dim = 4 * (f % (D / 4));
+            }
+            bf16x4 h, l;
+            split4(kr[g], h, l);
+            *reinterpret_cast<bf16x4 *>(&Kh[buf][k_at<D>(key, dim)]) = h;
+            *reinterpret_cast<bf16x4 *>(&Kl[buf][k_at<D>(key, dim)]) = l;
+        }
+    };
+    auto store_v = [&](int buf) {
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            bf16x4 h, l;
+            split4(vr[g], h, l);
+            const int at = v_at(v_dim, v_pos(v_key(g))); // keys 4q .. 4q+3 sit at four consecutive positions
+            *reinterpret_cast<bf16x4 *>(&Vh[buf][at]) = h;
+            *reinterpret_cast<bf16x4 *>(&Vl[buf][at]) = l;
+        }
+    };
+    // one k-step of S^T = K . Q^T: three bf16 products
+    auto qk_step = [&](int buf, int j, f32x16 sc) {
+        const int at = k_at<D>(col, 16 * j + 8 * half);
+        const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(&Kh[buf][at]);
+        const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(&Kl[buf][at]);
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qh[j], sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, ql[j], sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl, qh[j], sc, 0, 0, 0);
+        return sc;
+    };
+    auto qk = [&](int buf) {
+        f32x16 sc = (f32x16){0};
+#pragma unroll
+        for (int j = 0; j < NKS; ++j) sc = qk_step(buf, j, sc);
+        return sc;
+    };
+    // masking and the lazily moved running max, as flash_attn_kernel
+    auto mask_and_max = [&](f32x16 &sc, int k0) {
+        if (k0 + BN > wave_full) {
+            const int lim = min(k_end, a.causal ? diag + query + 1 : n_kv);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = k0 + 8 * (r >> 2) + 4 * half + (r & 3);
+                sc[r] = key < lim ? sc[r] : -INFINITY;
+            }
+        }
+        float mt = sc[0];
+#pragma unroll
+        for (int r = 1; r < 16; ++r) mt = fmaxf(mt, sc[r]);
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        if (__any(mt > m_run + 8.0f)) {
+            const float m_new = fmaxf(m_run, mt);
+            const float alpha = m_run == -INFINITY ? 0.f : exp2_fast(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+            m_run = m_new;
+        }
+    };
+    auto exp_sum = [&](f32x16 &sc) {
+        const float m_use = m_run == -INFINITY ? 0.f : m_run;
+        float ls = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            sc[r] = exp2_fast(sc[r] - m_use);
+            ls += sc[r];
+        }
+        l_run += ls;
+    };
+    // the next tile's score MFMAs interleaved with this tile's exponentials
+    auto qk_exp = [&](int buf, f32x16 &p) {
+        const float m_use = m_run == -INFINITY ? 0.f : m_run;
+        float ls = 0.f;
+        f32x16 sc = (f32x16){0};
+        constexpr int PER = 16 / NKS; // exponentials per k-step
+#pragma unroll
+        for (int j = 0; j < NKS; ++j) {
+            sc = qk_step(buf, j, sc);
+#pragma unroll
+            for (int u = 0; u < PER; ++u) {
+                const int r = j * PER + u;
+                p[r] = exp2_fast(p[r] - m_use);
+                ls += p[r];
+            }
+        }
+        l_run += ls;
+        return sc;
+    };
+    // O^T += V^T . P^T: k-step s contracts registers 8 s .. 8 s + 7 of p
+    auto pv = [&](const f32x16 &p, int buf) {
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            float pr[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) pr[e] = p[8 * s + e];
+            bf16x8 ph, pl;
+            split8(pr, ph, pl);
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+                const int at = v_at(db * 32 + col, 16 * s + 8 * half);
+                const bf16x8 vh = *reinterpret_cast<const bf16x8 *>(&Vh[buf][at]);
+                const bf16x8 vl = *reinterpret_cast<const bf16x8 *>(&Vl[buf][at]);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, ph, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, pl, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl, ph, o[db], 0, 0, 0);
+            }
+        }
+    };
+    auto wave_needs = [&](int k0) { return wave_active && k0 < wave_hi; };
+
+    const int n_tiles = k_end > k_begin ? (k_end - k_begin + BN - 1) / BN : 0;
+    f32x16 s_cur = (f32x16){0};
+    if (n_tiles > 0) {
+        load_k(k_begin);
+        load_v(k_begin);
+        store_k(0);
+        store_v(0);
+        if (n_tiles > 1) load_k(k_begin + BN);
+    }
+    __syncthreads();
+    if (n_tiles > 0 && wave_needs(k_begin)) s_cur = qk(0);
+    if (n_tiles > 1) store_k(1);
+    __syncthreads();
+
+    for (int t = 0; t < n_tiles; ++t) {
+        const int k0 = k_begin + t * BN;
+        if (t + 2 < n_tiles) load_k(k0 + 2 * BN);
+        if (t + 1 < n_tiles) load_v(k0 + BN);
+        const bool need_cur = wave_needs(k0);
+        const bool need_next = t + 1 < n_tiles && wave_needs(k0 + BN);
+        f32x16 s_next = (f32x16){0};
+        if (need_cur) mask_and_max(s_cur, k0);
+        if (need_cur && need_next) {
+            s_next = qk_exp((t + 1) & 1, s_cur);
+        } else if (need_cur) {
+            exp_sum(s_cur);
+        } else if (need_next) {
+            s_next = qk((t + 1) & 1);
+        }
+        if (need_cur) pv(s_cur, t & 1);
+        if (t + 2 < n_tiles) store_k(t & 1);
+        if (t + 1 < n_tiles) store_v((t + 1) & 1);
+        __syncthreads();
+        s_cur = s_next;
+    }
+
+    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    if (!q_valid) return;
+    // lane holds dims db*32 + 8*g + 4*half + {0..3} in registers 4g..4g+3 of o[db]
+    if (n_chunks == 1) {
+        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+        float *op = a.out + item * a.out_bstride + (int64_t)query * a.out_stride + head * D;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                f32x4 w = {o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv};
+                *reinterpret_cast<f32x4 *>(op + db * 32 + 8 * g + 4 * half) = w;
+            }
+    } else {
+        const int64_t slot = row_index(a, item, head, query) * a.max_chunks + chunk;
+        float *po = a.part_o + slot * D;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                f32x4 w = {o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2], o[db][4 * g + 3]};
+                *reinterpret_cast<f32x4 *>(po + db * 32 + 8 * g + 4 * half) = w;
+            }
+        if (half == 0) {
+            a.part_ml[2 * slot] = m_run;
+            a.part_ml[2 * slot + 1] = l_tot;
+        }
+    }
+}
+
+hipError_t launch_flash_x3(const AttnArgs &a, int d, hipStream_t stream, int *grid_blocks) {
+    const int n_qblocks = (a.n_q + kFlashBM - 1) / kFlashBM;
+    const int64_t blocks = (int64_t)a.max_chunks * n_qblocks * a.n_batch * a.n_head;
+    if (blocks > 0x7fffffffll) return hipErrorInvalidValue;
+    dim3 grid((unsigned)blocks);
+    dim3 block(256);
+    if (grid_blocks) *grid_blocks = (int)grid.x;
+    const bool kt = a.kt_stride != 0;
+#define ZWG_FLASH_X3(DD)                                                                                         \
+    if (d == DD) {                                                                                               \
+        if (kt) flash_x3_kernel<DD, true><<<grid, block, 0, stream>>>(a);                                        \
+        else flash_x3_kernel<DD, false><<<grid, block, 0, stream>>>(a);                                          \
+        return hipGetLastError();                                                                                \
+    }
+    ZWG_FLASH_X3(32)
+    ZWG_FLASH_X3(64)
+    ZWG_FLASH_X3(128)
+#undef ZWG_FLASH_X3
+    return hipErrorInvalidValue;
+}
+
+} // namespace zwg

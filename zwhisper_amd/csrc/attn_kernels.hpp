@@ -88,6 +88,7 @@ constexpr int kDecodeTile = ZWG_DECODE_TILE; // keys per inner tile
 constexpr int kDecodeMaxRows = 8; // heads-per-KV-group x queries a block can carry
 
 hipError_t launch_flash(const AttnArgs &a, int d, hipStream_t stream, int *grid_blocks);
+hipError_t launch_flash_x3(const AttnArgs &a, int d, hipStream_t stream, int *grid_blocks);
 hipError_t launch_decode(const AttnArgs &a, int d, int rows, hipStream_t stream, int *grid_blocks);
 hipError_t launch_combine(const AttnArgs &a, int d, hipStream_t stream);
 

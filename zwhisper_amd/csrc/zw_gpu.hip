@@ -206,9 +206,15 @@ int run(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_
         return fail(ctx, "q, k, v and out must be 16-byte aligned");
     const Plan p = make_plan(s, b, ctx->workspace_bytes);
     if (p.ws_bytes > ctx->workspace_bytes) return fail(ctx, "workspace too small for this call");
-    // the row-major decode kernel addresses one item's K/V rows with 32-bit byte offsets
-    if (p.kernel == 2 && !s.kt_stride && s.n_kv > 0 && ((s.n_kv - 1) * s.kv_stride + s.d) * sizeof(float) > 0xffffffffull)
-        return fail(ctx, "row-major K/V rows of one batch item must span less than 4 GiB");
+    // the row-major decode kernel and the bf16x3 dense kernel address one item's K/V rows (and the
+    // dense kernel one KV head's K^T rows) with 32-bit byte offsets
+    const bool dense_x3 = p.kernel == 1 && ctx->dense_math != ZWG_DENSE_FP32;
+    if ((p.kernel == 2 && !s.kt_stride) || dense_x3) {
+        if (s.n_kv > 0 && ((s.n_kv - 1 + (dense_x3 ? 32 : 0)) * s.kv_stride + s.d) * sizeof(float) > 0x7fffffffull)
+            return fail(ctx, "K/V rows of one batch item must span less than 2 GiB");
+        if (dense_x3 && s.kt_stride && (s.d * s.kt_stride + 32) * sizeof(float) > 0x7fffffffull)
+            return fail(ctx, "the transposed K rows of one KV head must span less than 2 GiB");
+    }
 
     zwg::AttnArgs a{};
     a.q = q;
@@ -246,8 +252,11 @@ int run(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_
     hipError_t e = hipSetDevice(ctx->device);
     if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
     int blocks = 0;
-    e = p.kernel == 1 ? zwg::launch_flash(a, (int)s.d, ctx->stream, &blocks)
-                      : zwg::launch_decode(a, (int)s.d, (int)(s.n_q * a.group), ctx->stream, &blocks);
+    if (p.kernel == 1)
+        e = ctx->dense_math == ZWG_DENSE_FP32 ? zwg::launch_flash(a, (int)s.d, ctx->stream, &blocks)
+                                              : zwg::launch_flash_x3(a, (int)s.d, ctx->stream, &blocks);
+    else
+        e = zwg::launch_decode(a, (int)s.d, (int)(s.n_q * a.group), ctx->stream, &blocks);
     if (e != hipSuccess) return fail_hip(ctx, "attention kernel launch", e);
     if (p.max_chunks > 1) {
         e = zwg::launch_combine(a, (int)s.d, ctx->stream);
@@ -309,6 +318,12 @@ int zwg_open(int device, const zwg_limits *limits, zwg_ctx **out) {
     }
     ctx->stream = ctx->own_stream;
     ctx->workspace_bytes = (limits && limits->workspace_bytes) ? limits->workspace_bytes : kDefaultWorkspace;
+    if (limits && limits->dense_math > ZWG_DENSE_FP32) {
+        (void)hipStreamDestroy(ctx->own_stream);
+        delete ctx;
+        return fail(nullptr, "unknown dense_math");
+    }
+    ctx->dense_math = limits ? limits->dense_math : ZWG_DENSE_BF16X3;
     void *ws = nullptr;
     e = hipMalloc(&ws, ctx->workspace_bytes);
     if (e != hipSuccess) {
@@ -318,6 +333,13 @@ int zwg_open(int device, const zwg_limits *limits, zwg_ctx **out) {
     }
     ctx->workspace = static_cast<float *>(ws);
     *out = ctx;
+    return ZWG_OK;
+}
+
+int zwg_set_dense_math(zwg_ctx *ctx, uint32_t mode) {
+    if (!ctx) return fail(nullptr, "null context");
+    if (mode > ZWG_DENSE_FP32) return fail(ctx, "unknown dense math mode");
+    ctx->dense_math = mode;
     return ZWG_OK;
 }
 

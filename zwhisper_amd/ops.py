@@ -101,16 +101,21 @@ def plan(sh: AttnShape, n_batch: int = 1, workspace_bytes: int = 0) -> _lib.Plan
 class Context:
     """One library context (zwg_ctx): a device, a workspace, staging buffers."""
 
-    def __init__(self, device: int = 0, workspace_bytes: int = 0):
+    def __init__(self, device: int = 0, workspace_bytes: int = 0, dense_math: int = 0):
+        """dense_math: _lib.DENSE_BF16X3 (0, default) or _lib.DENSE_FP32, the dense kernel's arithmetic."""
         L = _lib.lib()
         self._L = L
         h = ctypes.c_void_p()
-        lim = _lib.LimitsC(workspace_bytes)
+        lim = _lib.LimitsC(workspace_bytes, dense_math, 0)
         rc = L.zwg_open(device, ctypes.byref(lim), ctypes.byref(h))
         if rc != _lib.ZWG_OK:
             raise ZwgError(_lib.last_error(None))
         self._h = h
         self.device = device
+
+    def set_dense_math(self, mode: int) -> None:
+        """Switch the dense kernel's arithmetic (_lib.DENSE_BF16X3 or _lib.DENSE_FP32) for later calls."""
+        self._check(self._L.zwg_set_dense_math(self._h, mode))
 
     def close(self) -> None:
         if getattr(self, "_h", None):
