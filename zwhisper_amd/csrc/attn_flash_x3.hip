@@ -32,14 +32,16 @@ typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// bf16 hi/lo of eight floats
-__device__ __forceinline__ void split8(const float *x, bf16x8 &hi, bf16x8 &lo) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const __bf16 h = (__bf16)x[i];
-        hi[i] = h;
-        lo[i] = (__bf16)(x[i] - (float)h);
-    }
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+
+// bf16 hi/lo of eight / four floats, as vector conversions (two values per v_cvt_pk_bf16_f32)
+__device__ __forceinline__ void split8(const f32x8 &x, bf16x8 &hi, bf16x8 &lo) {
+    hi = __builtin_convertvector(x, bf16x8);
+    lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x8), bf16x8);
+}
+__device__ __forceinline__ void split4(const f32x4 &x, bf16x4 &hi, bf16x4 &lo) {
+    hi = __builtin_convertvector(x, bf16x4);
+    lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x4), bf16x4);
 }
 
 // K tile element (key, dim): rows of D bf16, 16-byte chunk c stored at c ^ (key / (128 / D))
@@ -125,7 +127,7 @@ __global__ __launch_bounds__(256) void flash_x3_kernel(AttnArgs a) {
     // this lane's query, pre-scaled into log2 units, dims 16 j + 8 half + 0..7, split
     bf16x8 qh[NKS], ql[NKS];
     {
-        float qv[8];
+        f32x8 qv;
 #pragma unroll
         for (int j = 0; j < NKS; ++j) {
             if (q_valid) {
@@ -162,16 +164,22 @@ __global__ __launch_bounds__(256) void flash_x3_kernel(AttnArgs a) {
     auto k_dim = [&](int g) { return 4 * (k_dq + 8 * g); };   // transposed K: quads k_dq, k_dq + 8, ..
     auto v_key = [&](int g) { return 4 * (v_kq + VTPD * g); }; // V: quads v_kq, v_kq + VTPD, ..
     // Branch-free loads through buffer descriptors (32-bit byte offsets; the host keeps an item's
-    // K and V spans below 4 GiB): V and row-major K end at the item's last key row, so a key at or
+    // K and V spans below 2 GiB): V and row-major K end at the item's last key row, so a key at or
     // past n_kv reads 0; transposed K ends at the last dim row's n_kv-th column, and a key past
     // n_kv in an earlier dim row reads that row's padding (finite by the reference's contract,
-    // src/ops.zig:477-492) -- masked out of the scores either way.
+    // src/ops.zig:477-492) -- masked out of the scores either way.  Each offset is a per-lane base
+    // fixed for the whole loop (one VGPR per tensor) plus a wave-uniform part in an SGPR: the
+    // tile's first key and the step between a thread's quads and elements.
     const uint32_t row_b = (uint32_t)a.kv_stride * 4u;
     const uint32_t kv_span = n_kv > 0 ? (uint32_t)(n_kv - 1) * row_b + 4u * D : 0u;
     const uint32_t kt_span = n_kv > 0 ? (uint32_t)((D - 1) * a.kt_stride + n_kv) * 4u : 0u;
     const __amdgpu_buffer_rsrc_t krs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(kp), 0, (int)(KT ? kt_span : kv_span), 0x00020000);
     const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(vp), 0, (int)kv_span, 0x00020000);
+    const uint32_t kt_row_b = (uint32_t)a.kt_stride * 4u;
+    const uint32_t k_base = KT ? (uint32_t)k_dim(0) * kt_row_b + 4u * (uint32_t)k_key
+                               : (uint32_t)(tid / (D / 4)) * row_b + 16u * (uint32_t)(tid % (D / 4));
+    const uint32_t v_base = (uint32_t)v_key(0) * row_b + 4u * (uint32_t)v_dim;
     auto load_k = [&](int k0) {
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
@@ -180,12 +188,11 @@ __global__ __launch_bounds__(256) void flash_x3_kernel(AttnArgs a) {
                 for (int j = 0; j < 4; ++j)
                     kr[g][j] = __builtin_bit_cast(
                         float, __builtin_amdgcn_raw_buffer_load_b32(
-                                   krs, (int)((uint32_t)((k_dim(g) + j) * a.kt_stride + k_key) * 4u), k0 * 4, 0));
+                                   krs, (int)k_base, (int)((uint32_t)k0 * 4u + (uint32_t)(32 * g + j) * kt_row_b), 0));
             } else {
-                const int f = tid + 256 * g;
                 kr[g] = __builtin_bit_cast(
                     f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                               krs, (int)((uint32_t)(f / (D / 4)) * row_b + 16u * (f % (D / 4))), (int)(k0 * row_b), 0));
+                               krs, (int)k_base, (int)((uint32_t)(k0 + (1024 / D) * g) * row_b), 0));
             }
         }
     };
@@ -196,14 +203,7 @@ __global__ __launch_bounds__(256) void flash_x3_kernel(AttnArgs a) {
             for (int j = 0; j < 4; ++j)
                 vr[g][j] = __builtin_bit_cast(
                     float, __builtin_amdgcn_raw_buffer_load_b32(
-                               vrs, (int)((uint32_t)(v_key(g) + j) * row_b + 4u * v_dim), (int)(k0 * row_b), 0));
-    };
-    auto split4 = [&](const f32x4 &x, bf16x4 &h, bf16x4 &l) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            h[j] = (__bf16)x[j];
-            l[j] = (__bf16)(x[j] - (float)h[j]);
-        }
+                               vrs, (int)v_base, (int)((uint32_t)(k0 + 4 * VTPD * g + j) * row_b), 0));
     };
     auto store_k = [&](int buf) {
 #pragma unroll
@@ -305,7 +305,7 @@ __global__ __launch_bounds__(256) void flash_x3_kernel(AttnArgs a) {
     auto pv = [&](const f32x16 &p, int buf) {
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            float pr[8];
+            f32x8 pr;
 #pragma unroll
             for (int e = 0; e < 8; ++e) pr[e] = p[8 * s + e];
             bf16x8 ph, pl;
