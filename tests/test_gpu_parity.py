@@ -43,6 +43,15 @@ def ctx(torch):
     c.close()
 
 
+@pytest.fixture(scope="module")
+def ctx_fp32(torch):
+    import zwhisper_amd as z
+
+    c = z.Context(0, dense_math=z.DENSE_FP32)
+    yield c
+    c.close()
+
+
 def assert_close(got: np.ndarray, ref: np.ndarray, what: str) -> tuple[float, float]:
     got = np.asarray(got, dtype=np.float64).reshape(-1)
     ref = np.asarray(ref, dtype=np.float64).reshape(-1)
@@ -66,6 +75,21 @@ def test_golden_device_pointers(torch, ctx, case):
     q, k, v = to_dev(torch, case.q), to_dev(torch, case.k), to_dev(torch, case.v)
     out = torch.full((max(sh.out_len(), 1),), SENTINEL, dtype=torch.float32, device="cuda")
     ctx.attention_dev(q, k, v, sh, out)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    m = head_columns_mask(sh)
+    assert_close(got[m], case.expected[m], case.name)
+    assert np.all(got[~m] == SENTINEL), f"{case.name}: wrote outside the head columns"
+
+
+@pytest.mark.parametrize("case", CASES, ids=CASE_IDS)
+def test_golden_dense_fp32_mode(torch, ctx_fp32, case):
+    """The same golden cases with the dense calls on the fp32-MFMA kernel (ZWG_DENSE_FP32)."""
+    print(f"case {case.name} (fp32 dense)", flush=True)
+    sh = case.shape
+    q, k, v = to_dev(torch, case.q), to_dev(torch, case.k), to_dev(torch, case.v)
+    out = torch.full((max(sh.out_len(), 1),), SENTINEL, dtype=torch.float32, device="cuda")
+    ctx_fp32.attention_dev(q, k, v, sh, out)
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     m = head_columns_mask(sh)

@@ -215,6 +215,36 @@ def test_split_and_unsplit_agree(torch):
             check(out.cpu().numpy(), ref2, f"dense causal, workspace {'default' if ws == 0 else 'none'}")
 
 
+@pytest.mark.parametrize("scale", [1.0, 6.0])
+def test_dense_math_modes(torch, scale):
+    """Both dense kernels (bf16x3 and fp32 MFMA) against f64, on ordinary scores and on scores
+    scaled up until the softmax is nearly one-hot (where the bf16 lo terms carry the result);
+    switching a context's mode applies to the next call, and an unknown mode is refused."""
+    import zwhisper_amd as z
+
+    sh = AttnShape(333, 777, 4, 4, 64, 256, 256, 256, False, 784)
+    q = W.normal(51, 333 * 256) * scale
+    kl = W.normal(52, 777 * 256).reshape(777, 4, 64) * scale
+    kt = W.to_kt(kl, 784)
+    v = W.normal(53, 777 * 256)
+    ref = naive.attention_f64(q, kt, v, sh)
+    outs = {}
+    with z.Context(0) as c:
+        for mode in (z.DENSE_BF16X3, z.DENSE_FP32, z.DENSE_BF16X3):
+            c.set_dense_math(mode)
+            out = torch.empty(333 * 256, device="cuda")
+            c.attention_dev(dev(torch, q), dev(torch, kt), dev(torch, v), sh, out)
+            torch.cuda.synchronize()
+            got = out.cpu().numpy()
+            check(got, ref, f"dense mode {mode}, scores x{scale * scale:g}")
+            if mode in outs:
+                assert np.array_equal(outs[mode], got), "same mode, same inputs: results differ"
+            outs[mode] = got
+        assert not np.array_equal(outs[z.DENSE_BF16X3], outs[z.DENSE_FP32]), "mode switch had no effect"
+        with pytest.raises(z.ZwgError):
+            c.set_dense_math(7)
+
+
 def test_deterministic_and_on_a_side_stream(torch, ctx):
     sh = AttnShape(300, 1000, 6, 6, 64, 384, 384, 384, False, None)
     q, k, v = (dev(torch, W.normal(s, n)) for s, n in ((41, 300 * 384), (42, 1000 * 384), (43, 1000 * 384)))

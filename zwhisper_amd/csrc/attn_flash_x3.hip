@@ -1,13 +1,21 @@
-// Dense attention on gfx950 bf16 MFMA with f32-level accuracy: the fp32 kernel of attn_flash.hip
-// (same workgroup geometry, tile pipeline, online softmax, split and merge), with each product
-// of Q.K^T and P.V computed as three bf16 MFMA products of split operands.
+// Dense attention on gfx950 16-bit MFMA with f32-level accuracy: the fp32 kernel of
+// attn_flash.hip (same workgroup geometry, tile pipeline, online softmax, split and merge), with
+// each product of Q.K^T and P.V computed as three 16-bit MFMA products of split operands.
 //
-// Split.  Every f32 operand x is written as hi + lo, hi = bf16(x), lo = bf16(x - hi): 16 of the
-// 24 significand bits, with f32's exponent range (no overflow, unlike an f16 split).  A product
-// a.b is then ah.bh + ah.bl + al.bh (the al.bl term is below 2^-16 of it), each on
-// v_mfma_f32_32x32x16_bf16 with f32 accumulation: 12 MFMAs of 32x32x16 per 32 x 32 tile of
-// Q.K^T (d = 64) and 12 for P.V, against 64 fp32 MFMAs of 32x32x2, so about 5x fewer MFMA cycles.
-// Measured against f64 on the Whisper shapes the outputs stay within ~2e-6 absolute.
+// Split.  Every f32 operand x is written as hi + lo with hi = t(x), lo = t(x - hi) for a 16-bit
+// type t, and a product a.b as ah.bh + ah.bl + al.bh (al.bl is below the rounding of lo), each on
+// a 32x32x16 MFMA with f32 accumulation: 12 MFMAs per 32 x 32 tile of Q.K^T (d = 64) and 12 for
+// P.V, against 64 fp32 MFMAs of 32x32x2, so about 5x fewer MFMA cycles.
+//   Q.K^T uses f16 (two terms carry 22 significand bits).  A score's error is absolute in the
+//   exponent, so it must not grow with the scores: with bf16 (16 bits) it does, by 2^-17 of
+//   sum |q_i k_i|, and scores spread 16x wider than unit-variance inputs give (large-logit heads)
+//   already cost 3e-4 at the output; with f16 the same inputs stay near 2e-5 (CPU emulation
+//   against f64).  f16's range is the price: Q enters pre-scaled by log2(e)/sqrt(d), and K must
+//   stay below 65504 in magnitude -- a larger key gives an infinite hi term and NaN outputs
+//   (never a silently wrong finite one; a masked key cannot poison anything).
+//   P.V uses bf16 (16 bits, f32's exponent range): P is at most 2^8 by the lazily moved running
+//   max and the output error is relative to |V| at ~2^-17, at any magnitude of V.
+// On Whisper-shaped unit-variance inputs the outputs stay within ~2e-6 of f64.
 //
 // Operands.  S^T = K . Q^T (M = keys, N = queries, K = head dims): lane l of the A operand (K)
 // holds key l%32, dims 16 j + 8 (l/32) + 0..7 of k-step j; the B operand (Q^T) the same dims of
@@ -18,8 +26,9 @@
 // + 0..3: the V^T tile is stored with keys 4..7 and 8..11 of every 16 swapped, so each lane's
 // eight keys are contiguous and one 16-byte read.
 //
-// LDS.  K tiles [key][dim] and V^T tiles [dim][key], bf16 hi and lo planes, double-buffered,
-// 16-byte chunks XOR-swizzled by row so a wave's operand reads are conflict-free.
+// LDS.  K tiles [key][dim] (f16) and V^T tiles [dim][key] (bf16), hi and lo planes,
+// double-buffered, 16-byte chunks XOR-swizzled by row so a wave's operand reads are
+// conflict-free.
 #include "attn_kernels.hpp"
 
 namespace zwg {
@@ -29,6 +38,8 @@ namespace {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -43,8 +54,17 @@ __device__ __forceinline__ void split4(const f32x4 &x, bf16x4 &hi, bf16x4 &lo) {
     hi = __builtin_convertvector(x, bf16x4);
     lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x4), bf16x4);
 }
+// the same with f16 terms (round to nearest even)
+__device__ __forceinline__ void split8(const f32x8 &x, f16x8 &hi, f16x8 &lo) {
+    hi = __builtin_convertvector(x, f16x8);
+    lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x8), f16x8);
+}
+__device__ __forceinline__ void split4(const f32x4 &x, f16x4 &hi, f16x4 &lo) {
+    hi = __builtin_convertvector(x, f16x4);
+    lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x4), f16x4);
+}
 
-// K tile element (key, dim): rows of D bf16, 16-byte chunk c stored at c ^ (key / (128 / D))
+// K tile element (key, dim): rows of D f16, 16-byte chunk c stored at c ^ (key / (128 / D))
 // mod (D / 8): the rows sharing LDS banks within a 16-lane read phase land in different chunks.
 template <int D>
 __device__ __forceinline__ int k_at(int key, int dim) {
@@ -69,8 +89,8 @@ __global__ __launch_bounds__(256) void flash_x3_kernel(AttnArgs a) {
     static_assert(BN * D == 256 * 4 * (D / 32), "each thread stages D/32 quads of each tile");
     static_assert(BN == 32, "the P.V key order assumes 32-key tiles");
 
-    __shared__ __align__(16) __bf16 Kh[2][BN * D];
-    __shared__ __align__(16) __bf16 Kl[2][BN * D];
+    __shared__ __align__(16) _Float16 Kh[2][BN * D];
+    __shared__ __align__(16) _Float16 Kl[2][BN * D];
     __shared__ __align__(16) __bf16 Vh[2][D * BN];
     __shared__ __align__(16) __bf16 Vl[2][D * BN];
 
@@ -125,7 +145,7 @@ __global__ __launch_bounds__(256) void flash_x3_kernel(AttnArgs a) {
     const int wave_full = min(k_end, a.causal ? diag + q_wave + 1 : n_kv);
 
     // this lane's query, pre-scaled into log2 units, dims 16 j + 8 half + 0..7, split
-    bf16x8 qh[NKS], ql[NKS];
+    f16x8 qh[NKS], ql[NKS];
     {
         f32x8 qv;
 #pragma unroll
@@ -153,7 +173,7 @@ __global__ __launch_bounds__(256) void flash_x3_kernel(AttnArgs a) {
     float l_run = 0.f;
 
     // Tile staging as in flash_attn_kernel: K two tiles ahead, V one tile ahead, one barrier per
-    // tile.  Each thread holds what it stores as contiguous bf16 quads: four dims of one key for K
+    // tile.  Each thread holds what it stores as contiguous 16-bit quads: four dims of one key for K
     // (row-major K: one 16-byte load; transposed K: four coalesced dword loads, one per dim row)
     // and four keys of one dim for V^T (four coalesced dword loads, one per key row).
     constexpr int NG = D / 32;        // quads per thread per tile, per tensor
@@ -217,10 +237,10 @@ __global__ __launch_bounds__(256) void flash_x3_kernel(AttnArgs a) {
                 key = f / (D / 4);
                 dim = 4 * (f % (D / 4));
             }
-            bf16x4 h, l;
+            f16x4 h, l;
             split4(kr[g], h, l);
-            *reinterpret_cast<bf16x4 *>(&Kh[buf][k_at<D>(key, dim)]) = h;
-            *reinterpret_cast<bf16x4 *>(&Kl[buf][k_at<D>(key, dim)]) = l;
+            *reinterpret_cast<f16x4 *>(&Kh[buf][k_at<D>(key, dim)]) = h;
+            *reinterpret_cast<f16x4 *>(&Kl[buf][k_at<D>(key, dim)]) = l;
         }
     };
     auto store_v = [&](int buf) {
@@ -233,14 +253,14 @@ __global__ __launch_bounds__(256) void flash_x3_kernel(AttnArgs a) {
             *reinterpret_cast<bf16x4 *>(&Vl[buf][at]) = l;
         }
     };
-    // one k-step of S^T = K . Q^T: three bf16 products
+    // one k-step of S^T = K . Q^T: three f16 products
     auto qk_step = [&](int buf, int j, f32x16 sc) {
         const int at = k_at<D>(col, 16 * j + 8 * half);
-        const bf16x8 kh = *reinterpret_cast<const bf16x8 *>(&Kh[buf][at]);
-        const bf16x8 kl = *reinterpret_cast<const bf16x8 *>(&Kl[buf][at]);
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, qh[j], sc, 0, 0, 0);
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kh, ql[j], sc, 0, 0, 0);
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kl, qh[j], sc, 0, 0, 0);
+        const f16x8 kh = *reinterpret_cast<const f16x8 *>(&Kh[buf][at]);
+        const f16x8 kl = *reinterpret_cast<const f16x8 *>(&Kl[buf][at]);
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, qh[j], sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, ql[j], sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, qh[j], sc, 0, 0, 0);
         return sc;
     };
     auto qk = [&](int buf) {
