@@ -8,8 +8,9 @@ in HBM.  The headline line (one JSON object on stdout) is workload 2, Whisper ba
 self-attention over 16 windows x 1500 frames (8 heads x 64, K transposed), in TFLOP/s of
 algorithmic work (4*d*H per visible (q, k) pair, src/bench.zig:76).  The other four workloads
 are measured too (unless --only) and reported under "workloads" in the same line, each with its
-own roofline: bf16 MFMA (2.5 PFLOP/s) for the dense ones, whose kernel computes each f32 product
-as three bf16 products of hi/lo-split operands (ceiling: a third of that peak), HBM (8 TB/s) for
+own roofline: 16-bit MFMA (2.5 PFLOP/s, f16 and bf16 alike) for the dense ones, whose kernel
+computes each f32 product as three 16-bit products of hi/lo-split operands (ceiling: a third of
+that peak), HBM (8 TB/s) for
 the decode ones.  Unless --only, the headline workload is also run on the fp32-MFMA kernel
 ("base_enc_x16_fp32mfma", fp32 peak 157.3 TFLOP/s).
 
@@ -45,7 +46,6 @@ sys.path.insert(0, ROOT)
 
 PEAK_MFMA_F32 = 157.3e12  # FLOP/s, MI355X dense fp32 matrix
 PEAK_MFMA_F16 = 2500e12  # FLOP/s, MI355X dense fp16 matrix
-PEAK_MFMA_BF16 = 2500e12  # FLOP/s, MI355X dense bf16 matrix
 PEAK_HBM = 8.0e12  # B/s, MI355X HBM3E
 
 
@@ -392,7 +392,7 @@ class EncoderLayerWorkload:
         self.lin_flops = 24.0 * rows * ns * ns
         self.attn_flops = 4.0 * self.n_ctx * self.n_ctx * ns * windows
         self.work = self.lin_flops + self.attn_flops
-        self.ideal_s = self.lin_flops * 2 / PEAK_MFMA_F16 + self.attn_flops * 3 / PEAK_MFMA_BF16
+        self.ideal_s = self.lin_flops * 2 / PEAK_MFMA_F16 + self.attn_flops * 3 / PEAK_MFMA_F16
 
     def step(self, i: int):
         # the layer updates x in place, so successive steps apply it to its own output, as the
@@ -645,22 +645,23 @@ def traffic_for(workload_name: str):
         return None
 
 
-DENSE_DTYPE = "bf16x3: f32 inputs split into bf16 hi + lo terms, three bf16 MFMA products per product, f32 accumulation"
+DENSE_DTYPE = ("x3: f32 inputs split into 16-bit hi + lo terms (f16 for Q.K^T, bf16 for P.V), three 16-bit MFMA "
+               "products per product, f32 accumulation")
 
 
 def dense_roofline(achieved: float, dense_math: int) -> dict:
     """MFMA roofline of a dense attention kernel at `achieved` algorithmic FLOP/s.
 
-    The bf16x3 kernel issues three bf16 MFMA products (hi*hi + hi*lo + lo*hi) per algorithmic
-    product, so it is priced against the bf16 dense peak with a ceiling of frac 1/3; the fp32
-    kernel against the fp32 dense peak.
+    The x3 kernel issues three 16-bit MFMA products (hi*hi + hi*lo + lo*hi) per algorithmic
+    product, so it is priced against the f16/bf16 dense peak with a ceiling of frac 1/3; the
+    fp32 kernel against the fp32 dense peak.
     """
     if dense_math == 0:
-        return {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_MFMA_BF16 / 1e12, "unit": "TFLOP/s",
-                "frac": achieved / PEAK_MFMA_BF16, "mfma_products_per_product": 3,
-                "issued_frac": 3 * achieved / PEAK_MFMA_BF16,
-                "note": "bf16 MFMA peak; three bf16 products per algorithmic product, so the kernel's ceiling "
-                        "is frac 1/3 and issued_frac is the share of the bf16 MFMA peak issued"}
+        return {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_MFMA_F16 / 1e12, "unit": "TFLOP/s",
+                "frac": achieved / PEAK_MFMA_F16, "mfma_products_per_product": 3,
+                "issued_frac": 3 * achieved / PEAK_MFMA_F16,
+                "note": "f16/bf16 MFMA peak; three 16-bit products per algorithmic product, so the kernel's "
+                        "ceiling is frac 1/3 and issued_frac is the share of the 16-bit MFMA peak issued"}
     return {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_MFMA_F32 / 1e12, "unit": "TFLOP/s",
             "frac": achieved / PEAK_MFMA_F32}
 
@@ -713,7 +714,7 @@ def main() -> int:
         per_step = wl.work
         if spec.bound == "mfma":
             achieved = per_step / (r["kernel_ms_mean"] * 1e-3)
-            roof = dense_roofline(achieved, z.DENSE_BF16X3)
+            roof = dense_roofline(achieved, z.DENSE_X3)
             value = per_step / (r["ms_per_step"] * 1e-3) / 1e12
             unit = "TFLOP/s"
         else:
@@ -806,11 +807,11 @@ def main() -> int:
                "value": wl.work / (r["ms_per_step"] * 1e-3) / 1e12, "unit": "TFLOP/s",
                "ms_per_step": r["ms_per_step"], "kernel_ms_mean": r["kernel_ms_mean"],
                "kernel_ms_min": r["kernel_ms_min"], "algorithmic_work_per_step": wl.work,
-               "dtype": "f32 (projections: f32 x f16 on f16 MFMA with x split into two f16 terms; attention: bf16x3 MFMA)",
+               "dtype": "f32 (projections: f32 x f16 on f16 MFMA with x split into two f16 terms; attention: x3 16-bit MFMA)",
                "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
                             "frac": achieved / peak, "traffic": None,
                             "note": "peak = the layer's flops over the time they take at their own peaks: "
-                                    "projections at half the f16 MFMA peak, attention at a third of the bf16 MFMA peak"}}
+                                    "projections at half the f16 MFMA peak, attention at a third of the 16-bit MFMA peak"}}
         if not args.no_cpu:
             res["cpu_baseline"] = wl.cpu_baseline(host_threads())
         results[wl.name] = res

@@ -79,19 +79,22 @@ typedef struct zwg_batch {
 /*
  * Arithmetic of the dense (encoder / prefill) attention kernel.  Both give results within the
  * 2e-4 bar of the reference's f32 attention:
- *   ZWG_DENSE_BF16X3 (default): every product of Q.K^T and P.V as three bf16 MFMA products of
- *     operands split into bf16 hi + lo (16 significand bits each side, f32 exponent range, f32
- *     accumulation): measured within ~2e-6 of f64 on the Whisper shapes, about 3x the fp32 rate.
- *   ZWG_DENSE_FP32: fp32 MFMA (v_mfma_f32_32x32x2_f32) throughout.
+ *   ZWG_DENSE_X3 (default): every product as three 16-bit MFMA products of operands split into
+ *     hi + lo terms, f32 accumulation, about 2.4x the fp32 kernel's rate.  Q.K^T splits into f16
+ *     (22 significand bits, so a score's error does not grow with large logits), P.V into bf16
+ *     (16 bits, f32 exponent range).  Measured within ~2e-6 of f64 on the Whisper shapes and
+ *     ~5e-5 with scores spread 36x wider.  Keys must stay below 65504 in magnitude (f16 range):
+ *     a larger one gives NaN outputs, never a silently wrong finite one.
+ *   ZWG_DENSE_FP32: fp32 MFMA (v_mfma_f32_32x32x2_f32) throughout, no range condition.
  * The decode kernels are f32 FMA in either mode.
  */
-#define ZWG_DENSE_BF16X3 0u
+#define ZWG_DENSE_X3 0u
 #define ZWG_DENSE_FP32 1u
 
 /* Sizes and modes fixed when a context opens.  Zero fields take the defaults. */
 typedef struct zwg_limits {
     uint64_t workspace_bytes; /* device memory for split-KV partial results; default 256 MiB */
-    uint32_t dense_math;      /* ZWG_DENSE_BF16X3 (0, default) or ZWG_DENSE_FP32 */
+    uint32_t dense_math;      /* ZWG_DENSE_X3 (0, default) or ZWG_DENSE_FP32 */
     uint32_t reserved;        /* must be 0 */
 } zwg_limits;
 
@@ -119,7 +122,7 @@ int zwg_set_stream(zwg_ctx *ctx, void *hip_stream);
 void *zwg_get_stream(const zwg_ctx *ctx);
 /* Wait for all work queued on the context's stream. */
 int zwg_sync(zwg_ctx *ctx);
-/* Switch the dense kernel's arithmetic (ZWG_DENSE_BF16X3 or ZWG_DENSE_FP32) for later calls. */
+/* Switch the dense kernel's arithmetic (ZWG_DENSE_X3 or ZWG_DENSE_FP32) for later calls. */
 int zwg_set_dense_math(zwg_ctx *ctx, uint32_t mode);
 
 /*

@@ -217,8 +217,8 @@ def test_split_and_unsplit_agree(torch):
 
 @pytest.mark.parametrize("scale", [1.0, 6.0])
 def test_dense_math_modes(torch, scale):
-    """Both dense kernels (bf16x3 and fp32 MFMA) against f64, on ordinary scores and on scores
-    scaled up until the softmax is nearly one-hot (where the bf16 lo terms carry the result);
+    """Both dense kernels (x3 16-bit and fp32 MFMA) against f64, on ordinary scores and on scores
+    scaled up until the softmax is nearly one-hot (where the split terms carry the result);
     switching a context's mode applies to the next call, and an unknown mode is refused."""
     import zwhisper_amd as z
 
@@ -230,7 +230,7 @@ def test_dense_math_modes(torch, scale):
     ref = naive.attention_f64(q, kt, v, sh)
     outs = {}
     with z.Context(0) as c:
-        for mode in (z.DENSE_BF16X3, z.DENSE_FP32, z.DENSE_BF16X3):
+        for mode in (z.DENSE_X3, z.DENSE_FP32, z.DENSE_X3):
             c.set_dense_math(mode)
             out = torch.empty(333 * 256, device="cuda")
             c.attention_dev(dev(torch, q), dev(torch, kt), dev(torch, v), sh, out)
@@ -240,7 +240,7 @@ def test_dense_math_modes(torch, scale):
             if mode in outs:
                 assert np.array_equal(outs[mode], got), "same mode, same inputs: results differ"
             outs[mode] = got
-        assert not np.array_equal(outs[z.DENSE_BF16X3], outs[z.DENSE_FP32]), "mode switch had no effect"
+        assert not np.array_equal(outs[z.DENSE_X3], outs[z.DENSE_FP32]), "mode switch had no effect"
         with pytest.raises(z.ZwgError):
             c.set_dense_math(7)
 

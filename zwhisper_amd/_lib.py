@@ -96,7 +96,7 @@ class KVInfoC(ctypes.Structure):
     ]
 
 
-DENSE_BF16X3 = 0
+DENSE_X3 = 0
 DENSE_FP32 = 1
 KV_ROW = 0
 KV_KT = 1

@@ -14,7 +14,7 @@ struct zwg_ctx {
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
     float *workspace = nullptr;
-    uint32_t dense_math = ZWG_DENSE_BF16X3; // products of the dense kernel (zwg_set_dense_math)
+    uint32_t dense_math = ZWG_DENSE_X3; // products of the dense kernel (zwg_set_dense_math)
     uint64_t workspace_bytes = 0;
     // device staging for the host-pointer calls: q, k, v, out
     float *stage[4] = {nullptr, nullptr, nullptr, nullptr};

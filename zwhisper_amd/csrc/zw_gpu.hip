@@ -206,7 +206,7 @@ int run(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_
         return fail(ctx, "q, k, v and out must be 16-byte aligned");
     const Plan p = make_plan(s, b, ctx->workspace_bytes);
     if (p.ws_bytes > ctx->workspace_bytes) return fail(ctx, "workspace too small for this call");
-    // the row-major decode kernel and the bf16x3 dense kernel address one item's K/V rows (and the
+    // the row-major decode kernel and the x3 dense kernel address one item's K/V rows (and the
     // dense kernel one KV head's K^T rows) with 32-bit byte offsets
     const bool dense_x3 = p.kernel == 1 && ctx->dense_math != ZWG_DENSE_FP32;
     if ((p.kernel == 2 && !s.kt_stride) || dense_x3) {
@@ -323,7 +323,7 @@ int zwg_open(int device, const zwg_limits *limits, zwg_ctx **out) {
         delete ctx;
         return fail(nullptr, "unknown dense_math");
     }
-    ctx->dense_math = limits ? limits->dense_math : ZWG_DENSE_BF16X3;
+    ctx->dense_math = limits ? limits->dense_math : ZWG_DENSE_X3;
     void *ws = nullptr;
     e = hipMalloc(&ws, ctx->workspace_bytes);
     if (e != hipSuccess) {

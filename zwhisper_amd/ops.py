@@ -102,7 +102,7 @@ class Context:
     """One library context (zwg_ctx): a device, a workspace, staging buffers."""
 
     def __init__(self, device: int = 0, workspace_bytes: int = 0, dense_math: int = 0):
-        """dense_math: _lib.DENSE_BF16X3 (0, default) or _lib.DENSE_FP32, the dense kernel's arithmetic."""
+        """dense_math: _lib.DENSE_X3 (0, default) or _lib.DENSE_FP32, the dense kernel's arithmetic."""
         L = _lib.lib()
         self._L = L
         h = ctypes.c_void_p()
@@ -114,7 +114,7 @@ class Context:
         self.device = device
 
     def set_dense_math(self, mode: int) -> None:
-        """Switch the dense kernel's arithmetic (_lib.DENSE_BF16X3 or _lib.DENSE_FP32) for later calls."""
+        """Switch the dense kernel's arithmetic (_lib.DENSE_X3 or _lib.DENSE_FP32) for later calls."""
         self._check(self._L.zwg_set_dense_math(self._h, mode))
 
     def close(self) -> None:
