@@ -49,6 +49,26 @@ PEAK_MFMA_F16 = 2500e12  # FLOP/s, MI355X dense fp16 matrix
 PEAK_HBM = 8.0e12  # B/s, MI355X HBM3E
 
 
+CPU_MIN_SECONDS = 2.0  # each CPU baseline repeats its sample for at least this long
+
+
+def time_cpu(run, min_reps: int = 5) -> tuple[float, float, int]:
+    """One warm-up call, then repeated calls until both `min_reps` runs and CPU_MIN_SECONDS have
+    passed (src/bench.zig:69-75 takes the best of 5 after one warm-up).  Returns (best, mean, runs)."""
+    run()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_reps or time.perf_counter() - t_start < CPU_MIN_SECONDS:
+        t0 = time.perf_counter()
+        run()
+        times.append(time.perf_counter() - t0)
+    return min(times), float(np.mean(times)), len(times)
+
+
+def cpu_timing(best: float, mean: float, runs: int) -> str:
+    return f"best of {runs} runs over {CPU_MIN_SECONDS:g}+ s after one warm-up (mean {1e3 * mean:.2f} ms)"
+
+
 def host_threads() -> int:
     """The reference's default thread count, CPUs - 1 (src/main.zig:126), on this host's share."""
     try:
@@ -257,7 +277,7 @@ class AppendWorkload:
 
     def cpu_baseline(self) -> dict:
         """oracle/kv.py's vectorised update (the reference's loops of src/llm.zig:182-190 and
-        src/decoder.zig:182-183, in numpy), best of 5, on this host."""
+        src/decoder.zig:182-183, in numpy) on this host."""
         from oracle import kv as okv
 
         kvw = self.hkv * self.d
@@ -274,15 +294,10 @@ class AppendWorkload:
                 kt.reshape(self.n_ctx, kvw)[self.pos] = self.host["k"]
                 cv.reshape(self.n_ctx, kvw)[self.pos] = self.host["v"]
 
-        run()
-        best = float("inf")
-        for _ in range(5):
-            t0 = time.perf_counter()
-            run()
-            best = min(best, time.perf_counter() - t0)
+        best, mean, runs = time_cpu(run)
         return {"value": self.work / best / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
-                "sample": "the whole update; oracle/kv.py llm_append_vec (numpy, one thread), best of 5",
-                "seconds": best}
+                "sample": "the whole update; oracle/kv.py llm_append_vec (numpy, one thread); "
+                          + cpu_timing(best, mean, runs), "seconds": best}
 
     def free(self):
         self.kv.close()
@@ -321,7 +336,7 @@ class LinearWorkload:
 
     def cpu_baseline(self, threads: int) -> dict:
         """The oracle's ops.linear with f16 weights (oracle/attn_oracle.c, the reference's ntBlock
-        over its Pool) on one of the 16 windows, best of 3 after a warm-up."""
+        over its Pool) on one of the 16 windows."""
         import oracle
 
         rows = 1500
@@ -335,17 +350,12 @@ class LinearWorkload:
             for (k, n), w, b in zip(self.layers, ws, bs):
                 o.linear_f16(xs[k], rows, k, w, b, n, out=outs[n])
 
-        run()
-        best = float("inf")
-        for _ in range(3):
-            t0 = time.perf_counter()
-            run()
-            best = min(best, time.perf_counter() - t0)
+        best, mean, runs = time_cpu(run, 3)
         o.close()
         work = self.work * rows / self.m
         return {"value": work / best / 1e12, "unit": "TFLOP/s", "cores": o.threads, "kind": "port",
-                "sample": "1 of 16 windows (1500 rows), all six layers; oracle/attn_oracle.c ora_linear_f16, "
-                          "best of 3 after one warm-up", "seconds": best}
+                "sample": "1 of 16 windows (1500 rows), all six layers; oracle/attn_oracle.c ora_linear_f16; "
+                          + cpu_timing(best, mean, runs), "seconds": best}
 
     def free(self):
         self.x = self.out = self.w = self.b = None
@@ -401,22 +411,17 @@ class EncoderLayerWorkload:
 
     def cpu_baseline(self, threads: int) -> dict:
         """The oracle's encoder layer (ops.layerNorm, ops.linear over f16, ops.attention, ops.gelu,
-        ops.add restated in oracle/attn_oracle.c) on one of the 16 windows, best of 3 after a warm-up."""
+        ops.add restated in oracle/attn_oracle.c) on one of the 16 windows."""
         import oracle
 
         w = {k: v.cpu().numpy() for k, v in self.w.items()}
         x = self.x0[0].cpu().numpy()
         o = oracle.Oracle(threads)
-        o.encoder_layer(x, self.n_ctx, self.ns, self.n_head, w)
-        best = float("inf")
-        for _ in range(3):
-            t0 = time.perf_counter()
-            o.encoder_layer(x, self.n_ctx, self.ns, self.n_head, w)
-            best = min(best, time.perf_counter() - t0)
+        best, mean, runs = time_cpu(lambda: o.encoder_layer(x, self.n_ctx, self.ns, self.n_head, w), 3)
         o.close()
         return {"value": self.work / self.windows / best / 1e12, "unit": "TFLOP/s", "cores": o.threads,
-                "kind": "port", "sample": "1 of 16 windows; oracle Oracle.encoder_layer (attn_oracle.c), best of 3 "
-                                          "after one warm-up", "seconds": best}
+                "kind": "port", "sample": "1 of 16 windows; oracle Oracle.encoder_layer (attn_oracle.c); "
+                                          + cpu_timing(best, mean, runs), "seconds": best}
 
     def free(self):
         self.w = self.x = self.x0 = self.scratch = None
@@ -485,7 +490,7 @@ class Q8LinearWorkload:
 
     def cpu_baseline(self, threads: int) -> dict:
         """The oracle's ops.linear over Q8 (oracle/attn_oracle.c: ntBlockQ over the reference's Pool),
-        on the first layers, best of 3 after a warm-up."""
+        on the first layers."""
         import oracle
 
         sample = self.layers[:len(self.raw)]
@@ -497,18 +502,13 @@ class Q8LinearWorkload:
             for (k, n, _), (q, sc, b) in zip(sample, self.raw):
                 o.linear_q8(xs[k], self.m, k, q, sc, b, n, out=outs[n])
 
-        run()
-        best = float("inf")
-        for _ in range(3):
-            t0 = time.perf_counter()
-            run()
-            best = min(best, time.perf_counter() - t0)
+        best, mean, runs = time_cpu(run, 3)
         o.close()
         work = float(sum(n * k + n * k // 32 * 4 + (n * 4 if hb else 0) + self.m * k * 4 + self.m * n * 4
                          for k, n, hb in sample))
         return {"value": work / best / 1e9, "unit": "GB/s", "cores": o.threads, "kind": "port",
                 "sample": f"{len(sample)} of {len(self.layers)} layers at the full {self.m} rows; "
-                          "oracle/attn_oracle.c ora_linear_q8, best of 3 after one warm-up", "seconds": best}
+                          "oracle/attn_oracle.c ora_linear_q8; " + cpu_timing(best, mean, runs), "seconds": best}
 
     def free(self):
         self.graphs = None
@@ -568,7 +568,7 @@ def cpu_baseline(number: int, threads: int) -> dict:
     o = oracle.Oracle(threads)
     calls = []  # (q, k, v, shape) of the sample
     if number in (1, 2):
-        n_items = 1 if number == 1 else 2
+        n_items = w.n_items
         for item in range(n_items):
             q, kl, v = W.make_dense(number, item)
             # encoder.zig:167 passes row-major K; attentionEx transposes it itself
@@ -589,7 +589,7 @@ def cpu_baseline(number: int, threads: int) -> dict:
         work = W.algorithmic_work(4)
     elif number == 3:
         ns = w.n_head * w.d
-        n_items = 8
+        n_items = w.n_items
         lengths = W.kv_lengths(3)
         for item in range(n_items):
             s = W.make_decoder_step(item)
@@ -601,7 +601,7 @@ def cpu_baseline(number: int, threads: int) -> dict:
         work = float(sum(2 * int(n) * ns * 4 + 2 * 1500 * ns * 4 + 4 * ns * 4 for n in lengths[:n_items]))
     else:
         ns, kvw = w.n_head * w.d, w.n_head_kv * w.d
-        n_items = 8
+        n_items = w.n_items
         lengths = W.kv_lengths(5)
         for item in range(n_items):
             q, kl, v, n_kv = W.make_llm_decode(item)
@@ -620,17 +620,12 @@ def cpu_baseline(number: int, threads: int) -> dict:
         for q, k, v, sh, out, scratch in prepared:
             o.attention_ex(q, k, v, sh, out=out, scratch=scratch)
 
-    run_all()  # warm-up, as src/bench.zig:69
-    best = float("inf")
-    for _ in range(5):  # best of 5, as src/bench.zig:70-75
-        t0 = time.perf_counter()
-        run_all()
-        best = min(best, time.perf_counter() - t0)
+    best, mean, runs = time_cpu(run_all)
     o.close()
     bound = W.WORKLOADS[number].bound
     value = work / best / (1e12 if bound == "mfma" else 1e9)
     return {"value": value, "unit": "TFLOP/s" if bound == "mfma" else "GB/s", "cores": o.threads,
-            "kind": "port", "sample": f"{sample}; oracle/attn_oracle.c, best of 5 after one warm-up",
+            "kind": "port", "sample": f"{sample}; oracle/attn_oracle.c; " + cpu_timing(best, mean, runs),
             "seconds": best}
 
 

@@ -148,7 +148,8 @@ int zwg_attention_batch_dev(zwg_ctx *ctx, const float *q, const float *k, const 
 
 /*
  * The plan a call with this shape and batch (NULL = one item) would use, for a context opened
- * with `workspace_bytes` of workspace (0 = default).  Host-only: needs no device.
+ * with `workspace_bytes` of workspace (0 = default) in the default dense mode (ZWG_DENSE_X3;
+ * ZWG_DENSE_FP32 splits causal calls into more chunks).  Host-only: needs no device.
  */
 int zwg_plan(const zwg_attn_shape *shape, const zwg_batch *batch, uint64_t workspace_bytes, zwg_plan_info *out);
 

@@ -368,24 +368,32 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
     const int item = (int)(ih / a.n_head);
     const float2 *ml = reinterpret_cast<const float2 *>(a.part_ml) + row * a.max_chunks;
     const float4 *po = reinterpret_cast<const float4 *>(a.part_o + row * a.max_chunks * D) + g;
-    // Every slot of the row (c < max_chunks, all inside the workspace) is loaded before the
-    // item's key count arrives, so the partials' round trip overlaps that of the count; slots past
-    // the row's chunk count are discarded below by selection (they may hold anything).
+    const int q_end = min((query / a.rows_per_unit + 1) * a.rows_per_unit, a.n_q);
+    auto row_chunks = [&](int n_kv) {
+        const int kv_hi = a.causal ? max(0, n_kv - a.n_q + q_end) : n_kv;
+        int chunk_keys;
+        return unit_split(kv_hi, a.split_tile, a.chunk_len, a.max_chunks, &chunk_keys);
+    };
+    // With one key count for every item the row's chunk count is known at once: rows the
+    // attention kernel finished (one chunk) load nothing, and the others load their own slots
+    // only.  With per-item counts in device memory, every slot of the row (c < max_chunks, all
+    // inside the workspace) is loaded before the count arrives, so the partials' round trip
+    // overlaps that of the count; slots past the row's chunk count are discarded below by
+    // selection (they may hold anything).
+    const int known_chunks = a.n_kv_item ? 0 : row_chunks(a.n_kv);
+    if (known_chunks == 1) return; // written by the attention kernel
+    const int last_slot = (known_chunks ? known_chunks : a.max_chunks) - 1;
     float2 mlr[MAXC > 0 ? MAXC : 1];
     float4 vr[MAXC > 0 ? MAXC : 1];
     if (MAXC > 0) {
 #pragma unroll
-        for (int c = 0; c < MAXC; ++c) { // slots past max_chunks reload the last one: no branches
-            const int cc = min(c, a.max_chunks - 1);
+        for (int c = 0; c < MAXC; ++c) { // slots past the last reload it: no branches
+            const int cc = min(c, last_slot);
             mlr[c] = ml[cc];
             vr[c] = po[(int64_t)cc * G4];
         }
     }
-    const int n_kv = item_kv(a, item);
-    const int q_end = min((query / a.rows_per_unit + 1) * a.rows_per_unit, a.n_q);
-    const int kv_hi = a.causal ? max(0, n_kv - a.n_q + q_end) : n_kv;
-    int chunk_keys;
-    const int n_chunks = unit_split(kv_hi, a.split_tile, a.chunk_len, a.max_chunks, &chunk_keys);
+    const int n_chunks = known_chunks ? known_chunks : row_chunks(item_kv(a, item));
     if (n_chunks == 1) return; // written by the attention kernel
 
     float M = -INFINITY, L = 0.f;

@@ -71,7 +71,10 @@ constexpr uint64_t kMaxSplitUnitsHint = 1ull << 22;
 #define ZWG_FLASH_BLOCKS_PER_CU 2 // dense grid aimed at when keys are split, per CU
 #endif
 #ifndef ZWG_FLASH_CAUSAL_BLOCKS_PER_CU
-#define ZWG_FLASH_CAUSAL_BLOCKS_PER_CU 6 // ... for causal calls, dispatched longest-first
+#define ZWG_FLASH_CAUSAL_BLOCKS_PER_CU 2 // ... for causal calls, dispatched longest-first
+#endif
+#ifndef ZWG_FLASH32_CAUSAL_BLOCKS_PER_CU
+#define ZWG_FLASH32_CAUSAL_BLOCKS_PER_CU 6 // ... the same for the fp32 dense kernel (ZWG_DENSE_FP32)
 #endif
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -138,7 +141,7 @@ uint64_t split_bound(uint64_t w, uint64_t tau) { return std::max<uint64_t>(1, (w
 // the machine, keys are split so the workgroups are about equal in work, two per CU.  Causal
 // calls (q-blocks of very unequal length) are always split, into about six workgroups per CU
 // dispatched longest q-block first, so slots freed by short work keep the machine busy.
-Plan make_plan(const zwg_attn_shape &s, const zwg_batch &b, uint64_t ws_cap) {
+Plan make_plan(const zwg_attn_shape &s, const zwg_batch &b, uint64_t ws_cap, uint32_t dense_math) {
     Plan p;
     const uint64_t group = s.n_head / s.n_head_kv;
     const uint64_t n_rows_total = b.n_batch * s.n_head * s.n_q;
@@ -173,7 +176,9 @@ Plan make_plan(const zwg_attn_shape &s, const zwg_batch &b, uint64_t ws_cap) {
         }
         tiles *= s.n_head * b.n_batch;
         w_max = std::max<uint64_t>(1, ceil_div(s.n_kv, tile));
-        const uint64_t target = (uint64_t)(s.causal ? ZWG_FLASH_CAUSAL_BLOCKS_PER_CU : ZWG_FLASH_BLOCKS_PER_CU) * kNumCUs;
+        const uint64_t causal_target =
+            dense_math == ZWG_DENSE_FP32 ? ZWG_FLASH32_CAUSAL_BLOCKS_PER_CU : ZWG_FLASH_CAUSAL_BLOCKS_PER_CU;
+        const uint64_t target = (uint64_t)(s.causal ? causal_target : ZWG_FLASH_BLOCKS_PER_CU) * kNumCUs;
         tau = w_max;
         if (s.causal || units < target) tau = std::min(w_max, std::max<uint64_t>(1, ceil_div(tiles, target)));
     }
@@ -204,7 +209,7 @@ int run(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_
     if (!q || !out || (s.n_kv && (!k || !v))) return fail(ctx, "null tensor pointer");
     if (!aligned16(q) || !aligned16(out) || (s.n_kv && (!aligned16(k) || !aligned16(v))))
         return fail(ctx, "q, k, v and out must be 16-byte aligned");
-    const Plan p = make_plan(s, b, ctx->workspace_bytes);
+    const Plan p = make_plan(s, b, ctx->workspace_bytes, ctx->dense_math);
     if (p.ws_bytes > ctx->workspace_bytes) return fail(ctx, "workspace too small for this call");
     // the row-major decode kernel and the x3 dense kernel address one item's K/V rows (and the
     // dense kernel one KV head's K^T rows) with 32-bit byte offsets
@@ -290,7 +295,7 @@ int zwg_plan(const zwg_attn_shape *shape, const zwg_batch *batch, uint64_t works
     std::string msg = check_shape(*shape);
     if (msg.empty()) msg = check_batch(*shape, b);
     if (!msg.empty()) return fail(nullptr, msg);
-    const Plan p = make_plan(*shape, b, workspace_bytes ? workspace_bytes : kDefaultWorkspace);
+    const Plan p = make_plan(*shape, b, workspace_bytes ? workspace_bytes : kDefaultWorkspace, ZWG_DENSE_X3);
     out->kernel = (uint32_t)p.kernel;
     out->rows_per_unit = (uint32_t)p.rows_per_unit;
     out->chunk_len = (uint64_t)p.chunk_len;
