@@ -804,7 +804,7 @@ def main() -> int:
                "kernel_ms_min": r["kernel_ms_min"], "algorithmic_work_per_step": wl.work,
                "dtype": "f32 (projections: f32 x f16 on f16 MFMA with x split into two f16 terms; attention: x3 16-bit MFMA)",
                "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
-                            "frac": achieved / peak, "traffic": None,
+                            "frac": achieved / peak, "traffic": traffic_for(wl.name),
                             "note": "peak = the layer's flops over the time they take at their own peaks: "
                                     "projections at half the f16 MFMA peak, attention at a third of the 16-bit MFMA peak"}}
         if not args.no_cpu:
