@@ -40,28 +40,86 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 
-// bf16 hi/lo of eight / four floats, as vector conversions (two values per v_cvt_pk_bf16_f32)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// Splits, six VALU per pair of bf16 values and four per pair of f16 values.
+//   bf16: one v_cvt_pk_bf16_f32 rounds a pair; the hi terms come back to f32 from the packed
+//   bits (a shift, an and), two subtracts give the remainders, a second v_cvt_pk rounds them.
+//   f16: one v_cvt_pk_f16_f32 rounds a pair; v_fma_mix_f32 reads each half as f16 and forms
+//   x - hi in f32 in one instruction (exact: hi is x rounded, so x - hi is representable).
+__device__ __forceinline__ uint32_t split2_bf16(float a, float b, uint32_t &lo) {
+    const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+    const float ha = __builtin_bit_cast(float, h << 16), hb = __builtin_bit_cast(float, h & 0xffff0000u);
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a - ha, b - hb}, bf16x2));
+    return h;
+}
+__device__ __forceinline__ float sub_f16_lo(uint32_t pair, float x) { // x - (float)low half of pair
+    float r;
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pair), "v"(x));
+    return r;
+}
+__device__ __forceinline__ float sub_f16_hi(uint32_t pair, float x) { // x - (float)high half of pair
+    float r;
+    asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pair), "v"(x));
+    return r;
+}
+__device__ __forceinline__ uint32_t split2_f16(float a, float b, uint32_t &lo) {
+    const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){sub_f16_lo(h, a), sub_f16_hi(h, b)}, f16x2));
+    return h;
+}
 __device__ __forceinline__ void split8(const f32x8 &x, bf16x8 &hi, bf16x8 &lo) {
-    hi = __builtin_convertvector(x, bf16x8);
-    lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x8), bf16x8);
+    u32x4 h, l;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t li;
+        h[i] = split2_bf16(x[2 * i], x[2 * i + 1], li);
+        l[i] = li;
+    }
+    hi = __builtin_bit_cast(bf16x8, h);
+    lo = __builtin_bit_cast(bf16x8, l);
 }
 __device__ __forceinline__ void split4(const f32x4 &x, bf16x4 &hi, bf16x4 &lo) {
-    hi = __builtin_convertvector(x, bf16x4);
-    lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x4), bf16x4);
+    u32x2 h, l;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        uint32_t li;
+        h[i] = split2_bf16(x[2 * i], x[2 * i + 1], li);
+        l[i] = li;
+    }
+    hi = __builtin_bit_cast(bf16x4, h);
+    lo = __builtin_bit_cast(bf16x4, l);
 }
-// the same with f16 terms (round to nearest even)
 __device__ __forceinline__ void split8(const f32x8 &x, f16x8 &hi, f16x8 &lo) {
-    hi = __builtin_convertvector(x, f16x8);
-    lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x8), f16x8);
+    u32x4 h, l;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        uint32_t li;
+        h[i] = split2_f16(x[2 * i], x[2 * i + 1], li);
+        l[i] = li;
+    }
+    hi = __builtin_bit_cast(f16x8, h);
+    lo = __builtin_bit_cast(f16x8, l);
 }
 __device__ __forceinline__ void split4(const f32x4 &x, f16x4 &hi, f16x4 &lo) {
-    hi = __builtin_convertvector(x, f16x4);
-    lo = __builtin_convertvector(x - __builtin_convertvector(hi, f32x4), f16x4);
+    u32x2 h, l;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        uint32_t li;
+        h[i] = split2_f16(x[2 * i], x[2 * i + 1], li);
+        l[i] = li;
+    }
+    hi = __builtin_bit_cast(f16x4, h);
+    lo = __builtin_bit_cast(f16x4, l);
 }
 
 // K tile element (key, dim): rows of D f16, 16-byte chunk c stored at c ^ (key / (128 / D))
