@@ -29,6 +29,8 @@
 // LDS.  K tiles [key][dim] (f16) and V^T tiles [dim][key] (bf16), hi and lo planes,
 // double-buffered, 16-byte chunks XOR-swizzled by row so a wave's operand reads are
 // conflict-free.
+#include <type_traits>
+
 #include "attn_kernels.hpp"
 
 namespace zwg {
@@ -122,6 +124,26 @@ __device__ __forceinline__ void split4(const f32x4 &x, f16x4 &hi, f16x4 &lo) {
     lo = __builtin_bit_cast(f16x4, l);
 }
 
+// max / sum over lanes l and l ^ 32 (the two halves of a query's keys): v_permlane32_swap
+// exchanges lanes 32..63 of its first register with lanes 0..31 of its second, so with x in both
+// the two hold x of lanes 0..31 and of lanes 32..63 in every lane -- no LDS round trip.  Issued
+// as inline asm: this compiler's __builtin_amdgcn_permlane32_swap returns the first register for
+// both results.  The s_nop gives the two wait states the instruction needs after a VALU write of
+// its operands.
+__device__ __forceinline__ f32x2 lane_halves(float x) {
+    float a = x, b = x;
+    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return (f32x2){a, b};
+}
+__device__ __forceinline__ float lane_pair_max(float x) {
+    const f32x2 h = lane_halves(x);
+    return fmaxf(h[0], h[1]);
+}
+__device__ __forceinline__ float lane_pair_sum(float x) {
+    const f32x2 h = lane_halves(x);
+    return h[0] + h[1];
+}
+
 // K tile element (key, dim): rows of D f16, 16-byte chunk c stored at c ^ (key / (128 / D))
 // mod (D / 8): the rows sharing LDS banks within a 16-lane read phase land in different chunks.
 template <int D>
@@ -138,8 +160,10 @@ __device__ __forceinline__ int v_at(int dim, int pos) {
 
 } // namespace
 
+// d = 128 needs just over 256 VGPRs unconstrained; capping it there keeps two waves per SIMD
 template <int D, bool KT>
-__global__ __launch_bounds__(256) void flash_x3_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : 1)))
+void flash_x3_kernel(AttnArgs a) {
     constexpr int BM = kFlashBM;
     constexpr int BN = kFlashBN;
     constexpr int NKS = D / 16;  // k-steps of the QK product
@@ -340,7 +364,7 @@ __global__ __launch_bounds__(256) void flash_x3_kernel(AttnArgs a) {
         float mt = sc[0];
 #pragma unroll
         for (int r = 1; r < 16; ++r) mt = fmaxf(mt, sc[r]);
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        mt = lane_pair_max(mt);
         if (__any(mt > m_run + 8.0f)) {
             const float m_new = fmaxf(m_run, mt);
             const float alpha = m_run == -INFINITY ? 0.f : exp2_fast(m_run - m_new);
@@ -352,18 +376,18 @@ __global__ __launch_bounds__(256) void flash_x3_kernel(AttnArgs a) {
     };
     auto exp_sum = [&](f32x16 &sc) {
         const float m_use = m_run == -INFINITY ? 0.f : m_run;
-        float ls = 0.f;
+        float ls;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             sc[r] = exp2_fast(sc[r] - m_use);
-            ls += sc[r];
+            ls = r == 0 ? sc[0] : ls + sc[r];
         }
         l_run += ls;
     };
     // the next tile's score MFMAs interleaved with this tile's exponentials
     auto qk_exp = [&](int buf, f32x16 &p) {
         const float m_use = m_run == -INFINITY ? 0.f : m_run;
-        float ls = 0.f;
+        float ls;
         f32x16 sc = (f32x16){0};
         constexpr int PER = 16 / NKS; // exponentials per k-step
 #pragma unroll
@@ -373,7 +397,7 @@ __global__ __launch_bounds__(256) void flash_x3_kernel(AttnArgs a) {
             for (int u = 0; u < PER; ++u) {
                 const int r = j * PER + u;
                 p[r] = exp2_fast(p[r] - m_use);
-                ls += p[r];
+                ls = r == 0 ? p[0] : ls + p[r];
             }
         }
         l_run += ls;
@@ -415,29 +439,40 @@ __global__ __launch_bounds__(256) void flash_x3_kernel(AttnArgs a) {
     if (n_tiles > 1) store_k(1);
     __syncthreads();
 
-    for (int t = 0; t < n_tiles; ++t) {
+    // one tile: t's buffer parity is a compile-time constant (the loop runs two tiles per turn),
+    // so LDS addresses are immediate offsets and the score registers alternate between sa and sb
+    // without copies
+    auto step = [&](auto parity, int t, f32x16 &s_cur, f32x16 &s_next) {
+        constexpr int cur = decltype(parity)::value, nxt = cur ^ 1;
         const int k0 = k_begin + t * BN;
         if (t + 2 < n_tiles) load_k(k0 + 2 * BN);
         if (t + 1 < n_tiles) load_v(k0 + BN);
         const bool need_cur = wave_needs(k0);
         const bool need_next = t + 1 < n_tiles && wave_needs(k0 + BN);
-        f32x16 s_next = (f32x16){0};
         if (need_cur) mask_and_max(s_cur, k0);
         if (need_cur && need_next) {
-            s_next = qk_exp((t + 1) & 1, s_cur);
+            s_next = qk_exp(nxt, s_cur);
         } else if (need_cur) {
             exp_sum(s_cur);
         } else if (need_next) {
-            s_next = qk((t + 1) & 1);
+            s_next = qk(nxt);
         }
-        if (need_cur) pv(s_cur, t & 1);
-        if (t + 2 < n_tiles) store_k(t & 1);
-        if (t + 1 < n_tiles) store_v((t + 1) & 1);
+        if (need_cur) pv(s_cur, cur);
+        if (t + 2 < n_tiles) store_k(cur);
+        if (t + 1 < n_tiles) store_v(nxt);
         __syncthreads();
-        s_cur = s_next;
+    };
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    f32x16 s_b = (f32x16){0};
+    int t = 0;
+    for (; t + 1 < n_tiles; t += 2) {
+        step(P0{}, t, s_cur, s_b);
+        step(P1{}, t + 1, s_b, s_cur);
     }
+    if (t < n_tiles) step(P0{}, t, s_cur, s_b);
 
-    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    const float l_tot = lane_pair_sum(l_run);
     if (!q_valid) return;
     // lane holds dims db*32 + 8*g + 4*half + {0..3} in registers 4g..4g+3 of o[db]
     if (n_chunks == 1) {
