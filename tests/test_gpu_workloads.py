@@ -245,6 +245,39 @@ def test_dense_math_modes(torch, scale):
             c.set_dense_math(7)
 
 
+DENSE_SHAPES = [
+    # (n_q, n_kv, heads, kv heads, d, causal, kt): every dense instantiation of both kernels
+    (300, 300, 12, 2, 128, True, True),    # Qwen2-1.5B prefill, transposed K, d = 128
+    (200, 333, 4, 4, 128, False, True),    # d = 128, transposed K, non-causal, ragged tiles
+    (150, 260, 6, 6, 32, False, True),     # d = 32, transposed K
+    (97, 97, 12, 12, 32, True, False),     # d = 32, row-major K, causal
+    (129, 400, 8, 2, 64, True, False),     # d = 64, row-major K, GQA, n_kv > n_q causal
+]
+
+
+@pytest.mark.parametrize("mode", ["x3", "fp32"])
+@pytest.mark.parametrize("shape", DENSE_SHAPES, ids=[f"q{a}k{b}h{c}g{e}d{f}{'c' if g else ''}{'kt' if h else 'rm'}"
+                                                      for a, b, c, e, f, g, h in DENSE_SHAPES])
+def test_dense_instantiations(torch, shape, mode):
+    """Each (d, K layout) instantiation of both dense kernels against f64, with partial last tiles
+    on both axes and key splits where the planner chooses them."""
+    import zwhisper_amd as z
+
+    n_q, n_kv, h, hkv, d, causal, kt = shape
+    ktw = (n_kv + 7) // 8 * 8 if kt else None
+    sh = AttnShape(n_q, n_kv, h, hkv, d, h * d, hkv * d, h * d, causal, ktw)
+    q = W.normal(61, n_q * h * d)
+    kl = W.normal(62, n_kv * hkv * d).reshape(n_kv, hkv, d)
+    v = W.normal(63, n_kv * hkv * d)
+    k = W.to_kt(kl, ktw) if kt else kl.reshape(-1)
+    ref = naive.attention_f64(q, k, v, sh)
+    with z.Context(0, dense_math=z.DENSE_X3 if mode == "x3" else z.DENSE_FP32) as c:
+        out = torch.empty(n_q * h * d, device="cuda")
+        c.attention_dev(dev(torch, q), dev(torch, k), dev(torch, v), sh, out)
+        torch.cuda.synchronize()
+        check(out.cpu().numpy(), ref, f"dense {mode} {shape}")
+
+
 def test_deterministic_and_on_a_side_stream(torch, ctx):
     sh = AttnShape(300, 1000, 6, 6, 64, 384, 384, 384, False, None)
     q, k, v = (dev(torch, W.normal(s, n)) for s, n in ((41, 300 * 384), (42, 1000 * 384), (43, 1000 * 384)))
