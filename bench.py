@@ -430,8 +430,10 @@ class EncoderLayerWorkload:
 class Q8LinearWorkload:
     """A decode step's linear layers over int8 block weights (gemm.Q8, src/gemm.zig:188-351), m rows
     (sequences or windows decoded in lockstep) per layer, with the weights resident in HBM in the
-    packed device layout (zwg_q8w_create, done once as the reference builds its Q8 at load) and
-    each layer run by zwg_linear_q8w_dev.
+    packed device layout (zwg_q8w_create, done once as the reference builds its Q8 at load).  The
+    layers that read the same x -- q/k/v, and the MLP's gate and up -- run as one
+    zwg_linear_q8w_group_dev call (`groups`: how many consecutive layers each call takes), the
+    others by zwg_linear_q8w_dev.
 
     Algorithmic bytes per step: for every layer its int8 weights (n k), f32 block scales (n k / 32 * 4),
     bias (n * 4, when it has one), the x rows read (m k * 4) and the out rows written (m n * 4): the
@@ -443,16 +445,19 @@ class Q8LinearWorkload:
     """
 
     def __init__(self, name: str, description: str, torch, ctx, m: int, layers, copies: int = 1,
-                 cpu_layers: int = 0):
+                 cpu_layers: int = 0, groups=None):
         import zwhisper_amd as z
 
         self.name, self.description = name, description
         self.torch, self.ctx, self.m = torch, ctx, m
         self.layers = layers  # (k, n, has_bias)
+        self.groups = list(groups) if groups else [1] * len(layers)
+        assert sum(self.groups) == len(layers)
         g = torch.Generator(device="cuda").manual_seed(0x0808)
         dims = sorted({k for k, _, _ in layers} | {n for _, n, _ in layers})
         self.x = {d: torch.randn(m, d, device="cuda", generator=g) for d in dims}
-        self.out = {d: torch.empty(m, d, device="cuda") for d in dims}
+        # outputs by (n, place in its call): the members of a grouped call write distinct buffers
+        self.out = {(d, j): torch.empty(m, d, device="cuda") for d in dims for j in range(max(self.groups))}
         self.sets = []
         self.raw = []  # unpacked copies of the first layers, for the CPU baseline
         for c in range(copies):
@@ -482,8 +487,16 @@ class Q8LinearWorkload:
         torch.cuda.synchronize()
 
     def _run(self, ws):
-        for (k, n, _), (w, b) in zip(self.layers, ws):
-            self.ctx.linear_q8w_dev(self.x[k], self.m, w, b, self.out[n])
+        i = 0
+        for gsize in self.groups:
+            (k, n, _), (w, b) = self.layers[i], ws[i]
+            if gsize == 1:
+                self.ctx.linear_q8w_dev(self.x[k], self.m, w, b, self.out[(n, 0)])
+            else:
+                mem = range(i, i + gsize)
+                self.ctx.linear_q8w_group_dev(self.x[k], self.m, [ws[j][0] for j in mem], [ws[j][1] for j in mem],
+                                              [self.out[(self.layers[j][1], j - i)] for j in mem])
+            i += gsize
 
     def step(self, i: int):
         self.graphs[i % len(self.graphs)].replay()
@@ -495,7 +508,7 @@ class Q8LinearWorkload:
 
         sample = self.layers[:len(self.raw)]
         xs = {d: v.cpu().numpy() for d, v in self.x.items()}
-        outs = {d: np.zeros(self.m * d, np.float32) for d in self.out}
+        outs = {d: np.zeros(self.m * d, np.float32) for d, _ in self.out}
         o = oracle.Oracle(threads)
 
         def run():
@@ -529,11 +542,13 @@ def q8_workloads(torch, ctx):
         "(src/llm.zig:214-216), int8 block weights", torch, ctx, 64, [(1536, 151936, False)], copies=2, cpu_layers=1)
     yield lambda: Q8LinearWorkload(
         "qwen15_decode_q8_linear_x64", "Qwen2.5-1.5B decode step, 64 sequences: q/k/v/o, gate/up/down of all "
-        "28 layers (196 linear calls), int8 block weights", torch, ctx, 64, qwen_layer * 28, cpu_layers=7)
+        "28 layers (196 linear layers in 112 calls: q/k/v and gate/up grouped), int8 block weights", torch, ctx, 64,
+        qwen_layer * 28, cpu_layers=7, groups=[3, 1, 2, 1] * 28)
     yield lambda: Q8LinearWorkload(
         "small_dec_q8_linear_x32", "Whisper small.en decoder step, 32 windows: q/k/v/o, cross q/o, MLP of all "
-        "12 layers and the 51864-token logits (97 linear calls), int8 block weights", torch, ctx, 32,
-        whisper_layer * 12 + [(768, 51864, False)], copies=2, cpu_layers=8)
+        "12 layers and the 51864-token logits (97 linear layers in 73 calls: q/k/v grouped), int8 block weights",
+        torch, ctx, 32, whisper_layer * 12 + [(768, 51864, False)], copies=2, cpu_layers=8,
+        groups=[3, 1, 1, 1, 1, 1] * 12 + [1])
 
 
 def time_workload(wl: Workload, steps: int, warmup: int) -> dict:

@@ -306,6 +306,18 @@ int zwg_linear_q8w_epi_dev(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q
                            uint32_t epilogue);
 
 /*
+ * Several linear layers over the same x at once: out[j] = x . w[j]^T (+ bias[j]) for n_w (1..4)
+ * resident weight sets that share k -- a decode step's q/k/v projections, or its MLP gate and up.
+ * bias may be NULL, or hold NULL entries.  For m <= 64 the sets share one x split, one
+ * weight-streaming launch and one split sum (three launches in all instead of three per set);
+ * larger m runs the sets one after another.  Results equal the single calls' to f32 rounding (the
+ * k split may differ).  No counterpart in the reference, which calls ops.linear
+ * (src/ops.zig:283-306) once per projection (src/llm.zig:179-207, src/decoder.zig:181-201).
+ */
+int zwg_linear_q8w_group_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t n_w, const zwg_q8w *const *w,
+                             const float *const *bias, float *const *out);
+
+/*
  * Row-wise and elementwise ops around the projections, device pointers, asynchronous:
  * ops.layerNormEps (src/ops.zig:388-395; ops.layerNorm is eps = 1e-5, BERT uses 1e-12):
  * out[i] = (x[i] - mean) / sqrt(var + eps) * w + b per row of x [m][n]; ops.gelu (src/ops.zig:

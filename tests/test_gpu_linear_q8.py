@@ -213,3 +213,66 @@ def test_resident_logits(torch, ctx):
     deq = (q.double().view(n, k // 32, 32) * sc.double().view(n, k // 32, 1)).view(n, k)
     err = float((out.double() - x.double() @ deq.T).abs().max())
     assert bool(torch.isfinite(out).all()) and err <= 2e-5 * np.sqrt(k)
+
+
+GROUPS = [
+    # Qwen2.5-1.5B q/k/v (src/llm.zig:179-190): biased, biased, biased; Whisper q/k/v: k unbiased
+    (1536, [(1536, True), (256, True), (256, True)]),
+    (768, [(768, True), (768, False), (768, True)]),
+    # Qwen2.5-1.5B MLP gate and up (src/llm.zig:203-205)
+    (1536, [(8960, False), (8960, False)]),
+]
+
+
+@pytest.mark.parametrize("m", [64, 17, 1, 100])
+@pytest.mark.parametrize("gi", range(len(GROUPS)))
+def test_resident_group(torch, ctx, m, gi):
+    """zwg_linear_q8w_group_dev: each output against its single call (to f32 rounding: the group's
+    k split can differ from a single call's), against f64, and the same call twice bit for bit;
+    m = 100 takes the per-set tiled path."""
+    import contextlib
+
+    k, sets = GROUPS[gi]
+    print(f"group {gi} m={m} k={k} sets={sets}", flush=True)
+    rng = np.random.default_rng(100 + gi * 7 + m)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    xd = torch.from_numpy(x).cuda()
+    qs, bs = [], []
+    for j, (n, hb) in enumerate(sets):
+        _, w, b = inputs(1000 + 13 * gi + j, 1, k, n, bias=hb)
+        qs.append(w)
+        bs.append(None if b is None else torch.from_numpy(b).cuda())
+    with contextlib.ExitStack() as stack:
+        rs = [stack.enter_context(w.resident(ctx)) for w in qs]
+        outs = [torch.full((m, w.n), float("nan"), device="cuda") for w in rs]
+        ctx.linear_q8w_group_dev(xd, m, rs, bs, outs)
+        again = [torch.full((m, w.n), float("nan"), device="cuda") for w in rs]
+        ctx.linear_q8w_group_dev(xd, m, rs, bs, again)
+        singles = []
+        for r, b in zip(rs, bs):
+            o = torch.full((m, r.n), float("nan"), device="cuda")
+            ctx.linear_q8w_dev(xd, m, r, b, o)
+            singles.append(o)
+        torch.cuda.synchronize()
+        for j, (w, b) in enumerate(zip(qs, bs)):
+            got, single = outs[j].cpu().numpy(), singles[j].cpu().numpy()
+            assert np.all(np.isfinite(got)), j
+            assert np.array_equal(got, again[j].cpu().numpy()), f"set {j}: not deterministic"
+            ref = ref64(x, w, None if b is None else b.cpu().numpy())
+            assert float(np.abs(got - ref).max()) <= 2e-5 * np.sqrt(k), f"set {j}: against f64"
+            assert float(np.abs(got - single).max()) <= 1e-6 * max(1.0, float(np.abs(single).max())), \
+                f"set {j}: against the single call"
+
+
+def test_resident_group_errors(torch, ctx):
+    import zwhisper_amd as z
+
+    _, w1, _ = inputs(1, 1, 256, 64, bias=False)
+    _, w2, _ = inputs(2, 1, 512, 64, bias=False)
+    x = torch.zeros(4 * 512, device="cuda")
+    out = [torch.zeros(4 * 64, device="cuda"), torch.zeros(4 * 64, device="cuda")]
+    with w1.resident(ctx) as r1, w2.resident(ctx) as r2:
+        with pytest.raises(z.ZwgError, match="share k"):
+            ctx.linear_q8w_group_dev(x, 4, [r1, r2], None, out)
+        with pytest.raises(z.ZwgError):
+            ctx.linear_q8w_group_dev(x, 4, [r1] * 5, None, out * 3)

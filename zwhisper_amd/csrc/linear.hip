@@ -59,13 +59,12 @@ std::string check_linear(uint64_t m, uint64_t k, uint32_t w_type, uint64_t n) {
 // the weight-streaming kernel.  Four waves of S slabs of 32 weight rows per workgroup (S = 2 when
 // that alone makes >= 256 workgroups, else 1); k is split over more workgroups, at chunk
 // granularity, until there are about 512 of them, as long as the partial sums fit the workspace.
+// (Raw-layout weights; the resident packed ones go through run_q8p_group.)
 template <int MT>
-int run_q8_stream_mt(zwg_ctx *ctx, const zwg_lin::Q8Args &base, const zwg_lin::Q8Packed *packed) {
+int run_q8_stream_mt(zwg_ctx *ctx, const zwg_lin::Q8Args &base) {
     zwg_lin::Q8Args a = base;
     const uint64_t m = (uint64_t)a.m, n = (uint64_t)a.n;
-    // the raw-layout kernel takes two slabs per wave on wide matrices; the pipelined packed kernel
-    // holds two stages of weights in registers and takes one
-    const int S = (!packed && (n + 255) / 256 >= 256) ? 2 : 1;
+    const int S = (n + 255) / 256 >= 256 ? 2 : 1;
     const int64_t gx = (int64_t)((n + 128 * S - 1) / (128 * S));
     const int n_chunks = (a.k + zwg_lin::kQ8Chunk - 1) / zwg_lin::kQ8Chunk;
     const uint64_t xcvt_bytes = (uint64_t)n_chunks * zwg_lin::q8_chunk_halves<MT>() * 2;
@@ -86,18 +85,72 @@ int run_q8_stream_mt(zwg_ctx *ctx, const zwg_lin::Q8Args &base, const zwg_lin::Q
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail_hip(ctx, "linear (int8) x preparation launch", e);
     dim3 grid((unsigned)gx, (unsigned)n_split);
-    if (packed) {
-        zwg_lin::linear_q8p_stream_kernel<MT, 1><<<grid, zwg_lin::kQ8Threads, 0, ctx->stream>>>(a, *packed, xcvt);
-    } else {
-        if (S == 2) zwg_lin::linear_q8_stream_kernel<MT, 2><<<grid, zwg_lin::kQ8Threads, 0, ctx->stream>>>(a, xcvt);
-        else zwg_lin::linear_q8_stream_kernel<MT, 1><<<grid, zwg_lin::kQ8Threads, 0, ctx->stream>>>(a, xcvt);
-    }
+    if (S == 2) zwg_lin::linear_q8_stream_kernel<MT, 2><<<grid, zwg_lin::kQ8Threads, 0, ctx->stream>>>(a, xcvt);
+    else zwg_lin::linear_q8_stream_kernel<MT, 1><<<grid, zwg_lin::kQ8Threads, 0, ctx->stream>>>(a, xcvt);
     e = hipGetLastError();
     if (e != hipSuccess) return fail_hip(ctx, "linear (int8 stream) kernel launch", e);
     if (n_split > 1) {
         const int64_t mn = (int64_t)(m * n);
         zwg_lin::linear_split_sum_kernel<<<(unsigned)((mn + 255) / 256), 256, 0, ctx->stream>>>(
             a.part, a.bias, a.out, mn, (int32_t)n, n_split, a.epi);
+        e = hipGetLastError();
+        if (e != hipSuccess) return fail_hip(ctx, "linear split-sum kernel launch", e);
+    }
+    return ZWG_OK;
+}
+
+// Resident packed weights with m <= 64, one or more weight sets over the same x (g.count sets;
+// q/scales/n_slabs/n/bias/out filled by the caller): one x split, one stream launch over every
+// set's workgroups (four slabs of 32 rows each), one split sum over every set's outputs.  The k
+// split is chosen from the group's total workgroup count, as for a single call.
+template <int MT>
+int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g) {
+    zwg_lin::Q8Args a = base;
+    const uint64_t m = (uint64_t)a.m;
+    int64_t gx = 0;
+    uint64_t n_tot = 0;
+    for (int j = 0; j < zwg_lin::kQ8MaxGroup; ++j) {
+        g.block_start[j] = (int32_t)gx;
+        g.elem_start[j] = (int64_t)(m * n_tot);
+        if (j < g.count) {
+            gx += (g.n[j] + 127) / 128;
+            n_tot += (uint64_t)g.n[j];
+        }
+    }
+    g.block_start[zwg_lin::kQ8MaxGroup] = (int32_t)gx;
+    g.elem_start[zwg_lin::kQ8MaxGroup] = (int64_t)(m * n_tot);
+    const int n_chunks = (a.k + zwg_lin::kQ8Chunk - 1) / zwg_lin::kQ8Chunk;
+    g.n_chunks = n_chunks;
+    const uint64_t xcvt_bytes = (uint64_t)n_chunks * zwg_lin::q8_chunk_halves<MT>() * 2;
+    const uint64_t part_off = (xcvt_bytes + 255) / 256 * 256;
+    if (part_off > ctx->workspace_bytes) return fail(ctx, "workspace too small for this linear call");
+    int n_split = 1;
+    if (gx < 512) n_split = (int)std::min<int64_t>(n_chunks, (512 + gx - 1) / gx);
+    while (n_split > 1 && part_off + (uint64_t)n_split * m * n_tot * 4 > ctx->workspace_bytes) --n_split;
+    a.chunks_per_split = (n_chunks + n_split - 1) / n_split;
+    n_split = (n_chunks + a.chunks_per_split - 1) / a.chunks_per_split; // no empty splits
+    a.n_split = n_split;
+    char *ws = reinterpret_cast<char *>(ctx->workspace);
+    uint64_t off = part_off;
+    for (int j = 0; j < zwg_lin::kQ8MaxGroup; ++j) {
+        g.part[j] = (j < g.count && n_split > 1) ? reinterpret_cast<float *>(ws + off) : nullptr;
+        if (j < g.count) off += (uint64_t)n_split * m * (uint64_t)g.n[j] * 4;
+    }
+    _Float16 *xcvt = reinterpret_cast<_Float16 *>(ctx->workspace);
+
+    const int64_t prep_threads = (int64_t)n_chunks * MT * 32 * (zwg_lin::kQ8Chunk / 4);
+    zwg_lin::linear_q8_xprep_kernel<MT><<<(unsigned)((prep_threads + 255) / 256), 256, 0, ctx->stream>>>(
+        a.x, xcvt, a.m, a.k, n_chunks);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail_hip(ctx, "linear (int8) x preparation launch", e);
+    dim3 grid((unsigned)gx, (unsigned)n_split);
+    zwg_lin::linear_q8p_stream_kernel<MT, 1><<<grid, zwg_lin::kQ8Threads, 0, ctx->stream>>>(a, g, xcvt);
+    e = hipGetLastError();
+    if (e != hipSuccess) return fail_hip(ctx, "linear (int8 stream) kernel launch", e);
+    if (n_split > 1) {
+        const int64_t elems = (int64_t)(m * n_tot);
+        zwg_lin::linear_split_sum_group_kernel<<<(unsigned)((elems + 255) / 256), 256, 0, ctx->stream>>>(
+            g, a.m, n_split, a.epi);
         e = hipGetLastError();
         if (e != hipSuccess) return fail_hip(ctx, "linear split-sum kernel launch", e);
     }
@@ -117,7 +170,7 @@ int run_q8_stream(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const in
     a.n = (int32_t)n;
     a.k = (int32_t)k;
     a.nb = (int32_t)(k / zwg_lin::kQ8Block);
-    return m > 32 ? run_q8_stream_mt<2>(ctx, a, nullptr) : run_q8_stream_mt<1>(ctx, a, nullptr);
+    return m > 32 ? run_q8_stream_mt<2>(ctx, a) : run_q8_stream_mt<1>(ctx, a);
 }
 
 int run_linear(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void *w, uint32_t w_type,
@@ -201,6 +254,29 @@ struct zwg_q8w {
 
 namespace {
 
+// The token-step path (m <= 64) over n_w resident weight sets sharing x and k (checked by the
+// callers).
+int run_q8w_token_step(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t n_w, const zwg_q8w *const *w,
+                       const float *const *bias, float *const *out, uint32_t epi) {
+    zwg_lin::Q8Args a{};
+    a.x = x;
+    a.m = (int32_t)m;
+    a.k = (int32_t)w[0]->k;
+    a.nb = (int32_t)(w[0]->k / zwg_lin::kQ8Block);
+    a.epi = epi;
+    zwg_lin::Q8Group g{};
+    g.count = (int32_t)n_w;
+    for (uint32_t j = 0; j < n_w; ++j) {
+        g.q[j] = w[j]->q;
+        g.scales[j] = w[j]->scales;
+        g.n_slabs[j] = w[j]->n_slabs;
+        g.n[j] = (int32_t)w[j]->n;
+        g.bias[j] = bias ? bias[j] : nullptr;
+        g.out[j] = out[j];
+    }
+    return m > 32 ? run_q8p_group<2>(ctx, a, g) : run_q8p_group<1>(ctx, a, g);
+}
+
 int run_linear_q8w(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, const float *bias, float *out,
                    uint32_t epi) {
     if (!w) return fail(ctx, "null weights");
@@ -213,19 +289,7 @@ int run_linear_q8w(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, c
     if (!al16(x) || !al16(out)) return fail(ctx, "x and out must be 16-byte aligned");
     hipError_t e = hipSetDevice(ctx->device);
     if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
-    const zwg_lin::Q8Packed p{w->q, w->scales, w->n_slabs, w->n_chunks};
-    if (m <= 64) {
-        zwg_lin::Q8Args a{};
-        a.x = x;
-        a.bias = bias;
-        a.out = out;
-        a.m = (int32_t)m;
-        a.n = (int32_t)w->n;
-        a.k = (int32_t)w->k;
-        a.nb = (int32_t)(w->k / zwg_lin::kQ8Block);
-        a.epi = epi;
-        return m > 32 ? run_q8_stream_mt<2>(ctx, a, &p) : run_q8_stream_mt<1>(ctx, a, &p);
-    }
+    if (m <= 64) return run_q8w_token_step(ctx, x, m, 1, &w, &bias, &out, epi);
     LinearArgs a{};
     a.x = x;
     a.w = w->q;
@@ -333,6 +397,33 @@ int zwg_linear_q8w_epi_dev(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q
                            uint32_t epilogue) {
     if (!ctx) return fail(nullptr, "null context");
     return run_linear_q8w(ctx, x, m, w, bias, out, epilogue);
+}
+
+int zwg_linear_q8w_group_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t n_w, const zwg_q8w *const *w,
+                             const float *const *bias, float *const *out) {
+    if (!ctx) return fail(nullptr, "null context");
+    if (n_w == 0 || n_w > (uint32_t)zwg_lin::kQ8MaxGroup) return fail(ctx, "n_w must be 1..4");
+    if (!w || !out) return fail(ctx, "null weight or output array");
+    const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    for (uint32_t j = 0; j < n_w; ++j) {
+        if (!w[j]) return fail(ctx, "null weights");
+        if (w[j]->k != w[0]->k) return fail(ctx, "the weights of a group must share k");
+        const std::string msg = check_linear(m, w[j]->k, ZWG_W_Q8, w[j]->n);
+        if (!msg.empty()) return fail(ctx, msg);
+        if (m && (!out[j] || !al16(out[j]))) return fail(ctx, "outputs must be non-null and 16-byte aligned");
+    }
+    if (m == 0) return ZWG_OK;
+    if (!x || !al16(x)) return fail(ctx, "x must be non-null and 16-byte aligned");
+    if (m > 64) { // prefill sizes: the tiled kernel, one call per set
+        for (uint32_t j = 0; j < n_w; ++j) {
+            const int r = run_linear_q8w(ctx, x, m, w[j], bias ? bias[j] : nullptr, out[j], zwg_ew::kEpiNone);
+            if (r != ZWG_OK) return r;
+        }
+        return ZWG_OK;
+    }
+    const hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
+    return run_q8w_token_step(ctx, x, m, n_w, w, bias, out, zwg_ew::kEpiNone);
 }
 
 int zwg_linear_epi_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void *w, uint32_t w_type,

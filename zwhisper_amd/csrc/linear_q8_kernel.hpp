@@ -240,6 +240,46 @@ struct Q8Packed {
     int32_t n_slabs, n_chunks;
 };
 
+// Weight sets of one token-step launch over the same x (a decode step's q/k/v, or gate/up): set j
+// takes workgroups block_start[j] .. block_start[j + 1] - 1 of the stream kernel and elements
+// elem_start[j] .. elem_start[j + 1] - 1 of the split sum; all sets share x, k and the k split.
+constexpr int kQ8MaxGroup = 4;
+struct Q8Group {
+    int32_t count;
+    int32_t n_chunks; // k / 256, rounded up: the same for every set
+    int32_t block_start[kQ8MaxGroup + 1];
+    int64_t elem_start[kQ8MaxGroup + 1];
+    const uint8_t *q[kQ8MaxGroup]; // packed weights of set j (Q8Packed)
+    const float *scales[kQ8MaxGroup];
+    int32_t n_slabs[kQ8MaxGroup];
+    int32_t n[kQ8MaxGroup];
+    const float *bias[kQ8MaxGroup];
+    float *out[kQ8MaxGroup];
+    float *part[kQ8MaxGroup]; // [n_split][m][n[j]] when the call is split
+};
+
+// entry j of a group field, by selects on the uniform j (no dynamic indexing of the kernel-
+// argument struct, which would go through scratch)
+template <typename T, int N>
+__device__ __forceinline__ T q8_pick(const T (&v)[N], int j) {
+    T r = v[0];
+#pragma unroll
+    for (int i = 1; i < N; ++i) r = j == i ? v[i] : r;
+    return r;
+}
+__device__ __forceinline__ int q8_group_of_block(const Q8Group &g, int bx) {
+    int j = 0;
+#pragma unroll
+    for (int i = 1; i < kQ8MaxGroup; ++i) j += (i < g.count && bx >= g.block_start[i]) ? 1 : 0;
+    return j;
+}
+__device__ __forceinline__ int q8_group_of_elem(const Q8Group &g, int64_t e) {
+    int j = 0;
+#pragma unroll
+    for (int i = 1; i < kQ8MaxGroup; ++i) j += (i < g.count && e >= g.elem_start[i]) ? 1 : 0;
+    return j;
+}
+
 __host__ __device__ inline int64_t q8p_q_bytes(int64_t n_slabs, int64_t n_chunks) {
     return n_slabs * n_chunks * kQ8ChunkBlocks * 1024;
 }
@@ -290,7 +330,7 @@ __global__ __launch_bounds__(256) void linear_q8_pack_kernel(const int8_t *q, co
 constexpr int kQ8StageBlocks = 4;
 
 template <int MT, int S>
-__global__ __launch_bounds__(kQ8Threads) void linear_q8p_stream_kernel(Q8Args a, Q8Packed w, const _Float16 *xcvt) {
+__global__ __launch_bounds__(kQ8Threads) void linear_q8p_stream_kernel(Q8Args a, Q8Group grp, const _Float16 *xcvt) {
     constexpr int NB = kQ8StageBlocks;
     constexpr int SLABS = 4 * S;                  // slabs of 32 weight rows per workgroup
     constexpr int PIECES = NB * MT * 4;           // 1 KB pieces of an x stage
@@ -298,10 +338,19 @@ __global__ __launch_bounds__(kQ8Threads) void linear_q8p_stream_kernel(Q8Args a,
     constexpr int STAGE_HALVES = PIECES * 512;
     __shared__ __align__(16) _Float16 xs[2][STAGE_HALVES];
 
+    // this workgroup's weight set and its index within the set
+    const int set = q8_group_of_block(grp, (int)blockIdx.x);
+    const int bx = (int)blockIdx.x - q8_pick(grp.block_start, set);
+    const Q8Packed w = {q8_pick(grp.q, set), q8_pick(grp.scales, set), q8_pick(grp.n_slabs, set), grp.n_chunks};
+    a.n = q8_pick(grp.n, set);
+    a.bias = q8_pick(grp.bias, set);
+    a.out = q8_pick(grp.out, set);
+    a.part = q8_pick(grp.part, set);
+
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // uniform: the LDS DMA base is per wave
     const int r32 = lane & 31, g = lane >> 5;
-    const int slab0 = blockIdx.x * SLABS + wave * S; // this wave's first slab
+    const int slab0 = bx * SLABS + wave * S; // this wave's first slab
     const int split = blockIdx.y;
     const int n_stages = (a.k + NB * kQ8Block - 1) / (NB * kQ8Block);
     const int t_begin = split * a.chunks_per_split * 2;
@@ -434,6 +483,24 @@ __global__ __launch_bounds__(256) void linear_split_sum_kernel(const float *part
     for (int p = 1; p < n_split; ++p) s += part[(int64_t)p * mn + e];
     if (bias) s += bias[e % n];
     zwg_ew::epilogue_store(&out[e], s, epi);
+}
+
+// The split sum over a group: element e of the concatenated outputs is element e - elem_start[j]
+// of set j, summed over the splits in split order, + bias, through the epilogue.
+__global__ __launch_bounds__(256) void linear_split_sum_group_kernel(Q8Group grp, int32_t m, int32_t n_split,
+                                                                    uint32_t epi) {
+    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (e >= grp.elem_start[kQ8MaxGroup]) return;
+    const int set = q8_group_of_elem(grp, e);
+    const int64_t le = e - q8_pick(grp.elem_start, set);
+    const int32_t n = q8_pick(grp.n, set);
+    const int64_t mn = (int64_t)m * n;
+    const float *part = q8_pick(grp.part, set);
+    const float *bias = q8_pick(grp.bias, set);
+    float s = part[le];
+    for (int p = 1; p < n_split; ++p) s += part[(int64_t)p * mn + le];
+    if (bias) s += bias[le % n];
+    zwg_ew::epilogue_store(&q8_pick(grp.out, set)[le], s, epi);
 }
 
 } // namespace zwg_lin

@@ -215,6 +215,27 @@ class Context:
         self._check(self._L.zwg_linear_q8w_dev(self._h, self._dev_ptr(x, "x"), m, w.handle,
                                                self._dev_ptr(bias, "bias"), self._dev_ptr(out, "out")))
 
+    def linear_q8w_group_dev(self, x, m: int, ws, biases, outs) -> None:
+        """outs[j][m][ws[j].n] = x[m][k] . ws[j]^T (+ biases[j]) for up to four resident weight sets
+        sharing k, in one x split, stream launch and split sum (zwg_linear_q8w_group_dev)."""
+        n_w = len(ws)
+        if not 1 <= n_w <= 4 or len(outs) != n_w or (biases is not None and len(biases) != n_w):
+            raise ZwgError("one to four weight sets, with as many outputs (and biases)")
+        for w, out in zip(ws, outs):
+            if not isinstance(w, Q8Resident):
+                raise ZwgError("weights must be Q8Resident (Q8.resident)")
+            if x.numel() < m * w.k or out.numel() < m * w.n:
+                raise ZwgError("a tensor is shorter than m, n and k need")
+        bias_list = list(biases) if biases is not None else [None] * n_w
+        for w, b in zip(ws, bias_list):
+            if b is not None and b.numel() < w.n:
+                raise ZwgError("a bias is shorter than n")
+        self._bind_torch_stream()
+        wa = (ctypes.c_void_p * n_w)(*[w.handle for w in ws])
+        ba = (_lib._fp * n_w)(*[self._dev_ptr(b, "bias") for b in bias_list])
+        oa = (_lib._fp * n_w)(*[self._dev_ptr(o, "out") for o in outs])
+        self._check(self._L.zwg_linear_q8w_group_dev(self._h, self._dev_ptr(x, "x"), m, n_w, wa, ba, oa))
+
     def linear_epi_dev(self, x, m: int, k: int, w, bias, n: int, out, epilogue: int, out_stride: int = 0) -> None:
         """linear_dev with an epilogue (_lib.EPI_NONE / EPI_GELU / EPI_ADD) and an output row stride."""
         import torch
