@@ -571,15 +571,19 @@ def time_workload(wl: Workload, steps: int, warmup: int) -> dict:
             "kernel_ms_min": float(np.min(kms)), "kernel_ms_median": float(np.median(kms))}
 
 
-def cpu_baseline(number: int, threads: int) -> dict:
-    """The oracle (C restatement of ops.attentionEx + Pool) on a bounded sample of the workload."""
+def cpu_baseline(number: int, threads: int, decode_pool: bool = True) -> dict:
+    """The oracle (C restatement of ops.attentionEx + Pool) on a bounded sample of the workload.
+
+    Decode workloads run on min(threads, 4) threads, the reference's decode pool (pool_dec,
+    src/transcribe.zig:106, src/llm.zig:151), unless decode_pool is False (all threads: the
+    stronger baseline)."""
     import oracle
     from zwhisper_amd import workloads as W
     from zwhisper_amd.ops import AttnShape
 
     w = W.WORKLOADS[number]
-    if number in (3, 5):
-        threads = min(threads, 4)  # the decode pool, pool_dec (src/transcribe.zig:106, src/llm.zig:151)
+    if number in (3, 5) and decode_pool:
+        threads = min(threads, 4)
     o = oracle.Oracle(threads)
     calls = []  # (q, k, v, shape) of the sample
     if number in (1, 2):
@@ -740,6 +744,8 @@ def main() -> int:
                "dtype": DENSE_DTYPE if spec.bound == "mfma" else "f32", "roofline": roof}
         if not args.no_cpu:
             res["cpu_baseline"] = cpu_baseline(n, host_threads())
+            if n in (3, 5):
+                res["cpu_baseline_all_threads"] = cpu_baseline(n, host_threads(), decode_pool=False)
         results[n] = res
         print(f"[bench] {spec.name}: {value:.2f} {unit} ({r['ms_per_step']:.4f} ms/step, kernel "
               f"{r['kernel_ms_mean']:.4f} ms, {100 * roof['frac']:.1f}% of {spec.bound} peak)"
@@ -874,6 +880,7 @@ def main() -> int:
                    "k_layout": "transposed" if spec.kt else "row-major", "parallelism": "single GPU"},
         "roofline": head["roofline"],
         "cpu_baseline": head.get("cpu_baseline"),
+        **({"cpu_baseline_all_threads": head["cpu_baseline_all_threads"]} if "cpu_baseline_all_threads" in head else {}),
         "workloads": {r["workload"]: {k: v for k, v in r.items() if k not in ("workload",)}
                       for n, r in results.items() if n != args.workload},
     }
