@@ -3,7 +3,7 @@
  *
  * It replaces the bodies of zwhisper's `ops.attentionEx` (src/ops.zig:562-590) and
  * `ops.attention` (src/ops.zig:593-605).  Those Zig functions keep their signatures; their
- * bodies call the entry points below (the Zig binding is spelt out in INTEGRATION.md).
+ * bodies call the entry points below through a small Zig binding of this header.
  * The whisper C ABI (include/zwhisper.h) is untouched: attention is internal to it.
  *
  * Conventions (those of include/zwhisper.h:34-42):

@@ -1,6 +1,6 @@
 """GPU parity: the HIP path (through the C ABI) against the f64 closed form and the CPU oracle.
 
-Tolerance for every output (f32 attention): max |gpu - ref| <= 2e-4 and
+Tolerance for every output (the f32 attention bar): max |gpu - ref| <= 2e-4 and
 normwise relative error ||gpu - ref||_inf / ||ref||_inf <= 1e-3.  Columns a call must not write
 (row gaps when out_stride > n_head * d) must keep their previous contents.
 """
