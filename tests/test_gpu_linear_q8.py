@@ -221,10 +221,12 @@ GROUPS = [
     (768, [(768, True), (768, False), (768, True)]),
     # Qwen2.5-1.5B MLP gate and up (src/llm.zig:203-205)
     (1536, [(8960, False), (8960, False)]),
+    # four sets, none a multiple of 128 rows, mixed biases
+    (544, [(130, True), (33, False), (257, True), (96, False)]),
 ]
 
 
-@pytest.mark.parametrize("m", [64, 17, 1, 100])
+@pytest.mark.parametrize("m", [64, 33, 17, 1, 100])
 @pytest.mark.parametrize("gi", range(len(GROUPS)))
 def test_resident_group(torch, ctx, m, gi):
     """zwg_linear_q8w_group_dev: each output against its single call (to f32 rounding: the group's
