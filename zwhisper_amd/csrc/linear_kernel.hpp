@@ -91,6 +91,16 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, uint32_
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
 }
 
+// MI355X deals consecutive workgroups round-robin over its 8 XCDs, each with its own L2.  The
+// tiles of a call are numbered so that each XCD runs one contiguous range of logical tiles,
+// column tiles fastest: the tiles that read the same rows of x run together on one XCD and share
+// its L2 instead of each fetching those rows from the fabric.
+__device__ __forceinline__ int64_t xcd_logical_tile(int64_t hw, int64_t n) {
+    constexpr int X = 8;
+    const int64_t xcd = hw % X, local = hw / X, q = n / X, r = n % X;
+    return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+}
+
 // half index of (row, 8-half chunk) in a swizzled LDS tile
 __device__ __forceinline__ int lds_at(int row, int chunk) { return row * BK + ((chunk ^ ((row ^ (row >> 2)) & 3)) << 3); }
 
@@ -114,7 +124,9 @@ __global__ __launch_bounds__(kThreads) void linear_mfma_kernel(LinearArgs a) {
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.x * BM, n0 = blockIdx.y * BN;
+    const int n_col_tiles = (a.n + BN - 1) / BN;
+    const int64_t tile = xcd_logical_tile(blockIdx.x, gridDim.x);
+    const int m0 = (int)(tile / n_col_tiles) * BM, n0 = (int)(tile % n_col_tiles) * BN;
     const int r32 = lane & 31, ch = lane >> 5;
 
     const int rows_x = min(BM, a.m - m0), rows_w = min(BN, a.n - n0);
@@ -307,8 +319,9 @@ __global__ __launch_bounds__(kThreads) void linear_mfma_kernel(LinearArgs a) {
 
 template <int BM, int BN, int WMODE>
 inline hipError_t launch_linear_tile(const LinearArgs &a, hipStream_t stream) {
-    dim3 grid((unsigned)((a.m + BM - 1) / BM), (unsigned)((a.n + BN - 1) / BN));
-    linear_mfma_kernel<BM, BN, WMODE><<<grid, kThreads, 0, stream>>>(a);
+    const int64_t tiles = (int64_t)((a.m + BM - 1) / BM) * ((a.n + BN - 1) / BN);
+    if (tiles > 0x7fffffffll) return hipErrorInvalidValue;
+    linear_mfma_kernel<BM, BN, WMODE><<<dim3((unsigned)tiles), kThreads, 0, stream>>>(a);
     return hipGetLastError();
 }
 
