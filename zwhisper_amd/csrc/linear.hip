@@ -33,15 +33,18 @@ int64_t tiles(uint64_t m, uint64_t n, int bm, int bn) { return (int64_t)((m + bm
 // 128 x 256 tile when it gives two workgroups per CU (256 CUs), else 64 x 256 when that fills
 // the CUs once, else 64 x 64 for the small single-window shapes, which are latency bound.  Int8
 // weights take 128 x 128 in place of 128 x 256: the block sums need 16 more VGPRs per tile row,
-// which would leave the larger tile one wave per SIMD.
+// which would leave the larger tile one wave per SIMD.  The x 256 tiles run 8 waves (2 x 4):
+// half the accumulators and staging registers per wave (76 and 124 VGPRs against 141 and 235),
+// so LDS rather than registers sets the occupancy -- twice the waves per SIMD, which hides more
+// of the per-stage load latency (measured 6-7% on the base.en projections and layer).
 template <int WMODE>
 hipError_t launch_tiled(const LinearArgs &a, hipStream_t stream) {
     if constexpr (WMODE != zwg_lin::kWF16) {
         if (tiles(a.m, a.n, 128, 128) >= 512) return zwg_lin::launch_linear_tile<128, 128, WMODE>(a, stream);
     } else {
-        if (tiles(a.m, a.n, 128, 256) >= 512) return zwg_lin::launch_linear_tile<128, 256, WMODE>(a, stream);
+        if (tiles(a.m, a.n, 128, 256) >= 512) return zwg_lin::launch_linear_tile<128, 256, WMODE, 4>(a, stream);
     }
-    if (tiles(a.m, a.n, 64, 256) >= 256) return zwg_lin::launch_linear_tile<64, 256, WMODE>(a, stream);
+    if (tiles(a.m, a.n, 64, 256) >= 256) return zwg_lin::launch_linear_tile<64, 256, WMODE, 4>(a, stream);
     return zwg_lin::launch_linear_tile<64, 64, WMODE>(a, stream);
 }
 

@@ -47,7 +47,6 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256;
 constexpr int BK = 32;                 // K per LDS stage: one 64-byte LDS row
 constexpr uint32_t kOutOfRange = 0x80000000u; // a buffer offset past every range the host allows
 
@@ -104,10 +103,12 @@ __device__ __forceinline__ int64_t xcd_logical_tile(int64_t hw, int64_t n) {
 // half index of (row, 8-half chunk) in a swizzled LDS tile
 __device__ __forceinline__ int lds_at(int row, int chunk) { return row * BK + ((chunk ^ ((row ^ (row >> 2)) & 3)) << 3); }
 
-template <int BM, int BN, int WMODE>
-__global__ __launch_bounds__(kThreads) void linear_mfma_kernel(LinearArgs a) {
+template <int BM, int BN, int WMODE, int NWN = 2>
+__global__ __launch_bounds__(128 * NWN) void linear_mfma_kernel(LinearArgs a) {
+    // 2 x NWN waves, each a (BM / 2) x (BN / NWN) block of the tile
+    constexpr int kThreads = 128 * NWN;
     constexpr bool Q8 = WMODE != kWF16;
-    constexpr int WM = BM / 2, WN = BN / 2;   // per wave
+    constexpr int WM = BM / 2, WN = BN / NWN; // per wave
     constexpr int TM = WM / 32, TN = WN / 32; // 32 x 32 MFMA tiles per wave
     constexpr int XL = BM * BK / 4 / kThreads; // float4 loads of x per thread per stage
     // 16-byte loads of w per stage: 8 halves (f16) or 16 int8 (Q8) each
@@ -123,7 +124,7 @@ __global__ __launch_bounds__(kThreads) void linear_mfma_kernel(LinearArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / NWN, wn = wave % NWN;
     const int n_col_tiles = (a.n + BN - 1) / BN;
     const int64_t tile = xcd_logical_tile(blockIdx.x, gridDim.x);
     const int m0 = (int)(tile / n_col_tiles) * BM, n0 = (int)(tile % n_col_tiles) * BN;
@@ -317,11 +318,11 @@ __global__ __launch_bounds__(kThreads) void linear_mfma_kernel(LinearArgs a) {
     }
 }
 
-template <int BM, int BN, int WMODE>
+template <int BM, int BN, int WMODE, int NWN = 2>
 inline hipError_t launch_linear_tile(const LinearArgs &a, hipStream_t stream) {
     const int64_t tiles = (int64_t)((a.m + BM - 1) / BM) * ((a.n + BN - 1) / BN);
     if (tiles > 0x7fffffffll) return hipErrorInvalidValue;
-    linear_mfma_kernel<BM, BN, WMODE><<<dim3((unsigned)tiles), kThreads, 0, stream>>>(a);
+    linear_mfma_kernel<BM, BN, WMODE, NWN><<<dim3((unsigned)tiles), 128 * NWN, 0, stream>>>(a);
     return hipGetLastError();
 }
 
