@@ -106,6 +106,13 @@ int run_q8_stream_mt(zwg_ctx *ctx, const zwg_lin::Q8Args &base) {
 // q/scales/n_slabs/n/bias/out filled by the caller): one x split, one stream launch over every
 // set's workgroups (four slabs of 32 rows each), one split sum over every set's outputs.  The k
 // split is chosen from the group's total workgroup count, as for a single call.
+#ifndef ZWG_Q8P_WAVES
+#define ZWG_Q8P_WAVES 4
+#endif
+// waves (one 32-row slab each) sharing each x stage of the packed stream kernel (8 measured
+// 5-9% slower on the logits and decode-step workloads: half the workgroups, longer tails)
+constexpr int kQ8pWaves = ZWG_Q8P_WAVES;
+
 template <int MT>
 int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g) {
     zwg_lin::Q8Args a = base;
@@ -116,7 +123,7 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g)
         g.block_start[j] = (int32_t)gx;
         g.elem_start[j] = (int64_t)(m * n_tot);
         if (j < g.count) {
-            gx += (g.n[j] + 127) / 128;
+            gx += (g.n[j] + 32 * kQ8pWaves - 1) / (32 * kQ8pWaves);
             n_tot += (uint64_t)g.n[j];
         }
     }
@@ -147,7 +154,7 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g)
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail_hip(ctx, "linear (int8) x preparation launch", e);
     dim3 grid((unsigned)gx, (unsigned)n_split);
-    zwg_lin::linear_q8p_stream_kernel<MT, 1><<<grid, zwg_lin::kQ8Threads, 0, ctx->stream>>>(a, g, xcvt);
+    zwg_lin::linear_q8p_stream_kernel<MT, 1, kQ8pWaves><<<grid, 64 * kQ8pWaves, 0, ctx->stream>>>(a, g, xcvt);
     e = hipGetLastError();
     if (e != hipSuccess) return fail_hip(ctx, "linear (int8 stream) kernel launch", e);
     if (n_split > 1) {

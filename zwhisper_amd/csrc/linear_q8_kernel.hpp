@@ -329,12 +329,13 @@ __global__ __launch_bounds__(256) void linear_q8_pack_kernel(const int8_t *q, co
 // Padding blocks (k is padded to 256) have scale 0 and x 0; a stage wholly past k is not run.
 constexpr int kQ8StageBlocks = 4;
 
-template <int MT, int S>
-__global__ __launch_bounds__(kQ8Threads) void linear_q8p_stream_kernel(Q8Args a, Q8Group grp, const _Float16 *xcvt) {
+template <int MT, int S, int NW>
+__global__ __launch_bounds__(64 * NW) void linear_q8p_stream_kernel(Q8Args a, Q8Group grp, const _Float16 *xcvt) {
     constexpr int NB = kQ8StageBlocks;
-    constexpr int SLABS = 4 * S;                  // slabs of 32 weight rows per workgroup
+    constexpr int SLABS = NW * S;                 // slabs of 32 weight rows per workgroup (NW waves)
     constexpr int PIECES = NB * MT * 4;           // 1 KB pieces of an x stage
-    constexpr int XL = PIECES / 4;                // pieces each wave copies
+    constexpr int XL = PIECES / NW;               // pieces each wave copies
+    static_assert(PIECES % NW == 0, "every wave copies whole pieces of the x stage");
     constexpr int STAGE_HALVES = PIECES * 512;
     __shared__ __align__(16) _Float16 xs[2][STAGE_HALVES];
 
@@ -373,7 +374,7 @@ __global__ __launch_bounds__(kQ8Threads) void linear_q8p_stream_kernel(Q8Args a,
         const bool live_t = t < t_end;
 #pragma unroll
         for (int u = 0; u < XL; ++u) {
-            const int piece = wave + 4 * u;
+            const int piece = wave + NW * u;
             const uint32_t off = live_t ? (uint32_t)((t * PIECES + piece) * 1024 + lane * 16) : kOutOfRange;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
                 x_src, (__attribute__((address_space(3))) void *)(&xs[buf][piece * 512]), 16, off, 0, 0, 0);
