@@ -278,6 +278,37 @@ def test_dense_instantiations(torch, shape, mode):
         check(out.cpu().numpy(), ref, f"dense {mode} {shape}")
 
 
+def test_x3_key_range(torch):
+    """The x3 dense mode's documented range condition: a key of magnitude >= 65504 (beyond f16)
+    gives NaN in exactly the rows that see it -- never a wrong finite value -- while rows the
+    causal mask hides it from are unaffected; the fp32 mode handles it exactly."""
+    import zwhisper_amd as z
+
+    n_q = n_kv = 96
+    h, d = 2, 64
+    sh = AttnShape(n_q, n_kv, h, h, d, h * d, h * d, h * d, True, None)
+    q = W.normal(71, n_q * h * d) * 0.01  # small q: the scores stay moderate even with the big key
+    k = W.normal(72, n_kv * h * d).reshape(n_kv, h * d)
+    v = W.normal(73, n_kv * h * d)
+    big = 50                       # key row 50, head 0, one dim
+    k[big, 3] = 1.0e5
+    k = k.reshape(-1)
+    ref = naive.attention_f64(q, k, v, sh).reshape(n_q, h * d)
+    outs = {}
+    for mode in (z.DENSE_X3, z.DENSE_FP32):
+        with z.Context(0, dense_math=mode) as c:
+            out = torch.empty(n_q * h * d, device="cuda")
+            c.attention_dev(dev(torch, q), dev(torch, k), dev(torch, v), sh, out)
+            torch.cuda.synchronize()
+            outs[mode] = out.cpu().numpy().reshape(n_q, h * d)
+    x3, f32 = outs[z.DENSE_X3], outs[z.DENSE_FP32]
+    check(f32, ref, "fp32 mode with a key of 1e5")
+    # causal: query i sees keys <= i, so rows < 50 never see the big key
+    check(x3[:big, :d], ref[:big, :d], "x3 rows before the big key, head 0")
+    check(x3[:, d:], ref[:, d:], "x3 head 1 (no big key)")
+    assert np.all(np.isnan(x3[big:, :d])), "x3 rows that see the big key must be NaN"
+
+
 def test_deterministic_and_on_a_side_stream(torch, ctx):
     sh = AttnShape(300, 1000, 6, 6, 64, 384, 384, 384, False, None)
     q, k, v = (dev(torch, W.normal(s, n)) for s, n in ((41, 300 * 384), (42, 1000 * 384), (43, 1000 * 384)))
