@@ -96,10 +96,11 @@ def test_add(torch, ctx):
     assert np.array_equal(t.cpu().numpy(), x + y)
 
 
-@pytest.mark.parametrize("m,k,n", [(1500, 384, 1536), (300, 512, 512), (7, 64, 40)])
+@pytest.mark.parametrize("m,k,n", [(1500, 384, 1536), (300, 512, 512), (7, 64, 40), (200, 2048, 512)])
 def test_linear_epilogues_exact(torch, ctx, m, k, n):
     """GELU and ADD epilogues equal the plain GEMM followed by zwg_gelu_dev / zwg_add_dev bit for bit,
-    and the output stride writes into a wider buffer without touching the other columns."""
+    and the output stride writes into a wider buffer without touching the other columns; the last
+    two shapes split k, so the split sum's epilogue and stride are the ones checked."""
     from zwhisper_amd import _lib
 
     rng = np.random.default_rng(m)
@@ -125,9 +126,11 @@ def test_linear_epilogues_exact(torch, ctx, m, k, n):
     assert bool((wide[:, :n] == 7.0).all()) and bool((wide[:, 2 * n:] == 7.0).all())
 
 
-@pytest.mark.parametrize("m,k,n", [(32, 768, 3072), (64, 1536, 256), (64, 8960, 1536), (300, 768, 768)])
+@pytest.mark.parametrize("m,k,n", [(32, 768, 3072), (64, 1536, 256), (64, 8960, 1536), (300, 768, 768),
+                                   (256, 4864, 896)])
 def test_q8_epilogues_exact(torch, ctx, m, k, n):
-    """The same for resident int8 weights: the token-step kernel, its k-split sum, and the tiled kernel."""
+    """The same for resident int8 weights: the token-step kernel, its k-split sum, and the tiled kernel
+    with and without its own k split."""
     import zwhisper_amd as z
     from zwhisper_amd import _lib
 

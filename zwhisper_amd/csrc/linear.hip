@@ -37,15 +37,77 @@ int64_t tiles(uint64_t m, uint64_t n, int bm, int bn) { return (int64_t)((m + bm
 // half the accumulators and staging registers per wave (76 and 124 VGPRs against 141 and 235),
 // so LDS rather than registers sets the occupancy -- twice the waves per SIMD, which hides more
 // of the per-stage load latency (measured 6-7% on the base.en projections and layer).
-template <int WMODE>
-hipError_t launch_tiled(const LinearArgs &a, hipStream_t stream) {
-    if constexpr (WMODE != zwg_lin::kWF16) {
-        if (tiles(a.m, a.n, 128, 128) >= 512) return zwg_lin::launch_linear_tile<128, 128, WMODE>(a, stream);
+// The split sum of n_split partial products part[s][m][n] into out (row stride ldo)
+hipError_t launch_split_sum(const float *part, const float *bias, float *out, int64_t mn, int32_t n, int n_split,
+                            uint32_t epi, int64_t ldo, hipStream_t stream) {
+    if (n % 4 == 0 && (reinterpret_cast<uintptr_t>(part) & 15) == 0) {
+        const int64_t threads = mn / 4;
+        zwg_lin::linear_split_sum_kernel<4><<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(
+            part, bias, out, mn, n, n_split, epi, ldo);
     } else {
-        if (tiles(a.m, a.n, 128, 256) >= 512) return zwg_lin::launch_linear_tile<128, 256, WMODE, 4>(a, stream);
+        zwg_lin::linear_split_sum_kernel<1><<<(unsigned)((mn + 255) / 256), 256, 0, stream>>>(
+            part, bias, out, mn, n, n_split, epi, ldo);
     }
-    if (tiles(a.m, a.n, 64, 256) >= 256) return zwg_lin::launch_linear_tile<64, 256, WMODE, 4>(a, stream);
-    return zwg_lin::launch_linear_tile<64, 64, WMODE>(a, stream);
+    return hipGetLastError();
+}
+
+struct TileChoice {
+    int bm, bn;
+};
+template <int WMODE>
+TileChoice choose_tile(uint64_t m, uint64_t n) {
+    if constexpr (WMODE != zwg_lin::kWF16) {
+        if (tiles(m, n, 128, 128) >= 512) return {128, 128};
+    } else {
+        if (tiles(m, n, 128, 256) >= 512) return {128, 256};
+    }
+    if (tiles(m, n, 64, 256) >= 256) return {64, 256};
+    return {64, 64};
+}
+
+template <int WMODE>
+hipError_t launch_tiled(const LinearArgs &a, TileChoice tc, int n_split, hipStream_t stream) {
+    if constexpr (WMODE != zwg_lin::kWF16) {
+        if (tc.bm == 128) return zwg_lin::launch_linear_tile<128, 128, WMODE>(a, n_split, stream);
+    } else {
+        if (tc.bm == 128) return zwg_lin::launch_linear_tile<128, 256, WMODE, 4>(a, n_split, stream);
+    }
+    if (tc.bn == 256) return zwg_lin::launch_linear_tile<64, 256, WMODE, 4>(a, n_split, stream);
+    if (n_split > 1) return zwg_lin::launch_linear_tile<64, 64, WMODE, 2, true>(a, n_split, stream);
+    return zwg_lin::launch_linear_tile<64, 64, WMODE>(a, n_split, stream);
+}
+
+// A call with fewer tiles than two per CU and a long k (prefill batches of a few hundred rows
+// through a wide MLP, single windows) splits k over more workgroups, about 512 in all, as long as
+// the partial sums fit the workspace; a second kernel adds the splits in a fixed order, so results
+// stay deterministic.  Each split keeps at least 16 stages of 32 (8 below 64 tiles, where the
+// fill gained outweighs everything): shorter splits measured slower than none, the partials'
+// round trip and second launch costing more than the extra workgroups hide.  Only 64 x 64 tiles
+// split (a wider tile is chosen only when there would be 1024 or more 64 x 64 tiles, twice what a
+// split aims for), and the split kernel is an instantiation of its own, so the unsplit one is
+// compiled exactly as without it.
+template <int WMODE>
+int run_tiled(zwg_ctx *ctx, LinearArgs a) {
+    const TileChoice tc = choose_tile<WMODE>((uint64_t)a.m, (uint64_t)a.n);
+    const int64_t n_tiles = tiles((uint64_t)a.m, (uint64_t)a.n, tc.bm, tc.bn);
+    const int stages = (a.k + zwg_lin::BK - 1) / zwg_lin::BK;
+    const uint64_t mn = (uint64_t)a.m * (uint64_t)a.n;
+    int n_split = 1;
+    if (tc.bn == 64 && n_tiles < 512 && stages >= 16) {
+        n_split = (int)std::min<int64_t>((512 + n_tiles - 1) / n_tiles, stages / (n_tiles < 64 ? 8 : 16));
+        while (n_split > 1 && (uint64_t)n_split * mn * 4 > ctx->workspace_bytes) --n_split;
+    }
+    const int split_stages = (stages + n_split - 1) / n_split;
+    a.k_split = split_stages * zwg_lin::BK;
+    n_split = (stages + split_stages - 1) / split_stages; // no empty splits
+    a.part = n_split > 1 ? reinterpret_cast<float *>(ctx->workspace) : nullptr;
+    hipError_t e = launch_tiled<WMODE>(a, tc, n_split, ctx->stream);
+    if (e != hipSuccess) return fail_hip(ctx, "linear kernel launch", e);
+    if (n_split > 1) {
+        e = launch_split_sum(a.part, a.bias, a.out, (int64_t)mn, a.n, n_split, a.epi, a.ldo, ctx->stream);
+        if (e != hipSuccess) return fail_hip(ctx, "linear split-sum kernel launch", e);
+    }
+    return ZWG_OK;
 }
 
 std::string check_linear(uint64_t m, uint64_t k, uint32_t w_type, uint64_t n) {
@@ -94,9 +156,7 @@ int run_q8_stream_mt(zwg_ctx *ctx, const zwg_lin::Q8Args &base) {
     if (e != hipSuccess) return fail_hip(ctx, "linear (int8 stream) kernel launch", e);
     if (n_split > 1) {
         const int64_t mn = (int64_t)(m * n);
-        zwg_lin::linear_split_sum_kernel<<<(unsigned)((mn + 255) / 256), 256, 0, ctx->stream>>>(
-            a.part, a.bias, a.out, mn, (int32_t)n, n_split, a.epi);
-        e = hipGetLastError();
+        e = launch_split_sum(a.part, a.bias, a.out, mn, (int32_t)n, n_split, a.epi, (int64_t)n, ctx->stream);
         if (e != hipSuccess) return fail_hip(ctx, "linear split-sum kernel launch", e);
     }
     return ZWG_OK;
@@ -215,9 +275,7 @@ int run_linear(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void 
     a.k = (int32_t)k;
     a.nb = (int32_t)(k / 32);
     a.epi = epi;
-    e = w_type == ZWG_W_Q8 ? launch_tiled<zwg_lin::kWQ8>(a, ctx->stream) : launch_tiled<zwg_lin::kWF16>(a, ctx->stream);
-    if (e != hipSuccess) return fail_hip(ctx, "linear kernel launch", e);
-    return ZWG_OK;
+    return w_type == ZWG_W_Q8 ? run_tiled<zwg_lin::kWQ8>(ctx, a) : run_tiled<zwg_lin::kWF16>(ctx, a);
 }
 
 // Host-pointer form: stages x (slot 0), the weights (slot 1), the scales and bias (slot 2) and
@@ -314,9 +372,7 @@ int run_linear_q8w(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, c
     a.k = (int32_t)w->k;
     a.nb = (int32_t)(w->k / 32);
     a.epi = epi;
-    e = launch_tiled<zwg_lin::kWQ8P>(a, ctx->stream);
-    if (e != hipSuccess) return fail_hip(ctx, "linear kernel launch", e);
-    return ZWG_OK;
+    return run_tiled<zwg_lin::kWQ8P>(ctx, a);
 }
 
 } // namespace

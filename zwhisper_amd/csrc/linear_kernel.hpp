@@ -65,6 +65,11 @@ struct LinearArgs {
     int64_t ldx, ldw, ldo;
     int32_t m, n, k, nb;
     uint32_t epi; // zwg_ew::kEpi*: store v, gelu(v) or out + v, v = x . w + b
+    // K split over gridDim.y workgroups when a call has too few tiles to fill the GPU: split s
+    // takes k in [s k_split, (s + 1) k_split) (a multiple of BK) and stores its raw sums in
+    // part[s][m][n]; a second kernel adds the splits in order, then bias and epilogue
+    int32_t k_split;
+    float *part;
 };
 
 // Eight int8 (two dwords) to eight exact f16: the biased byte b + 128 is placed under the
@@ -103,7 +108,7 @@ __device__ __forceinline__ int64_t xcd_logical_tile(int64_t hw, int64_t n) {
 // half index of (row, 8-half chunk) in a swizzled LDS tile
 __device__ __forceinline__ int lds_at(int row, int chunk) { return row * BK + ((chunk ^ ((row ^ (row >> 2)) & 3)) << 3); }
 
-template <int BM, int BN, int WMODE, int NWN = 2>
+template <int BM, int BN, int WMODE, int NWN = 2, bool KSPLIT = false>
 __global__ __launch_bounds__(128 * NWN) void linear_mfma_kernel(LinearArgs a) {
     // 2 x NWN waves, each a (BM / 2) x (BN / NWN) block of the tile
     constexpr int kThreads = 128 * NWN;
@@ -127,6 +132,9 @@ __global__ __launch_bounds__(128 * NWN) void linear_mfma_kernel(LinearArgs a) {
     const int wm = wave / NWN, wn = wave % NWN;
     const int n_col_tiles = (a.n + BN - 1) / BN;
     const int64_t tile = xcd_logical_tile(blockIdx.x, gridDim.x);
+    // KSPLIT: workgroup (tile, s) takes k in [s k_split, (s + 1) k_split); k_lo is 0 otherwise
+    const int split = KSPLIT ? (int)blockIdx.y : 0;
+    const int k_lo = split * a.k_split;
     const int m0 = (int)(tile / n_col_tiles) * BM, n0 = (int)(tile % n_col_tiles) * BN;
     const int r32 = lane & 31, ch = lane >> 5;
 
@@ -282,8 +290,8 @@ __global__ __launch_bounds__(128 * NWN) void linear_mfma_kernel(LinearArgs a) {
         }
     };
 
-    const int n_k = (a.k + BK - 1) / BK;
-    load(0);
+    const int n_k = KSPLIT ? min((a.k - k_lo + BK - 1) / BK, a.k_split / BK) : (a.k + BK - 1) / BK;
+    load(k_lo);
     store(0);
     if constexpr (Q8) {
 #pragma unroll
@@ -291,7 +299,7 @@ __global__ __launch_bounds__(128 * NWN) void linear_mfma_kernel(LinearArgs a) {
     }
     __syncthreads();
     for (int t = 0; t + 1 < n_k; ++t) {
-        load((t + 1) * BK);
+        load(k_lo + (t + 1) * BK);
         compute(t & 1);
         store((t + 1) & 1);
         if constexpr (Q8) {
@@ -303,26 +311,30 @@ __global__ __launch_bounds__(128 * NWN) void linear_mfma_kernel(LinearArgs a) {
     compute((n_k - 1) & 1);
 
     // epilogue: register r of lane l is out[8 (r / 4) + 4 (l / 32) + r % 4][l % 32] of its tile
+    float *part = KSPLIT ? a.part + (int64_t)split * a.m * a.n : nullptr;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int col = n0 + wn * WN + j * 32 + r32;
         if (col >= a.n) continue;
-        const float bj = a.bias ? a.bias[col] : 0.f;
+        const float bj = (!KSPLIT && a.bias) ? a.bias[col] : 0.f;
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (row < a.m) zwg_ew::epilogue_store(&a.out[(int64_t)row * a.ldo + col], acc[i][j][r] + bj, a.epi);
+                if (row >= a.m) continue;
+                if constexpr (KSPLIT) part[(int64_t)row * a.n + col] = acc[i][j][r];
+                else zwg_ew::epilogue_store(&a.out[(int64_t)row * a.ldo + col], acc[i][j][r] + bj, a.epi);
             }
     }
 }
 
-template <int BM, int BN, int WMODE, int NWN = 2>
-inline hipError_t launch_linear_tile(const LinearArgs &a, hipStream_t stream) {
+// KSPLIT launches n_split workgroups per tile (a.k_split, a.part set); otherwise n_split is 1
+template <int BM, int BN, int WMODE, int NWN = 2, bool KSPLIT = false>
+inline hipError_t launch_linear_tile(const LinearArgs &a, int n_split, hipStream_t stream) {
     const int64_t tiles = (int64_t)((a.m + BM - 1) / BM) * ((a.n + BN - 1) / BN);
-    if (tiles > 0x7fffffffll) return hipErrorInvalidValue;
-    linear_mfma_kernel<BM, BN, WMODE, NWN><<<dim3((unsigned)tiles), 128 * NWN, 0, stream>>>(a);
+    if (tiles > 0x7fffffffll || n_split < 1 || n_split > 65535 || (!KSPLIT && n_split != 1)) return hipErrorInvalidValue;
+    linear_mfma_kernel<BM, BN, WMODE, NWN, KSPLIT><<<dim3((unsigned)tiles, (unsigned)n_split), 128 * NWN, 0, stream>>>(a);
     return hipGetLastError();
 }
 

@@ -39,6 +39,8 @@
 
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "linear_kernel.hpp"
 
 namespace zwg_lin {
@@ -475,15 +477,40 @@ __global__ __launch_bounds__(64 * NW) void linear_q8p_stream_kernel(Q8Args a, Q8
     }
 }
 
-// out[i][o] = epilogue(sum over splits (in split order) of part[split][i][o], + bias[o]).
+// out[i][o] (row stride ldo) = epilogue(sum over splits (in split order) of part[split][i][o],
+// + bias[o]).  V consecutive elements of one row per thread (V = 4 needs n % 4 == 0 and 16-byte
+// aligned partials).  The loads of up to kSumBatch splits are all issued before the first add, so
+// a sum waits for one memory latency per batch rather than one per split; the adds stay in split
+// order.
+constexpr int kSumBatch = 16;
+template <int V>
 __global__ __launch_bounds__(256) void linear_split_sum_kernel(const float *part, const float *bias, float *out,
-                                                              int64_t mn, int32_t n, int32_t n_split, uint32_t epi) {
-    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+                                                              int64_t mn, int32_t n, int32_t n_split, uint32_t epi,
+                                                              int64_t ldo) {
+    using vec = typename std::conditional<V == 1, float, float __attribute__((ext_vector_type(4)))>::type;
+    static_assert(V == 1 || V == 4, "one or four elements per thread");
+    const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V;
     if (e >= mn) return;
-    float s = part[e];
-    for (int p = 1; p < n_split; ++p) s += part[(int64_t)p * mn + e];
-    if (bias) s += bias[e % n];
-    zwg_ew::epilogue_store(&out[e], s, epi);
+    const vec *p = reinterpret_cast<const vec *>(part + e);
+    const int64_t step = mn / V;
+    vec s{};
+    for (int q0 = 0; q0 < n_split; q0 += kSumBatch) {
+        vec v[kSumBatch];
+#pragma unroll
+        for (int j = 0; j < kSumBatch; ++j)
+            if (q0 + j < n_split) v[j] = p[(q0 + j) * step];
+#pragma unroll
+        for (int j = 0; j < kSumBatch; ++j)
+            if (q0 + j < n_split) s = q0 + j == 0 ? v[j] : s + v[j];
+    }
+    const int64_t row = e / n, col = e - row * n;
+    if constexpr (V == 1) {
+        zwg_ew::epilogue_store(&out[row * ldo + col], bias ? s + bias[col] : s, epi);
+    } else {
+#pragma unroll
+        for (int v = 0; v < V; ++v)
+            zwg_ew::epilogue_store(&out[row * ldo + col + v], bias ? s[v] + bias[col + v] : s[v], epi);
+    }
 }
 
 // The split sum over a group: element e of the concatenated outputs is element e - elem_start[j]
@@ -498,8 +525,17 @@ __global__ __launch_bounds__(256) void linear_split_sum_group_kernel(Q8Group grp
     const int64_t mn = (int64_t)m * n;
     const float *part = q8_pick(grp.part, set);
     const float *bias = q8_pick(grp.bias, set);
-    float s = part[le];
-    for (int p = 1; p < n_split; ++p) s += part[(int64_t)p * mn + le];
+    const float *p = part + le;
+    float s = 0.f;
+    for (int q0 = 0; q0 < n_split; q0 += kSumBatch) { // loads of a batch issued together, adds in split order
+        float v[kSumBatch];
+#pragma unroll
+        for (int j = 0; j < kSumBatch; ++j)
+            if (q0 + j < n_split) v[j] = p[(q0 + j) * mn];
+#pragma unroll
+        for (int j = 0; j < kSumBatch; ++j)
+            if (q0 + j < n_split) s = q0 + j == 0 ? v[j] : s + v[j];
+    }
     if (bias) s += bias[le % n];
     zwg_ew::epilogue_store(&q8_pick(grp.out, set)[le], s, epi);
 }
