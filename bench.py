@@ -30,6 +30,10 @@ oracle's ops.linear timed beside it, and three decode steps' linear layers over 
 weights (HBM-bound; "qwen15_logits_q8_x64", "qwen15_decode_q8_linear_x64",
 "small_dec_q8_linear_x32") with the oracle's ops.linear over Q8 timed beside them, and one whole
 base.en encoder layer over the 16 windows ("base_enc_layer_x16") with the oracle's layer beside it.
+
+Each attention workload also carries "rate": windows/s for the encoders, tokens/s for the decoder
+step, the prefill and the LLM decode step, at wall time per step.  The prefill's CPU baseline runs
+as llm.prompt does (8 calls of 256 rows); "cpu_baseline_one_call" times it as one 2048-row call.
 """
 from __future__ import annotations
 
@@ -571,12 +575,13 @@ def time_workload(wl: Workload, steps: int, warmup: int) -> dict:
             "kernel_ms_min": float(np.min(kms)), "kernel_ms_median": float(np.median(kms))}
 
 
-def cpu_baseline(number: int, threads: int, decode_pool: bool = True) -> dict:
+def cpu_baseline(number: int, threads: int, decode_pool: bool = True, one_call: bool = False) -> dict:
     """The oracle (C restatement of ops.attentionEx + Pool) on a bounded sample of the workload.
 
     Decode workloads run on min(threads, 4) threads, the reference's decode pool (pool_dec,
     src/transcribe.zig:106, src/llm.zig:151), unless decode_pool is False (all threads: the
-    stronger baseline)."""
+    stronger baseline).  The prefill runs as llm.prompt feeds it, 8 calls of 256 rows, unless
+    one_call is True: then as one 2048-row call, for comparison."""
     import oracle
     from zwhisper_amd import workloads as W
     from zwhisper_amd.ops import AttnShape
@@ -601,10 +606,11 @@ def cpu_baseline(number: int, threads: int, decode_pool: bool = True) -> dict:
         kt = W.to_kt(kl, w.n_kv_cap)
         ns, kvw = w.n_head * w.d, w.n_head_kv * w.d
         # llm.prompt feeds batches of 256 rows with kt_stride = n_ctx (src/llm.zig:258-266, :191-202)
-        for b0 in range(0, w.n_q, 256):
-            calls.append((q[b0:b0 + 256], kt, v[: b0 + 256],
-                          AttnShape(256, b0 + 256, w.n_head, w.n_head_kv, w.d, ns, kvw, ns, True, w.n_kv_cap)))
-        sample = "the whole prefill as 8 calls of 256 rows"
+        rows = w.n_q if one_call else 256
+        for b0 in range(0, w.n_q, rows):
+            calls.append((q[b0:b0 + rows], kt, v[: b0 + rows],
+                          AttnShape(rows, b0 + rows, w.n_head, w.n_head_kv, w.d, ns, kvw, ns, True, w.n_kv_cap)))
+        sample = "the whole prefill as one 2048-row call" if one_call else "the whole prefill as 8 calls of 256 rows"
         work = W.algorithmic_work(4)
     elif number == 3:
         ns = w.n_head * w.d
@@ -661,6 +667,20 @@ def traffic_for(workload_name: str):
 
 DENSE_DTYPE = ("x3: f32 inputs split into 16-bit hi + lo terms (f16 for Q.K^T, bf16 for P.V), three 16-bit MFMA "
                "products per product, f32 accumulation")
+
+
+def step_rate(number: int, ms_per_step: float) -> dict:
+    """Windows/s (encoders) or tokens/s (decoder and LLM) of a workload's steps, at wall time."""
+    from zwhisper_amd import workloads as W
+
+    w = W.WORKLOADS[number]
+    per_s = 1e3 / ms_per_step
+    if number in (1, 2):
+        return {"value": w.n_items * per_s, "unit": "windows/s", "per_step": w.n_items}
+    if number == 4:
+        return {"value": w.n_q * per_s, "unit": "tokens/s", "per_step": w.n_q, "note": "prompt tokens"}
+    return {"value": w.n_items * per_s, "unit": "tokens/s", "per_step": w.n_items,
+            "note": "one new token per window or sequence"}
 
 
 def dense_roofline(achieved: float, dense_math: int) -> dict:
@@ -739,6 +759,7 @@ def main() -> int:
             unit = "GB/s"
         roof["traffic"] = traffic_for(spec.name)
         res = {"workload": spec.name, "description": spec.description, "value": value, "unit": unit,
+               "rate": step_rate(n, r["ms_per_step"]),
                "ms_per_step": r["ms_per_step"], "kernel_ms_mean": r["kernel_ms_mean"],
                "kernel_ms_min": r["kernel_ms_min"], "algorithmic_work_per_step": per_step,
                "dtype": DENSE_DTYPE if spec.bound == "mfma" else "f32", "roofline": roof}
@@ -746,6 +767,8 @@ def main() -> int:
             res["cpu_baseline"] = cpu_baseline(n, host_threads())
             if n in (3, 5):
                 res["cpu_baseline_all_threads"] = cpu_baseline(n, host_threads(), decode_pool=False)
+            if n == 4:
+                res["cpu_baseline_one_call"] = cpu_baseline(n, host_threads(), one_call=True)
         results[n] = res
         print(f"[bench] {spec.name}: {value:.2f} {unit} ({r['ms_per_step']:.4f} ms/step, kernel "
               f"{r['kernel_ms_mean']:.4f} ms, {100 * roof['frac']:.1f}% of {spec.bound} peak)"
@@ -879,6 +902,7 @@ def main() -> int:
                    "n_head": spec.n_head, "n_head_kv": spec.n_head_kv, "head_dim": spec.d, "causal": spec.causal,
                    "k_layout": "transposed" if spec.kt else "row-major", "parallelism": "single GPU"},
         "roofline": head["roofline"],
+        "rate": head["rate"],
         "cpu_baseline": head.get("cpu_baseline"),
         **({"cpu_baseline_all_threads": head["cpu_baseline_all_threads"]} if "cpu_baseline_all_threads" in head else {}),
         "workloads": {r["workload"]: {k: v for k, v in r.items() if k not in ("workload",)}
