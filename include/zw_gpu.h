@@ -93,7 +93,8 @@ typedef struct zwg_batch {
 
 /* Sizes and modes fixed when a context opens.  Zero fields take the defaults. */
 typedef struct zwg_limits {
-    uint64_t workspace_bytes; /* device memory for split-KV partial results; default 256 MiB */
+    uint64_t workspace_bytes; /* device memory for split partial results (attention key splits,
+                                 linear k splits); default 256 MiB */
     uint32_t dense_math;      /* ZWG_DENSE_X3 (0, default) or ZWG_DENSE_FP32 */
     uint32_t reserved;        /* must be 0 */
 } zwg_limits;
@@ -233,7 +234,9 @@ int zwg_kv_read(zwg_kv *kv, uint64_t layer, uint64_t seq, float *k_host, float *
  * x f32 [m][k], w [n][k] of type w_type, bias f32 [n] or NULL, out f32 [m][n].
  * Computed on f16 MFMA with each x split into two f16 terms (f32-level accuracy; |x| must be
  * within f16's range, 65504, or its output row turns inf).  k a multiple of 8; pointers 16-byte
- * aligned.
+ * aligned.  A call with too few output tiles to fill the GPU and a long k splits k and keeps the
+ * partial sums in the context's workspace (as many splits as fit); the splits are added in a
+ * fixed order, so results do not vary from call to call.
  */
 #define ZWG_W_F16 1u /* IEEE binary16 weights, as src/encoder.zig loads them */
 
