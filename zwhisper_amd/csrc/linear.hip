@@ -37,15 +37,23 @@ int64_t tiles(uint64_t m, uint64_t n, int bm, int bn) { return (int64_t)((m + bm
 // half the accumulators and staging registers per wave (76 and 124 VGPRs against 141 and 235),
 // so LDS rather than registers sets the occupancy -- twice the waves per SIMD, which hides more
 // of the per-stage load latency (measured 6-7% on the base.en projections and layer).
+// Threads per workgroup of the short element-wise kernels around the int8 and split paths (the
+// x split, the split sums): 64 when the call has fewer than 1024 workgroups' worth at 256, so a
+// small call's one round of loads comes from every CU rather than a few (as the attention merge)
+inline int small_block(int64_t threads) { return threads < 1024ll * 256 ? 64 : 256; }
+inline unsigned blocks_for(int64_t threads, int bs) { return (unsigned)((threads + bs - 1) / bs); }
+
 // The split sum of n_split partial products part[s][m][n] into out (row stride ldo)
 hipError_t launch_split_sum(const float *part, const float *bias, float *out, int64_t mn, int32_t n, int n_split,
                             uint32_t epi, int64_t ldo, hipStream_t stream) {
     if (n % 4 == 0 && (reinterpret_cast<uintptr_t>(part) & 15) == 0) {
         const int64_t threads = mn / 4;
-        zwg_lin::linear_split_sum_kernel<4><<<(unsigned)((threads + 255) / 256), 256, 0, stream>>>(
+        const int bs = small_block(threads);
+        zwg_lin::linear_split_sum_kernel<4><<<blocks_for(threads, bs), bs, 0, stream>>>(
             part, bias, out, mn, n, n_split, epi, ldo);
     } else {
-        zwg_lin::linear_split_sum_kernel<1><<<(unsigned)((mn + 255) / 256), 256, 0, stream>>>(
+        const int bs = small_block(mn);
+        zwg_lin::linear_split_sum_kernel<1><<<blocks_for(mn, bs), bs, 0, stream>>>(
             part, bias, out, mn, n, n_split, epi, ldo);
     }
     return hipGetLastError();
@@ -145,7 +153,8 @@ int run_q8_stream_mt(zwg_ctx *ctx, const zwg_lin::Q8Args &base) {
     a.part = n_split > 1 ? reinterpret_cast<float *>(reinterpret_cast<char *>(ctx->workspace) + part_off) : nullptr;
 
     const int64_t prep_threads = (int64_t)n_chunks * MT * 32 * (zwg_lin::kQ8Chunk / 4);
-    zwg_lin::linear_q8_xprep_kernel<MT><<<(unsigned)((prep_threads + 255) / 256), 256, 0, ctx->stream>>>(
+    const int prep_bs = small_block(prep_threads);
+    zwg_lin::linear_q8_xprep_kernel<MT><<<blocks_for(prep_threads, prep_bs), prep_bs, 0, ctx->stream>>>(
         a.x, xcvt, a.m, a.k, n_chunks);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail_hip(ctx, "linear (int8) x preparation launch", e);
@@ -209,7 +218,8 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g)
     _Float16 *xcvt = reinterpret_cast<_Float16 *>(ctx->workspace);
 
     const int64_t prep_threads = (int64_t)n_chunks * MT * 32 * (zwg_lin::kQ8Chunk / 4);
-    zwg_lin::linear_q8_xprep_kernel<MT><<<(unsigned)((prep_threads + 255) / 256), 256, 0, ctx->stream>>>(
+    const int prep_bs = small_block(prep_threads);
+    zwg_lin::linear_q8_xprep_kernel<MT><<<blocks_for(prep_threads, prep_bs), prep_bs, 0, ctx->stream>>>(
         a.x, xcvt, a.m, a.k, n_chunks);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return fail_hip(ctx, "linear (int8) x preparation launch", e);
@@ -219,7 +229,8 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g)
     if (e != hipSuccess) return fail_hip(ctx, "linear (int8 stream) kernel launch", e);
     if (n_split > 1) {
         const int64_t elems = (int64_t)(m * n_tot);
-        zwg_lin::linear_split_sum_group_kernel<<<(unsigned)((elems + 255) / 256), 256, 0, ctx->stream>>>(
+        const int bs = small_block(elems);
+        zwg_lin::linear_split_sum_group_kernel<<<blocks_for(elems, bs), bs, 0, ctx->stream>>>(
             g, a.m, n_split, a.epi);
         e = hipGetLastError();
         if (e != hipSuccess) return fail_hip(ctx, "linear split-sum kernel launch", e);

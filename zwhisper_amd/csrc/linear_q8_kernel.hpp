@@ -90,7 +90,7 @@ __device__ __forceinline__ int q8_xs_at(int b, int i, int hl, int s, int lane) {
 template <int MT>
 __global__ __launch_bounds__(256) void linear_q8_xprep_kernel(const float *x, _Float16 *xcvt, int32_t m, int32_t k,
                                                              int32_t n_chunks) {
-    const int64_t f = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t f = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t per_chunk = MT * 32 * (kQ8Chunk / 4);
     if (f >= per_chunk * n_chunks) return;
     const int c = (int)(f / per_chunk), rem = (int)(f % per_chunk);
@@ -489,7 +489,7 @@ __global__ __launch_bounds__(256) void linear_split_sum_kernel(const float *part
                                                               int64_t ldo) {
     using vec = typename std::conditional<V == 1, float, float __attribute__((ext_vector_type(4)))>::type;
     static_assert(V == 1 || V == 4, "one or four elements per thread");
-    const int64_t e = ((int64_t)blockIdx.x * 256 + threadIdx.x) * V;
+    const int64_t e = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * V;
     if (e >= mn) return;
     const vec *p = reinterpret_cast<const vec *>(part + e);
     const int64_t step = mn / V;
@@ -517,7 +517,7 @@ __global__ __launch_bounds__(256) void linear_split_sum_kernel(const float *part
 // of set j, summed over the splits in split order, + bias, through the epilogue.
 __global__ __launch_bounds__(256) void linear_split_sum_group_kernel(Q8Group grp, int32_t m, int32_t n_split,
                                                                     uint32_t epi) {
-    const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= grp.elem_start[kQ8MaxGroup]) return;
     const int set = q8_group_of_elem(grp, e);
     const int64_t le = e - q8_pick(grp.elem_start, set);
