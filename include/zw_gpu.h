@@ -14,8 +14,15 @@
  *   - one context per host thread; calls on one context are not thread-safe
  *     (as the zw_* handles, src/capi.zig:3-4).
  *
- * Arithmetic is f32 throughout (fp32 MFMA for the dense kernel, f32 FMA for the streaming
- * decode kernel); results match the reference's f32 attention within max abs 2e-4.
+ * Arithmetic and tolerances (against the f64 closed form of the reference's attention):
+ *   - decode (split-K streaming) kernel: f32 FMA.  Bar: max abs 2e-4, normwise relative 1e-3
+ *     (||gpu - ref||_inf / ||ref||_inf), the reference's f32 bar; measured ~1e-7.
+ *   - dense (encoder / prefill) kernel, ZWG_DENSE_X3 (the default, below): f32 operands split into
+ *     16-bit hi + lo terms, three 16-bit MFMA products per product, f32 accumulation.  Its own bar
+ *     on N(0,1) inputs: max abs 5e-5 and normwise relative 3e-5 (measured at most 1.9e-5 and
+ *     1.1e-5 on the five Whisper / Qwen2 workloads); with scores spread 36x wider it measures
+ *     4.5e-5, inside the f32 bar.
+ *   - dense kernel, ZWG_DENSE_FP32: fp32 MFMA (v_mfma_f32_32x32x2_f32) throughout; the f32 bar.
  */
 #ifndef ZW_GPU_H
 #define ZW_GPU_H
@@ -77,14 +84,14 @@ typedef struct zwg_batch {
 } zwg_batch;
 
 /*
- * Arithmetic of the dense (encoder / prefill) attention kernel.  Both give results within the
- * 2e-4 bar of the reference's f32 attention:
+ * Arithmetic of the dense (encoder / prefill) attention kernel (tolerances at the top of this
+ * file):
  *   ZWG_DENSE_X3 (default): every product as three 16-bit MFMA products of operands split into
- *     hi + lo terms, f32 accumulation, about 2.4x the fp32 kernel's rate.  Q.K^T splits into f16
+ *     hi + lo terms, f32 accumulation, about 2.5x the fp32 kernel's rate.  Q.K^T splits into f16
  *     (22 significand bits, so a score's error does not grow with large logits), P.V into bf16
- *     (16 bits, f32 exponent range).  Measured within ~2e-6 of f64 on the Whisper shapes and
- *     ~5e-5 with scores spread 36x wider.  Keys must stay below 65504 in magnitude (f16 range):
- *     a larger one gives NaN outputs, never a silently wrong finite one.
+ *     (16 bits, f32 exponent range).  Keys must stay below 65504 in magnitude (f16 range): a
+ *     larger one gives NaN outputs, never a silently wrong finite one (zwg_attention_ex then
+ *     recomputes the call in ZWG_DENSE_FP32).
  *   ZWG_DENSE_FP32: fp32 MFMA (v_mfma_f32_32x32x2_f32) throughout, no range condition.
  * The decode kernels are f32 FMA in either mode.
  */
@@ -118,7 +125,9 @@ const char *zwg_last_error(const zwg_ctx *ctx);
 
 /* Queue the context's work on a caller's hipStream_t (NULL is HIP's null stream) / the stream
  * in use.  A context starts on a stream of its own; zwg_get_stream right after zwg_open
- * returns it, to switch back later. */
+ * returns it, to switch back later.  Every call of a context uses the same workspace, so a
+ * switch orders the new stream after the work already queued on the old one (an event recorded
+ * on the old stream, waited on by the new); calls issued on one stream run in issue order. */
 int zwg_set_stream(zwg_ctx *ctx, void *hip_stream);
 void *zwg_get_stream(const zwg_ctx *ctx);
 /* Wait for all work queued on the context's stream. */
@@ -130,6 +139,9 @@ int zwg_set_dense_math(zwg_ctx *ctx, uint32_t mode);
  * Drop-in for ops.attentionEx (src/ops.zig:562): host pointers, synchronous — `out` holds the
  * result on return, and only each query row's n_head*d columns are written, as in the
  * reference.  Stages q/k/v through device buffers the context keeps (grown on first need).
+ * It keeps the reference's contract for any finite input: when the x3 dense kernel's result
+ * holds a non-finite value (a key or scaled query beyond f16 range), the call is computed
+ * again on the fp32-MFMA kernel, which has no range condition.
  */
 int zwg_attention_ex(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_attn_shape *shape,
                      float *out);
@@ -139,7 +151,9 @@ int zwg_attention_ex(zwg_ctx *ctx, const float *q, const float *k, const float *
 int zwg_attention(zwg_ctx *ctx, const float *q, const float *k, const float *v, uint64_t n_q, uint64_t n_kv,
                   uint64_t n_state, uint64_t n_head, int causal, float *out);
 
-/* Device pointers (inputs already in HBM): queued on the context's stream, asynchronous. */
+/* Device pointers (inputs already in HBM): queued on the context's stream, asynchronous.  In
+ * ZWG_DENSE_X3 mode dense calls need |k| < 65504 and |q| / sqrt(d) * log2(e) < 65504 (rows that
+ * see a larger value come out NaN); ZWG_DENSE_FP32 mode has no such condition. */
 int zwg_attention_dev(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_attn_shape *shape,
                       float *out);
 
@@ -202,7 +216,9 @@ typedef struct zwg_kv_info {
 #define ZWG_ROWS_ON_HOST 1u
 
 /* Allocate the caches of `desc` on ctx's device (zeroed; rotary tables built on the host in
- * f64 and rounded to f32, as src/llm.zig:128-137).  *out is NULL on failure. */
+ * f64 and rounded to f32, as src/llm.zig:128-137).  *out is NULL on failure.  zwg_close of the
+ * context frees the caches of a zwg_kv not destroyed yet; the zwg_kv itself then only accepts
+ * zwg_kv_destroy (other calls fail). */
 int zwg_kv_create(zwg_ctx *ctx, const zwg_kv_desc *desc, zwg_kv **out);
 void zwg_kv_destroy(zwg_kv *kv);
 int zwg_kv_get_info(const zwg_kv *kv, zwg_kv_info *out);
@@ -276,8 +292,9 @@ int zwg_linear_q8_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, cons
  * the GPU: it copies the Q8's two arrays into HBM once, repacked so that the token-step kernel
  * reads every weight byte in contiguous 1 KB wave-loads (tiles of 32 rows x 32 k in lane order,
  * scales grouped per 32 rows; zero padding to 32 rows and 256 k).  zwg_linear_q8w_dev computes
- * exactly what zwg_linear_q8_dev computes with the unpacked arrays.  Destroy the weights before
- * closing their context.
+ * exactly what zwg_linear_q8_dev computes with the unpacked arrays.  zwg_close of the context
+ * frees the packed copy of weights not destroyed yet; such weights then only accept
+ * zwg_q8w_destroy (calls that use them fail).
  */
 typedef struct zwg_q8w zwg_q8w;
 #define ZWG_Q8W_FROM_HOST 1u /* q and scales are host memory (else device memory) */

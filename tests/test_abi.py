@@ -144,7 +144,9 @@ def test_plan_invariants(sh, nb):
         assert 1 <= n <= p.max_chunks
         assert keys % tile == 0 and (n - 1) * keys < max(hi, 1) <= n * keys or hi == 0
     rows = nb * sh.n_head * sh.n_q
-    assert p.workspace_bytes == (rows * p.max_chunks * (sh.d + 2) * 4 if p.max_chunks > 1 else 0)
+    # (max, sum) pairs, then the sums from the next 256-byte boundary (aligned 16-byte accesses)
+    pairs = -(-(2 * rows * p.max_chunks) // 64) * 64
+    assert p.workspace_bytes == ((pairs + rows * p.max_chunks * sh.d) * 4 if p.max_chunks > 1 else 0)
     if p.kernel == 2:
         assert p.grid_blocks == p.max_chunks * sh.n_head_kv * nb
     else:

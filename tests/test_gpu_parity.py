@@ -1,9 +1,14 @@
 """GPU parity: the HIP path (through the C ABI) against the f64 closed form and the CPU oracle.
 
-Tolerance for every output (the f32 attention bar): max |gpu - ref| <= 2e-4 and
-normwise relative error ||gpu - ref||_inf / ||ref||_inf <= 1e-3.  The elementwise relative error
-over outputs with |ref| >= 1e-2 is printed beside them (reported, no bound of its own).  Columns a
-call must not write (row gaps when out_stride > n_head * d) must keep their previous contents.
+Tolerances, by the arithmetic of the context (include/zw_gpu.h states the same):
+  * fp32 dense mode and the decode kernels -- the reference's f32 attention bar: max |gpu - ref|
+    <= 2e-4 and normwise relative error ||gpu - ref||_inf / ||ref||_inf <= 1e-3;
+  * the x3 dense mode (the default; split 16-bit MFMA products) -- its own bar: max abs <= 5e-5
+    and normwise relative <= 3e-5.  A context in x3 mode is held to it for every call, its decode
+    calls (f32 FMA, ~1e-7) included.
+The elementwise relative error over outputs with |ref| >= 1e-2 is printed beside them (reported,
+no bound of its own).  Columns a call must not write (row gaps when out_stride > n_head * d) must
+keep their previous contents.
 """
 from __future__ import annotations
 
@@ -18,8 +23,10 @@ from _golden import head_columns_mask, load_cases
 
 pytestmark = pytest.mark.gpu
 
-TOL_ABS = 2e-4
+TOL_ABS = 2e-4  # f32 bar
 TOL_REL = 1e-3
+TOL_ABS_X3 = 5e-5  # x3 dense mode
+TOL_REL_X3 = 3e-5
 SENTINEL = 7.25
 
 CASES = load_cases()
@@ -53,7 +60,10 @@ def ctx_fp32(torch):
     c.close()
 
 
-def assert_close(got: np.ndarray, ref: np.ndarray, what: str) -> tuple[float, float]:
+def assert_close(got: np.ndarray, ref: np.ndarray, what: str, x3: bool = True) -> tuple[float, float]:
+    """Max abs and normwise relative error of got against ref, held to the x3 bar (x3=True) or
+    the f32 bar."""
+    tol_abs, tol_rel = (TOL_ABS_X3, TOL_REL_X3) if x3 else (TOL_ABS, TOL_REL)
     got = np.asarray(got, dtype=np.float64).reshape(-1)
     ref = np.asarray(ref, dtype=np.float64).reshape(-1)
     if ref.size == 0:
@@ -65,7 +75,8 @@ def assert_close(got: np.ndarray, ref: np.ndarray, what: str) -> tuple[float, fl
     erel = float((np.abs(got - ref)[big] / np.abs(ref[big])).max()) if big.any() else 0.0
     print(f"{what}: max abs {err:.3e}, normwise rel {rel:.3e}, elementwise rel (|ref| >= 1e-2) {erel:.3e}",
           flush=True)
-    assert err <= TOL_ABS and rel <= TOL_REL, f"{what}: max abs {err:.3e} (<= {TOL_ABS}), normwise rel {rel:.3e}"
+    assert err <= tol_abs and rel <= tol_rel, (f"{what}: max abs {err:.3e} (<= {tol_abs}), normwise rel {rel:.3e} "
+                                               f"(<= {tol_rel})")
     return err, rel
 
 
@@ -98,7 +109,7 @@ def test_golden_dense_fp32_mode(torch, ctx_fp32, case):
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     m = head_columns_mask(sh)
-    assert_close(got[m], case.expected[m], case.name)
+    assert_close(got[m], case.expected[m], case.name, x3=False)
     assert np.all(got[~m] == SENTINEL), f"{case.name}: wrote outside the head columns"
 
 

@@ -1,8 +1,10 @@
 """GPU parity at the benchmark workloads' full sizes, and the batch/stream/split paths.
 
 Each workload is checked against the f64 closed form (oracle/naive.py) on the same seeded
-inputs the benchmark uses, to the f32 bar: max abs error <= 2e-4 and normwise relative error
-||gpu - ref||_inf / ||ref||_inf <= 1e-3.  Where a full f64 reference of every item would be slow,
+inputs the benchmark uses.  Bars (include/zw_gpu.h): a context in the x3 dense mode (the
+default) is held to max abs error <= 5e-5 and normwise relative error ||gpu - ref||_inf /
+||ref||_inf <= 3e-5 for every call; the fp32 dense mode to the reference's f32 bar, 2e-4 and
+1e-3.  The dense workloads run in both modes.  Where a full f64 reference of every item would be slow,
 some items are compared directly and the rest through properties that hold at any size:
 each output lies in the per-dimension hull of the visible value rows, and a batched call agrees
 with per-item calls.
@@ -18,8 +20,11 @@ from zwhisper_amd.ops import AttnShape
 
 pytestmark = pytest.mark.gpu
 
-TOL_ABS = 2e-4
+TOL_ABS = 2e-4  # f32 bar
 TOL_REL = 1e-3
+TOL_ABS_X3 = 5e-5  # x3 dense mode
+TOL_REL_X3 = 3e-5
+MODES = ["x3", "fp32"]
 
 
 @pytest.fixture(scope="module")
@@ -40,22 +45,39 @@ def ctx(torch):
     c.close()
 
 
-def check(got, ref, what):
+@pytest.fixture(scope="module")
+def ctx_fp32(torch):
+    import zwhisper_amd as z
+
+    c = z.Context(0, dense_math=z.DENSE_FP32)
+    yield c
+    c.close()
+
+
+def check(got, ref, what, x3: bool = True):
+    """Max abs and normwise relative error against ref, to the x3 bar (x3=True) or the f32 bar."""
+    tol_abs, tol_rel = (TOL_ABS_X3, TOL_REL_X3) if x3 else (TOL_ABS, TOL_REL)
     got = np.asarray(got, np.float64).reshape(-1)
     ref = np.asarray(ref, np.float64).reshape(-1)
     assert np.all(np.isfinite(got)), f"{what}: non-finite output"
     err = float(np.abs(got - ref).max())
     rel = err / max(float(np.abs(ref).max()), 1e-30)
     print(f"{what}: max abs {err:.2e}, normwise rel {rel:.2e}", flush=True)
-    assert err <= TOL_ABS and rel <= TOL_REL, f"{what}: max abs {err:.3e}, rel {rel:.3e}"
+    assert err <= tol_abs and rel <= tol_rel, f"{what}: max abs {err:.3e} (<= {tol_abs}), rel {rel:.3e} (<= {tol_rel})"
+
+
+def mode_ctx(request, mode):
+    return request.getfixturevalue("ctx" if mode == "x3" else "ctx_fp32")
 
 
 def dev(torch, a):
     return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()
 
 
-def test_tiny_encoder_full(torch, ctx):
-    """Workload 1: 1500 x 1500, 6 heads x 64, transposed K (kt_stride 1504)."""
+@pytest.mark.parametrize("mode", MODES)
+def test_tiny_encoder_full(torch, request, mode):
+    """Workload 1: 1500 x 1500, 6 heads x 64, transposed K (kt_stride 1504), both dense modes."""
+    ctx = mode_ctx(request, mode)
     w = W.WORKLOADS[1]
     q, kl, v = W.make_dense(1, 0)
     sh = AttnShape(1500, 1500, 6, 6, 64, 384, 384, 384, False, 1504)
@@ -63,12 +85,14 @@ def test_tiny_encoder_full(torch, ctx):
     out = torch.empty(1500 * 384, device="cuda")
     ctx.attention_dev(dev(torch, q), dev(torch, kt), dev(torch, v), sh, out)
     torch.cuda.synchronize()
-    check(out.cpu().numpy(), naive.attention_f64(q, kt, v, sh), w.name)
+    check(out.cpu().numpy(), naive.attention_f64(q, kt, v, sh), f"{w.name} ({mode})", x3=mode == "x3")
 
 
-def test_base_encoder_batch(torch, ctx):
+@pytest.mark.parametrize("mode", MODES)
+def test_base_encoder_batch(torch, request, mode):
     """Workload 2: 16 windows in one batched call; windows 0 and 15 against f64, all windows
-    against per-window calls."""
+    against per-window calls; both dense modes."""
+    ctx = mode_ctx(request, mode)
     w = W.WORKLOADS[2]
     sh = AttnShape(1500, 1500, 8, 8, 64, 512, 512, 512, False, 1504)
     qs, kts, vs = [], [], []
@@ -83,7 +107,7 @@ def test_base_encoder_batch(torch, ctx):
     torch.cuda.synchronize()
     got = out.cpu().numpy()
     for i in (0, 15):
-        check(got[i], naive.attention_f64(qs[i], kts[i], vs[i], sh), f"{w.name} window {i}")
+        check(got[i], naive.attention_f64(qs[i], kts[i], vs[i], sh), f"{w.name} window {i} ({mode})", x3=mode == "x3")
     one = torch.empty(1500, 512, device="cuda")
     for i in range(16):
         ctx.attention_dev(q[i], kt[i], v[i], sh, one)
@@ -127,8 +151,11 @@ def test_decoder_step_all_windows(torch, ctx):
               f"{w.name} cross window {i}")
 
 
-def test_qwen_prefill_full(torch, ctx):
-    """Workload 4: 2048 tokens causal, 14 query / 2 KV heads, transposed cache of 2048 columns."""
+@pytest.mark.parametrize("mode", MODES)
+def test_qwen_prefill_full(torch, request, mode):
+    """Workload 4: 2048 tokens causal, 14 query / 2 KV heads, transposed cache of 2048 columns,
+    both dense modes."""
+    ctx = mode_ctx(request, mode)
     w = W.WORKLOADS[4]
     q, kl, v = W.make_dense(4, 0)
     kt = W.to_kt(kl, 2048)
@@ -136,7 +163,7 @@ def test_qwen_prefill_full(torch, ctx):
     out = torch.empty(2048 * 896, device="cuda")
     ctx.attention_dev(dev(torch, q), dev(torch, kt), dev(torch, v), sh, out)
     torch.cuda.synchronize()
-    check(out.cpu().numpy(), naive.attention_f64(q, kt, v, sh), w.name)
+    check(out.cpu().numpy(), naive.attention_f64(q, kt, v, sh), f"{w.name} ({mode})", x3=mode == "x3")
 
 
 def test_qwen_decode_all_sequences(torch, ctx):
@@ -236,7 +263,9 @@ def test_dense_math_modes(torch, scale):
             c.attention_dev(dev(torch, q), dev(torch, kt), dev(torch, v), sh, out)
             torch.cuda.synchronize()
             got = out.cpu().numpy()
-            check(got, ref, f"dense mode {mode}, scores x{scale * scale:g}")
+            # on unit-variance inputs each mode meets its own bar; with scores spread 36x wider both
+            # are held to the f32 bar (measured 4.5e-5 for x3, 5.2e-5 for fp32)
+            check(got, ref, f"dense mode {mode}, scores x{scale * scale:g}", x3=mode == z.DENSE_X3 and scale == 1.0)
             if mode in outs:
                 assert np.array_equal(outs[mode], got), "same mode, same inputs: results differ"
             outs[mode] = got
@@ -275,7 +304,7 @@ def test_dense_instantiations(torch, shape, mode):
         out = torch.empty(n_q * h * d, device="cuda")
         c.attention_dev(dev(torch, q), dev(torch, k), dev(torch, v), sh, out)
         torch.cuda.synchronize()
-        check(out.cpu().numpy(), ref, f"dense {mode} {shape}")
+        check(out.cpu().numpy(), ref, f"dense {mode} {shape}", x3=mode == "x3")
 
 
 def test_x3_key_range(torch):
@@ -302,7 +331,7 @@ def test_x3_key_range(torch):
             torch.cuda.synchronize()
             outs[mode] = out.cpu().numpy().reshape(n_q, h * d)
     x3, f32 = outs[z.DENSE_X3], outs[z.DENSE_FP32]
-    check(f32, ref, "fp32 mode with a key of 1e5")
+    check(f32, ref, "fp32 mode with a key of 1e5", x3=False)
     # causal: query i sees keys <= i, so rows < 50 never see the big key
     check(x3[:big, :d], ref[:big, :d], "x3 rows before the big key, head 0")
     check(x3[:, d:], ref[:, d:], "x3 head 1 (no big key)")
@@ -342,3 +371,72 @@ def test_host_dropin_matches_device_path(torch, ctx):
     z.attention(None, q, k, v, n, n, ns, h, False, None, out)
     sh = AttnShape(n, n, h, h, ns // h, ns, ns, ns, False)
     check(out, naive.attention_f64(q, k, v, sh), "ops.attention drop-in, 1500 x 384")
+
+
+def test_x3_dropin_recomputes_out_of_range_keys(ctx):
+    """zwg_attention_ex keeps the reference's contract for any finite input: a key beyond f16
+    range (NaN rows on the x3 kernel) makes the drop-in compute the call again on the fp32
+    kernel, so every row is finite and within the f32 bar of f64."""
+    n_q = n_kv = 96
+    h, d = 2, 64
+    sh = AttnShape(n_q, n_kv, h, h, d, h * d, h * d, h * d, True, None)
+    q = W.normal(81, n_q * h * d) * 0.01
+    k = W.normal(82, n_kv * h * d).reshape(n_kv, h * d)
+    k[40, 5] = -2.0e5
+    k = k.reshape(-1)
+    v = W.normal(83, n_kv * h * d)
+    out = np.zeros(n_q * h * d, np.float32)
+    ctx.attention_ex_host(q, k, v, sh, out)
+    check(out, naive.attention_f64(q, k, v, sh), "drop-in with a key of -2e5", x3=False)
+
+
+def test_two_unordered_streams_share_the_workspace(torch, ctx):
+    """Two split calls of one context on two streams that do not wait for each other: the
+    context orders the second stream after the first when it switches (both write their split
+    partials to the same workspace), so both results are right."""
+    sh = AttnShape(1, 3000, 12, 2, 128, 1536, 256, 1536, True, 3000)
+    import zwhisper_amd as z
+
+    assert z.plan(sh).max_chunks > 1, "the case must split its keys"
+    inputs, refs = [], []
+    for seed in (91, 95):
+        q = W.normal(seed, 1536)
+        kl = W.normal(seed + 1, 3000 * 256).reshape(3000, 2, 128)
+        kt = W.to_kt(kl, 3000)
+        v = W.normal(seed + 2, 3000 * 256)
+        inputs.append((dev(torch, q), dev(torch, kt), dev(torch, v), torch.empty(1536, device="cuda")))
+        refs.append(naive.attention_f64(q, kt, v, sh))
+    torch.cuda.synchronize()
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    for _ in range(3):
+        with torch.cuda.stream(sa):
+            q, k, v, o = inputs[0]
+            ctx.attention_dev(q, k, v, sh, o)
+        with torch.cuda.stream(sb):
+            q, k, v, o = inputs[1]
+            ctx.attention_dev(q, k, v, sh, o)
+        torch.cuda.synchronize()
+        for (_, _, _, o), ref, name in zip(inputs, refs, ("stream a", "stream b")):
+            check(o.cpu().numpy(), ref, f"decode on {name}")
+
+
+def test_children_outlive_their_closed_context(torch):
+    """zwg_close frees the device memory of caches and int8 weights made from the context and not
+    destroyed yet; the orphaned objects then refuse to be used and can still be destroyed."""
+    import zwhisper_amd as z
+
+    c = z.Context(0)
+    kv = z.KVCache(c, 1, 1, 64, 2, 64)
+    rng = np.random.default_rng(5)
+    w = z.Q8(rng.integers(-127, 128, (64, 64), dtype=np.int8), np.ones((64, 2), np.float32), 64, 64).resident(c)
+    c._children.clear()  # bypass the Python-side close of the children: the C ABI's own rule
+    c.close()
+    x = torch.zeros(64, device="cuda")
+    out = torch.empty(64, device="cuda")
+    with z.Context(0) as c2:
+        with pytest.raises(z.ZwgError):
+            c2.linear_q8w_dev(x, 1, w, None, out)
+    with pytest.raises(z.ZwgError):
+        kv.read(0, 0)
+    kv.close()
+    w.close()

@@ -293,6 +293,29 @@ int append(zwg_kv *kv, uint64_t layer, uint64_t seq0, uint64_t pos0, uint64_t n,
 
 } // namespace
 
+namespace {
+
+const char *const kKvClosed = "the kv cache's context is closed";
+
+// Free a cache's device memory (after the work queued on its context's stream).
+void free_caches(zwg_kv *kv) {
+    (void)hipSetDevice(kv->ctx->device);
+    (void)hipStreamSynchronize(kv->ctx->stream);
+    for (float **p : {&kv->k, &kv->v, &kv->cos, &kv->sin}) {
+        if (*p) (void)hipFree(*p);
+        *p = nullptr;
+    }
+}
+
+// zwg_close of the cache's context: the caches go with it
+void detach_kv(void *obj) {
+    auto *kv = static_cast<zwg_kv *>(obj);
+    free_caches(kv);
+    kv->ctx = nullptr;
+}
+
+} // namespace
+
 extern "C" {
 
 int zwg_kv_create(zwg_ctx *ctx, const zwg_kv_desc *desc, zwg_kv **out) {
@@ -332,24 +355,27 @@ int zwg_kv_create(zwg_ctx *ctx, const zwg_kv_desc *desc, zwg_kv **out) {
     }
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) {
-        zwg_kv_destroy(kv);
+        free_caches(kv);
+        delete kv;
         return fail_hip(ctx, "kv cache allocation", e);
     }
+    add_child(ctx, kv, detach_kv);
     *out = kv;
     return ZWG_OK;
 }
 
 void zwg_kv_destroy(zwg_kv *kv) {
     if (!kv) return;
-    (void)hipSetDevice(kv->ctx->device);
-    (void)hipStreamSynchronize(kv->ctx->stream);
-    for (float *p : {kv->k, kv->v, kv->cos, kv->sin})
-        if (p) (void)hipFree(p);
+    if (kv->ctx) {
+        remove_child(kv->ctx, kv);
+        free_caches(kv);
+    }
     delete kv;
 }
 
 int zwg_kv_get_info(const zwg_kv *kv, zwg_kv_info *out) {
     if (!kv || !out) return fail(kv ? kv->ctx : nullptr, "null kv or output");
+    if (!kv->ctx) return fail(nullptr, kKvClosed);
     out->k = kv->k;
     out->v = kv->v;
     out->layer_stride = kv->desc.n_seq * kv->per_seq;
@@ -362,18 +388,21 @@ int zwg_kv_get_info(const zwg_kv *kv, zwg_kv_info *out) {
 int zwg_kv_append(zwg_kv *kv, uint64_t layer, uint64_t seq, uint64_t pos, uint64_t n, const float *k_rows,
                   const float *v_rows, float *q, uint64_t n_head, uint64_t q_stride, uint32_t flags) {
     if (!kv) return fail(nullptr, "null kv");
+    if (!kv->ctx) return fail(nullptr, kKvClosed);
     return append(kv, layer, seq, pos, n, nullptr, k_rows, v_rows, q, n_head, q_stride, flags);
 }
 
 int zwg_kv_append_batch(zwg_kv *kv, uint64_t layer, uint64_t seq0, uint64_t n_seq, const int32_t *pos_dev,
                         const float *k_rows, const float *v_rows, float *q, uint64_t n_head, uint64_t q_stride) {
     if (!kv) return fail(nullptr, "null kv");
+    if (!kv->ctx) return fail(nullptr, kKvClosed);
     if (!pos_dev) return fail(kv->ctx, "null position array");
     return append(kv, layer, seq0, 0, n_seq, pos_dev, k_rows, v_rows, q, n_head, q_stride, 0);
 }
 
 int zwg_kv_read(zwg_kv *kv, uint64_t layer, uint64_t seq, float *k_host, float *v_host) {
     if (!kv) return fail(nullptr, "null kv");
+    if (!kv->ctx) return fail(nullptr, kKvClosed);
     zwg_ctx *ctx = kv->ctx;
     if (layer >= kv->desc.n_layer || seq >= kv->desc.n_seq) return fail(ctx, "kv layer or sequence out of range");
     hipError_t e = hipSetDevice(ctx->device);

@@ -333,6 +333,25 @@ struct zwg_q8w {
 
 namespace {
 
+const char *const kQ8wClosed = "the int8 weights' context is closed";
+
+// Free the packed weights' device memory (after the work queued on their context's stream).
+void free_q8w(zwg_q8w *w) {
+    (void)hipSetDevice(w->ctx->device);
+    (void)hipStreamSynchronize(w->ctx->stream);
+    if (w->q) (void)hipFree(w->q);
+    if (w->scales) (void)hipFree(w->scales);
+    w->q = nullptr;
+    w->scales = nullptr;
+}
+
+// zwg_close of the weights' context: the packed copy goes with it
+void detach_q8w(void *obj) {
+    auto *w = static_cast<zwg_q8w *>(obj);
+    free_q8w(w);
+    w->ctx = nullptr;
+}
+
 // The token-step path (m <= 64) over n_w resident weight sets sharing x and k (checked by the
 // callers).
 int run_q8w_token_step(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t n_w, const zwg_q8w *const *w,
@@ -359,6 +378,7 @@ int run_q8w_token_step(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t n_w, c
 int run_linear_q8w(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, const float *bias, float *out,
                    uint32_t epi) {
     if (!w) return fail(ctx, "null weights");
+    if (!w->ctx) return fail(ctx, kQ8wClosed);
     if (epi > zwg_ew::kEpiAdd) return fail(ctx, "unknown epilogue");
     const std::string msg = check_linear(m, w->k, ZWG_W_Q8, w->n);
     if (!msg.empty()) return fail(ctx, msg);
@@ -445,20 +465,22 @@ int zwg_q8w_create(zwg_ctx *ctx, const int8_t *q, const float *scales, uint64_t 
         delete w;
         return fail_hip(ctx, "int8 weight packing (q 16-byte and scales 4-byte aligned?)", e);
     }
+    add_child(ctx, w, detach_q8w);
     *out = w;
     return ZWG_OK;
 }
 
 void zwg_q8w_destroy(zwg_q8w *w) {
     if (!w) return;
-    (void)hipSetDevice(w->ctx->device);
-    (void)hipStreamSynchronize(w->ctx->stream);
-    (void)hipFree(w->q);
-    (void)hipFree(w->scales);
+    if (w->ctx) {
+        remove_child(w->ctx, w);
+        free_q8w(w);
+    }
     delete w;
 }
 
 int zwg_q8w_shape(const zwg_q8w *w, uint64_t *n, uint64_t *k) {
+    if (w && !w->ctx) return fail(nullptr, kQ8wClosed);
     if (!w) return fail(nullptr, "null weights");
     if (n) *n = w->n;
     if (k) *k = w->k;
@@ -484,6 +506,7 @@ int zwg_linear_q8w_group_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t 
     const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
     for (uint32_t j = 0; j < n_w; ++j) {
         if (!w[j]) return fail(ctx, "null weights");
+        if (!w[j]->ctx) return fail(ctx, kQ8wClosed);
         if (w[j]->k != w[0]->k) return fail(ctx, "the weights of a group must share k");
         const std::string msg = check_linear(m, w[j]->k, ZWG_W_Q8, w[j]->n);
         if (!msg.empty()) return fail(ctx, msg);

@@ -1,24 +1,38 @@
 // The library context behind the opaque zwg_ctx of include/zw_gpu.h, and the error / staging
-// helpers the C ABI translation units share (zw_gpu.hip, kv_cache.hip).
+// helpers the C ABI translation units share (zw_gpu.hip, kv_cache.hip, linear.hip).
 #pragma once
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include <string>
+#include <vector>
 
 #include "zw_gpu.h"
+
+// An object made from a context (a zwg_kv, a zwg_q8w) that holds device memory of its own.
+// zwg_close detaches the ones still alive: `detach` frees their device memory and clears their
+// context pointer, so a later destroy only frees the host struct and other calls fail cleanly.
+struct ZwgChild {
+    void *obj;
+    void (*detach)(void *obj);
+};
 
 struct zwg_ctx {
     int device = 0;
     hipStream_t own_stream = nullptr;
     hipStream_t stream = nullptr;
+    // recorded on the old stream and waited on by the new one whenever zwg_set_stream switches
+    // streams: every call shares the workspace, so work queued on one stream must finish before
+    // work on the next touches it
+    hipEvent_t switch_event = nullptr;
     float *workspace = nullptr;
     uint32_t dense_math = ZWG_DENSE_X3; // products of the dense kernel (zwg_set_dense_math)
     uint64_t workspace_bytes = 0;
     // device staging for the host-pointer calls: q, k, v, out
     float *stage[4] = {nullptr, nullptr, nullptr, nullptr};
     uint64_t stage_bytes[4] = {0, 0, 0, 0};
+    std::vector<ZwgChild> children;
     std::string err;
 };
 
@@ -29,5 +43,8 @@ int fail(zwg_ctx *ctx, const std::string &msg);
 int fail_hip(zwg_ctx *ctx, const char *what, hipError_t e);
 // Grow staging buffer i of ctx to at least `bytes` (synchronises the stream when it grows).
 int ensure_stage(zwg_ctx *ctx, int i, uint64_t bytes);
+// Register / unregister an object made from ctx (see ZwgChild).
+void add_child(zwg_ctx *ctx, void *obj, void (*detach)(void *));
+void remove_child(zwg_ctx *ctx, void *obj);
 
 } // namespace zwg_host

@@ -44,6 +44,17 @@ int ensure_stage(zwg_ctx *ctx, int i, uint64_t bytes) {
     return ZWG_OK;
 }
 
+void add_child(zwg_ctx *ctx, void *obj, void (*detach)(void *)) { ctx->children.push_back({obj, detach}); }
+
+void remove_child(zwg_ctx *ctx, void *obj) {
+    auto &c = ctx->children;
+    for (size_t i = 0; i < c.size(); ++i)
+        if (c[i].obj == obj) {
+            c.erase(c.begin() + (ptrdiff_t)i);
+            return;
+        }
+}
+
 } // namespace zwg_host
 
 using namespace zwg_host;
@@ -131,6 +142,14 @@ struct Plan {
 
 uint64_t ceil_div(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
 
+// Split partials in the workspace: (max, sum) pairs [row][chunk][2], then, from the next 256-byte
+// boundary (so the kernels' 16-byte partial stores and the merge's loads stay aligned), the sums
+// [row][chunk][d].  Floats before part_o, and bytes of the whole layout:
+uint64_t part_o_offset(uint64_t n_rows, uint64_t chunks) { return (2 * n_rows * chunks + 63) / 64 * 64; }
+uint64_t split_ws_bytes(uint64_t n_rows, uint64_t chunks, uint64_t d) {
+    return chunks > 1 ? (part_o_offset(n_rows, chunks) + n_rows * chunks * d) * sizeof(float) : 0;
+}
+
 // Chunks of about tau tiles that a unit of w tiles is split into (unit_split's count before
 // the last chunk is trimmed): an upper bound on the chunks of any unit of at most w tiles.
 uint64_t split_bound(uint64_t w, uint64_t tau) { return std::max<uint64_t>(1, (w + tau / 2) / tau); }
@@ -145,7 +164,6 @@ Plan make_plan(const zwg_attn_shape &s, const zwg_batch &b, uint64_t ws_cap, uin
     Plan p;
     const uint64_t group = s.n_head / s.n_head_kv;
     const uint64_t n_rows_total = b.n_batch * s.n_head * s.n_q;
-    const uint64_t row_bytes = (s.d + 2) * sizeof(float);
     uint64_t tile = 0, tau = 1, w_max = 1, units = 0;
     if (s.n_q * group <= (uint64_t)zwg::kDecodeMaxRows) {
         p.kernel = 2;
@@ -184,7 +202,7 @@ Plan make_plan(const zwg_attn_shape &s, const zwg_batch &b, uint64_t ws_cap, uin
     }
     if (units > kMaxSplitUnitsHint) tau = w_max;
     uint64_t chunks = split_bound(w_max, tau);
-    while (chunks > 1 && (n_rows_total * chunks * row_bytes > ws_cap || chunks > kMaxChunks)) {
+    while (chunks > 1 && (split_ws_bytes(n_rows_total, chunks, s.d) > ws_cap || chunks > kMaxChunks)) {
         ++tau;
         chunks = split_bound(w_max, tau);
     }
@@ -192,7 +210,7 @@ Plan make_plan(const zwg_attn_shape &s, const zwg_batch &b, uint64_t ws_cap, uin
     p.max_chunks = (int)chunks;
     p.split_tile = (int)tile;
     p.grid_blocks = p.kernel == 2 ? chunks * s.n_head_kv * b.n_batch : chunks * units;
-    p.ws_bytes = p.max_chunks > 1 ? n_rows_total * p.max_chunks * row_bytes : 0;
+    p.ws_bytes = split_ws_bytes(n_rows_total, (uint64_t)p.max_chunks, s.d);
     p.heavy_first = p.kernel == 1 && s.causal;
     // unsplit non-causal calls: each head's q-blocks on one XCD (measured: same time, 5x fewer
     // L2 misses on the base.en encoder); split ones keep the hardware order (measured faster)
@@ -200,8 +218,23 @@ Plan make_plan(const zwg_attn_shape &s, const zwg_batch &b, uint64_t ws_cap, uin
     return p;
 }
 
-int run(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_attn_shape &s, const zwg_batch &b,
-        float *out) {
+// Where and how a call runs: the context's device, stream, workspace and dense mode, or, for the
+// allocation-free entry point, the caller's stream and the library's static scratch.
+struct Exec {
+    int device;       // hipSetDevice first; -1: the calling thread's current device
+    hipStream_t stream;
+    float *ws;        // split partials
+    uint64_t ws_bytes;
+    uint32_t dense_math;
+};
+
+Exec ctx_exec(const zwg_ctx *ctx) {
+    return Exec{ctx->device, ctx->stream, ctx->workspace, ctx->workspace_bytes, ctx->dense_math};
+}
+
+// Shape and pointer checks, the plan, and the launches.  ctx (may be null) receives the error.
+int run(zwg_ctx *ctx, const Exec &x, const float *q, const float *k, const float *v, const zwg_attn_shape &s,
+        const zwg_batch &b, float *out, Plan *plan_out = nullptr) {
     std::string msg = check_shape(s);
     if (msg.empty()) msg = check_batch(s, b);
     if (!msg.empty()) return fail(ctx, msg);
@@ -209,11 +242,12 @@ int run(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_
     if (!q || !out || (s.n_kv && (!k || !v))) return fail(ctx, "null tensor pointer");
     if (!aligned16(q) || !aligned16(out) || (s.n_kv && (!aligned16(k) || !aligned16(v))))
         return fail(ctx, "q, k, v and out must be 16-byte aligned");
-    const Plan p = make_plan(s, b, ctx->workspace_bytes, ctx->dense_math);
-    if (p.ws_bytes > ctx->workspace_bytes) return fail(ctx, "workspace too small for this call");
+    const Plan p = make_plan(s, b, x.ws_bytes, x.dense_math);
+    if (plan_out) *plan_out = p;
+    if (p.ws_bytes > x.ws_bytes) return fail(ctx, "workspace too small for this call");
     // the row-major decode kernel and the x3 dense kernel address one item's K/V rows (and the
     // dense kernel one KV head's K^T rows) with 32-bit byte offsets
-    const bool dense_x3 = p.kernel == 1 && ctx->dense_math != ZWG_DENSE_FP32;
+    const bool dense_x3 = p.kernel == 1 && x.dense_math != ZWG_DENSE_FP32;
     if ((p.kernel == 2 && !s.kt_stride) || dense_x3) {
         if (s.n_kv > 0 && ((s.n_kv - 1 + (dense_x3 ? 32 : 0)) * s.kv_stride + s.d) * sizeof(float) > 0x7fffffffull)
             return fail(ctx, "K/V rows of one batch item must span less than 2 GiB");
@@ -251,23 +285,39 @@ int run(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_
     a.heavy_first = p.heavy_first;
     a.xcd_group = p.xcd_group;
     a.rows_per_unit = p.rows_per_unit;
-    a.part_ml = ctx->workspace;
-    a.part_o = ctx->workspace + (p.max_chunks > 1 ? 2 * b.n_batch * s.n_head * s.n_q * (uint64_t)p.max_chunks : 0);
+    const uint64_t n_rows = b.n_batch * s.n_head * s.n_q;
+    a.part_ml = x.ws;
+    a.part_o = x.ws + (p.max_chunks > 1 ? part_o_offset(n_rows, (uint64_t)p.max_chunks) : 0);
 
-    hipError_t e = hipSetDevice(ctx->device);
+    hipError_t e = hipSuccess;
+    if (x.device >= 0) e = hipSetDevice(x.device);
     if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
     int blocks = 0;
     if (p.kernel == 1)
-        e = ctx->dense_math == ZWG_DENSE_FP32 ? zwg::launch_flash(a, (int)s.d, ctx->stream, &blocks)
-                                              : zwg::launch_flash_x3(a, (int)s.d, ctx->stream, &blocks);
+        e = x.dense_math == ZWG_DENSE_FP32 ? zwg::launch_flash(a, (int)s.d, x.stream, &blocks)
+                                            : zwg::launch_flash_x3(a, (int)s.d, x.stream, &blocks);
     else
-        e = zwg::launch_decode(a, (int)s.d, (int)(s.n_q * a.group), ctx->stream, &blocks);
+        e = zwg::launch_decode(a, (int)s.d, (int)(s.n_q * a.group), x.stream, &blocks);
     if (e != hipSuccess) return fail_hip(ctx, "attention kernel launch", e);
     if (p.max_chunks > 1) {
-        e = zwg::launch_combine(a, (int)s.d, ctx->stream);
+        e = zwg::launch_combine(a, (int)s.d, x.stream);
         if (e != hipSuccess) return fail_hip(ctx, "combine kernel launch", e);
     }
     return ZWG_OK;
+}
+
+// True when any of the n_rows rows of `cols` floats at `stride` holds an infinity or a NaN.
+bool any_non_finite(const float *p, uint64_t n_rows, uint64_t cols, uint64_t stride) {
+    uint32_t bad = 0;
+    for (uint64_t r = 0; r < n_rows; ++r) {
+        const float *row = p + r * stride;
+        for (uint64_t c = 0; c < cols; ++c) {
+            uint32_t bits;
+            std::memcpy(&bits, row + c, sizeof bits);
+            bad |= (uint32_t)((bits & 0x7f800000u) == 0x7f800000u);
+        }
+    }
+    return bad != 0;
 }
 
 } // namespace
@@ -329,9 +379,16 @@ int zwg_open(int device, const zwg_limits *limits, zwg_ctx **out) {
         return fail(nullptr, "unknown dense_math");
     }
     ctx->dense_math = limits ? limits->dense_math : ZWG_DENSE_X3;
+    e = hipEventCreateWithFlags(&ctx->switch_event, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        (void)hipStreamDestroy(ctx->own_stream);
+        delete ctx;
+        return fail_hip(nullptr, "hipEventCreate", e);
+    }
     void *ws = nullptr;
     e = hipMalloc(&ws, ctx->workspace_bytes);
     if (e != hipSuccess) {
+        (void)hipEventDestroy(ctx->switch_event);
         (void)hipStreamDestroy(ctx->own_stream);
         delete ctx;
         return fail_hip(nullptr, "hipMalloc (workspace)", e);
@@ -352,16 +409,29 @@ void zwg_close(zwg_ctx *ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    // objects made from this context and not destroyed yet lose their device memory now
+    const std::vector<ZwgChild> children = ctx->children;
+    for (const ZwgChild &c : children) c.detach(c.obj);
+    ctx->children.clear();
     for (auto &s : ctx->stage)
         if (s) (void)hipFree(s);
     if (ctx->workspace) (void)hipFree(ctx->workspace);
+    if (ctx->switch_event) (void)hipEventDestroy(ctx->switch_event);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
 }
 
 int zwg_set_stream(zwg_ctx *ctx, void *hip_stream) {
     if (!ctx) return fail(nullptr, "null context");
-    ctx->stream = static_cast<hipStream_t>(hip_stream);
+    hipStream_t next = static_cast<hipStream_t>(hip_stream);
+    if (next == ctx->stream) return ZWG_OK;
+    // every call of the context writes the same workspace (split partials, staging), so work
+    // queued on the new stream waits for what is already queued on the old one
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e == hipSuccess) e = hipEventRecord(ctx->switch_event, ctx->stream);
+    if (e == hipSuccess) e = hipStreamWaitEvent(next, ctx->switch_event, 0);
+    if (e != hipSuccess) return fail_hip(ctx, "stream switch ordering", e);
+    ctx->stream = next;
     return ZWG_OK;
 }
 
@@ -378,13 +448,13 @@ int zwg_attention_dev(zwg_ctx *ctx, const float *q, const float *k, const float 
                       float *out) {
     if (!ctx || !shape) return fail(ctx, "null context or shape");
     const zwg_batch one{1, 0, 0, 0, 0, nullptr};
-    return run(ctx, q, k, v, *shape, one, out);
+    return run(ctx, ctx_exec(ctx), q, k, v, *shape, one, out);
 }
 
 int zwg_attention_batch_dev(zwg_ctx *ctx, const float *q, const float *k, const float *v,
                             const zwg_attn_shape *shape, const zwg_batch *batch, float *out) {
     if (!ctx || !shape || !batch) return fail(ctx, "null context, shape or batch");
-    return run(ctx, q, k, v, *shape, *batch, out);
+    return run(ctx, ctx_exec(ctx), q, k, v, *shape, *batch, out);
 }
 
 int zwg_attention_ex(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_attn_shape *shape,
@@ -413,7 +483,9 @@ int zwg_attention_ex(zwg_ctx *ctx, const float *q, const float *k, const float *
     if (e == hipSuccess && v_n) e = hipMemcpyAsync(ctx->stage[2], v, v_n * F, hipMemcpyHostToDevice, ctx->stream);
     if (e != hipSuccess) return fail_hip(ctx, "hipMemcpyAsync (upload)", e);
     const zwg_batch one{1, 0, 0, 0, 0, nullptr};
-    int rc = run(ctx, ctx->stage[0], ctx->stage[1], ctx->stage[2], s, one, ctx->stage[3]);
+    Exec x = ctx_exec(ctx);
+    Plan p;
+    int rc = run(ctx, x, ctx->stage[0], ctx->stage[1], ctx->stage[2], s, one, ctx->stage[3], &p);
     if (rc != ZWG_OK) return rc;
     // copy back only each row's n_head*d columns: out's other columns stay the caller's
     e = hipMemcpy2DAsync(out, s.out_stride * F, ctx->stage[3], s.out_stride * F, hd * F, s.n_q, hipMemcpyDeviceToHost,
@@ -421,6 +493,21 @@ int zwg_attention_ex(zwg_ctx *ctx, const float *q, const float *k, const float *
     if (e != hipSuccess) return fail_hip(ctx, "hipMemcpy2DAsync (download)", e);
     e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) return fail_hip(ctx, "hipStreamSynchronize", e);
+    // The x3 dense kernel needs keys (and scaled queries) within f16 range; outside it the rows
+    // that see such a key come out NaN.  The reference gives finite results for any finite
+    // input (src/ops.zig:562-590), so a non-finite result of the x3 kernel is computed again on
+    // the fp32-MFMA kernel, which has no range condition (and reproduces any NaN or infinity the
+    // inputs themselves carry).
+    if (p.kernel == 1 && x.dense_math != ZWG_DENSE_FP32 && any_non_finite(out, s.n_q, hd, s.out_stride)) {
+        x.dense_math = ZWG_DENSE_FP32;
+        rc = run(ctx, x, ctx->stage[0], ctx->stage[1], ctx->stage[2], s, one, ctx->stage[3]);
+        if (rc != ZWG_OK) return rc;
+        e = hipMemcpy2DAsync(out, s.out_stride * F, ctx->stage[3], s.out_stride * F, hd * F, s.n_q,
+                             hipMemcpyDeviceToHost, ctx->stream);
+        if (e != hipSuccess) return fail_hip(ctx, "hipMemcpy2DAsync (download)", e);
+        e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) return fail_hip(ctx, "hipStreamSynchronize", e);
+    }
     return ZWG_OK;
 }
 

@@ -18,6 +18,7 @@ from __future__ import annotations
 
 import ctypes
 import threading
+import weakref
 from dataclasses import dataclass
 from typing import Optional
 
@@ -112,6 +113,11 @@ class Context:
             raise ZwgError(_lib.last_error(None))
         self._h = h
         self.device = device
+        # objects made from this context (KVCache, Q8Resident): closed before the context is
+        self._children = weakref.WeakSet()
+
+    def _adopt(self, child) -> None:
+        self._children.add(child)
 
     def set_dense_math(self, mode: int) -> None:
         """Switch the dense kernel's arithmetic (_lib.DENSE_X3 or _lib.DENSE_FP32) for later calls."""
@@ -119,6 +125,8 @@ class Context:
 
     def close(self) -> None:
         if getattr(self, "_h", None):
+            for child in list(getattr(self, "_children", ())):
+                child.close()
             self._L.zwg_close(self._h)
             self._h = None
 
@@ -136,6 +144,8 @@ class Context:
 
     @property
     def handle(self):
+        if not self._h:
+            raise ZwgError("the context is closed")
         return self._h
 
     def _check(self, rc: int) -> None:
@@ -343,6 +353,7 @@ class KVCache:
         self.kvw = n_head_kv * d
         self.info = _lib.KVInfoC()
         ctx._check(self._L.zwg_kv_get_info(self._h, ctypes.byref(self.info)))
+        ctx._adopt(self)
 
     def close(self) -> None:
         if getattr(self, "_h", None):
@@ -534,6 +545,7 @@ class Q8Resident:
                                        ctypes.byref(h))
         ctx._check(rc)
         self._h = h.value
+        ctx._adopt(self)
 
     @property
     def handle(self):
