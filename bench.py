@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
 """Benchmark of zwhisper's attention hot path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--workload N] [--only] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--workload N] [--only] [--dense-math x3|fp32]
+                    [--extra NAME] [--no-cpu] [--no-parity]
 
 A step is one pass of the attention path over one batch of synthetic input, already resident
 in HBM.  The headline line (one JSON object on stdout) is workload 2, Whisper base.en encoder
@@ -10,16 +11,25 @@ algorithmic work (4*d*H per visible (q, k) pair, src/bench.zig:76).  The other f
 are measured too (unless --only) and reported under "workloads" in the same line, each with its
 own roofline: 16-bit MFMA (2.5 PFLOP/s, f16 and bf16 alike) for the dense ones, whose kernel
 computes each f32 product as three 16-bit products of hi/lo-split operands (ceiling: a third of
-that peak), HBM (8 TB/s) for
-the decode ones.  Unless --only, the headline workload is also run on the fp32-MFMA kernel
-("base_enc_x16_fp32mfma", fp32 peak 157.3 TFLOP/s).
+that peak), HBM (8 TB/s) for the decode ones.  Unless --only, the three dense workloads are also
+run on the fp32-MFMA kernel ("*_fp32mfma", fp32 peak 157.3 TFLOP/s).  Every attention workload
+carries "parity": its outputs against the f64 closed form, checked after the timed region, with
+the bar of the arithmetic that ran.  The two encoder workloads also carry "dropin_host_buffers":
+the host-pointer drop-in (zwg_attention_ex, H2D + kernels + D2H per window), which includes PCIe
+and is never the headline value.
 
 Timing: W untimed warm-up steps, then exactly K steps bracketed by torch.cuda.synchronize();
 each step's launches are also bracketed by HIP events on the stream they run on, whose mean is
 the kernel time used for the roofline.  Decode workloads rotate between two copies of their
 inputs so no step finds its K/V in the 256 MB last-level cache left by the previous one.
 The CPU baseline is the C restatement of the reference's multithreaded attention (oracle/),
-timed on this host's cores on a bounded sample of the same workload.
+timed on this host's cores on a bounded sample of the same workload, on CPUs - 1 threads (the
+reference's default pool) over the CPUs this job may use (affinity, cgroup quota and
+OMP_NUM_THREADS; "host" in the line gives them and the CPU model), and on min(that, 4) threads for
+decode (the reference's decode pool).
+
+--extra NAME measures one of the workloads around the attention path alone; --workload N --only
+[--dense-math fp32] one attention workload alone (the forms the rocprofv3 counter runs use).
 
 Unless --only, the line also carries the device cache updates of three of the workloads (the K/V
 rows of a step written into the HBM-resident caches, with rotary positions for Qwen2), as
@@ -39,6 +49,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -73,13 +84,54 @@ def cpu_timing(best: float, mean: float, runs: int) -> str:
     return f"best of {runs} runs over {CPU_MIN_SECONDS:g}+ s after one warm-up (mean {1e3 * mean:.2f} ms)"
 
 
-def host_threads() -> int:
-    """The reference's default thread count, CPUs - 1 (src/main.zig:126), on this host's share."""
+def _cgroup_cpus():
+    """CPUs this process's cgroup may use (cpu.max quota / period), or None when unlimited."""
+    for path in ("/sys/fs/cgroup/cpu.max",):
+        try:
+            with open(path) as f:
+                quota, period = f.read().split()[:2]
+            if quota != "max":
+                return float(quota) / float(period)
+        except (OSError, ValueError):
+            pass
+    return None
+
+
+def host_cpus() -> dict:
+    """The CPUs this process may use: the affinity mask (what `nproc` reports), bounded by the
+    cgroup's CPU quota and by OMP_NUM_THREADS when set (the share a shared host grants this job),
+    and the CPU model."""
     try:
-        n = len(os.sched_getaffinity(0))
+        nproc = len(os.sched_getaffinity(0))
     except AttributeError:
-        n = os.cpu_count() or 1
-    return max(1, min(n, 16) - 1)
+        nproc = os.cpu_count() or 1
+    quota = _cgroup_cpus()
+    try:
+        omp = int(os.environ.get("OMP_NUM_THREADS", "")) or None
+    except ValueError:
+        omp = None
+    limits = [nproc]
+    if quota is not None:
+        limits.append(int(math.ceil(quota)))
+    if omp is not None:
+        limits.append(omp)
+    cpus = min(limits)
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": nproc, "cgroup_cpus": quota, "omp_num_threads": omp, "cpus": max(1, cpus), "cpu_model": model}
+
+
+def host_threads() -> int:
+    """The reference's default pool size, CPUs - 1 (src/main.zig:126, src/capi.zig:71), over the
+    CPUs this process may use (host_cpus)."""
+    return max(1, host_cpus()["cpus"] - 1)
 
 
 class Workload:
@@ -119,6 +171,7 @@ class Workload:
             q, k, v = np.stack(qs), np.stack(ks), np.stack(vs)
             self.shape = AttnShape(w.n_q, w.n_kv_cap, w.n_head, w.n_head_kv, w.d, w.n_head * w.d,
                                    w.n_head_kv * w.d, w.n_head * w.d, w.causal, kt)
+            self.host = {"q": q, "k": k, "v": v}
             base = {"q": self._dev(q), "k": self._dev(k), "v": self._dev(v)}
             base["out"] = t.empty((w.n_items, w.n_q, w.n_head * w.d), dtype=t.float32, device="cuda")
             self.bstrides = (q[0].size, k[0].size, v[0].size, w.n_q * w.n_head * w.d)
@@ -169,6 +222,7 @@ class Workload:
 
     # ---- one step
     def step(self, i: int):
+        self.last = i
         s = self.sets[i % len(self.sets)]
         w, ctx = self.spec, self.ctx
         if self.number in (1, 2, 4):
@@ -184,6 +238,79 @@ class Workload:
         else:
             qb, kb, vb, ob = self.bstrides
             ctx.attention_batch_dev(s["q"], s["k"], s["v"], self.shape, s["out"], w.n_items, qb, kb, vb, ob, s["nkv"])
+
+    def parity(self, x3: bool) -> dict:
+        """The last step's outputs against the f64 closed form (oracle/naive.py), outside the timed
+        region: max abs error and normwise relative error ||gpu - ref||_inf / ||ref||_inf, with the
+        bar of the arithmetic that ran (x3 dense: 5e-5 and 3e-5; f32: 2e-4 and 1e-3)."""
+        from oracle import naive
+        from zwhisper_amd.ops import AttnShape
+
+        self.torch.cuda.synchronize()
+        w, n, W = self.spec, self.number, self.W
+        s = self.sets[self.last % len(self.sets)]
+        pairs = []  # (got, ref)
+        if n in (1, 2, 4):
+            out = s["out"].cpu().numpy()
+            items = [0, 7, 15] if n == 2 else [0]
+            for i in items:
+                pairs.append((out[i], naive.attention_f64(self.host["q"][i], self.host["k"][i], self.host["v"][i],
+                                                          self.shape)))
+            what = f"items {items} of {w.n_items}, every output"
+        elif n == 3:
+            ns = w.n_head * w.d
+            os_, oc = s["os"].cpu().numpy(), s["oc"].cpu().numpy()
+            h = self.host
+            for i in range(w.n_items):
+                L = int(self.lengths[i])
+                sh = AttnShape(1, L, w.n_head, w.n_head, w.d, ns, ns, ns, True, None)
+                pairs.append((os_[i], naive.attention_f64(h["qs"][i], h["ks"][i, :L], h["vs"][i, :L], sh)))
+                pairs.append((oc[i], naive.attention_f64(h["qc"][i], h["kc"][i], h["vc"][i], self.shape_cross)))
+            what = f"all {w.n_items} windows, self and cross"
+            x3 = False
+        else:
+            ns, kvw, cap = w.n_head * w.d, w.n_head_kv * w.d, w.n_kv_cap
+            out = s["out"].cpu().numpy()
+            h = self.host
+            for i in range(w.n_items):
+                L = int(self.lengths[i])
+                sh = AttnShape(1, L, w.n_head, w.n_head_kv, w.d, ns, kvw, ns, True, cap)
+                pairs.append((out[i], naive.attention_f64(h["q"][i], h["k"][i], h["v"][i], sh)))
+            what = f"all {w.n_items} sequences"
+            x3 = False
+        err = max(float(np.abs(g.astype(np.float64).reshape(-1) - r).max()) for g, r in pairs)
+        ref_max = max(float(np.abs(r).max()) for _, r in pairs)
+        bar = {"max_abs": 5e-5, "normwise_rel": 3e-5} if x3 else {"max_abs": 2e-4, "normwise_rel": 1e-3}
+        rel = err / max(ref_max, 1e-30)
+        return {"vs": "f64 closed form (oracle/naive.py)", "checked": what, "max_abs": err, "normwise_rel": rel,
+                "bar": bar, "within_bar": err <= bar["max_abs"] and rel <= bar["normwise_rel"]}
+
+    def dropin(self, reps: int = 3) -> dict:
+        """The host-pointer drop-in (zwg_attention_ex, what the unchanged src/encoder.zig:167 call
+        binds): one synchronous call per window on pageable host buffers, H2D of q/k/v, the kernels
+        and D2H of out, timed on the host clock.  Includes PCIe: never the headline value."""
+        w, n = self.spec, self.number
+        assert n in (1, 2)
+        calls = []
+        for i in range(w.n_items):
+            calls.append((np.ascontiguousarray(self.host["q"][i]).reshape(-1),
+                          np.ascontiguousarray(self.host["k"][i]).reshape(-1),
+                          np.ascontiguousarray(self.host["v"][i]).reshape(-1),
+                          np.zeros(w.n_q * w.n_head * w.d, np.float32)))
+
+        def run():
+            for q, k, v, out in calls:
+                self.ctx.attention_ex_host(q, k, v, self.shape, out)
+
+        best, mean, runs = time_cpu(run, reps)
+        dev_out = self.sets[self.last % len(self.sets)]["out"].cpu().numpy()
+        same = all(np.array_equal(out, dev_out[i].reshape(-1)) for i, (_, _, _, out) in enumerate(calls))
+        moved = sum(q.nbytes + k.nbytes + v.nbytes + out.nbytes for q, k, v, out in calls)
+        return {"value": self.work / best / 1e12, "unit": "TFLOP/s", "ms_per_step": 1e3 * best,
+                "ms_per_step_mean": 1e3 * mean, "calls_per_step": w.n_items, "pcie_bytes_per_step": moved,
+                "equals_device_result": bool(same),
+                "note": "zwg_attention_ex per window on pageable host buffers (H2D q/k/v + kernels + D2H out), "
+                        "synchronous; best of " + f"{runs} runs"}
 
     def free(self):
         self.sets = []
@@ -700,6 +827,129 @@ def dense_roofline(achieved: float, dense_math: int) -> dict:
             "frac": achieved / PEAK_MFMA_F32}
 
 
+def _attention_line(wl: Workload, r: dict, dense_math: int) -> dict:
+    """Result record of an attention workload: value at wall time per step, roofline at the
+    kernels' event time per step."""
+    spec = wl.spec
+    per_step = wl.work
+    achieved = per_step / (r["kernel_ms_mean"] * 1e-3)
+    if spec.bound == "mfma":
+        roof = dense_roofline(achieved, dense_math)
+        value = per_step / (r["ms_per_step"] * 1e-3) / 1e12
+        unit = "TFLOP/s"
+        dtype = DENSE_DTYPE if dense_math == 0 else "f32 (fp32 MFMA)"
+    else:
+        roof = {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                "frac": achieved / PEAK_HBM}
+        value = per_step / (r["ms_per_step"] * 1e-3) / 1e9
+        unit = "GB/s"
+        dtype = "f32"
+    return {"workload": spec.name, "description": spec.description, "value": value, "unit": unit,
+            "rate": step_rate(wl.number, r["ms_per_step"]), "ms_per_step": r["ms_per_step"],
+            "kernel_ms_mean": r["kernel_ms_mean"], "kernel_ms_median": r["kernel_ms_median"],
+            "kernel_ms_min": r["kernel_ms_min"], "algorithmic_work_per_step": per_step, "dtype": dtype,
+            "roofline": roof}
+
+
+def _say(name: str, res: dict, peak_name: str) -> None:
+    cpu = res.get("cpu_baseline")
+    par = res.get("parity")
+    print(f"[bench] {name}: {res['value']:.2f} {res['unit']} ({res['ms_per_step']:.4f} ms/step, kernels "
+          f"{res['kernel_ms_mean']:.4f} ms, {100 * res['roofline']['frac']:.1f}% of {peak_name})"
+          + (f", parity max abs {par['max_abs']:.2e} rel {par['normwise_rel']:.2e}" if par else "")
+          + (f", cpu {cpu['value']:.3f} {cpu['unit']} on {cpu['cores']} threads" if cpu else ""),
+          file=sys.stderr, flush=True)
+
+
+EXTRAS = ("small_dec_kv_append_x32", "qwen15_kv_append_x64", "qwen05_prefill_kv_append", "base_enc_linear_x16",
+          "base_enc_layer_x16", "qwen15_logits_q8_x64", "qwen15_decode_q8_linear_x64", "small_dec_q8_linear_x32")
+
+
+def run_extra(name: str, torch, ctx, args, threads: int) -> dict:
+    """One of the measurements around the attention path (cache updates, projections, a whole
+    encoder layer, int8 decode-step projections)."""
+    if name in ("small_dec_kv_append_x32", "qwen15_kv_append_x64", "qwen05_prefill_kv_append"):
+        wl = AppendWorkload(name, torch, ctx)
+        r = time_workload(wl, args.steps, args.warmup)
+        dev_ms = wl.device_time(max(args.steps, 20))
+        achieved = wl.work / (dev_ms * 1e-3)
+        res = {"workload": name, "description": wl.description,
+               "value": wl.work / (r["ms_per_step"] * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": r["ms_per_step"],
+               "kernel_ms_mean": dev_ms, "kernel_ms_note": "device time per update, from a HIP graph of "
+               "back-to-back updates; ms_per_step includes this Python harness's launch overhead",
+               "algorithmic_work_per_step": wl.work,
+               "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                            "frac": achieved / PEAK_HBM, "traffic": None}}
+        if not args.no_cpu:
+            res["cpu_baseline"] = wl.cpu_baseline()
+        wl.free()
+        _say(name, res, "hbm peak")
+        return res
+    if name == "base_enc_linear_x16":
+        wl = LinearWorkload(torch, ctx)
+        r = time_workload(wl, args.steps, args.warmup)
+        achieved = wl.work / (r["kernel_ms_mean"] * 1e-3)
+        res = {"workload": wl.name, "description": wl.description,
+               "value": wl.work / (r["ms_per_step"] * 1e-3) / 1e12, "unit": "TFLOP/s",
+               "ms_per_step": r["ms_per_step"], "kernel_ms_mean": r["kernel_ms_mean"],
+               "kernel_ms_median": r["kernel_ms_median"], "kernel_ms_min": r["kernel_ms_min"],
+               "algorithmic_work_per_step": wl.work,
+               "dtype": "f32 activations x f16 weights, f32 accumulation (f16 MFMA, x split into two f16 terms)",
+               "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_MFMA_F16 / 1e12,
+                            "unit": "TFLOP/s", "frac": achieved / PEAK_MFMA_F16, "traffic": traffic_for(wl.name),
+                            "note": "two f16 MFMAs per f32 x f16 product: the kernels' ceiling is frac 0.5"}}
+        if not args.no_cpu:
+            res["cpu_baseline"] = wl.cpu_baseline(threads)
+        wl.free()
+        _say(name, res, "f16 mfma peak")
+        return res
+    if name == "base_enc_layer_x16":
+        wl = EncoderLayerWorkload(torch, ctx)
+        r = time_workload(wl, args.steps, args.warmup)
+        achieved = wl.work / (r["kernel_ms_mean"] * 1e-3)
+        peak = wl.work / wl.ideal_s
+        res = {"workload": wl.name, "description": wl.description,
+               "value": wl.work / (r["ms_per_step"] * 1e-3) / 1e12, "unit": "TFLOP/s",
+               "ms_per_step": r["ms_per_step"], "kernel_ms_mean": r["kernel_ms_mean"],
+               "kernel_ms_median": r["kernel_ms_median"], "kernel_ms_min": r["kernel_ms_min"],
+               "algorithmic_work_per_step": wl.work,
+               "dtype": "f32 (projections: f32 x f16 on f16 MFMA with x split into two f16 terms; attention: x3 "
+                        "16-bit MFMA)",
+               "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
+                            "frac": achieved / peak, "traffic": traffic_for(wl.name),
+                            "note": "peak = the layer's flops over the time they take at their own peaks: "
+                                    "projections at half the f16 MFMA peak, attention at a third of the 16-bit MFMA "
+                                    "peak"}}
+        if not args.no_cpu:
+            res["cpu_baseline"] = wl.cpu_baseline(threads)
+        wl.free()
+        _say(name, res, "the layer's mfma roofline")
+        return res
+    for make in q8_workloads(torch, ctx):
+        wl = make()
+        if wl.name != name:
+            wl.free()
+            continue
+        r = time_workload(wl, args.steps, args.warmup)
+        achieved = wl.work / (r["kernel_ms_mean"] * 1e-3)
+        res = {"workload": wl.name, "description": wl.description,
+               "value": wl.work / (r["ms_per_step"] * 1e-3) / 1e9, "unit": "GB/s",
+               "ms_per_step": r["ms_per_step"], "kernel_ms_mean": r["kernel_ms_mean"],
+               "kernel_ms_median": r["kernel_ms_median"], "kernel_ms_min": r["kernel_ms_min"],
+               "algorithmic_work_per_step": wl.work,
+               "dtype": "f32 activations x int8 block weights, f32 accumulation (f16 MFMA, x split into two "
+                        "f16 terms, block sums scaled in f32)",
+               "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
+                            "frac": achieved / PEAK_HBM, "traffic": traffic_for(wl.name)}}
+        if not args.no_cpu:
+            res["cpu_baseline"] = wl.cpu_baseline(threads)
+        wl.free()
+        torch.cuda.empty_cache()
+        _say(name, res, "hbm peak")
+        return res
+    raise ValueError(f"unknown workload {name}")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -707,7 +957,12 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", type=int, default=2, choices=[1, 2, 3, 4, 5], help="headline workload")
     ap.add_argument("--only", action="store_true", help="measure the headline workload only")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--dense-math", choices=["x3", "fp32"], default="x3",
+                    help="arithmetic of the dense kernel for the headline workload")
+    ap.add_argument("--extra", choices=EXTRAS, default=None,
+                    help="measure only this workload around the attention path (no attention workloads)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--no-parity", action="store_true", help="skip the f64 parity checks of the outputs")
     ap.add_argument("--calibrate-copy", type=int, metavar="MIB", default=0,
                     help="only run a plain device copy of MIB MiB five times (the reference kernel that "
                          "scales rocprofv3's FETCH_SIZE/WRITE_SIZE counters to bytes)")
@@ -737,151 +992,81 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "launches": 5}), flush=True)
         return 0
+    host = host_cpus()
+    threads = host_threads()
+    print(f"[bench] host: {host['cpu_model']}, nproc {host['nproc']}, CPUs for this job {host['cpus']}, "
+          f"CPU baselines on {threads} threads (4 for decode)", file=sys.stderr, flush=True)
+    head_math = z.DENSE_FP32 if args.dense_math == "fp32" else z.DENSE_X3
     ctx = z.Context(0)
-    numbers = [args.workload] + ([] if args.only else [n for n in (1, 2, 3, 4, 5) if n != args.workload])
     results = {}
+    if args.extra:
+        res = run_extra(args.extra, torch, ctx, args, threads)
+        ctx.close()
+        if "cpu_baseline" in res:
+            res["cpu_baseline"].update({"nproc": host["nproc"], "cpus_for_job": host["cpus"],
+                                        "cpu_model": host["cpu_model"]})
+        line = {"metric": res["workload"], "value": res["value"], "unit": res["unit"], "n_gpus": 1,
+                "steps": args.steps, "warmup": args.warmup, "ms_per_step": res["ms_per_step"],
+                "higher_is_better": True, "host": host, "result": res}
+        print(json.dumps(line), flush=True)
+        return 0
+
+    numbers = [args.workload] + ([] if args.only else [n for n in (1, 2, 3, 4, 5) if n != args.workload])
+    head_ctx = z.Context(0, dense_math=head_math) if head_math != z.DENSE_X3 else ctx
     for n in numbers:
         spec = W.WORKLOADS[n]
         copies = 2 if spec.bound == "hbm" else 1
-        wl = Workload(n, torch, ctx, copies)
+        c = head_ctx if n == args.workload else ctx
+        dm = head_math if n == args.workload else z.DENSE_X3
+        wl = Workload(n, torch, c, copies)
         r = time_workload(wl, args.steps, args.warmup)
-        per_step = wl.work
-        if spec.bound == "mfma":
-            achieved = per_step / (r["kernel_ms_mean"] * 1e-3)
-            roof = dense_roofline(achieved, z.DENSE_X3)
-            value = per_step / (r["ms_per_step"] * 1e-3) / 1e12
-            unit = "TFLOP/s"
-        else:
-            achieved = per_step / (r["kernel_ms_mean"] * 1e-3)
-            roof = {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                    "frac": achieved / PEAK_HBM}
-            value = per_step / (r["ms_per_step"] * 1e-3) / 1e9
-            unit = "GB/s"
-        roof["traffic"] = traffic_for(spec.name)
-        res = {"workload": spec.name, "description": spec.description, "value": value, "unit": unit,
-               "rate": step_rate(n, r["ms_per_step"]),
-               "ms_per_step": r["ms_per_step"], "kernel_ms_mean": r["kernel_ms_mean"],
-               "kernel_ms_min": r["kernel_ms_min"], "algorithmic_work_per_step": per_step,
-               "dtype": DENSE_DTYPE if spec.bound == "mfma" else "f32", "roofline": roof}
+        res = _attention_line(wl, r, dm)
+        res["roofline"]["traffic"] = traffic_for(spec.name if dm == z.DENSE_X3 else spec.name + "_fp32mfma")
+        if not args.no_parity:
+            res["parity"] = wl.parity(x3=dm == z.DENSE_X3)
+        if not args.only and n in (1, 2) and dm == z.DENSE_X3:
+            res["dropin_host_buffers"] = wl.dropin()
         if not args.no_cpu:
-            res["cpu_baseline"] = cpu_baseline(n, host_threads())
+            res["cpu_baseline"] = cpu_baseline(n, threads)
             if n in (3, 5):
-                res["cpu_baseline_all_threads"] = cpu_baseline(n, host_threads(), decode_pool=False)
+                res["cpu_baseline_all_threads"] = cpu_baseline(n, threads, decode_pool=False)
             if n == 4:
-                res["cpu_baseline_one_call"] = cpu_baseline(n, host_threads(), one_call=True)
+                res["cpu_baseline_one_call"] = cpu_baseline(n, threads, one_call=True)
         results[n] = res
-        print(f"[bench] {spec.name}: {value:.2f} {unit} ({r['ms_per_step']:.4f} ms/step, kernel "
-              f"{r['kernel_ms_mean']:.4f} ms, {100 * roof['frac']:.1f}% of {spec.bound} peak)"
-              + (f", cpu {res['cpu_baseline']['value']:.3f} {res['cpu_baseline']['unit']}" if not args.no_cpu else ""),
-              file=sys.stderr, flush=True)
+        _say(spec.name, res, f"{spec.bound} peak")
         wl.free()
         del wl
         torch.cuda.empty_cache()
+    if head_ctx is not ctx:
+        head_ctx.close()
     if not args.only:
-        # the headline dense workload again on the fp32-MFMA kernel (ZWG_DENSE_FP32), for comparison
-        spec = W.WORKLOADS[2]
+        # the dense workloads again on the fp32-MFMA kernel (ZWG_DENSE_FP32), for comparison
         ctx32 = z.Context(0, dense_math=z.DENSE_FP32)
-        wl = Workload(2, torch, ctx32, 1)
-        r = time_workload(wl, args.steps, args.warmup)
-        achieved = wl.work / (r["kernel_ms_mean"] * 1e-3)
-        name = spec.name + "_fp32mfma"
-        res = {"workload": name, "description": spec.description + "; fp32 MFMA kernel (ZWG_DENSE_FP32)",
-               "value": wl.work / (r["ms_per_step"] * 1e-3) / 1e12, "unit": "TFLOP/s",
-               "ms_per_step": r["ms_per_step"], "kernel_ms_mean": r["kernel_ms_mean"],
-               "kernel_ms_min": r["kernel_ms_min"], "algorithmic_work_per_step": wl.work, "dtype": "f32",
-               "roofline": dense_roofline(achieved, z.DENSE_FP32)}
-        res["roofline"]["traffic"] = traffic_for(name)
-        results[name] = res
-        print(f"[bench] {name}: {res['value']:.2f} TFLOP/s ({r['ms_per_step']:.4f} ms/step, kernel "
-              f"{r['kernel_ms_mean']:.4f} ms, {100 * res['roofline']['frac']:.1f}% of fp32 mfma peak)",
-              file=sys.stderr, flush=True)
-        wl.free()
-        del wl
-        ctx32.close()
-        torch.cuda.empty_cache()
-        for name in ("small_dec_kv_append_x32", "qwen15_kv_append_x64", "qwen05_prefill_kv_append"):
-            wl = AppendWorkload(name, torch, ctx)
+        for n in (2, 1, 4):
+            spec = W.WORKLOADS[n]
+            wl = Workload(n, torch, ctx32, 1)
             r = time_workload(wl, args.steps, args.warmup)
-            dev_ms = wl.device_time(max(args.steps, 20))
-            achieved = wl.work / (dev_ms * 1e-3)
-            res = {"workload": name, "description": wl.description,
-                   "value": wl.work / (r["ms_per_step"] * 1e-3) / 1e9, "unit": "GB/s", "ms_per_step": r["ms_per_step"],
-                   "kernel_ms_mean": dev_ms, "kernel_ms_note": "device time per update, from a HIP graph of "
-                   "back-to-back updates; ms_per_step includes this Python harness's launch overhead",
-                   "algorithmic_work_per_step": wl.work,
-                   "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                                "frac": achieved / PEAK_HBM, "traffic": None}}
-            if not args.no_cpu:
-                res["cpu_baseline"] = wl.cpu_baseline()
+            name = spec.name + "_fp32mfma"
+            res = _attention_line(wl, r, z.DENSE_FP32)
+            res["workload"] = name
+            res["description"] = spec.description + "; fp32 MFMA kernel (ZWG_DENSE_FP32)"
+            res["roofline"]["traffic"] = traffic_for(name)
+            if not args.no_parity:
+                res["parity"] = wl.parity(x3=False)
             results[name] = res
-            print(f"[bench] {name}: {res['value']:.2f} GB/s ({r['ms_per_step']:.4f} ms/step, device "
-                  f"{dev_ms:.4f} ms, {100 * res['roofline']['frac']:.1f}% of hbm peak)"
-                  + (f", cpu {res['cpu_baseline']['value']:.3f} GB/s" if not args.no_cpu else ""),
-                  file=sys.stderr, flush=True)
-            wl.free()
-        wl = LinearWorkload(torch, ctx)
-        r = time_workload(wl, args.steps, args.warmup)
-        achieved = wl.work / (r["kernel_ms_mean"] * 1e-3)
-        res = {"workload": wl.name, "description": wl.description,
-               "value": wl.work / (r["ms_per_step"] * 1e-3) / 1e12, "unit": "TFLOP/s",
-               "ms_per_step": r["ms_per_step"], "kernel_ms_mean": r["kernel_ms_mean"],
-               "kernel_ms_min": r["kernel_ms_min"], "algorithmic_work_per_step": wl.work,
-               "dtype": "f32 activations x f16 weights, f32 accumulation (f16 MFMA, x split into two f16 terms)",
-               "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_MFMA_F16 / 1e12,
-                            "unit": "TFLOP/s", "frac": achieved / PEAK_MFMA_F16, "traffic": traffic_for(wl.name),
-                            "note": "two f16 MFMAs per f32 x f16 product: the kernels' ceiling is frac 0.5"}}
-        if not args.no_cpu:
-            res["cpu_baseline"] = wl.cpu_baseline(host_threads())
-        results[wl.name] = res
-        print(f"[bench] {wl.name}: {res['value']:.2f} TFLOP/s ({r['ms_per_step']:.4f} ms/step, kernels "
-              f"{r['kernel_ms_mean']:.4f} ms, {100 * res['roofline']['frac']:.1f}% of f16 mfma peak)"
-              + (f", cpu {res['cpu_baseline']['value']:.3f} TFLOP/s" if not args.no_cpu else ""),
-              file=sys.stderr, flush=True)
-        wl.free()
-        wl = EncoderLayerWorkload(torch, ctx)
-        r = time_workload(wl, args.steps, args.warmup)
-        achieved = wl.work / (r["kernel_ms_mean"] * 1e-3)
-        peak = wl.work / wl.ideal_s
-        res = {"workload": wl.name, "description": wl.description,
-               "value": wl.work / (r["ms_per_step"] * 1e-3) / 1e12, "unit": "TFLOP/s",
-               "ms_per_step": r["ms_per_step"], "kernel_ms_mean": r["kernel_ms_mean"],
-               "kernel_ms_min": r["kernel_ms_min"], "algorithmic_work_per_step": wl.work,
-               "dtype": "f32 (projections: f32 x f16 on f16 MFMA with x split into two f16 terms; attention: x3 16-bit MFMA)",
-               "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
-                            "frac": achieved / peak, "traffic": traffic_for(wl.name),
-                            "note": "peak = the layer's flops over the time they take at their own peaks: "
-                                    "projections at half the f16 MFMA peak, attention at a third of the 16-bit MFMA peak"}}
-        if not args.no_cpu:
-            res["cpu_baseline"] = wl.cpu_baseline(host_threads())
-        results[wl.name] = res
-        print(f"[bench] {wl.name}: {res['value']:.2f} TFLOP/s ({r['ms_per_step']:.4f} ms/step, kernels "
-              f"{r['kernel_ms_mean']:.4f} ms, {100 * res['roofline']['frac']:.1f}% of the layer's mfma roofline)"
-              + (f", cpu {res['cpu_baseline']['value']:.3f} TFLOP/s" if not args.no_cpu else ""),
-              file=sys.stderr, flush=True)
-        wl.free()
-        for make in q8_workloads(torch, ctx):
-            wl = make()
-            r = time_workload(wl, args.steps, args.warmup)
-            achieved = wl.work / (r["kernel_ms_mean"] * 1e-3)
-            res = {"workload": wl.name, "description": wl.description,
-                   "value": wl.work / (r["ms_per_step"] * 1e-3) / 1e9, "unit": "GB/s",
-                   "ms_per_step": r["ms_per_step"], "kernel_ms_mean": r["kernel_ms_mean"],
-                   "kernel_ms_min": r["kernel_ms_min"], "algorithmic_work_per_step": wl.work,
-                   "dtype": "f32 activations x int8 block weights, f32 accumulation (f16 MFMA, x split into two "
-                            "f16 terms, block sums scaled in f32)",
-                   "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                                "frac": achieved / PEAK_HBM, "traffic": traffic_for(wl.name)}}
-            if not args.no_cpu:
-                res["cpu_baseline"] = wl.cpu_baseline(host_threads())
-            results[wl.name] = res
-            print(f"[bench] {wl.name}: {res['value']:.2f} GB/s ({r['ms_per_step']:.4f} ms/step, kernels "
-                  f"{r['kernel_ms_mean']:.4f} ms, {100 * res['roofline']['frac']:.1f}% of hbm peak)"
-                  + (f", cpu {res['cpu_baseline']['value']:.3f} GB/s" if not args.no_cpu else ""),
-                  file=sys.stderr, flush=True)
+            _say(name, res, "fp32 mfma peak")
             wl.free()
             del wl
             torch.cuda.empty_cache()
+        ctx32.close()
+        for name in EXTRAS:
+            results[name] = run_extra(name, torch, ctx, args, threads)
     ctx.close()
+    # every CPU baseline states the host it ran on
+    for res in results.values():
+        for key, val in res.items():
+            if key.startswith("cpu_baseline") and isinstance(val, dict):
+                val.update({"nproc": host["nproc"], "cpus_for_job": host["cpus"], "cpu_model": host["cpu_model"]})
 
     head = results[args.workload]
     spec = W.WORKLOADS[args.workload]
@@ -903,8 +1088,12 @@ def main() -> int:
                    "k_layout": "transposed" if spec.kt else "row-major", "parallelism": "single GPU"},
         "roofline": head["roofline"],
         "rate": head["rate"],
+        "kernel_ms_median": head["kernel_ms_median"],
+        "parity": head.get("parity"),
+        "host": host,
         "cpu_baseline": head.get("cpu_baseline"),
         **({"cpu_baseline_all_threads": head["cpu_baseline_all_threads"]} if "cpu_baseline_all_threads" in head else {}),
+        **({"dropin_host_buffers": head["dropin_host_buffers"]} if "dropin_host_buffers" in head else {}),
         "workloads": {r["workload"]: {k: v for k, v in r.items() if k not in ("workload",)}
                       for n, r in results.items() if n != args.workload},
     }
