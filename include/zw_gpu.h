@@ -162,6 +162,25 @@ int zwg_attention_batch_dev(zwg_ctx *ctx, const float *q, const float *k, const 
                             const zwg_attn_shape *shape, const zwg_batch *batch, float *out);
 
 /*
+ * zwg_attention_batch_dev without a context and without any device allocation.  No counterpart in
+ * the reference (its attention never allocates: the caller passes scratch, src/ops.zig:1-2,
+ * :562); this is for callers that cannot call hipMalloc -- code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation.  It runs on the calling thread's current
+ * device and on `hip_stream` (NULL: the null stream), with the dense arithmetic `dense_math`, and
+ * plans and computes exactly as a context opened with the default workspace (same kernels, same
+ * key splits, same results).  batch may be NULL (one item).
+ * Split partial results go to a static device array of ZWG_NOALLOC_SCRATCH_BYTES per GPU, which
+ * the library holds until the process ends: a call whose partials would need more is refused
+ * with an error (zwg_last_error(NULL)) before touching the device.  Nothing in it needs clearing
+ * between calls (every partial a merge reads is written by the same call first).  All calls on
+ * one GPU share that array: calls that overlap in time on one GPU (different streams, or threads)
+ * race on it and give wrong results; calls on one stream run in order and are safe.
+ */
+#define ZWG_NOALLOC_SCRATCH_BYTES (64ull << 20)
+int zwg_attention_batch_noalloc(const float *q, const float *k, const float *v, const zwg_attn_shape *shape,
+                                const zwg_batch *batch, float *out, uint32_t dense_math, void *hip_stream);
+
+/*
  * The plan a call with this shape and batch (NULL = one item) would use, for a context opened
  * with `workspace_bytes` of workspace (0 = default) in the default dense mode (ZWG_DENSE_X3;
  * ZWG_DENSE_FP32 splits causal calls into more chunks).  Host-only: needs no device.

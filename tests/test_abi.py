@@ -218,3 +218,17 @@ def test_bench_refuses_more_than_one_gpu():
                        timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def test_noalloc_refuses_beyond_its_scratch_before_the_device():
+    """zwg_attention_batch_noalloc checks the call's split partials against its static scratch
+    before it touches a device: a too-large call fails with that reason, GPU or not."""
+    import ctypes
+
+    sh = S(2048, 2048, 32, 32, 128, True)
+    assert z.plan(sh).workspace_bytes > _lib.NOALLOC_SCRATCH_BYTES
+    c = sh.to_c()
+    fake = 1 << 20  # an aligned, never dereferenced address
+    rc = _lib.lib().zwg_attention_batch_noalloc(fake, fake, fake, ctypes.byref(c), None, fake, 0, None)
+    assert rc == _lib.ZWG_ERROR
+    assert "static scratch" in _lib.last_error(None)

@@ -107,6 +107,7 @@ EPI_NONE = 0
 EPI_GELU = 1
 EPI_ADD = 2
 ROWS_ON_HOST = 1
+NOALLOC_SCRATCH_BYTES = 64 << 20  # ZWG_NOALLOC_SCRATCH_BYTES
 
 
 def declared_symbols() -> list[str]:
@@ -150,6 +151,9 @@ def lib() -> ctypes.CDLL:
     L.zwg_attention_dev.argtypes = [vp, _fp, _fp, _fp, ctypes.POINTER(ShapeC), _fp]
     L.zwg_attention_batch_dev.restype = c_int
     L.zwg_attention_batch_dev.argtypes = [vp, _fp, _fp, _fp, ctypes.POINTER(ShapeC), ctypes.POINTER(BatchC), _fp]
+    L.zwg_attention_batch_noalloc.restype = c_int
+    L.zwg_attention_batch_noalloc.argtypes = [_fp, _fp, _fp, ctypes.POINTER(ShapeC), ctypes.POINTER(BatchC), _fp,
+                                              ctypes.c_uint32, vp]
     L.zwg_plan.restype = c_int
     L.zwg_plan.argtypes = [ctypes.POINTER(ShapeC), ctypes.POINTER(BatchC), _u64, ctypes.POINTER(PlanC)]
     L.zwg_check_shape.restype = c_int

@@ -7,6 +7,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "attn_kernels.hpp"
@@ -226,10 +227,13 @@ struct Exec {
     float *ws;        // split partials
     uint64_t ws_bytes;
     uint32_t dense_math;
+    uint64_t plan_cap; // workspace bytes the planner may use (>= ws_bytes: a bigger plan is refused)
+    const char *ws_name;
 };
 
 Exec ctx_exec(const zwg_ctx *ctx) {
-    return Exec{ctx->device, ctx->stream, ctx->workspace, ctx->workspace_bytes, ctx->dense_math};
+    return Exec{ctx->device, ctx->stream, ctx->workspace, ctx->workspace_bytes, ctx->dense_math,
+                ctx->workspace_bytes, "the context's workspace"};
 }
 
 // Shape and pointer checks, the plan, and the launches.  ctx (may be null) receives the error.
@@ -242,9 +246,14 @@ int run(zwg_ctx *ctx, const Exec &x, const float *q, const float *k, const float
     if (!q || !out || (s.n_kv && (!k || !v))) return fail(ctx, "null tensor pointer");
     if (!aligned16(q) || !aligned16(out) || (s.n_kv && (!aligned16(k) || !aligned16(v))))
         return fail(ctx, "q, k, v and out must be 16-byte aligned");
-    const Plan p = make_plan(s, b, x.ws_bytes, x.dense_math);
+    const Plan p = make_plan(s, b, x.plan_cap, x.dense_math);
     if (plan_out) *plan_out = p;
-    if (p.ws_bytes > x.ws_bytes) return fail(ctx, "workspace too small for this call");
+    if (p.ws_bytes > x.ws_bytes) {
+        char buf[200];
+        snprintf(buf, sizeof buf, "this call's split partials need %llu bytes, more than the %llu bytes of %s",
+                 (unsigned long long)p.ws_bytes, (unsigned long long)x.ws_bytes, x.ws_name);
+        return fail(ctx, buf);
+    }
     // the row-major decode kernel and the x3 dense kernel address one item's K/V rows (and the
     // dense kernel one KV head's K^T rows) with 32-bit byte offsets
     const bool dense_x3 = p.kernel == 1 && x.dense_math != ZWG_DENSE_FP32;
@@ -528,4 +537,71 @@ int zwg_attention(zwg_ctx *ctx, const float *q, const float *k, const float *v, 
     return zwg_attention_ex(ctx, q, k, v, &s, out);
 }
 
+// ---- the allocation-free entry point -------------------------------------------------------
+//
+// Split partials live in a file-scope device array of this library, one copy per GPU (the code
+// object's own global memory, set up when the library's kernels are loaded on that GPU).  In host
+// code `scratch` names a host-side stand-in, not device memory: its device address is taken once
+// per GPU with hipGetSymbolAddress, with that GPU current, and only that address is passed on.
+
 } // extern "C"
+
+namespace {
+
+constexpr uint64_t kScratchBytes = ZWG_NOALLOC_SCRATCH_BYTES;
+static_assert(kScratchBytes % 256 == 0, "scratch size");
+static __device__ __align__(256) float scratch[kScratchBytes / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float *g_scratch_ptr[kMaxDevices] = {};
+
+// scratch's address on the current device (taken on the first call there)
+hipError_t scratch_on_current_device(float **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[dev] = static_cast<float *>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
+
+} // namespace
+
+extern "C" int zwg_attention_batch_noalloc(const float *q, const float *k, const float *v, const zwg_attn_shape *shape,
+                                           const zwg_batch *batch, float *out, uint32_t dense_math,
+                                           void *hip_stream) {
+    if (!shape) return fail(nullptr, "null shape");
+    if (dense_math > ZWG_DENSE_FP32) return fail(nullptr, "unknown dense_math");
+    const zwg_batch one{1, 0, 0, 0, 0, nullptr};
+    const zwg_batch &b = batch ? *batch : one;
+    std::string msg = check_shape(*shape);
+    if (msg.empty()) msg = check_batch(*shape, b);
+    if (!msg.empty()) return fail(nullptr, msg);
+    // the plan of a context with the default workspace; refused here when its partials exceed
+    // the static scratch, before the device is touched
+    const Plan p = make_plan(*shape, b, kDefaultWorkspace, dense_math);
+    if (p.ws_bytes > kScratchBytes) {
+        char buf[200];
+        snprintf(buf, sizeof buf,
+                 "this call's split partials need %llu bytes, more than the %llu-byte static scratch of "
+                 "zwg_attention_batch_noalloc (use a context)",
+                 (unsigned long long)p.ws_bytes, (unsigned long long)kScratchBytes);
+        return fail(nullptr, buf);
+    }
+    float *ws = nullptr;
+    if (p.ws_bytes > 0) {
+        const hipError_t e = scratch_on_current_device(&ws);
+        if (e != hipSuccess) return fail_hip(nullptr, "hipGetSymbolAddress (static scratch)", e);
+    }
+    const Exec x{-1, static_cast<hipStream_t>(hip_stream), ws, kScratchBytes, dense_math, kDefaultWorkspace,
+                 "the static scratch"};
+    return run(nullptr, x, q, k, v, *shape, b, out);
+}

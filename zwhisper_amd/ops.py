@@ -333,6 +333,31 @@ class Context:
                                                     self._dev_ptr(out, "out")))
 
 
+def attention_batch_noalloc(q, k, v, sh: AttnShape, out, n_batch: int = 1, q_bstride: int = 0, k_bstride: int = 0,
+                            v_bstride: int = 0, out_bstride: int = 0, n_kv_dev=None, dense_math: int = 0,
+                            stream=None) -> None:
+    """zwg_attention_batch_noalloc: a batch of problems on CUDA float32 tensors with no context and
+    no device allocation (split partials in the library's static scratch, ZWG_NOALLOC_SCRATCH_BYTES
+    per GPU), on the current device and `stream` (a torch stream; None: torch's current stream).
+    Same plan and results as Context.attention_batch_dev on a context with the default workspace;
+    calls on one GPU that overlap in time race on the shared scratch."""
+    import torch
+
+    nkv = 0
+    if n_kv_dev is not None:
+        if not n_kv_dev.is_cuda or n_kv_dev.dtype != torch.int32 or n_kv_dev.numel() < n_batch:
+            raise ZwgError("n_kv_dev must be a CUDA int32 tensor with n_batch entries")
+        nkv = n_kv_dev.data_ptr()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    c = sh.to_c()
+    b = _lib.BatchC(n_batch, q_bstride, k_bstride, v_bstride, out_bstride, nkv)
+    rc = _lib.lib().zwg_attention_batch_noalloc(Context._dev_ptr(q, "q"), Context._dev_ptr(k, "k"),
+                                                Context._dev_ptr(v, "v"), ctypes.byref(c), ctypes.byref(b),
+                                                Context._dev_ptr(out, "out"), dense_math, s.cuda_stream)
+    if rc != _lib.ZWG_OK:
+        raise ZwgError(_lib.last_error(None))
+
+
 class KVCache:
     """Device-resident KV caches of one context (zwg_kv_*): per (layer, sequence), in the Whisper
     decoder's row-major layout (layout=KV_ROW) or Qwen2's transposed-key layout (layout=KV_KT),
