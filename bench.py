@@ -18,9 +18,10 @@ the bar of the arithmetic that ran.  The two encoder workloads also carry "dropi
 the host-pointer drop-in (zwg_attention_ex, H2D + kernels + D2H per window), which includes PCIe
 and is never the headline value.
 
-Timing: W untimed warm-up steps, then exactly K steps bracketed by torch.cuda.synchronize();
-each step's launches are also bracketed by HIP events on the stream they run on, whose mean is
-the kernel time used for the roofline.  Decode workloads rotate between two copies of their
+Timing: W untimed warm-up steps, then exactly K steps bracketed by torch.cuda.synchronize() and
+by one pair of HIP events on the stream the kernels run on; the events' elapsed time over K is
+the kernel time used for the roofline (kernel_ms_mean).  K further steps, each between its own
+pair of events, give kernel_ms_median and kernel_ms_min.  Decode workloads rotate between two copies of their
 inputs so no step finds its K/V in the 256 MB last-level cache left by the previous one.
 The CPU baseline is the C restatement of the reference's multithreaded attention (oracle/),
 timed on this host's cores on a bounded sample of the same workload, on CPUs - 1 threads (the
@@ -303,14 +304,16 @@ class Workload:
                 self.ctx.attention_ex_host(q, k, v, self.shape, out)
 
         best, mean, runs = time_cpu(run, reps)
+        self.torch.cuda.synchronize()
         dev_out = self.sets[self.last % len(self.sets)]["out"].cpu().numpy()
-        same = all(np.array_equal(out, dev_out[i].reshape(-1)) for i, (_, _, _, out) in enumerate(calls))
+        diff = max(float(np.abs(out - dev_out[i].reshape(-1)).max()) for i, (_, _, _, out) in enumerate(calls))
         moved = sum(q.nbytes + k.nbytes + v.nbytes + out.nbytes for q, k, v, out in calls)
         return {"value": self.work / best / 1e12, "unit": "TFLOP/s", "ms_per_step": 1e3 * best,
                 "ms_per_step_mean": 1e3 * mean, "calls_per_step": w.n_items, "pcie_bytes_per_step": moved,
-                "equals_device_result": bool(same),
+                "max_abs_vs_device_line": diff,
                 "note": "zwg_attention_ex per window on pageable host buffers (H2D q/k/v + kernels + D2H out), "
-                        "synchronous; best of " + f"{runs} runs"}
+                        "synchronous; best of " + f"{runs} runs; a one-window call plans its own key split, so it "
+                        "can round differently from the batched device call"}
 
     def free(self):
         self.sets = []
@@ -682,23 +685,36 @@ def q8_workloads(torch, ctx):
         groups=[3, 1, 1, 1, 1, 1] * 12 + [1])
 
 
-def time_workload(wl: Workload, steps: int, warmup: int) -> dict:
+def time_workload(wl, steps: int, warmup: int) -> dict:
+    """W warm-up steps, then exactly K timed steps bracketed by torch.cuda.synchronize(), with one
+    pair of HIP events on the stream the kernels run on around the K steps: kernel_ms_mean is
+    their elapsed time over K, the device time per step with nothing inserted between the steps.
+    Afterwards (outside the timed region) K more steps each bracketed by their own events give the
+    per-step median and minimum; an event pair between launches adds a short gap, so those run a
+    little above the mean."""
     torch = wl.torch
     for i in range(warmup):
         wl.step(i)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    e0.record(stream)
     for i in range(steps):
-        ev[i][0].record(stream)
         wl.step(warmup + i)
-        ev[i][1].record(stream)
+    e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    kernel_ms_mean = e0.elapsed_time(e1) / steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for i in range(steps):
+        ev[i][0].record(stream)
+        wl.step(warmup + steps + i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
     kms = [a.elapsed_time(b) for a, b in ev]
-    return {"wall_s": wall, "ms_per_step": 1e3 * wall / steps, "kernel_ms_mean": float(np.mean(kms)),
+    return {"wall_s": wall, "ms_per_step": 1e3 * wall / steps, "kernel_ms_mean": kernel_ms_mean,
             "kernel_ms_min": float(np.min(kms)), "kernel_ms_median": float(np.median(kms))}
 
 

@@ -134,7 +134,8 @@ def unit_split(kv_hi, tile, chunk_len, max_chunks):
 ])
 def test_plan_invariants(sh, nb):
     p = z.plan(sh, nb)
-    tile = 256 if p.kernel == 2 else 32
+    # decode: 256-key tiles, or 64 for row-major caches of at most 512 keys; dense: 32
+    tile = (64 if not sh.kt_stride and sh.n_kv <= 512 else 256) if p.kernel == 2 else 32
     assert p.chunk_len % tile == 0 and p.chunk_len > 0
     # every unit's keys are covered by at most max_chunks non-empty chunks
     his = ([sh.n_kv - sh.n_q + min(sh.n_q, (qb + 1) * 128) if sh.causal else sh.n_kv

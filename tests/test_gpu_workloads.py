@@ -440,3 +440,32 @@ def test_children_outlive_their_closed_context(torch):
         kv.read(0, 0)
     kv.close()
     w.close()
+
+
+@pytest.mark.parametrize("n_items,kt", [(300, True), (300, False), (256, True)])
+def test_decode_many_ragged_items(torch, ctx, n_items, kt):
+    """Per-item key counts over more items than the decode kernels map onto the list of non-empty
+    chunks (256): those calls keep the plain (item, chunk, KV head) grid.  Both grids, both key
+    layouts, every item against f64."""
+    cap, h, hkv, d = 512, 4, 2, 64
+    rng = np.random.default_rng(n_items)
+    lengths = rng.integers(0, cap + 1, n_items).astype(np.int32)
+    lengths[:3] = [0, 1, cap]
+    q = W.normal(101, n_items * h * d).reshape(n_items, h * d)
+    kl = W.normal(102, n_items * cap * hkv * d).reshape(n_items, cap, hkv, d)
+    v = W.normal(103, n_items * cap * hkv * d).reshape(n_items, cap, hkv * d)
+    kstore = np.stack([W.to_kt(kl[i], cap) for i in range(n_items)]) if kt else kl.reshape(n_items, cap, hkv * d)
+    sh = AttnShape(1, cap, h, hkv, d, h * d, hkv * d, h * d, False, cap if kt else None)
+    out = torch.full((n_items, h * d), 9.0, device="cuda")
+    ctx.attention_batch_dev(dev(torch, q), dev(torch, kstore), dev(torch, v), sh, out, n_items, h * d,
+                            kstore[0].size, cap * hkv * d, h * d, torch.from_numpy(lengths).cuda())
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for i in range(n_items):
+        L = int(lengths[i])
+        if L == 0:
+            assert np.all(got[i] == 0.0), f"item {i} with no keys must give zeros"
+            continue
+        shi = AttnShape(1, L, h, hkv, d, h * d, hkv * d, h * d, False, None)
+        ref = naive.attention_f64(q[i], kl[i, :L].reshape(-1), v[i, :L].reshape(-1), shi)
+        check(got[i], ref, f"{n_items} items, item {i} n_kv={L} ({'kt' if kt else 'row-major'})")

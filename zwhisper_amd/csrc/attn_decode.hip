@@ -72,10 +72,16 @@ __global__ __launch_bounds__(64) void decode_kt_kernel(AttnArgs a) {
     __shared__ __align__(16) float p_s[R][T];
 
     const int lane = threadIdx.x;
-    // one wave per (item, chunk, KV head), KV head fastest
-    const int hk = blockIdx.x % a.n_head_kv;
-    const int chunk = (blockIdx.x / a.n_head_kv) % a.max_chunks;
-    const int item = blockIdx.x / (a.n_head_kv * a.max_chunks);
+    // one wave per (item, chunk, KV head), KV head fastest; over the non-empty chunks only when the
+    // items have their own key counts (decode_compact_unit)
+    int hk, chunk, item;
+    if (a.n_kv_item && a.n_batch <= kDecodeCompactItems) {
+        if (!decode_compact_unit(a, T, blockIdx.x, &item, &chunk, &hk)) return;
+    } else {
+        hk = blockIdx.x % a.n_head_kv;
+        chunk = (blockIdx.x / a.n_head_kv) % a.max_chunks;
+        item = blockIdx.x / (a.n_head_kv * a.max_chunks);
+    }
 
     const int n_q = a.n_q;
     const int G = a.group;
@@ -245,10 +251,13 @@ __global__ __launch_bounds__(64) void decode_kt_kernel(AttnArgs a) {
 
 // Loads go in batches of ZWG_DECODE_RM_BATCH rows per thread: measured on MI355X, deeper
 // per-thread queues stream a cache more slowly, not faster.
-template <int D, int R>
+// T: keys per tile, 256 or, for short caches, 64 (the planner's split_tile): a chunk then loads
+// only the rows it owns, so short caches can be cut into many small chunks that spread over every
+// CU instead of a few long ones that leave most CUs idle.
+template <int D, int R, int T>
 __global__ __launch_bounds__(kDecodeThreads) void decode_rm_kernel(AttnArgs a) {
     constexpr int NT = kDecodeThreads;
-    constexpr int T = kDecodeTile;
+    static_assert(T % 64 == 0 && T >= 64, "the softmax pass gives each lane T / 64 keys");
     constexpr int NW = NT / 64;
     constexpr int L = D / 4;   // lanes per key row
     constexpr int P = NT / L;  // key rows per pass
@@ -269,10 +278,16 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_rm_kernel(AttnArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    // one workgroup per (item, chunk, KV head), KV head fastest
-    const int hk = blockIdx.x % a.n_head_kv;
-    const int chunk = (blockIdx.x / a.n_head_kv) % a.max_chunks;
-    const int item = blockIdx.x / (a.n_head_kv * a.max_chunks);
+    // one workgroup per (item, chunk, KV head), KV head fastest; over the non-empty chunks only
+    // when the items have their own key counts (decode_compact_unit; every wave finds the same)
+    int hk, chunk, item;
+    if (a.n_kv_item && a.n_batch <= kDecodeCompactItems) {
+        if (!decode_compact_unit(a, T, blockIdx.x, &item, &chunk, &hk)) return;
+    } else {
+        hk = blockIdx.x % a.n_head_kv;
+        chunk = (blockIdx.x / a.n_head_kv) % a.max_chunks;
+        item = blockIdx.x / (a.n_head_kv * a.max_chunks);
+    }
 
     const int n_q = a.n_q;
     const int G = a.group;
@@ -467,13 +482,17 @@ hipError_t launch_decode(const AttnArgs &a, int d, int rows, hipStream_t stream,
     dim3 grid((unsigned)blocks);
     if (grid_blocks) *grid_blocks = (int)blocks;
     const bool kt = a.kt_stride != 0;
+    if (kt ? a.split_tile != kDecodeTile : a.split_tile != kDecodeTile && a.split_tile != kDecodeShortTile)
+        return hipErrorInvalidValue;
     const int R = rows <= 1 ? 1 : rows <= 2 ? 2 : rows <= 4 ? 4 : rows <= 6 ? 6 : 8;
     if (rows > kDecodeMaxRows) return hipErrorInvalidValue;
 #define ZWG_DEC(DD, RR)                                                                                          \
     if (kt)                                                                                                      \
         decode_kt_kernel<DD, RR><<<grid, dim3(64), 0, stream>>>(a);                                               \
+    else if (a.split_tile == kDecodeShortTile)                                                                   \
+        decode_rm_kernel<DD, RR, kDecodeShortTile><<<grid, dim3(kDecodeThreads), 0, stream>>>(a);                 \
     else                                                                                                         \
-        decode_rm_kernel<DD, RR><<<grid, dim3(kDecodeThreads), 0, stream>>>(a);
+        decode_rm_kernel<DD, RR, kDecodeTile><<<grid, dim3(kDecodeThreads), 0, stream>>>(a);
 #define ZWG_DEC_R(DD)                                                                                            \
     switch (R) {                                                                                                 \
     case 1: ZWG_DEC(DD, 1); break;                                                                               \

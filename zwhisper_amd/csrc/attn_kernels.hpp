@@ -63,6 +63,49 @@ __device__ inline int item_kv(const AttnArgs &a, int item) {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// Decode grids over items with their own key counts (n_kv_item): the launch covers max_chunks
+// chunks of every (item, KV head), but an item of few keys has fewer non-empty chunks.  MI355X
+// deals consecutive workgroups round-robin over its XCDs and their CUs, so with the plain
+// (item, chunk, KV head) order every CU would keep meeting the same chunk index: the CUs given the
+// first chunks would stream full loads while those given the last ones sat idle.  Instead the
+// workgroups are renumbered over the list of non-empty chunks, item by item (chunk, then KV head,
+// fastest), so consecutive workgroups -- and so every CU -- get an even share; workgroups past the
+// list's end exit.  Each wave computes the list from the key counts itself (items = lanes,
+// kDecodeCompactItems at most).  Returns false for a workgroup past the end.
+constexpr int kDecodeCompactItems = 256;
+__device__ inline bool decode_compact_unit(const AttnArgs &a, int tile, int64_t wg, int *item, int *chunk, int *hk) {
+    const int lane = (int)(threadIdx.x & 63);
+    const int H = a.n_head_kv;
+    int base = 0; // workgroups of the items before this lane group
+#pragma unroll
+    for (int k = 0; k < kDecodeCompactItems / 64; ++k) {
+        const int it = lane + 64 * k;
+        int c = 0;
+        if (it < a.n_batch) {
+            int ck;
+            c = unit_split(item_kv(a, it), tile, a.chunk_len, a.max_chunks, &ck) * H;
+        }
+        int incl = c; // inclusive scan over the lanes
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const int v = __shfl_up(incl, off);
+            if (lane >= off) incl += v;
+        }
+        const unsigned long long hit = __ballot(it < a.n_batch && base + incl > wg);
+        if (hit) {
+            const int first = __builtin_ctzll(hit);
+            const int excl = base + __shfl(incl - c, first);
+            const int local = (int)(wg - excl);
+            *item = first + 64 * k;
+            *chunk = local / H;
+            *hk = local - *chunk * H;
+            return true;
+        }
+        base += __shfl(incl, 63);
+    }
+    return false;
+}
+
 // MI355X deals consecutive workgroups round-robin over its 8 XCDs, each with its own L2.
 // xcd_logical_block renumbers them so that consecutive logical ids run on the same XCD:
 // hardware ids x, x+8, x+16, ... (all on XCD x) become one contiguous range of logical ids.
@@ -85,6 +128,10 @@ constexpr int kFlashBN = 32;                              // keys per MFMA tile
 #endif
 constexpr int kDecodeThreads = 256;
 constexpr int kDecodeTile = ZWG_DECODE_TILE; // keys per inner tile
+#ifndef ZWG_DECODE_SHORT_TILE
+#define ZWG_DECODE_SHORT_TILE 64
+#endif
+constexpr int kDecodeShortTile = ZWG_DECODE_SHORT_TILE; // row-major K: tile of short caches
 constexpr int kDecodeMaxRows = 8; // heads-per-KV-group x queries a block can carry
 
 hipError_t launch_flash(const AttnArgs &a, int d, hipStream_t stream, int *grid_blocks);

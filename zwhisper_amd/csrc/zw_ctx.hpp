@@ -32,6 +32,9 @@ struct zwg_ctx {
     // device staging for the host-pointer calls: q, k, v, out
     float *stage[4] = {nullptr, nullptr, nullptr, nullptr};
     uint64_t stage_bytes[4] = {0, 0, 0, 0};
+    // pinned host staging for results whose rows are not contiguous in the caller's buffer
+    float *host_stage = nullptr;
+    uint64_t host_stage_bytes = 0;
     std::vector<ZwgChild> children;
     std::string err;
 };
@@ -43,6 +46,11 @@ int fail(zwg_ctx *ctx, const std::string &msg);
 int fail_hip(zwg_ctx *ctx, const char *what, hipError_t e);
 // Grow staging buffer i of ctx to at least `bytes` (synchronises the stream when it grows).
 int ensure_stage(zwg_ctx *ctx, int i, uint64_t bytes);
+// Copy n_rows rows of `cols` floats, `stride` floats apart, from device `src` to host `dst` (same
+// layout; the gaps of dst are left alone), queued on ctx's stream and waited for: one copy when
+// the rows are contiguous, else one copy of the whole span into pinned staging and row copies on
+// the host.
+int download_rows(zwg_ctx *ctx, float *dst, const float *src, uint64_t n_rows, uint64_t cols, uint64_t stride);
 // Register / unregister an object made from ctx (see ZwgChild).
 void add_child(zwg_ctx *ctx, void *obj, void (*detach)(void *));
 void remove_child(zwg_ctx *ctx, void *obj);

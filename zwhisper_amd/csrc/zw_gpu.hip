@@ -45,6 +45,36 @@ int ensure_stage(zwg_ctx *ctx, int i, uint64_t bytes) {
     return ZWG_OK;
 }
 
+int download_rows(zwg_ctx *ctx, float *dst, const float *src, uint64_t n_rows, uint64_t cols, uint64_t stride) {
+    const uint64_t F = sizeof(float);
+    if (n_rows == 0) return ZWG_OK;
+    hipError_t e;
+    if (stride == cols || n_rows == 1) {
+        e = hipMemcpyAsync(dst, src, ((n_rows - 1) * stride + cols) * F, hipMemcpyDeviceToHost, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) return fail_hip(ctx, "download", e);
+        return ZWG_OK;
+    }
+    const uint64_t span = ((n_rows - 1) * stride + cols) * F;
+    if (ctx->host_stage_bytes < span) {
+        e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) return fail_hip(ctx, "hipStreamSynchronize", e);
+        if (ctx->host_stage) (void)hipHostFree(ctx->host_stage);
+        ctx->host_stage = nullptr;
+        ctx->host_stage_bytes = 0;
+        void *p = nullptr;
+        e = hipHostMalloc(&p, span, hipHostMallocDefault);
+        if (e != hipSuccess) return fail_hip(ctx, "hipHostMalloc (result staging)", e);
+        ctx->host_stage = static_cast<float *>(p);
+        ctx->host_stage_bytes = span;
+    }
+    e = hipMemcpyAsync(ctx->host_stage, src, span, hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) return fail_hip(ctx, "download", e);
+    for (uint64_t r = 0; r < n_rows; ++r) std::memcpy(dst + r * stride, ctx->host_stage + r * stride, cols * F);
+    return ZWG_OK;
+}
+
 void add_child(zwg_ctx *ctx, void *obj, void (*detach)(void *)) { ctx->children.push_back({obj, detach}); }
 
 void remove_child(zwg_ctx *ctx, void *obj) {
@@ -78,6 +108,9 @@ constexpr uint64_t kMaxSplitUnitsHint = 1ull << 22;
 #endif
 #ifndef ZWG_DECODE_NOSPLIT_TILES
 #define ZWG_DECODE_NOSPLIT_TILES 0 // ... or when a unit has at most this many 256-key tiles
+#endif
+#ifndef ZWG_DECODE_SHORT_KV
+#define ZWG_DECODE_SHORT_KV 512 // row-major decode calls up to this many keys use the short key tile
 #endif
 #ifndef ZWG_FLASH_BLOCKS_PER_CU
 #define ZWG_FLASH_BLOCKS_PER_CU 2 // dense grid aimed at when keys are split, per CU
@@ -169,7 +202,8 @@ Plan make_plan(const zwg_attn_shape &s, const zwg_batch &b, uint64_t ws_cap, uin
     if (s.n_q * group <= (uint64_t)zwg::kDecodeMaxRows) {
         p.kernel = 2;
         p.rows_per_unit = (int)s.n_q;
-        tile = zwg::kDecodeTile;
+        // row-major caches of at most ZWG_DECODE_SHORT_KV keys go in short tiles
+        tile = !s.kt_stride && s.n_kv <= (uint64_t)ZWG_DECODE_SHORT_KV ? zwg::kDecodeShortTile : zwg::kDecodeTile;
         units = b.n_batch * s.n_head_kv;
         w_max = std::max<uint64_t>(1, ceil_div(s.n_kv, tile));
         uint64_t want_chunks =
@@ -424,6 +458,7 @@ void zwg_close(zwg_ctx *ctx) {
     ctx->children.clear();
     for (auto &s : ctx->stage)
         if (s) (void)hipFree(s);
+    if (ctx->host_stage) (void)hipHostFree(ctx->host_stage);
     if (ctx->workspace) (void)hipFree(ctx->workspace);
     if (ctx->switch_event) (void)hipEventDestroy(ctx->switch_event);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
@@ -497,11 +532,8 @@ int zwg_attention_ex(zwg_ctx *ctx, const float *q, const float *k, const float *
     int rc = run(ctx, x, ctx->stage[0], ctx->stage[1], ctx->stage[2], s, one, ctx->stage[3], &p);
     if (rc != ZWG_OK) return rc;
     // copy back only each row's n_head*d columns: out's other columns stay the caller's
-    e = hipMemcpy2DAsync(out, s.out_stride * F, ctx->stage[3], s.out_stride * F, hd * F, s.n_q, hipMemcpyDeviceToHost,
-                         ctx->stream);
-    if (e != hipSuccess) return fail_hip(ctx, "hipMemcpy2DAsync (download)", e);
-    e = hipStreamSynchronize(ctx->stream);
-    if (e != hipSuccess) return fail_hip(ctx, "hipStreamSynchronize", e);
+    rc = download_rows(ctx, out, ctx->stage[3], s.n_q, hd, s.out_stride);
+    if (rc != ZWG_OK) return rc;
     // The x3 dense kernel needs keys (and scaled queries) within f16 range; outside it the rows
     // that see such a key come out NaN.  The reference gives finite results for any finite
     // input (src/ops.zig:562-590), so a non-finite result of the x3 kernel is computed again on
@@ -511,11 +543,8 @@ int zwg_attention_ex(zwg_ctx *ctx, const float *q, const float *k, const float *
         x.dense_math = ZWG_DENSE_FP32;
         rc = run(ctx, x, ctx->stage[0], ctx->stage[1], ctx->stage[2], s, one, ctx->stage[3]);
         if (rc != ZWG_OK) return rc;
-        e = hipMemcpy2DAsync(out, s.out_stride * F, ctx->stage[3], s.out_stride * F, hd * F, s.n_q,
-                             hipMemcpyDeviceToHost, ctx->stream);
-        if (e != hipSuccess) return fail_hip(ctx, "hipMemcpy2DAsync (download)", e);
-        e = hipStreamSynchronize(ctx->stream);
-        if (e != hipSuccess) return fail_hip(ctx, "hipStreamSynchronize", e);
+        rc = download_rows(ctx, out, ctx->stage[3], s.n_q, hd, s.out_stride);
+        if (rc != ZWG_OK) return rc;
     }
     return ZWG_OK;
 }
