@@ -48,7 +48,8 @@ typedef struct zwg_ctx zwg_ctx;
  * causal: query i sees keys j <= n_kv - n_q + i (src/ops.zig:466), so n_kv >= n_q is required.
  *
  * Limits of this build (checked; ZWG_ERROR otherwise): d in {32, 64, 128}; q_stride, kv_stride,
- * out_stride and kt_stride multiples of 4; q, k, v, out 16-byte aligned; every count < 2^31.
+ * out_stride and kt_stride multiples of 4; q, k, v, out 16-byte aligned; n_q, n_kv and n_head
+ * below 2^30; n_head * n_batch below 2^31.
  * Device buffers: with kt_stride, the last transposed row is read in 16-byte groups, so k must
  * hold (n_head_kv*d - 1)*kt_stride + round_up(n_kv, 4) floats -- no more than the reference
  * itself reads (round_up(n_kv, V) columns of every row, src/ops.zig:529-530).

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "attn_geometry.hpp"
+
 namespace zwg {
 
 // Everything a kernel needs for one call, passed by value.  Counts are int32 (checked on
@@ -35,24 +37,6 @@ struct AttnArgs {
 // Rows of a call are numbered ((item * n_head + head) * n_q + query).
 __host__ __device__ inline int64_t row_index(const AttnArgs &a, int item, int head, int query) {
     return ((int64_t)item * a.n_head + head) * a.n_q + query;
-}
-
-// Key split of one work unit whose rows see keys [0, kv_hi): its W = ceil(kv_hi / tile) tiles are
-// dealt into chunks of equal length (the last may be shorter), about tau = chunk_len / tile
-// tiles each, at most max_chunks.  Returns the number of chunks (>= 1) and sets *chunk_keys to
-// the chunk length in keys.  The kernels, the merge pass and the planner all split this way.
-__host__ __device__ inline int unit_split(int kv_hi, int tile, int chunk_len, int max_chunks, int *chunk_keys) {
-    const int w = (kv_hi + tile - 1) / tile;
-    if (w <= 0) {
-        *chunk_keys = tile;
-        return 1;
-    }
-    const int tau = chunk_len / tile > 1 ? chunk_len / tile : 1;
-    int nc = (w + tau / 2) / tau; // round(w / tau)
-    nc = nc < 1 ? 1 : nc > max_chunks ? max_chunks : nc;
-    const int lt = (w + nc - 1) / nc;
-    *chunk_keys = lt * tile;
-    return (w + lt - 1) / lt;
 }
 
 // Keys of batch item `item`: its own count when the call has per-item counts, clamped to the
@@ -115,24 +99,6 @@ __device__ __forceinline__ int64_t xcd_logical_block(int64_t hw, int64_t n) {
     const int64_t q = n / kNumXCD, r = n % kNumXCD;
     return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
 }
-
-// Flash (dense, MFMA) kernel geometry.
-constexpr int kFlashWaves = 4;
-constexpr int kFlashRowsPerWave = 32;
-constexpr int kFlashBM = kFlashWaves * kFlashRowsPerWave; // query rows per workgroup
-constexpr int kFlashBN = 32;                              // keys per MFMA tile
-
-// Decode (split-K streaming) kernel geometry.
-#ifndef ZWG_DECODE_TILE
-#define ZWG_DECODE_TILE 256
-#endif
-constexpr int kDecodeThreads = 256;
-constexpr int kDecodeTile = ZWG_DECODE_TILE; // keys per inner tile
-#ifndef ZWG_DECODE_SHORT_TILE
-#define ZWG_DECODE_SHORT_TILE 64
-#endif
-constexpr int kDecodeShortTile = ZWG_DECODE_SHORT_TILE; // row-major K: tile of short caches
-constexpr int kDecodeMaxRows = 8; // heads-per-KV-group x queries a block can carry
 
 hipError_t launch_flash(const AttnArgs &a, int d, hipStream_t stream, int *grid_blocks);
 hipError_t launch_flash_x3(const AttnArgs &a, int d, hipStream_t stream, int *grid_blocks);
