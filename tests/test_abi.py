@@ -233,3 +233,23 @@ def test_noalloc_refuses_beyond_its_scratch_before_the_device():
     rc = _lib.lib().zwg_attention_batch_noalloc(fake, fake, fake, ctypes.byref(c), None, fake, 0, None)
     assert rc == _lib.ZWG_ERROR
     assert "static scratch" in _lib.last_error(None)
+
+
+def test_zig_binding_declares_the_whole_header():
+    """zig/gpu.zig (the binding a maintainer drops into src/gpu.zig; no Zig toolchain here to
+    compile it) declares every function of include/zw_gpu.h, and its extern structs carry the C
+    structs' fields in the same order."""
+    import re
+
+    text = open(os.path.join(ROOT, "zig", "gpu.zig")).read()
+    zig_fns = sorted(set(re.findall(r'pub extern "zwgpu" fn (zwg_[a-z_0-9]+)\(', text)))
+    assert zig_fns == _lib.declared_symbols()
+
+    def zig_fields(name):
+        body = re.search(r"pub const %s = extern struct \{(.*?)\n\};" % name, text, re.S).group(1)
+        return re.findall(r"^\s+([a-z_0-9]+):", body, re.M)
+
+    for zname, cstruct in (("Shape", _lib.ShapeC), ("Batch", _lib.BatchC), ("Limits", _lib.LimitsC),
+                           ("PlanInfo", _lib.PlanC), ("KvDesc", _lib.KVDescC), ("KvInfo", _lib.KVInfoC),
+                           ("EncLayer", _lib.EncLayerC)):
+        assert zig_fields(zname) == [f for f, _ in cstruct._fields_], zname
