@@ -18,11 +18,13 @@
  *   - decode (split-K streaming) kernel: f32 FMA.  Bar: max abs 2e-4, normwise relative 1e-3
  *     (||gpu - ref||_inf / ||ref||_inf), the reference's f32 bar; measured ~1e-7.
  *   - dense (encoder / prefill) kernel, ZWG_DENSE_X3 (the default, below): f32 operands split into
- *     16-bit hi + lo terms, three 16-bit MFMA products per product, f32 accumulation.  Its own bar
- *     on N(0,1) inputs: max abs 5e-5 and normwise relative 3e-5 (measured at most 1.9e-5 and
- *     1.1e-5 on the five Whisper / Qwen2 workloads); with scores spread 36x wider it measures
- *     4.5e-5, inside the f32 bar.
+ *     f16 hi + lo terms (22 significand bits), three f16 MFMA products per product, f32
+ *     accumulation.  Its own bar on N(0,1) inputs: max abs 5e-5 and normwise relative 3e-5
+ *     (measured at most 8.4e-7 and 2.6e-7 on the Whisper / Qwen2 workloads); with scores spread
+ *     36x wider it measures 4.5e-5, inside the f32 bar.
  *   - dense kernel, ZWG_DENSE_FP32: fp32 MFMA (v_mfma_f32_32x32x2_f32) throughout; the f32 bar.
+ * The absolute bars are for values of order one: an output row is a weighted mean of value rows,
+ * so with values up to M in magnitude they scale by M.
  */
 #ifndef ZW_GPU_H
 #define ZW_GPU_H
@@ -87,12 +89,13 @@ typedef struct zwg_batch {
 /*
  * Arithmetic of the dense (encoder / prefill) attention kernel (tolerances at the top of this
  * file):
- *   ZWG_DENSE_X3 (default): every product as three 16-bit MFMA products of operands split into
- *     hi + lo terms, f32 accumulation, about 2.5x the fp32 kernel's rate.  Q.K^T splits into f16
- *     (22 significand bits, so a score's error does not grow with large logits), P.V into bf16
- *     (16 bits, f32 exponent range).  Keys must stay below 65504 in magnitude (f16 range): a
- *     larger one gives NaN outputs, never a silently wrong finite one (zwg_attention_ex then
- *     recomputes the call in ZWG_DENSE_FP32).
+ *   ZWG_DENSE_X3 (default): every product as three f16 MFMA products of operands split into
+ *     hi + lo terms (22 significand bits, so a score's error does not grow with large logits),
+ *     f32 accumulation, about 2.5x the fp32 kernel's rate.  Keys and values must stay below 65504
+ *     in magnitude (f16 range): a larger key gives NaN in the rows that see it, a larger value NaN
+ *     in its own output column (head, dimension) of the rows whose 32-row group loads its 32-key
+ *     tile -- never a silently wrong finite result
+ *     (zwg_attention_ex then recomputes the call in ZWG_DENSE_FP32).
  *   ZWG_DENSE_FP32: fp32 MFMA (v_mfma_f32_32x32x2_f32) throughout, no range condition.
  * The decode kernels are f32 FMA in either mode.
  */
@@ -141,7 +144,7 @@ int zwg_set_dense_math(zwg_ctx *ctx, uint32_t mode);
  * result on return, and only each query row's n_head*d columns are written, as in the
  * reference.  Stages q/k/v through device buffers the context keeps (grown on first need).
  * It keeps the reference's contract for any finite input: when the x3 dense kernel's result
- * holds a non-finite value (a key or scaled query beyond f16 range), the call is computed
+ * holds a non-finite value (a key, value or scaled query beyond f16 range), the call is computed
  * again on the fp32-MFMA kernel, which has no range condition.
  */
 int zwg_attention_ex(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_attn_shape *shape,
@@ -153,8 +156,8 @@ int zwg_attention(zwg_ctx *ctx, const float *q, const float *k, const float *v, 
                   uint64_t n_state, uint64_t n_head, int causal, float *out);
 
 /* Device pointers (inputs already in HBM): queued on the context's stream, asynchronous.  In
- * ZWG_DENSE_X3 mode dense calls need |k| < 65504 and |q| / sqrt(d) * log2(e) < 65504 (rows that
- * see a larger value come out NaN); ZWG_DENSE_FP32 mode has no such condition. */
+ * ZWG_DENSE_X3 mode dense calls need |k| < 65504, |v| < 65504 and |q| / sqrt(d) * log2(e) < 65504
+ * (rows that meet a larger value come out NaN); ZWG_DENSE_FP32 mode has no such condition. */
 int zwg_attention_dev(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_attn_shape *shape,
                       float *out);
 

@@ -80,7 +80,17 @@ int main() {
                 if (kv <= s.n_kv) check_unit(p, (int)kv, s);
         } else {
             const uint64_t n_qb = ceil_div(s.n_q, zwg::kFlashBM);
-            CHECK(p.grid_blocks == (uint64_t)p.max_chunks * n_qb * s.n_head * b.n_batch, "dense grid");
+            if (p.heavy_first == 2) {
+                uint64_t live = 0;
+                for (uint64_t qb = 0; qb < n_qb; ++qb) {
+                    int ck = 0;
+                    live += (uint64_t)zwg::unit_split((int)(s.n_kv - s.n_q + std::min(s.n_q, (qb + 1) * zwg::kFlashBM)),
+                                                      p.split_tile, p.chunk_len, p.max_chunks, &ck);
+                }
+                CHECK(p.grid_blocks == live * s.n_head * b.n_batch, "live dense grid");
+            } else {
+                CHECK(p.grid_blocks == (uint64_t)p.max_chunks * n_qb * s.n_head * b.n_batch, "dense grid");
+            }
             for (uint64_t qb : {uint64_t(0), n_qb / 2, n_qb ? n_qb - 1 : 0}) {
                 const uint64_t q_end = std::min(s.n_q, (qb + 1) * zwg::kFlashBM);
                 const uint64_t hi = s.causal ? s.n_kv - s.n_q + q_end : s.n_kv;

@@ -150,6 +150,11 @@ def test_plan_invariants(sh, nb):
     assert p.workspace_bytes == ((pairs + rows * p.max_chunks * sh.d) * 4 if p.max_chunks > 1 else 0)
     if p.kernel == 2:
         assert p.grid_blocks == p.max_chunks * sh.n_head_kv * nb
+    elif sh.causal:
+        # causal dense calls launch only the (q-block, chunk, head) triples that have keys
+        live = sum(unit_split(sh.n_kv - sh.n_q + min(sh.n_q, (qb + 1) * 128), tile, p.chunk_len, p.max_chunks)[0]
+                   for qb in range(-(-sh.n_q // 128)))
+        assert p.grid_blocks == live * sh.n_head * nb
     else:
         assert p.grid_blocks == p.max_chunks * -(-sh.n_q // 128) * sh.n_head * nb
 

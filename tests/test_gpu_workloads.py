@@ -54,9 +54,12 @@ def ctx_fp32(torch):
     c.close()
 
 
-def check(got, ref, what, x3: bool = True):
-    """Max abs and normwise relative error against ref, to the x3 bar (x3=True) or the f32 bar."""
+def check(got, ref, what, x3: bool = True, v_scale: float = 1.0):
+    """Max abs and normwise relative error against ref, to the x3 bar (x3=True) or the f32 bar.
+    The absolute bars hold for values of order one; an output row is a weighted mean of value
+    rows, so for values up to v_scale in magnitude the absolute bar scales by v_scale."""
     tol_abs, tol_rel = (TOL_ABS_X3, TOL_REL_X3) if x3 else (TOL_ABS, TOL_REL)
+    tol_abs *= max(v_scale, 1.0)
     got = np.asarray(got, np.float64).reshape(-1)
     ref = np.asarray(ref, np.float64).reshape(-1)
     assert np.all(np.isfinite(got)), f"{what}: non-finite output"
@@ -469,3 +472,47 @@ def test_decode_many_ragged_items(torch, ctx, n_items, kt):
         shi = AttnShape(1, L, h, hkv, d, h * d, hkv * d, h * d, False, None)
         ref = naive.attention_f64(q[i], kl[i, :L].reshape(-1), v[i, :L].reshape(-1), shi)
         check(got[i], ref, f"{n_items} items, item {i} n_kv={L} ({'kt' if kt else 'row-major'})")
+
+
+def test_x3_value_range(torch, ctx):
+    """The x3 dense mode's value-range condition: a value of magnitude >= 65504 (beyond f16) gives
+    NaN in its own output column (its head and dimension) of the rows that load its 32-key tile --
+    never a wrong finite result -- while the fp32 mode and the host drop-in (which recomputes such
+    a call in fp32) stay within the f32 bar."""
+    import zwhisper_amd as z
+
+    n_q = n_kv = 96
+    h, d = 2, 64
+    sh = AttnShape(n_q, n_kv, h, h, d, h * d, h * d, h * d, True, None)
+    q = W.normal(74, n_q * h * d)
+    k = W.normal(75, n_kv * h * d)
+    v = W.normal(76, n_kv * h * d).reshape(n_kv, h * d)
+    v[70, 7] = 2.0e5  # key 70 (third 32-key tile), head 0, dimension 7
+    v = v.reshape(-1)
+    ref = naive.attention_f64(q, k, v, sh).reshape(n_q, h * d)
+    with z.Context(0, dense_math=z.DENSE_FP32) as c:
+        out = torch.empty(n_q * h * d, device="cuda")
+        c.attention_dev(dev(torch, q), dev(torch, k), dev(torch, v), sh, out)
+        torch.cuda.synchronize()
+        check(out.cpu().numpy().reshape(n_q, h * d), ref, "fp32 mode with a value of 2e5", x3=False, v_scale=2.0e5)
+    out = torch.empty(n_q * h * d, device="cuda")
+    ctx.attention_dev(dev(torch, q), dev(torch, k), dev(torch, v), sh, out)
+    torch.cuda.synchronize()
+    x3 = out.cpu().numpy().reshape(n_q, h * d)
+    # causal: the waves of queries < 64 never load the tile of keys 64..95, so column 7 is exact
+    # there; every other column of every row, and all of head 1, never meets the big value
+    other = np.ones(h * d, bool)
+    other[7] = False
+    check(x3[:, other], ref[:, other], "x3 columns without the big value")
+    check(x3[:64, 7], ref[:64, 7], "x3 column 7, rows before the big value's tile")
+    # rows 70.. see key 70: hi term +inf, lo term -inf, so NaN; rows 64..69 mask it (p = 0, and
+    # 0 * inf is NaN in IEEE arithmetic): NaN or, were the product flushed, the exact value
+    assert np.all(np.isnan(x3[70:, 7])), "x3 column 7 of the rows that see the big value must be NaN"
+    masked = x3[64:70, 7]
+    fin = np.isfinite(masked)
+    print(f"x3 column 7, rows 64..69 (big value masked): {int(np.sum(~fin))} of 6 NaN", flush=True)
+    if fin.any():
+        check(masked[fin], ref[64:70, 7][fin], "x3 column 7, finite rows 64..69")
+    host = np.zeros(n_q * h * d, np.float32)
+    ctx.attention_ex_host(q, k, v, sh, host)
+    check(host, ref, "drop-in with a value of 2e5", x3=False, v_scale=2.0e5)

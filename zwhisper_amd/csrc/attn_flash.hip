@@ -66,7 +66,9 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
     //               hardware deals round-robin over the 8 XCDs -- carry equal work
     const int64_t n_ih = (int64_t)a.n_batch * a.n_head;
     int chunk, qb, ih;
-    if (a.heavy_first) {
+    if (a.heavy_first == 2) {
+        dense_live_unit(a, lb, n_qblocks, BM, BN, &qb, &chunk, &ih);
+    } else if (a.heavy_first) {
         ih = (int)(lb % n_ih);
         const int64_t t = lb / n_ih;
         chunk = (int)(t % a.max_chunks);
@@ -441,7 +443,7 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
 hipError_t launch_flash(const AttnArgs &a, int d, hipStream_t stream, int *grid_blocks) {
     const int n_qblocks = (a.n_q + kFlashBM - 1) / kFlashBM;
     const int max_chunks = a.max_chunks;
-    const int64_t blocks = (int64_t)max_chunks * n_qblocks * a.n_batch * a.n_head;
+    const int64_t blocks = a.heavy_first == 2 ? a.live_blocks : (int64_t)max_chunks * n_qblocks * a.n_batch * a.n_head;
     if (blocks > 0x7fffffffll) return hipErrorInvalidValue;
     dim3 grid((unsigned)blocks);
     dim3 block(256);

@@ -1,21 +1,22 @@
-// Dense attention on gfx950 16-bit MFMA with f32-level accuracy: the fp32 kernel of
-// attn_flash.hip (same workgroup geometry, tile pipeline, online softmax, split and merge), with
-// each product of Q.K^T and P.V computed as three 16-bit MFMA products of split operands.
+// Dense attention on gfx950 f16 MFMA with f32-level accuracy: the fp32 kernel of attn_flash.hip
+// (same workgroup geometry, tile pipeline, online softmax, split and merge), with each product of
+// Q.K^T and P.V computed as three f16 MFMA products of split operands.
 //
-// Split.  Every f32 operand x is written as hi + lo with hi = t(x), lo = t(x - hi) for a 16-bit
-// type t, and a product a.b as ah.bh + ah.bl + al.bh (al.bl is below the rounding of lo), each on
-// a 32x32x16 MFMA with f32 accumulation: 12 MFMAs per 32 x 32 tile of Q.K^T (d = 64) and 12 for
-// P.V, against 64 fp32 MFMAs of 32x32x2, so about 5x fewer MFMA cycles.
-//   Q.K^T uses f16 (two terms carry 22 significand bits).  A score's error is absolute in the
-//   exponent, so it must not grow with the scores: with bf16 (16 bits) it does, by 2^-17 of
-//   sum |q_i k_i|, and scores spread 16x wider than unit-variance inputs give (large-logit heads)
-//   already cost 3e-4 at the output; with f16 the same inputs stay near 2e-5 (CPU emulation
-//   against f64).  f16's range is the price: Q enters pre-scaled by log2(e)/sqrt(d), and K must
-//   stay below 65504 in magnitude -- a larger key gives an infinite hi term and NaN outputs
-//   (never a silently wrong finite one; a masked key cannot poison anything).
-//   P.V uses bf16 (16 bits, f32's exponent range): P is at most 2^8 by the lazily moved running
-//   max and the output error is relative to |V| at ~2^-17, at any magnitude of V.
-// On Whisper-shaped unit-variance inputs the outputs stay within ~2e-6 of f64.
+// Split.  Every f32 operand x is written as hi + lo with hi = f16(x), lo = f16(x - hi) (together
+// 22 significand bits), and a product a.b as ah.bh + ah.bl + al.bh (al.bl is below the rounding of
+// lo), each on a 32x32x16 MFMA with f32 accumulation: 12 MFMAs per 32 x 32 tile of Q.K^T (d = 64)
+// and 12 for P.V, against 64 fp32 MFMAs of 32x32x2, so about 5x fewer MFMA cycles.
+//   A score's error is absolute in the exponent, so it must not grow with the scores: with bf16
+//   terms (16 bits) it does, by 2^-17 of sum |q_i k_i|, and scores spread 16x wider than
+//   unit-variance inputs give (large-logit heads) already cost 3e-4 at the output; with f16 the
+//   same inputs stay near 2e-5 (CPU emulation against f64).  P.V on f16 terms keeps the output's
+//   error near 2^-23 of |V| (bf16 terms gave 2^-17: measured 2e-5 on the Qwen2 prefill, 8e-7 now).
+//   f16's range is the price: Q enters pre-scaled by log2(e)/sqrt(d), and K and V must stay
+//   below 65504 in magnitude.  A larger key gives an infinite hi term and NaN in the rows that see
+//   it (a masked key is replaced by -inf before the softmax and cannot poison anything); a larger
+//   value gives NaN in its own output column of every row whose wave loads its 32-key tile, since
+//   inf - inf and 0 * inf are NaN -- never a silently wrong finite result.  P is at most 2^8 by the lazily moved running max.  f16 subnormals are
+//   kept by the MFMA, so small lo terms keep their absolute accuracy.
 //
 // Operands.  S^T = K . Q^T (M = keys, N = queries, K = head dims): lane l of the A operand (K)
 // holds key l%32, dims 16 j + 8 (l/32) + 0..7 of k-step j; the B operand (Q^T) the same dims of
@@ -26,9 +27,8 @@
 // + 0..3: the V^T tile is stored with keys 4..7 and 8..11 of every 16 swapped, so each lane's
 // eight keys are contiguous and one 16-byte read.
 //
-// LDS.  K tiles [key][dim] (f16) and V^T tiles [dim][key] (bf16), hi and lo planes,
-// double-buffered, 16-byte chunks XOR-swizzled by row so a wave's operand reads are
-// conflict-free.
+// LDS.  K tiles [key][dim] and V^T tiles [dim][key], f16 hi and lo planes, double-buffered,
+// 16-byte chunks XOR-swizzled by row so a wave's operand reads are conflict-free.
 #include <type_traits>
 
 #include "attn_kernels.hpp"
@@ -38,8 +38,6 @@ namespace zwg {
 namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
@@ -51,19 +49,10 @@ typedef float f32x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-// Splits, six VALU per pair of bf16 values and four per pair of f16 values.
-//   bf16: one v_cvt_pk_bf16_f32 rounds a pair; the hi terms come back to f32 from the packed
-//   bits (a shift, an and), two subtracts give the remainders, a second v_cvt_pk rounds them.
-//   f16: one v_cvt_pk_f16_f32 rounds a pair; v_fma_mix_f32 reads each half as f16 and forms
-//   x - hi in f32 in one instruction (exact: hi is x rounded, so x - hi is representable).
-__device__ __forceinline__ uint32_t split2_bf16(float a, float b, uint32_t &lo) {
-    const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
-    const float ha = __builtin_bit_cast(float, h << 16), hb = __builtin_bit_cast(float, h & 0xffff0000u);
-    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a - ha, b - hb}, bf16x2));
-    return h;
-}
+// f16 split of a pair, four VALU: one v_cvt_pk_f16_f32 rounds the pair; v_fma_mix_f32 reads each
+// half as f16 and forms x - hi in f32 in one instruction (exact: hi is x rounded, so x - hi is
+// representable); a second v_cvt_pk rounds the remainders.
 __device__ __forceinline__ float sub_f16_lo(uint32_t pair, float x) { // x - (float)low half of pair
     float r;
     asm("v_fma_mix_f32 %0, %1, -1.0, %2 op_sel:[0,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pair), "v"(x));
@@ -78,28 +67,6 @@ __device__ __forceinline__ uint32_t split2_f16(float a, float b, uint32_t &lo) {
     const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, f16x2));
     lo = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){sub_f16_lo(h, a), sub_f16_hi(h, b)}, f16x2));
     return h;
-}
-__device__ __forceinline__ void split8(const f32x8 &x, bf16x8 &hi, bf16x8 &lo) {
-    u32x4 h, l;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        uint32_t li;
-        h[i] = split2_bf16(x[2 * i], x[2 * i + 1], li);
-        l[i] = li;
-    }
-    hi = __builtin_bit_cast(bf16x8, h);
-    lo = __builtin_bit_cast(bf16x8, l);
-}
-__device__ __forceinline__ void split4(const f32x4 &x, bf16x4 &hi, bf16x4 &lo) {
-    u32x2 h, l;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        uint32_t li;
-        h[i] = split2_bf16(x[2 * i], x[2 * i + 1], li);
-        l[i] = li;
-    }
-    hi = __builtin_bit_cast(bf16x4, h);
-    lo = __builtin_bit_cast(bf16x4, l);
 }
 __device__ __forceinline__ void split8(const f32x8 &x, f16x8 &hi, f16x8 &lo) {
     u32x4 h, l;
@@ -153,7 +120,7 @@ __device__ __forceinline__ int k_at(int key, int dim) {
 }
 // V^T tile position of a key: bits 2 and 3 swapped (keys 4..7 <-> 8..11 of every 16)
 __device__ __forceinline__ int v_pos(int key) { return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1); }
-// V^T tile element (dim, pos): rows of 32 bf16 (64 bytes, 4 chunks), chunk c at c ^ ((dim >> 2) & 3)
+// V^T tile element (dim, pos): rows of 32 f16 (64 bytes, 4 chunks), chunk c at c ^ ((dim >> 2) & 3)
 __device__ __forceinline__ int v_at(int dim, int pos) {
     return dim * kFlashBN + ((((pos >> 3) ^ ((dim >> 2) & 3)) << 3) | (pos & 7));
 }
@@ -173,8 +140,8 @@ void flash_x3_kernel(AttnArgs a) {
 
     __shared__ __align__(16) _Float16 Kh[2][BN * D];
     __shared__ __align__(16) _Float16 Kl[2][BN * D];
-    __shared__ __align__(16) __bf16 Vh[2][D * BN];
-    __shared__ __align__(16) __bf16 Vl[2][D * BN];
+    __shared__ __align__(16) _Float16 Vh[2][D * BN];
+    __shared__ __align__(16) _Float16 Vl[2][D * BN];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -187,7 +154,9 @@ void flash_x3_kernel(AttnArgs a) {
     const int64_t lb = a.xcd_group ? xcd_logical_block(blockIdx.x, (int64_t)gridDim.x) : (int64_t)blockIdx.x;
     const int64_t n_ih = (int64_t)a.n_batch * a.n_head;
     int chunk, qb, ih;
-    if (a.heavy_first) {
+    if (a.heavy_first == 2) {
+        dense_live_unit(a, lb, n_qblocks, BM, BN, &qb, &chunk, &ih);
+    } else if (a.heavy_first) {
         ih = (int)(lb % n_ih);
         const int64_t t = lb / n_ih;
         chunk = (int)(t % a.max_chunks);
@@ -328,11 +297,11 @@ void flash_x3_kernel(AttnArgs a) {
     auto store_v = [&](int buf) {
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
-            bf16x4 h, l;
+            f16x4 h, l;
             split4(vr[g], h, l);
             const int at = v_at(v_dim, v_pos(v_key(g))); // keys 4q .. 4q+3 sit at four consecutive positions
-            *reinterpret_cast<bf16x4 *>(&Vh[buf][at]) = h;
-            *reinterpret_cast<bf16x4 *>(&Vl[buf][at]) = l;
+            *reinterpret_cast<f16x4 *>(&Vh[buf][at]) = h;
+            *reinterpret_cast<f16x4 *>(&Vl[buf][at]) = l;
         }
     };
     // one k-step of S^T = K . Q^T: three f16 products
@@ -414,16 +383,16 @@ void flash_x3_kernel(AttnArgs a) {
             f32x8 pr;
 #pragma unroll
             for (int e = 0; e < 8; ++e) pr[e] = p[8 * s + e];
-            bf16x8 ph, pl;
+            f16x8 ph, pl;
             split8(pr, ph, pl);
 #pragma unroll
             for (int db = 0; db < NDB; ++db) {
                 const int at = v_at(db * 32 + col, 16 * s + 8 * half);
-                const bf16x8 vh = *reinterpret_cast<const bf16x8 *>(&Vh[buf][at]);
-                const bf16x8 vl = *reinterpret_cast<const bf16x8 *>(&Vl[buf][at]);
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, ph, o[db], 0, 0, 0);
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vh, pl, o[db], 0, 0, 0);
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vl, ph, o[db], 0, 0, 0);
+                const f16x8 vh = *reinterpret_cast<const f16x8 *>(&Vh[buf][at]);
+                const f16x8 vl = *reinterpret_cast<const f16x8 *>(&Vl[buf][at]);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, ph, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, pl, o[db], 0, 0, 0);
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, ph, o[db], 0, 0, 0);
             }
         }
         __builtin_amdgcn_s_setprio(0);
@@ -509,7 +478,7 @@ void flash_x3_kernel(AttnArgs a) {
 
 hipError_t launch_flash_x3(const AttnArgs &a, int d, hipStream_t stream, int *grid_blocks) {
     const int n_qblocks = (a.n_q + kFlashBM - 1) / kFlashBM;
-    const int64_t blocks = (int64_t)a.max_chunks * n_qblocks * a.n_batch * a.n_head;
+    const int64_t blocks = a.heavy_first == 2 ? a.live_blocks : (int64_t)a.max_chunks * n_qblocks * a.n_batch * a.n_head;
     if (blocks > 0x7fffffffll) return hipErrorInvalidValue;
     dim3 grid((unsigned)blocks);
     dim3 block(256);

@@ -30,6 +30,7 @@ struct AttnArgs {
     int32_t heavy_first; // dense kernel: dispatch the longest (causal) q-blocks first
     int32_t xcd_group;   // dense kernel: run each head's q-blocks on one XCD (xcd_logical_block)
     int32_t rows_per_unit; // query rows sharing one key range (flash: BM; decode: n_q)
+    int64_t live_blocks;   // dense, heavy_first == 2: workgroups of the grid (dense_live_unit)
     float *part_o;      // [row][max_chunks][d]   unnormalised sum of p*v
     float *part_ml;     // [row][max_chunks][2]   (running max in log2 units, sum of p)
 };
@@ -88,6 +89,37 @@ __device__ inline bool decode_compact_unit(const AttnArgs &a, int tile, int64_t 
         base += __shfl(incl, 63);
     }
     return false;
+}
+
+// Causal dense calls with one key count for every item (heavy_first == 2): the grid holds only the
+// (q-block, chunk, item*head) triples that have keys -- a chunk index past its q-block's chunk
+// count would leave a workgroup with nothing to do, scattered through the grid -- ranked longest
+// q-block first, then chunk, with item*head fastest.  The hardware deals workgroup b to CU
+// b mod 256, so each band of 256 ranks puts one workgroup on every CU; the odd bands are dealt in
+// reverse (the CU given a band's heaviest workgroup gets the next band's lightest), which evens
+// out each CU's total.  A partial last band keeps its order.
+__device__ inline void dense_live_unit(const AttnArgs &a, int64_t lb, int n_qblocks, int bm, int bn, int *qb,
+                                       int *chunk, int *ih) {
+    const int64_t n_ih = (int64_t)a.n_batch * a.n_head;
+    const int64_t band = lb >> 8;
+    int64_t rank = lb;
+    if ((band & 1) && (band + 1) * 256 <= (int64_t)gridDim.x) rank = (band << 8) + 255 - (lb & 255);
+    int q = n_qblocks - 1;
+    int n_ch = 1;
+    for (; q > 0; --q) {
+        const int q_end = min((q + 1) * bm, a.n_q);
+        int ck;
+        n_ch = unit_split(max(0, a.n_kv - a.n_q + q_end), bn, a.chunk_len, a.max_chunks, &ck);
+        if (rank < (int64_t)n_ch * n_ih) break;
+        rank -= (int64_t)n_ch * n_ih;
+    }
+    if (q == 0) {
+        int ck;
+        n_ch = unit_split(max(0, a.n_kv - a.n_q + min(bm, a.n_q)), bn, a.chunk_len, a.max_chunks, &ck);
+    }
+    *qb = q;
+    *chunk = (int)(rank / n_ih);
+    *ih = (int)(rank - (int64_t)*chunk * n_ih);
 }
 
 // MI355X deals consecutive workgroups round-robin over its 8 XCDs, each with its own L2.

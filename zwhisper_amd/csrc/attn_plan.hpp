@@ -167,6 +167,19 @@ inline Plan make_plan(const zwg_attn_shape &s, const zwg_batch &b, uint64_t ws_c
     p.grid_blocks = p.kernel == 2 ? chunks * s.n_head_kv * b.n_batch : chunks * units;
     p.ws_bytes = split_ws_bytes(n_rows_total, (uint64_t)p.max_chunks, s.d);
     p.heavy_first = p.kernel == 1 && s.causal;
+    if (p.heavy_first && !b.n_kv_dev) {
+        // one key count for every item: the grid holds only the (q-block, chunk, item*head)
+        // triples with keys (dense_live_unit)
+        const uint64_t BM = zwg::kFlashBM, n_qb = ceil_div(s.n_q, BM);
+        uint64_t live = 0;
+        for (uint64_t qb = 0; qb < n_qb; ++qb) {
+            const uint64_t q_end = std::min(s.n_q, (qb + 1) * BM);
+            int ck = 0;
+            live += (uint64_t)zwg::unit_split((int)(s.n_kv - s.n_q + q_end), (int)tile, p.chunk_len, p.max_chunks, &ck);
+        }
+        p.grid_blocks = live * s.n_head * b.n_batch;
+        p.heavy_first = 2;
+    }
     // unsplit non-causal calls: each head's q-blocks on one XCD (measured: same time, 5x fewer
     // L2 misses on the base.en encoder); split ones keep the hardware order (measured faster)
     p.xcd_group = p.kernel == 1 && !s.causal && p.max_chunks == 1;

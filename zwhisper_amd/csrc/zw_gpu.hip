@@ -172,6 +172,7 @@ int run(zwg_ctx *ctx, const Exec &x, const float *q, const float *k, const float
     a.heavy_first = p.heavy_first;
     a.xcd_group = p.xcd_group;
     a.rows_per_unit = p.rows_per_unit;
+    a.live_blocks = (int64_t)p.grid_blocks;
     const uint64_t n_rows = b.n_batch * s.n_head * s.n_q;
     a.part_ml = x.ws;
     a.part_o = x.ws + (p.max_chunks > 1 ? part_o_offset(n_rows, (uint64_t)p.max_chunks) : 0);
