@@ -808,7 +808,7 @@ def traffic_for(workload_name: str):
         return None
 
 
-DENSE_DTYPE = ("x3: f32 inputs split into 16-bit hi + lo terms (f16 for Q.K^T, bf16 for P.V), three 16-bit MFMA "
+DENSE_DTYPE = ("x3: f32 inputs split into 16-bit hi + lo terms (f16 for Q.K^T and for P.V), three 16-bit MFMA "
                "products per product, f32 accumulation")
 
 

@@ -17,9 +17,14 @@
 //   wave-private LDS row to the V pass, where lanes run along the head dims.
 //
 // decode_rm_kernel -- row-major K ([key][kv_stride], the Whisper decoder caches,
-//   src/decoder.zig:39-42).  One 256-thread workgroup per chunk, walked in 256-key tiles:
+//   src/decoder.zig:39-42).  One 256-thread workgroup per chunk, walked in tiles of T keys
+//   (256, or 64 for caches of at most 512 keys, so short caches still split over many chunks):
 //   D/4 lanes per key row with a butterfly sum for the scores, the tile's softmax in LDS, then
 //   D/4 lanes per V row; loads are issued in batches so a thread has several in flight.
+//
+// With per-item key counts (n_kv_item) both kernels number their workgroups over the list of
+// non-empty chunks (decode_compact_unit), so the CUs share the work evenly however the counts
+// differ.
 #include "attn_kernels.hpp"
 
 namespace zwg {
