@@ -172,8 +172,9 @@ int run_q8_stream_mt(zwg_ctx *ctx, const zwg_lin::Q8Args &base) {
 }
 
 // Resident packed weights with m <= 64, one or more weight sets over the same x (g.count sets;
-// q/scales/n_slabs/n/bias/out filled by the caller): one x split, one stream launch over every
-// set's workgroups (four slabs of 32 rows each), one split sum over every set's outputs.  The k
+// q/scales/n_slabs/n/bias/out filled by the caller): one stream launch over every set's
+// workgroups (four slabs of 32 rows each), preceded by one x split for 64-row calls (32-row calls
+// split x inside the stream kernel), and when k is split, one split sum over every set's outputs.  The k
 // split is chosen from the group's total workgroup count, as for a single call.
 #ifndef ZWG_Q8P_WAVES
 #define ZWG_Q8P_WAVES 4
@@ -181,6 +182,7 @@ int run_q8_stream_mt(zwg_ctx *ctx, const zwg_lin::Q8Args &base) {
 // waves (one 32-row slab each) sharing each x stage of the packed stream kernel (8 measured
 // 5-9% slower on the logits and decode-step workloads: half the workgroups, longer tails)
 constexpr int kQ8pWaves = ZWG_Q8P_WAVES;
+
 
 template <int MT>
 int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g) {
@@ -200,7 +202,9 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g)
     g.elem_start[zwg_lin::kQ8MaxGroup] = (int64_t)(m * n_tot);
     const int n_chunks = (a.k + zwg_lin::kQ8Chunk - 1) / zwg_lin::kQ8Chunk;
     g.n_chunks = n_chunks;
-    const uint64_t xcvt_bytes = (uint64_t)n_chunks * zwg_lin::q8_chunk_halves<MT>() * 2;
+    // 32-row calls split x inside the stream kernel; 64-row ones in a pass of their own first
+    constexpr bool XS = MT == 1;
+    const uint64_t xcvt_bytes = XS ? 0 : (uint64_t)n_chunks * zwg_lin::q8_chunk_halves<MT>() * 2;
     const uint64_t part_off = (xcvt_bytes + 255) / 256 * 256;
     if (part_off > ctx->workspace_bytes) return fail(ctx, "workspace too small for this linear call");
     int n_split = 1;
@@ -215,16 +219,18 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g)
         g.part[j] = (j < g.count && n_split > 1) ? reinterpret_cast<float *>(ws + off) : nullptr;
         if (j < g.count) off += (uint64_t)n_split * m * (uint64_t)g.n[j] * 4;
     }
-    _Float16 *xcvt = reinterpret_cast<_Float16 *>(ctx->workspace);
-
-    const int64_t prep_threads = (int64_t)n_chunks * MT * 32 * (zwg_lin::kQ8Chunk / 4);
-    const int prep_bs = small_block(prep_threads);
-    zwg_lin::linear_q8_xprep_kernel<MT><<<blocks_for(prep_threads, prep_bs), prep_bs, 0, ctx->stream>>>(
-        a.x, xcvt, a.m, a.k, n_chunks);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return fail_hip(ctx, "linear (int8) x preparation launch", e);
+    _Float16 *xcvt = XS ? nullptr : reinterpret_cast<_Float16 *>(ctx->workspace);
+    hipError_t e;
+    if (!XS) {
+        const int64_t prep_threads = (int64_t)n_chunks * MT * 32 * (zwg_lin::kQ8Chunk / 4);
+        const int prep_bs = small_block(prep_threads);
+        zwg_lin::linear_q8_xprep_kernel<MT><<<blocks_for(prep_threads, prep_bs), prep_bs, 0, ctx->stream>>>(
+            a.x, xcvt, a.m, a.k, n_chunks);
+        e = hipGetLastError();
+        if (e != hipSuccess) return fail_hip(ctx, "linear (int8) x preparation launch", e);
+    }
     dim3 grid((unsigned)gx, (unsigned)n_split);
-    zwg_lin::linear_q8p_stream_kernel<MT, 1, kQ8pWaves><<<grid, 64 * kQ8pWaves, 0, ctx->stream>>>(a, g, xcvt);
+    zwg_lin::linear_q8p_stream_kernel<MT, 1, kQ8pWaves, XS><<<grid, 64 * kQ8pWaves, 0, ctx->stream>>>(a, g, xcvt);
     e = hipGetLastError();
     if (e != hipSuccess) return fail_hip(ctx, "linear (int8 stream) kernel launch", e);
     if (n_split > 1) {

@@ -324,21 +324,34 @@ __global__ __launch_bounds__(256) void linear_q8_pack_kernel(const int8_t *q, co
 
 // The stream kernel over packed weights, software-pipelined.  k is walked in stages of 4 blocks
 // (128 k).  x stages sit in LDS double-buffered and each wave keeps two register sets of weights
-// and scales, so the loads of stage t + 1 (x by LDS DMA, then weights, then scales) are in flight
-// while stage t's MFMAs run: at the top of stage t the wave waits only for its own x pieces of
-// stage t (loads complete in order, and stage t's weights were issued after them), and the
-// barrier that follows also tells every wave that stage t - 1's LDS buffer is free again.
+// and scales, so the loads of stage t + 1 (x, then weights, then scales) are in flight while stage
+// t's MFMAs run: at the top of stage t the wave waits only for its x of stage t (loads complete in
+// order, and stage t's weights were issued after them), and the barrier that follows tells every
+// wave that the stage's x is in LDS (and that stage t - 1's buffer is free again).  Two x paths:
+//   XS = false: x was split into f16 hi/lo halves in the MFMA A-operand order (q8_xs_at) by
+//     linear_q8_xprep_kernel; each stage's pieces are copied into LDS by direct global-to-LDS loads
+//     (no VGPRs, no VALU).
+//   XS = true: no separate pass.  A stage's f32 x rows arrive in registers (coalesced 16-byte
+//     loads) and each workgroup splits them and writes them into the LDS stage itself before the
+//     barrier.  This costs registers and a short split before each barrier, and saves a launch:
+//     the better trade for 32-row calls (measured: Whisper small.en decoder step 784 -> 681 us),
+//     the worse one at 64 rows (Qwen2.5-1.5B logits 109 -> 150 us).
 // Padding blocks (k is padded to 256) have scale 0 and x 0; a stage wholly past k is not run.
 constexpr int kQ8StageBlocks = 4;
+constexpr int kQ8StageK = kQ8StageBlocks * kQ8Block;
 
-template <int MT, int S, int NW>
-__global__ __launch_bounds__(64 * NW) void linear_q8p_stream_kernel(Q8Args a, Q8Group grp, const _Float16 *xcvt) {
+template <int MT, int S, int NW, bool XS>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
+void linear_q8p_stream_kernel(Q8Args a, Q8Group grp, const _Float16 *xcvt) {
     constexpr int NB = kQ8StageBlocks;
+    constexpr int NT = 64 * NW;
     constexpr int SLABS = NW * S;                 // slabs of 32 weight rows per workgroup (NW waves)
     constexpr int PIECES = NB * MT * 4;           // 1 KB pieces of an x stage
-    constexpr int XL = PIECES / NW;               // pieces each wave copies
+    constexpr int XL = PIECES / NW;               // pieces each wave copies (XS = false)
     static_assert(PIECES % NW == 0, "every wave copies whole pieces of the x stage");
     constexpr int STAGE_HALVES = PIECES * 512;
+    constexpr int XQ = XS ? MT * 32 * kQ8StageK / 4 / NT : 1; // 16-byte x loads per thread (XS = true)
+    static_assert(!XS || XQ * 4 * NT == MT * 32 * kQ8StageK, "every thread loads whole quads of the x stage");
     __shared__ __align__(16) _Float16 xs[2][STAGE_HALVES];
 
     // this workgroup's weight set and its index within the set
@@ -359,7 +372,10 @@ __global__ __launch_bounds__(64 * NW) void linear_q8p_stream_kernel(Q8Args a, Q8
     const int t_begin = split * a.chunks_per_split * 2;
     const int t_end = min(t_begin + a.chunks_per_split * 2, n_stages);
 
-    const __amdgpu_buffer_rsrc_t x_src = rsrc(xcvt, (uint32_t)w.n_chunks * 2u * (uint32_t)PIECES * 1024u);
+    // XS: x [m][k] f32, rows past m read as 0 (range), columns past k get an out-of-range offset;
+    // otherwise the call's split x chunks
+    const __amdgpu_buffer_rsrc_t x_src =
+        XS ? rsrc(a.x, (uint32_t)a.m * (uint32_t)a.k * 4u) : rsrc(xcvt, (uint32_t)w.n_chunks * 2u * (uint32_t)PIECES * 1024u);
     // slabs past the matrix (the last workgroup's) read as 0
     const int live = __builtin_amdgcn_readfirstlane(max(0, min(S, w.n_slabs - slab0)));
     const int64_t slab_q = (int64_t)w.n_chunks * kQ8ChunkBlocks * 1024;
@@ -368,18 +384,39 @@ __global__ __launch_bounds__(64 * NW) void linear_q8p_stream_kernel(Q8Args a, Q8
     const __amdgpu_buffer_rsrc_t s_src =
         rsrc(reinterpret_cast<const char *>(w.scales) + (int64_t)slab0 * slab_s, (uint32_t)(live * slab_s));
 
-    // stage t: x pieces into LDS buffer `buf`, then this wave's weights and scales into (wq, sc).
-    // Past the last stage (t >= t_end) the same loads go out with out-of-range offsets: they return
-    // zeros without touching memory, and every path through the loop then has the same loads in
-    // flight, so the compiler's in-order wait counts stay exact.
-    auto issue = [&](int t, int buf, u32x4 (&wq)[S][NB], f32x4 (&sc)[S]) {
+    // XS: x quad e of this thread in a stage is row x_r0 + XR e, k 4 (tid % 32) of the stage; 32
+    // consecutive threads read 512 contiguous bytes of a row.  The per-lane part of the offset is
+    // one VGPR; the row step and the stage's k go in the scalar offset.  The quad's place in the
+    // A-operand order: block, k-step and half of a lane's 8 elements follow the column, the m-tile
+    // and lane the row.
+    constexpr int XR = NT / 32; // rows between a thread's quads
+    const int x_r0 = tid >> 5, x_c = 4 * (tid & 31);
+    const uint32_t x_lane = ((uint32_t)x_r0 * (uint32_t)a.k + (uint32_t)x_c) * 4u;
+    const uint32_t x_rstep = (uint32_t)XR * (uint32_t)a.k * 4u;
+    const int x_b = x_c >> 5, x_kb = x_c & 31;
+    const int x_s = (x_kb >> 3) & 1, x_j = x_kb & 7;
+
+    // stage t: its x (into LDS buffer `buf`, or into xr), then this wave's weights and scales into
+    // (wq, sc).  Past the last stage (t >= t_end) the same loads go out with out-of-range offsets:
+    // they return zeros without touching memory, and every path through the loop then has the same
+    // loads in flight, so the compiler's in-order wait counts stay exact.
+    auto issue = [&](int t, int buf, f32x4 (&xr)[XQ], u32x4 (&wq)[S][NB], f32x4 (&sc)[S]) {
         const bool live_t = t < t_end;
+        if constexpr (XS) {
+            const uint32_t xv = live_t && t * kQ8StageK + x_c < a.k ? x_lane : kOutOfRange;
 #pragma unroll
-        for (int u = 0; u < XL; ++u) {
-            const int piece = wave + NW * u;
-            const uint32_t off = live_t ? (uint32_t)((t * PIECES + piece) * 1024 + lane * 16) : kOutOfRange;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                x_src, (__attribute__((address_space(3))) void *)(&xs[buf][piece * 512]), 16, off, 0, 0, 0);
+            for (int e = 0; e < XQ; ++e)
+                xr[e] = __builtin_bit_cast(
+                    f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                               x_src, (int)xv, (int)((uint32_t)e * x_rstep + (uint32_t)(t * kQ8StageK) * 4u), 0));
+        } else {
+#pragma unroll
+            for (int u = 0; u < XL; ++u) {
+                const int piece = wave + NW * u;
+                const uint32_t off = live_t ? (uint32_t)((t * PIECES + piece) * 1024 + lane * 16) : kOutOfRange;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    x_src, (__attribute__((address_space(3))) void *)(&xs[buf][piece * 512]), 16, off, 0, 0, 0);
+            }
         }
 #pragma unroll
         for (int s = 0; s < S; ++s) {
@@ -395,6 +432,25 @@ __global__ __launch_bounds__(64 * NW) void linear_q8p_stream_kernel(Q8Args a, Q8
                 live_t ? (uint32_t)(s * slab_s + (((t >> 1) * 32 + r32) * kQ8ChunkBlocks + 4 * (t & 1)) * 4)
                        : kOutOfRange;
             sc[s] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(s_src, (int)off, 0, kQ8CachePolicyNT));
+        }
+    };
+    // XS: the stage's x quads, split into f16 hi/lo halves, into LDS buffer `buf` (a quad is half of
+    // one lane's 8-element piece)
+    auto put_x = [&](int buf, const f32x4 (&xr)[XQ]) {
+        if constexpr (XS) {
+#pragma unroll
+            for (int e = 0; e < XQ; ++e) {
+                const int row = x_r0 + XR * e;
+                const int i = row >> 5, l = (row & 31) + 32 * (x_kb >> 4);
+                half4 hi, lo;
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    hi[c] = (_Float16)xr[e][c];
+                    lo[c] = (_Float16)(xr[e][c] - (float)hi[c]);
+                }
+                *reinterpret_cast<half4 *>(&xs[buf][q8_xs_at<MT>(x_b, i, 0, x_s, l) + x_j]) = hi;
+                *reinterpret_cast<half4 *>(&xs[buf][q8_xs_at<MT>(x_b, i, 1, x_s, l) + x_j]) = lo;
+            }
         }
     };
 
@@ -433,26 +489,30 @@ __global__ __launch_bounds__(64 * NW) void linear_q8p_stream_kernel(Q8Args a, Q8
         }
     };
 
-    // Two register sets (A for even stages, B for odd) so every index is static.
+    // Two weight and scale register sets (A for even stages, B for odd) so every index is static;
+    // with XS one x register set, written into LDS at the top of its stage and then reloaded.
+    f32x4 xr[XQ];
     u32x4 wqA[S][NB], wqB[S][NB];
     f32x4 scA[S], scB[S];
     constexpr int LOADS = S * (NB + 1); // weight and scale loads of one stage, issued after its x
-    issue(t_begin, 0, wqA, scA);
+    issue(t_begin, 0, xr, wqA, scA);
     for (int t = t_begin; t < t_end; t += 2) {
         // stage t (set A, buffer 0)
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(q8_vmcnt(LOADS));
+        put_x(0, xr);
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
-        issue(t + 1, 1, wqB, scB);
+        issue(t + 1, 1, xr, wqB, scB);
         __builtin_amdgcn_sched_barrier(0);
         compute(0, wqA, scA);
         // stage t + 1 (set B, buffer 1); a no-op past the end (its loads returned zeros)
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(q8_vmcnt(LOADS));
+        put_x(1, xr);
         __syncthreads();
         __builtin_amdgcn_sched_barrier(0);
-        issue(t + 2, 0, wqA, scA);
+        issue(t + 2, 0, xr, wqA, scA);
         __builtin_amdgcn_sched_barrier(0);
         if (t + 1 < t_end) compute(1, wqB, scB);
     }
