@@ -78,6 +78,22 @@ def test_linear_matches_reference(torch, ctx, m, k, n):
         assert float(np.abs(got - ora).max()) <= err + bar
 
 
+@pytest.mark.parametrize("m,k,n", [
+    (24033, 1000, 1288),  # the 128 x 256 tiles: a partial row tile, a partial column tile, k % 32 = 8
+    (8200, 264, 520),     # the 64 x 256 tiles, the same tails
+])
+def test_linear_large_tiles(torch, ctx, m, k, n):
+    """Shapes large enough for the x 256 tiles (the encoder's 16-window projections take them),
+    with tails in every dimension, against f64."""
+    x, w, b = inputs(m + 3 * n + k, m, k, n)
+    got = run_dev(torch, ctx, x, w, b, m, k, n)
+    ref = ref64(x, w, b)
+    err = float(np.abs(got - ref).max())
+    bar = 2e-5 * np.sqrt(k)
+    print(f"linear {m}x{k}x{n}: max abs {err:.2e} (bar {bar:.1e})", flush=True)
+    assert np.all(np.isfinite(got)) and err <= bar
+
+
 def split_product(x, wv):
     """What one weight times x gives through the two-term split: f32(wv*hi + wv*lo), hi = f16(x),
     lo = f16(x - hi) -- both products exact in f32, one rounding for the sum."""
