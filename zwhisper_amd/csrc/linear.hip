@@ -174,14 +174,23 @@ int run_q8_stream_mt(zwg_ctx *ctx, const zwg_lin::Q8Args &base) {
 // Resident packed weights with m <= 64, one or more weight sets over the same x (g.count sets;
 // q/scales/n_slabs/n/bias/out filled by the caller): one stream launch over every set's
 // workgroups (four slabs of 32 rows each), preceded by one x split for 64-row calls (32-row calls
-// split x inside the stream kernel), and when k is split, one split sum over every set's outputs.  The k
-// split is chosen from the group's total workgroup count, as for a single call.
+// split x inside the stream kernel), and when k is split, one split sum over every set's outputs.
+// The k split is chosen from the group's total workgroup count, as for a single call: a call of
+// fewer than ZWG_Q8P_SPLIT_BELOW workgroups is split until it has about 512.
 #ifndef ZWG_Q8P_WAVES
 #define ZWG_Q8P_WAVES 4
 #endif
 // waves (one 32-row slab each) sharing each x stage of the packed stream kernel (8 measured
 // 5-9% slower on the logits and decode-step workloads: half the workgroups, longer tails)
 constexpr int kQ8pWaves = ZWG_Q8P_WAVES;
+// k is split only for calls below this many workgroups.  A call at or above it streams unsplit:
+// its partial sums would be as large as half its weights (the Qwen2.5-1.5B gate/up, 140
+// workgroups: split 3 ways, 13.8 MB of partials for 27.5 MB of weights).  Measured on one box,
+// splitting below 512 / 160 / 100 / 64 workgroups: Qwen2.5-1.5B decode step 2297 / 2297 / 2126 /
+// 2118 us, small.en decoder step 690 / 675 / 675 / 675 us.
+#ifndef ZWG_Q8P_SPLIT_BELOW
+#define ZWG_Q8P_SPLIT_BELOW 128
+#endif
 
 
 template <int MT>
@@ -208,7 +217,7 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g)
     const uint64_t part_off = (xcvt_bytes + 255) / 256 * 256;
     if (part_off > ctx->workspace_bytes) return fail(ctx, "workspace too small for this linear call");
     int n_split = 1;
-    if (gx < 512) n_split = (int)std::min<int64_t>(n_chunks, (512 + gx - 1) / gx);
+    if (gx < ZWG_Q8P_SPLIT_BELOW) n_split = (int)std::min<int64_t>(n_chunks, (512 + gx - 1) / gx);
     while (n_split > 1 && part_off + (uint64_t)n_split * m * n_tot * 4 > ctx->workspace_bytes) --n_split;
     a.chunks_per_split = (n_chunks + n_split - 1) / n_split;
     n_split = (n_chunks + a.chunks_per_split - 1) / a.chunks_per_split; // no empty splits
