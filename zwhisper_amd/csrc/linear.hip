@@ -188,6 +188,9 @@ constexpr int kQ8pWaves = ZWG_Q8P_WAVES;
 // workgroups: split 3 ways, 13.8 MB of partials for 27.5 MB of weights).  Measured on one box,
 // splitting below 512 / 160 / 100 / 64 workgroups: Qwen2.5-1.5B decode step 2297 / 2297 / 2126 /
 // 2118 us, small.en decoder step 690 / 675 / 675 / 675 us.
+#ifndef ZWG_Q8P_XS_SPLIT
+#define ZWG_Q8P_XS_SPLIT 1
+#endif
 #ifndef ZWG_Q8P_SPLIT_BELOW
 #define ZWG_Q8P_SPLIT_BELOW 128
 #endif
@@ -211,13 +214,16 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g)
     g.elem_start[zwg_lin::kQ8MaxGroup] = (int64_t)(m * n_tot);
     const int n_chunks = (a.k + zwg_lin::kQ8Chunk - 1) / zwg_lin::kQ8Chunk;
     g.n_chunks = n_chunks;
-    // 32-row calls split x inside the stream kernel; 64-row ones in a pass of their own first
-    constexpr bool XS = MT == 1;
+    // 32-row calls split x inside the stream kernel; 64-row ones too when k is split (small
+    // calls, where the separate pass's launch costs more than the fused split), otherwise in a
+    // pass of their own first
+    const bool split_k = gx < ZWG_Q8P_SPLIT_BELOW && n_chunks > 1;
+    const bool XS = MT == 1 || (ZWG_Q8P_XS_SPLIT && split_k);
     const uint64_t xcvt_bytes = XS ? 0 : (uint64_t)n_chunks * zwg_lin::q8_chunk_halves<MT>() * 2;
     const uint64_t part_off = (xcvt_bytes + 255) / 256 * 256;
     if (part_off > ctx->workspace_bytes) return fail(ctx, "workspace too small for this linear call");
     int n_split = 1;
-    if (gx < ZWG_Q8P_SPLIT_BELOW) n_split = (int)std::min<int64_t>(n_chunks, (512 + gx - 1) / gx);
+    if (split_k) n_split = (int)std::min<int64_t>(n_chunks, (512 + gx - 1) / gx);
     while (n_split > 1 && part_off + (uint64_t)n_split * m * n_tot * 4 > ctx->workspace_bytes) --n_split;
     a.chunks_per_split = (n_chunks + n_split - 1) / n_split;
     n_split = (n_chunks + a.chunks_per_split - 1) / a.chunks_per_split; // no empty splits
@@ -239,7 +245,8 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g)
         if (e != hipSuccess) return fail_hip(ctx, "linear (int8) x preparation launch", e);
     }
     dim3 grid((unsigned)gx, (unsigned)n_split);
-    zwg_lin::linear_q8p_stream_kernel<MT, 1, kQ8pWaves, XS><<<grid, 64 * kQ8pWaves, 0, ctx->stream>>>(a, g, xcvt);
+    if (XS) zwg_lin::linear_q8p_stream_kernel<MT, 1, kQ8pWaves, true><<<grid, 64 * kQ8pWaves, 0, ctx->stream>>>(a, g, xcvt);
+    else zwg_lin::linear_q8p_stream_kernel<MT, 1, kQ8pWaves, false><<<grid, 64 * kQ8pWaves, 0, ctx->stream>>>(a, g, xcvt);
     e = hipGetLastError();
     if (e != hipSuccess) return fail_hip(ctx, "linear (int8 stream) kernel launch", e);
     if (n_split > 1) {

@@ -334,8 +334,9 @@ __global__ __launch_bounds__(256) void linear_q8_pack_kernel(const int8_t *q, co
 //   XS = true: no separate pass.  A stage's f32 x rows arrive in registers (coalesced 16-byte
 //     loads) and each workgroup splits them and writes them into the LDS stage itself before the
 //     barrier.  This costs registers and a short split before each barrier, and saves a launch:
-//     the better trade for 32-row calls (measured: Whisper small.en decoder step 784 -> 681 us),
-//     the worse one at 64 rows (Qwen2.5-1.5B logits 109 -> 150 us).
+//     the better trade for 32-row calls and for small 64-row calls whose k is split (measured:
+//     Whisper small.en decoder step 784 -> 681 us, Qwen2.5-1.5B decode step 2095 -> 1960 us), the
+//     worse one for a large unsplit 64-row call (Qwen2.5-1.5B logits 109 -> 150 us).
 // Padding blocks (k is padded to 256) have scale 0 and x 0; a stage wholly past k is not run.
 constexpr int kQ8StageBlocks = 4;
 constexpr int kQ8StageK = kQ8StageBlocks * kQ8Block;
