@@ -52,33 +52,9 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
     const int col = lane & 31;
     const int half = lane >> 5;
 
-    // logical block = ((item * n_head + head) * n_qblocks + qb) * max_chunks + chunk, so the
-    // q-blocks and splits of one head (which share its K/V) are neighbours on one XCD
     const int n_qblocks = (a.n_q + BM - 1) / BM;
-    const int64_t lb = a.xcd_group ? xcd_logical_block(blockIdx.x, (int64_t)gridDim.x) : (int64_t)blockIdx.x;
-    // workgroup -> (item*head, q-block, chunk):
-    //  default      ((item * n_head + head) * n_qblocks + qb) * max_chunks + chunk; with
-    //               xcd_group the q-blocks of a head, which read the same K and V, share an
-    //               XCD and its L2, so K/V leave HBM about once per head
-    //  heavy_first  ((n_qblocks - 1 - qb) * max_chunks + chunk) * n_batch*n_head + item*head:
-    //               the longest (causal) q-blocks start first and shorter work fills the slots
-    //               they free; heads vary fastest, so neighbouring workgroups -- which the
-    //               hardware deals round-robin over the 8 XCDs -- carry equal work
-    const int64_t n_ih = (int64_t)a.n_batch * a.n_head;
     int chunk, qb, ih;
-    if (a.heavy_first == 2) {
-        dense_live_unit(a, lb, n_qblocks, BM, BN, &qb, &chunk, &ih);
-    } else if (a.heavy_first) {
-        ih = (int)(lb % n_ih);
-        const int64_t t = lb / n_ih;
-        chunk = (int)(t % a.max_chunks);
-        qb = n_qblocks - 1 - (int)(t / a.max_chunks);
-    } else {
-        chunk = (int)(lb % a.max_chunks);
-        const int64_t lq = lb / a.max_chunks;
-        qb = (int)(lq % n_qblocks);
-        ih = (int)(lq / n_qblocks);
-    }
+    dense_unit(a, n_qblocks, BM, BN, &qb, &chunk, &ih);
     const int item = ih / a.n_head;
     const int head = ih - item * a.n_head;
     const int hk = head / a.group;

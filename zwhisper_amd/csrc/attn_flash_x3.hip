@@ -149,24 +149,9 @@ void flash_x3_kernel(AttnArgs a) {
     const int col = lane & 31;
     const int half = lane >> 5;
 
-    // workgroup -> (item*head, q-block, chunk), as flash_attn_kernel
     const int n_qblocks = (a.n_q + BM - 1) / BM;
-    const int64_t lb = a.xcd_group ? xcd_logical_block(blockIdx.x, (int64_t)gridDim.x) : (int64_t)blockIdx.x;
-    const int64_t n_ih = (int64_t)a.n_batch * a.n_head;
     int chunk, qb, ih;
-    if (a.heavy_first == 2) {
-        dense_live_unit(a, lb, n_qblocks, BM, BN, &qb, &chunk, &ih);
-    } else if (a.heavy_first) {
-        ih = (int)(lb % n_ih);
-        const int64_t t = lb / n_ih;
-        chunk = (int)(t % a.max_chunks);
-        qb = n_qblocks - 1 - (int)(t / a.max_chunks);
-    } else {
-        chunk = (int)(lb % a.max_chunks);
-        const int64_t lq = lb / a.max_chunks;
-        qb = (int)(lq % n_qblocks);
-        ih = (int)(lq / n_qblocks);
-    }
+    dense_unit(a, n_qblocks, BM, BN, &qb, &chunk, &ih);
     const int item = ih / a.n_head;
     const int head = ih - item * a.n_head;
     const int hk = head / a.group;

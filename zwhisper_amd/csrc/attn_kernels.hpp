@@ -28,7 +28,7 @@ struct AttnArgs {
     int32_t chunk_len;  // keys per split aimed at, a multiple of split_tile
     int32_t max_chunks; // partial slots per row; 1 = the kernel writes `out` itself
     int32_t heavy_first; // dense kernel: dispatch the longest (causal) q-blocks first
-    int32_t xcd_group;   // dense kernel: run each head's q-blocks on one XCD (xcd_logical_block)
+    int32_t xcd_group;   // dense kernel: run each head's q-blocks on one XCD (dense_unit)
     int32_t rows_per_unit; // query rows sharing one key range (flash: BM; decode: n_q)
     int64_t live_blocks;   // dense, heavy_first == 2: workgroups of the grid (dense_live_unit)
     float *part_o;      // [row][max_chunks][d]   unnormalised sum of p*v
@@ -130,6 +130,32 @@ __device__ __forceinline__ int64_t xcd_logical_block(int64_t hw, int64_t n) {
     const int64_t xcd = hw % kNumXCD, local = hw / kNumXCD;
     const int64_t q = n / kNumXCD, r = n % kNumXCD;
     return xcd < r ? xcd * (q + 1) + local : r * (q + 1) + (xcd - r) * q + local;
+}
+
+// Workgroup -> (item*head, q-block, chunk) of the dense kernels:
+//  heavy_first 2  dense_live_unit (causal, one key count for every item)
+//  heavy_first 1  ((n_qblocks - 1 - qb) * max_chunks + chunk) * n_batch*n_head + item*head: the
+//                 longest (causal) q-blocks start first and shorter work fills the slots they
+//                 free; heads vary fastest, so neighbouring workgroups -- which the hardware deals
+//                 round-robin over the 8 XCDs -- carry equal work
+//  otherwise      ((item*head) * n_qblocks + qb) * max_chunks + chunk, over xcd_logical_block when
+//                 xcd_group is 1 (unsplit calls: a head's q-blocks share an XCD)
+__device__ inline void dense_unit(const AttnArgs &a, int n_qblocks, int bm, int bn, int *qb, int *chunk, int *ih) {
+    const int64_t lb = a.xcd_group ? xcd_logical_block(blockIdx.x, (int64_t)gridDim.x) : (int64_t)blockIdx.x;
+    const int64_t n_ih = (int64_t)a.n_batch * a.n_head;
+    if (a.heavy_first == 2) {
+        dense_live_unit(a, lb, n_qblocks, bm, bn, qb, chunk, ih);
+    } else if (a.heavy_first) {
+        *ih = (int)(lb % n_ih);
+        const int64_t t = lb / n_ih;
+        *chunk = (int)(t % a.max_chunks);
+        *qb = n_qblocks - 1 - (int)(t / a.max_chunks);
+    } else {
+        *chunk = (int)(lb % a.max_chunks);
+        const int64_t lq = lb / a.max_chunks;
+        *qb = (int)(lq % n_qblocks);
+        *ih = (int)(lq / n_qblocks);
+    }
 }
 
 hipError_t launch_flash(const AttnArgs &a, int d, hipStream_t stream, int *grid_blocks);
