@@ -44,7 +44,7 @@ int main() {
         s.n_kv = big ? rng() % (1ull << 31) : pick({0, 1, 5, 17, 90, 255, 256, 257, 448, 1500, 2048, 4096, 32768});
         s.n_head_kv = pick({1, 2, 4, 8});
         s.n_head = s.n_head_kv * pick({1, 2, 6, 7});
-        s.d = pick({16, 32, 64, 128});
+        s.d = pick({0, 4, 16, 32, 48, 64, 100, 128, 132});
         s.causal = rng() % 2;
         const uint64_t hd = s.n_head * s.d, kvd = s.n_head_kv * s.d;
         s.q_stride = hd + 4 * (rng() % 3);
@@ -68,7 +68,8 @@ int main() {
               p.split_tile);
         CHECK(p.max_chunks >= 1 && (uint64_t)p.max_chunks <= kMaxChunks, "max_chunks %d", p.max_chunks);
         const uint64_t rows = b.n_batch * s.n_head * s.n_q;
-        CHECK(p.ws_bytes == split_ws_bytes(rows, (uint64_t)p.max_chunks, s.d), "ws bytes");
+        CHECK(p.ws_bytes == split_ws_bytes(rows, (uint64_t)p.max_chunks, kernel_d(s.d)), "ws bytes");
+        CHECK(kernel_d(s.d) >= s.d && (kernel_d(s.d) == 32 || kernel_d(s.d) == 64 || kernel_d(s.d) == 128), "kernel d");
         CHECK(p.max_chunks == 1 || p.ws_bytes <= cap, "partials %llu over the workspace %llu",
               (unsigned long long)p.ws_bytes, (unsigned long long)cap);
         if (p.max_chunks > 1) CHECK(part_o_offset(rows, (uint64_t)p.max_chunks) % 64 == 0, "part_o alignment");

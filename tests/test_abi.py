@@ -72,15 +72,17 @@ def S(n_q, n_kv, h, hkv, d, causal, kt=None, qs=None, kvs=None, os_=None):
 @pytest.mark.parametrize("sh", [
     S(1500, 1500, 6, 6, 64, False, kt=1504), S(1, 448, 12, 12, 64, True), S(2048, 2048, 14, 2, 64, True, kt=2048),
     S(1, 4096, 12, 2, 128, True, kt=4096), S(20, 20, 12, 12, 32, False), S(0, 0, 1, 1, 64, False),
-    S(3, 0, 2, 2, 64, False),
+    S(3, 0, 2, 2, 64, False), S(2, 3, 2, 2, 48, False), S(2, 3, 2, 2, 16, False), S(5, 9, 4, 2, 4, True, kt=12),
+    S(7, 7, 2, 1, 100, False),
 ])
 def test_check_shape_accepts(sh):
     z.check_shape(sh)
 
 
 @pytest.mark.parametrize("sh,msg", [
-    (S(2, 3, 2, 2, 48, False), "head dim"),
-    (S(2, 3, 2, 2, 16, False), "head dim"),
+    (S(2, 3, 2, 2, 50, False), "head dim"),
+    (S(2, 3, 2, 2, 132, False), "head dim"),
+    (S(2, 3, 2, 2, 0, False), "head dim"),
     (S(2, 3, 3, 2, 64, False), "multiple of n_head_kv"),
     (S(2, 3, 0, 1, 64, False), "multiple of n_head_kv"),
     (S(4, 3, 2, 2, 64, True), "n_kv >= n_q"),

@@ -162,5 +162,12 @@ hipError_t launch_flash(const AttnArgs &a, int d, hipStream_t stream, int *grid_
 hipError_t launch_flash_x3(const AttnArgs &a, int d, hipStream_t stream, int *grid_blocks);
 hipError_t launch_decode(const AttnArgs &a, int d, int rows, hipStream_t stream, int *grid_blocks);
 hipError_t launch_combine(const AttnArgs &a, int d, hipStream_t stream);
+// head dims without kernels of their own (attn_pad.hip): zero-padded copies to the next built dim
+hipError_t launch_pad_rows(const float *src, float *dst, int n_batch, int rows, int segs, int d, int D, int64_t srs,
+                           int64_t sbs, const int32_t *n_rows_item, hipStream_t stream);
+hipError_t launch_pad_kt(const float *src, float *dst, int n_batch, int n_head_kv, int d, int D, int kt, int n_kv,
+                         int64_t sbs, const int32_t *n_kv_item, hipStream_t stream);
+hipError_t launch_unpad_rows(const float *src, float *dst, int n_batch, int rows, int segs, int d, int D, int64_t drs,
+                             int64_t dbs, hipStream_t stream);
 
 } // namespace zwg

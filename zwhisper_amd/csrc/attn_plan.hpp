@@ -50,8 +50,9 @@ inline std::string check_shape(const zwg_attn_shape &s) {
     const uint64_t lim = 1ull << 30; // keeps every key and row index, plus a tile, within int32
     char buf[256];
     if (s.reserved != 0) return "shape.reserved must be 0";
-    if (s.d != 32 && s.d != 64 && s.d != 128) {
-        snprintf(buf, sizeof buf, "head dim d=%llu unsupported (this build: 32, 64, 128)", (unsigned long long)s.d);
+    if (s.d == 0 || s.d % 4 != 0 || s.d > 128) {
+        snprintf(buf, sizeof buf, "head dim d=%llu unsupported (this build: multiples of 4 up to 128)",
+                 (unsigned long long)s.d);
         return buf;
     }
     if (s.n_head == 0 || s.n_head_kv == 0 || s.n_head % s.n_head_kv != 0) {
@@ -81,6 +82,10 @@ inline std::string check_batch(const zwg_attn_shape &s, const zwg_batch &b) {
     if (s.n_head * b.n_batch > 0x7fffffffull) return "n_head * n_batch must be below 2^31";
     return "";
 }
+
+// The head dim the kernels run at: d itself for the built dims 32, 64 and 128, else the next
+// of them, over zero-padded copies of the tensors (attn_pad.hip).
+inline uint64_t kernel_d(uint64_t d) { return d <= 32 ? 32 : d <= 64 ? 64 : 128; }
 
 struct Plan {
     int kernel = 0; // 1 flash, 2 decode
@@ -157,7 +162,7 @@ inline Plan make_plan(const zwg_attn_shape &s, const zwg_batch &b, uint64_t ws_c
     }
     if (units > kMaxSplitUnitsHint) tau = w_max;
     uint64_t chunks = split_bound(w_max, tau);
-    while (chunks > 1 && (split_ws_bytes(n_rows_total, chunks, s.d) > ws_cap || chunks > kMaxChunks)) {
+    while (chunks > 1 && (split_ws_bytes(n_rows_total, chunks, kernel_d(s.d)) > ws_cap || chunks > kMaxChunks)) {
         ++tau;
         chunks = split_bound(w_max, tau);
     }
@@ -165,7 +170,7 @@ inline Plan make_plan(const zwg_attn_shape &s, const zwg_batch &b, uint64_t ws_c
     p.max_chunks = (int)chunks;
     p.split_tile = (int)tile;
     p.grid_blocks = p.kernel == 2 ? chunks * s.n_head_kv * b.n_batch : chunks * units;
-    p.ws_bytes = split_ws_bytes(n_rows_total, (uint64_t)p.max_chunks, s.d);
+    p.ws_bytes = split_ws_bytes(n_rows_total, (uint64_t)p.max_chunks, kernel_d(s.d));
     p.heavy_first = p.kernel == 1 && s.causal;
     if (p.heavy_first && !b.n_kv_dev) {
         // one key count for every item: the grid holds only the (q-block, chunk, item*head)

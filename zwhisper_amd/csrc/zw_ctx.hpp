@@ -29,9 +29,10 @@ struct zwg_ctx {
     float *workspace = nullptr;
     uint32_t dense_math = ZWG_DENSE_X3; // products of the dense kernel (zwg_set_dense_math)
     uint64_t workspace_bytes = 0;
-    // device staging for the host-pointer calls: q, k, v, out
-    float *stage[4] = {nullptr, nullptr, nullptr, nullptr};
-    uint64_t stage_bytes[4] = {0, 0, 0, 0};
+    // device staging: q, k, v, out of the host-pointer calls (0-3), and the zero-padded q, k, v, out
+    // of calls whose head dim has no kernels of its own (4-7)
+    float *stage[8] = {};
+    uint64_t stage_bytes[8] = {};
     // pinned host staging for results whose rows are not contiguous in the caller's buffer
     float *host_stage = nullptr;
     uint64_t host_stage_bytes = 0;

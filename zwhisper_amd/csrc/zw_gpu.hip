@@ -114,16 +114,10 @@ Exec ctx_exec(const zwg_ctx *ctx) {
                 ctx->workspace_bytes, "the context's workspace"};
 }
 
-// Shape and pointer checks, the plan, and the launches.  ctx (may be null) receives the error.
-int run(zwg_ctx *ctx, const Exec &x, const float *q, const float *k, const float *v, const zwg_attn_shape &s,
-        const zwg_batch &b, float *out, Plan *plan_out = nullptr) {
-    std::string msg = check_shape(s);
-    if (msg.empty()) msg = check_batch(s, b);
-    if (!msg.empty()) return fail(ctx, msg);
-    if (s.n_q == 0) return ZWG_OK;
-    if (!q || !out || (s.n_kv && (!k || !v))) return fail(ctx, "null tensor pointer");
-    if (!aligned16(q) || !aligned16(out) || (s.n_kv && (!aligned16(k) || !aligned16(v))))
-        return fail(ctx, "q, k, v and out must be 16-byte aligned");
+// The plan and the launches of a checked call whose head dim has kernels (32, 64, 128); scale is
+// f32(1/sqrt(d)) of the caller's head dim.  ctx (may be null) receives the error.
+int run_kernels(zwg_ctx *ctx, const Exec &x, const float *q, const float *k, const float *v, const zwg_attn_shape &s,
+                const zwg_batch &b, float *out, Plan *plan_out, float scale) {
     const Plan p = make_plan(s, b, x.plan_cap, x.dense_math);
     if (plan_out) *plan_out = p;
     if (p.ws_bytes > x.ws_bytes) {
@@ -163,9 +157,7 @@ int run(zwg_ctx *ctx, const Exec &x, const float *q, const float *k, const float
     a.group = (int32_t)(s.n_head / s.n_head_kv);
     a.n_batch = (int32_t)b.n_batch;
     a.causal = s.causal ? 1 : 0;
-    // f32(1/sqrt(d)) as the reference computes it (src/ops.zig:531), then to log2 units
-    const float scl = 1.0f / std::sqrt((float)s.d);
-    a.scale_log2 = scl * 1.4426950408889634f;
+    a.scale_log2 = scale * 1.4426950408889634f; // log2 units
     a.split_tile = p.split_tile;
     a.chunk_len = p.chunk_len;
     a.max_chunks = p.max_chunks;
@@ -191,6 +183,69 @@ int run(zwg_ctx *ctx, const Exec &x, const float *q, const float *k, const float
         e = zwg::launch_combine(a, (int)s.d, x.stream);
         if (e != hipSuccess) return fail_hip(ctx, "combine kernel launch", e);
     }
+    return ZWG_OK;
+}
+
+// Shape and pointer checks, then the call on the kernels: directly for the built head dims, else
+// over zero-padded copies in the context's staging (attn_pad.hip).  ctx (may be null) receives
+// the error.
+int run(zwg_ctx *ctx, const Exec &x, const float *q, const float *k, const float *v, const zwg_attn_shape &s,
+        const zwg_batch &b, float *out, Plan *plan_out = nullptr) {
+    std::string msg = check_shape(s);
+    if (msg.empty()) msg = check_batch(s, b);
+    if (!msg.empty()) return fail(ctx, msg);
+    if (s.n_q == 0) return ZWG_OK;
+    if (!q || !out || (s.n_kv && (!k || !v))) return fail(ctx, "null tensor pointer");
+    if (!aligned16(q) || !aligned16(out) || (s.n_kv && (!aligned16(k) || !aligned16(v))))
+        return fail(ctx, "q, k, v and out must be 16-byte aligned");
+    // f32(1/sqrt(d)) as the reference computes it (src/ops.zig:531), of the caller's d
+    const float scale = 1.0f / std::sqrt((float)s.d);
+    const uint64_t D = kernel_d(s.d);
+    if (D == s.d) return run_kernels(ctx, x, q, k, v, s, b, out, plan_out, scale);
+    if (!ctx)
+        return fail(nullptr, "head dims other than 32, 64 and 128 run over zero-padded copies, which need a context "
+                             "(zwg_attention_batch_dev)");
+
+    // the same call at head dim D: q, v, out as [item][row][head][D], K row-major likewise or
+    // transposed as [item][KV head][D][kt_stride]
+    const uint64_t H = s.n_head, Hk = s.n_head_kv, B = b.n_batch;
+    zwg_attn_shape s2 = s;
+    s2.d = D;
+    s2.q_stride = H * D;
+    s2.out_stride = H * D;
+    s2.kv_stride = Hk * D;
+    zwg_batch b2 = b;
+    b2.q_bstride = s.n_q * H * D;
+    b2.out_bstride = s.n_q * H * D;
+    b2.k_bstride = s.kt_stride ? Hk * D * s.kt_stride : s.n_kv * Hk * D;
+    b2.v_bstride = s.n_kv * Hk * D;
+    const uint64_t F = sizeof(float);
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
+    if (ensure_stage(ctx, 4, B * b2.q_bstride * F) || ensure_stage(ctx, 5, (B * b2.k_bstride + 4) * F) ||
+        ensure_stage(ctx, 6, (B * b2.v_bstride + 4) * F) || ensure_stage(ctx, 7, B * b2.out_bstride * F))
+        return ZWG_ERROR;
+    float *qp = ctx->stage[4], *kp = ctx->stage[5], *vp = ctx->stage[6], *op = ctx->stage[7];
+    const int d = (int)s.d, Di = (int)D;
+    e = zwg::launch_pad_rows(q, qp, (int)B, (int)s.n_q, (int)H, d, Di, (int64_t)s.q_stride, (int64_t)b.q_bstride,
+                             nullptr, x.stream);
+    if (e == hipSuccess && s.n_kv) {
+        if (s.kt_stride)
+            e = zwg::launch_pad_kt(k, kp, (int)B, (int)Hk, d, Di, (int)s.kt_stride, (int)s.n_kv, (int64_t)b.k_bstride,
+                                   b.n_kv_dev, x.stream);
+        else
+            e = zwg::launch_pad_rows(k, kp, (int)B, (int)s.n_kv, (int)Hk, d, Di, (int64_t)s.kv_stride,
+                                     (int64_t)b.k_bstride, b.n_kv_dev, x.stream);
+        if (e == hipSuccess)
+            e = zwg::launch_pad_rows(v, vp, (int)B, (int)s.n_kv, (int)Hk, d, Di, (int64_t)s.kv_stride,
+                                     (int64_t)b.v_bstride, b.n_kv_dev, x.stream);
+    }
+    if (e != hipSuccess) return fail_hip(ctx, "head-dim padding launch", e);
+    const int rc = run_kernels(ctx, x, qp, kp, vp, s2, b2, op, plan_out, scale);
+    if (rc != ZWG_OK) return rc;
+    e = zwg::launch_unpad_rows(op, out, (int)B, (int)s.n_q, (int)H, d, Di, (int64_t)s.out_stride,
+                               (int64_t)b.out_bstride, x.stream);
+    if (e != hipSuccess) return fail_hip(ctx, "head-dim unpadding launch", e);
     return ZWG_OK;
 }
 
