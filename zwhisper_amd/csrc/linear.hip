@@ -180,9 +180,15 @@ int run_q8_stream_mt(zwg_ctx *ctx, const zwg_lin::Q8Args &base) {
 #ifndef ZWG_Q8P_WAVES
 #define ZWG_Q8P_WAVES 4
 #endif
-// waves (one 32-row slab each) sharing each x stage of the packed stream kernel (8 measured
-// 5-9% slower on the logits and decode-step workloads: half the workgroups, longer tails)
-constexpr int kQ8pWaves = ZWG_Q8P_WAVES;
+#ifndef ZWG_Q8P_WAVES_32
+#define ZWG_Q8P_WAVES_32 2
+#endif
+// waves (one 32-row slab each) sharing each x stage of the packed stream kernel: four for 64-row
+// calls (8 measured 5-9% slower on the logits and decode-step workloads: half the workgroups,
+// longer tails; 2 measured 4% slower on the Qwen2.5-1.5B step and 26% on its logits), two for
+// 32-row calls, whose x stage is half as large (Whisper small.en step 675 -> 651 us against 4)
+template <int MT>
+constexpr int q8p_waves() { return MT == 1 ? ZWG_Q8P_WAVES_32 : ZWG_Q8P_WAVES; }
 // k is split only for calls below this many workgroups.  A call at or above it streams unsplit:
 // its partial sums would be as large as half its weights (the Qwen2.5-1.5B gate/up, 140
 // workgroups: split 3 ways, 13.8 MB of partials for 27.5 MB of weights).  Measured on one box,
@@ -198,6 +204,7 @@ constexpr int kQ8pWaves = ZWG_Q8P_WAVES;
 
 template <int MT>
 int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g) {
+    constexpr int kQ8pWaves = q8p_waves<MT>();
     zwg_lin::Q8Args a = base;
     const uint64_t m = (uint64_t)a.m;
     int64_t gx = 0;
