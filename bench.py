@@ -23,6 +23,10 @@ by one pair of HIP events on the stream the kernels run on; the events' elapsed 
 the kernel time used for the roofline (kernel_ms_mean).  K further steps, each between its own
 pair of events, give kernel_ms_median and kernel_ms_min.  Decode workloads rotate between two copies of their
 inputs so no step finds its K/V in the 256 MB last-level cache left by the previous one.
+The card raises its clocks over the first tens of milliseconds of continuous load, so the K timed
+steps after a few warm-up steps include part of that ramp.  After them, each workload keeps running
+untimed for 0.3 s and K more steps are timed with one event pair: "sustained" reports that device
+time per step and its roofline fraction, the rate a serving loop sees.  It is never "value".
 The CPU baseline is the C restatement of the reference's multithreaded attention (oracle/),
 timed on this host's cores on a bounded sample of the same workload, on CPUs - 1 threads (the
 reference's default pool) over the CPUs this job may use (affinity, cgroup quota and
@@ -714,8 +718,44 @@ def time_workload(wl, steps: int, warmup: int) -> dict:
         ev[i][1].record(stream)
     torch.cuda.synchronize()
     kms = [a.elapsed_time(b) for a, b in ev]
+    # Sustained rate, after everything above and outside the reported figures: the card raises its
+    # clocks over the first tens of milliseconds of continuous load, so a short run measures part of
+    # that ramp.  Steps keep running untimed for SETTLE_S, then K more are timed with one event pair.
+    i = warmup + 2 * steps
+    t_settle = time.perf_counter()
+    while time.perf_counter() - t_settle < SETTLE_S:
+        for _ in range(16):
+            wl.step(i)
+            i += 1
+        torch.cuda.synchronize()
+    settle_s = time.perf_counter() - t_settle
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s0.record(stream)
+    for _ in range(steps):
+        wl.step(i)
+        i += 1
+    s1.record(stream)
+    torch.cuda.synchronize()
     return {"wall_s": wall, "ms_per_step": 1e3 * wall / steps, "kernel_ms_mean": kernel_ms_mean,
-            "kernel_ms_min": float(np.min(kms)), "kernel_ms_median": float(np.median(kms))}
+            "kernel_ms_min": float(np.min(kms)), "kernel_ms_median": float(np.median(kms)),
+            "sustained_kernel_ms": s0.elapsed_time(s1) / steps, "settle_s": settle_s}
+
+
+SETTLE_S = 0.3  # untimed continuous load before the sustained-rate steps
+
+
+def sustained(r: dict, work: float, unit: str, peak: float, products: int = 1) -> dict:
+    """The sustained-rate record of a workload (reported beside `value`, never as it): device time
+    per step of K steps timed after SETTLE_S of untimed continuous load, and the roofline fraction
+    at that time."""
+    scale = 1e12 if unit == "TFLOP/s" else 1e9
+    achieved = work / (r["sustained_kernel_ms"] * 1e-3)
+    out = {"kernel_ms_per_step": r["sustained_kernel_ms"], "achieved": achieved / scale, "unit": unit,
+           "frac": achieved / peak, "settle_s": r["settle_s"],
+           "note": "device time per step after the clocks settle under continuous load; not the timed steps"}
+    if products > 1:
+        out["issued_frac"] = products * achieved / peak
+    return out
 
 
 def cpu_baseline(number: int, threads: int, decode_pool: bool = True, one_call: bool = False) -> dict:
@@ -860,11 +900,16 @@ def _attention_line(wl: Workload, r: dict, dense_math: int) -> dict:
         value = per_step / (r["ms_per_step"] * 1e-3) / 1e9
         unit = "GB/s"
         dtype = "f32"
+    if spec.bound == "mfma":
+        sus = sustained(r, per_step, "TFLOP/s", PEAK_MFMA_F16 if dense_math == 0 else PEAK_MFMA_F32,
+                        3 if dense_math == 0 else 1)
+    else:
+        sus = sustained(r, per_step, "GB/s", PEAK_HBM)
     return {"workload": spec.name, "description": spec.description, "value": value, "unit": unit,
             "rate": step_rate(wl.number, r["ms_per_step"]), "ms_per_step": r["ms_per_step"],
             "kernel_ms_mean": r["kernel_ms_mean"], "kernel_ms_median": r["kernel_ms_median"],
             "kernel_ms_min": r["kernel_ms_min"], "algorithmic_work_per_step": per_step, "dtype": dtype,
-            "roofline": roof}
+            "roofline": roof, "sustained": sus}
 
 
 def _say(name: str, res: dict, peak_name: str) -> None:
@@ -872,6 +917,8 @@ def _say(name: str, res: dict, peak_name: str) -> None:
     par = res.get("parity")
     print(f"[bench] {name}: {res['value']:.2f} {res['unit']} ({res['ms_per_step']:.4f} ms/step, kernels "
           f"{res['kernel_ms_mean']:.4f} ms, {100 * res['roofline']['frac']:.1f}% of {peak_name})"
+          + (f", sustained {res['sustained']['kernel_ms_per_step']:.4f} ms ({100 * res['sustained']['frac']:.1f}%)"
+             if "sustained" in res else "")
           + (f", parity max abs {par['max_abs']:.2e} rel {par['normwise_rel']:.2e}" if par else "")
           + (f", cpu {cpu['value']:.3f} {cpu['unit']} on {cpu['cores']} threads" if cpu else ""),
           file=sys.stderr, flush=True)
@@ -913,7 +960,8 @@ def run_extra(name: str, torch, ctx, args, threads: int) -> dict:
                "dtype": "f32 activations x f16 weights, f32 accumulation (f16 MFMA, x split into two f16 terms)",
                "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_MFMA_F16 / 1e12,
                             "unit": "TFLOP/s", "frac": achieved / PEAK_MFMA_F16, "traffic": traffic_for(wl.name),
-                            "note": "two f16 MFMAs per f32 x f16 product: the kernels' ceiling is frac 0.5"}}
+                            "note": "two f16 MFMAs per f32 x f16 product: the kernels' ceiling is frac 0.5"},
+               "sustained": sustained(r, wl.work, "TFLOP/s", PEAK_MFMA_F16, 2)}
         if not args.no_cpu:
             res["cpu_baseline"] = wl.cpu_baseline(threads)
         wl.free()
@@ -935,7 +983,8 @@ def run_extra(name: str, torch, ctx, args, threads: int) -> dict:
                             "frac": achieved / peak, "traffic": traffic_for(wl.name),
                             "note": "peak = the layer's flops over the time they take at their own peaks: "
                                     "projections at half the f16 MFMA peak, attention at a third of the 16-bit MFMA "
-                                    "peak"}}
+                                    "peak"},
+               "sustained": sustained(r, wl.work, "TFLOP/s", peak)}
         if not args.no_cpu:
             res["cpu_baseline"] = wl.cpu_baseline(threads)
         wl.free()
@@ -956,7 +1005,8 @@ def run_extra(name: str, torch, ctx, args, threads: int) -> dict:
                "dtype": "f32 activations x int8 block weights, f32 accumulation (f16 MFMA, x split into two "
                         "f16 terms, block sums scaled in f32)",
                "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
-                            "frac": achieved / PEAK_HBM, "traffic": traffic_for(wl.name)}}
+                            "frac": achieved / PEAK_HBM, "traffic": traffic_for(wl.name)},
+               "sustained": sustained(r, wl.work, "GB/s", PEAK_HBM)}
         if not args.no_cpu:
             res["cpu_baseline"] = wl.cpu_baseline(threads)
         wl.free()
@@ -1103,6 +1153,7 @@ def main() -> int:
                    "n_head": spec.n_head, "n_head_kv": spec.n_head_kv, "head_dim": spec.d, "causal": spec.causal,
                    "k_layout": "transposed" if spec.kt else "row-major", "parallelism": "single GPU"},
         "roofline": head["roofline"],
+        "sustained": head["sustained"],
         "rate": head["rate"],
         "kernel_ms_median": head["kernel_ms_median"],
         "parity": head.get("parity"),
