@@ -670,19 +670,19 @@ class Q8LinearWorkload:
 
 
 def q8_workloads(torch, ctx):
-    """Constructors of the three int8 decode-step measurements."""
+    """(name, constructor) of the three int8 decode-step measurements."""
     qwen_layer = [(1536, 1536, True), (1536, 256, True), (1536, 256, True), (1536, 1536, False),
                   (1536, 8960, False), (1536, 8960, False), (8960, 1536, False)]  # src/llm.zig:179-207
     whisper_layer = [(768, 768, True), (768, 768, False), (768, 768, True), (768, 768, True),
                      (768, 768, True), (768, 768, True), (768, 3072, True), (3072, 768, True)]  # src/decoder.zig:181-201
-    yield lambda: Q8LinearWorkload(
+    yield "qwen15_logits_q8_x64", lambda: Q8LinearWorkload(
         "qwen15_logits_q8_x64", "Qwen2.5-1.5B output projection over the 151936-token vocabulary, 64 sequences "
         "(src/llm.zig:214-216), int8 block weights", torch, ctx, 64, [(1536, 151936, False)], copies=2, cpu_layers=1)
-    yield lambda: Q8LinearWorkload(
+    yield "qwen15_decode_q8_linear_x64", lambda: Q8LinearWorkload(
         "qwen15_decode_q8_linear_x64", "Qwen2.5-1.5B decode step, 64 sequences: q/k/v/o, gate/up/down of all "
         "28 layers (196 linear layers in 112 calls: q/k/v and gate/up grouped), int8 block weights", torch, ctx, 64,
         qwen_layer * 28, cpu_layers=7, groups=[3, 1, 2, 1] * 28)
-    yield lambda: Q8LinearWorkload(
+    yield "small_dec_q8_linear_x32", lambda: Q8LinearWorkload(
         "small_dec_q8_linear_x32", "Whisper small.en decoder step, 32 windows: q/k/v/o, cross q/o, MLP of all "
         "12 layers and the 51864-token logits (97 linear layers in 73 calls: q/k/v grouped), int8 block weights",
         torch, ctx, 32, whisper_layer * 12 + [(768, 51864, False)], copies=2, cpu_layers=8,
@@ -990,11 +990,10 @@ def run_extra(name: str, torch, ctx, args, threads: int) -> dict:
         wl.free()
         _say(name, res, "the layer's mfma roofline")
         return res
-    for make in q8_workloads(torch, ctx):
-        wl = make()
-        if wl.name != name:
-            wl.free()
+    for q8_name, make in q8_workloads(torch, ctx):
+        if q8_name != name:
             continue
+        wl = make()
         r = time_workload(wl, args.steps, args.warmup)
         achieved = wl.work / (r["kernel_ms_mean"] * 1e-3)
         res = {"workload": wl.name, "description": wl.description,
