@@ -278,3 +278,49 @@ def test_resident_group_errors(torch, ctx):
             ctx.linear_q8w_group_dev(x, 4, [r1, r2], None, out)
         with pytest.raises(z.ZwgError):
             ctx.linear_q8w_group_dev(x, 4, [r1] * 5, None, out * 3)
+
+
+def test_split_calls_in_graph_replays(torch, ctx):
+    """A Whisper small.en decode step's k-split calls (q/k/v grouped, split 3; MLP up, split 3; MLP
+    down, split 12), captured in a HIP graph: every replay, with eager calls of other inputs between
+    replays, gives the eager results bit for bit."""
+    import contextlib
+
+    m = 32
+    rng = np.random.default_rng(21)
+    shapes = [(768, 768, True), (768, 768, False), (768, 768, True), (768, 3072, True), (3072, 768, True)]
+    ws, bs = [], []
+    for j, (k, n, hb) in enumerate(shapes):
+        _, w, b = inputs(400 + j, 1, k, n, bias=hb)
+        ws.append(w)
+        bs.append(None if b is None else torch.from_numpy(b).cuda())
+    x768 = torch.from_numpy(rng.standard_normal((m, 768)).astype(np.float32)).cuda()
+    x3072 = torch.from_numpy(rng.standard_normal((m, 3072)).astype(np.float32)).cuda()
+    other768, other3072 = x768.flip(0).contiguous(), x3072.flip(0).contiguous()
+    with contextlib.ExitStack() as stack:
+        rs = [stack.enter_context(w.resident(ctx)) for w in ws]
+
+        def step(a768, a3072):
+            outs = [torch.empty((m, r.n), device="cuda") for r in rs]
+            ctx.linear_q8w_group_dev(a768, m, rs[:3], bs[:3], outs[:3])
+            ctx.linear_q8w_dev(a768, m, rs[3], bs[3], outs[3])
+            ctx.linear_q8w_dev(a3072, m, rs[4], bs[4], outs[4])
+            return outs
+
+        eager = [o.cpu().numpy() for o in step(x768, x3072)]
+        for j, (w, b) in enumerate(zip(ws, bs)):
+            xin = x768 if shapes[j][0] == 768 else x3072
+            ref = ref64(xin.cpu().numpy(), w, None if b is None else b.cpu().numpy())
+            assert float(np.abs(eager[j] - ref).max()) <= 2e-5 * np.sqrt(shapes[j][0]), f"call {j}: against f64"
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            captured = step(x768, x3072)
+        for rep in range(3):
+            for o in captured:
+                o.fill_(float("nan"))
+            graph.replay()
+            torch.cuda.synchronize()
+            for j in range(len(shapes)):
+                assert np.array_equal(captured[j].cpu().numpy(), eager[j]), f"replay {rep}, call {j}"
+            step(other768, other3072)  # eager calls between replays
+            torch.cuda.synchronize()
