@@ -180,27 +180,9 @@ void flash_x3_kernel(AttnArgs a) {
     const int wave_hi = min(k_end, a.causal ? diag + q_wave_last + 1 : n_kv);
     const int wave_full = min(k_end, a.causal ? diag + q_wave + 1 : n_kv);
 
-    // this lane's query, pre-scaled into log2 units, dims 16 j + 8 half + 0..7, split
+    // this lane's query, pre-scaled into log2 units, dims 16 j + 8 half + 0..7, split (loaded
+    // after the first tile's K and V loads are issued, so the two wait out one memory latency)
     f16x8 qh[NKS], ql[NKS];
-    {
-        f32x8 qv;
-#pragma unroll
-        for (int j = 0; j < NKS; ++j) {
-            if (q_valid) {
-                const f32x4 *src = reinterpret_cast<const f32x4 *>(qp + (int64_t)query * a.q_stride + 16 * j + 8 * half);
-                const f32x4 t0 = src[0], t1 = src[1];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    qv[e] = t0[e] * a.scale_log2;
-                    qv[4 + e] = t1[e] * a.scale_log2;
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) qv[e] = 0.f;
-            }
-            split8(qv, qh[j], ql[j]);
-        }
-    }
 
     f32x16 o[NDB];
 #pragma unroll
@@ -389,6 +371,33 @@ void flash_x3_kernel(AttnArgs a) {
     if (n_tiles > 0) {
         load_k(k_begin);
         load_v(k_begin);
+    }
+    {
+        // all of the row's loads go out together, then one wait
+        f32x4 qraw[2 * NKS];
+        if (q_valid) {
+            const f32x4 *src = reinterpret_cast<const f32x4 *>(qp + (int64_t)query * a.q_stride + 8 * half);
+#pragma unroll
+            for (int j = 0; j < NKS; ++j) {
+                qraw[2 * j] = src[4 * j];
+                qraw[2 * j + 1] = src[4 * j + 1];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 2 * NKS; ++j) qraw[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int j = 0; j < NKS; ++j) {
+            f32x8 qv;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                qv[e] = qraw[2 * j][e] * a.scale_log2;
+                qv[4 + e] = qraw[2 * j + 1][e] * a.scale_log2;
+            }
+            split8(qv, qh[j], ql[j]);
+        }
+    }
+    if (n_tiles > 0) {
         store_k(0);
         store_v(0);
         if (n_tiles > 1) load_k(k_begin + BN);
