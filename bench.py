@@ -324,6 +324,37 @@ class Workload:
         self.host = None
 
 
+class PromptWorkload(Workload):
+    """Workload 4 (the Qwen2.5-0.5B 2048-token prefill) as llm.prompt feeds it
+    (src/llm.zig:258-266): one step is 8 zwg_attention_dev calls of 256 query rows, call i over the
+    cache's first 256 (i + 1) keys of the transposed cache (2048 columns), each writing its rows of
+    the output.  Same visible pairs, so the same algorithmic work and results as the one-call
+    prefill; eight launches (and merges) instead of one."""
+
+    name = "qwen05_prefill_8x256"
+    calls = 8
+
+    def __init__(self, torch, ctx):
+        super().__init__(4, torch, ctx, 1)
+        from zwhisper_amd.ops import AttnShape
+
+        w = self.spec
+        rows = w.n_q // self.calls
+        self.rows = rows
+        self.shapes = [AttnShape(rows, rows * (i + 1), w.n_head, w.n_head_kv, w.d, w.n_head * w.d,
+                                 w.n_head_kv * w.d, w.n_head * w.d, True, w.n_kv_cap) for i in range(self.calls)]
+        s = self.sets[0]
+        ns = w.n_head * w.d
+        self.views = [(s["q"][0].view(w.n_q, ns)[rows * i: rows * (i + 1)], s["out"][0][rows * i: rows * (i + 1)])
+                      for i in range(self.calls)]
+
+    def step(self, i: int):
+        self.last = i
+        s = self.sets[0]
+        for sh, (q, out) in zip(self.shapes, self.views):
+            self.ctx.attention_dev(q, s["k"][0], s["v"][0], sh, out)
+
+
 class AppendWorkload:
     """A cache update of one step (zwg_kv_append / _batch): the new K/V rows (and q) of a step
     written into the device-resident caches, with rotary positions for the Qwen2 shapes.
@@ -924,13 +955,28 @@ def _say(name: str, res: dict, peak_name: str) -> None:
           file=sys.stderr, flush=True)
 
 
-EXTRAS = ("small_dec_kv_append_x32", "qwen15_kv_append_x64", "qwen05_prefill_kv_append", "base_enc_linear_x16",
+EXTRAS = ("qwen05_prefill_8x256", "small_dec_kv_append_x32", "qwen15_kv_append_x64", "qwen05_prefill_kv_append",
+          "base_enc_linear_x16",
           "base_enc_layer_x16", "qwen15_logits_q8_x64", "qwen15_decode_q8_linear_x64", "small_dec_q8_linear_x32")
 
 
 def run_extra(name: str, torch, ctx, args, threads: int) -> dict:
     """One of the measurements around the attention path (cache updates, projections, a whole
     encoder layer, int8 decode-step projections)."""
+    if name == "qwen05_prefill_8x256":
+        wl = PromptWorkload(torch, ctx)
+        r = time_workload(wl, args.steps, args.warmup)
+        res = _attention_line(wl, r, 0)
+        res["workload"] = wl.name
+        res["description"] = wl.spec.description + "; as llm.prompt feeds it: 8 calls of 256 rows over growing caches"
+        res["calls_per_step"] = wl.calls
+        res["roofline"]["traffic"] = None
+        if not args.no_parity:
+            res["parity"] = wl.parity(x3=True)
+        res["cpu_baseline_note"] = "the qwen05_prefill line's cpu_baseline times the oracle in this same 8 x 256 form"
+        wl.free()
+        _say(name, res, "mfma peak")
+        return res
     if name in ("small_dec_kv_append_x32", "qwen15_kv_append_x64", "qwen05_prefill_kv_append"):
         wl = AppendWorkload(name, torch, ctx)
         r = time_workload(wl, args.steps, args.warmup)

@@ -169,6 +169,25 @@ def test_qwen_prefill_full(torch, request, mode):
     check(out.cpu().numpy(), naive.attention_f64(q, kt, v, sh), f"{w.name} ({mode})", x3=mode == "x3")
 
 
+@pytest.mark.parametrize("mode", ["x3", "fp32"])
+def test_qwen_prefill_as_llm_prompt(torch, request, mode):
+    """Workload 4 as llm.prompt feeds it (src/llm.zig:258-266): 8 calls of 256 rows, call i with the
+    cache's first 256 (i + 1) keys (transposed cache of 2048 columns), rows written into one
+    output; the result is the one-call prefill's, checked against f64."""
+    ctx = mode_ctx(request, mode)
+    q, kl, v = W.make_dense(4, 0)
+    kt = W.to_kt(kl, 2048)
+    qd, kd, vd = dev(torch, q), dev(torch, kt), dev(torch, v)
+    out = torch.full((2048, 896), float("nan"), device="cuda")
+    for i in range(8):
+        sh = AttnShape(256, 256 * (i + 1), 14, 2, 64, 896, 128, 896, True, 2048)
+        ctx.attention_dev(qd.view(2048, 896)[256 * i: 256 * (i + 1)], kd, vd, sh, out[256 * i: 256 * (i + 1)])
+    torch.cuda.synchronize()
+    full = AttnShape(2048, 2048, 14, 2, 64, 896, 128, 896, True, 2048)
+    check(out.cpu().numpy().reshape(-1), naive.attention_f64(q, kt, v, full), f"prefill 8 x 256 ({mode})",
+          x3=mode == "x3")
+
+
 def test_qwen_decode_all_sequences(torch, ctx):
     """Workload 5: 64 sequences with cache lengths 1024..4096, 12/2 heads x 128, one batched call."""
     w = W.WORKLOADS[5]
