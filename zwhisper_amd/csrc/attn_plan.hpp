@@ -40,10 +40,11 @@ constexpr uint64_t kMaxSplitUnitsHint = 1ull << 22;
 #ifndef ZWG_FLASH_CAUSAL_BLOCKS_PER_CU
 #define ZWG_FLASH_CAUSAL_BLOCKS_PER_CU 2 // ... for causal calls, dispatched longest-first
 #endif
-// Key tiles a dense split chunk is given at least: a small causal call (the 256-row prompt
+// Key tiles an x3 dense split chunk is given at least: a small causal call (the 256-row prompt
 // batches of a Qwen2.5-0.5B prefill) would otherwise be cut into chunks of 4 tiles whose fixed
 // costs and merge outweigh the parallelism (8 calls of 256 rows: 156 us at 1, 149 at 6, 150 at 8,
-// 179 at 12; the 2048-row call and tiny.en unchanged at 6)
+// 179 at 12; the 2048-row call and tiny.en unchanged at 6).  The fp32 kernel keeps its finer
+// split (its 2048-row prefill: 101 us at 5 tiles a chunk, 109 us held to 6).
 #ifndef ZWG_FLASH_MIN_CHUNK_TILES
 #define ZWG_FLASH_MIN_CHUNK_TILES 6
 #endif
@@ -166,7 +167,8 @@ inline Plan make_plan(const zwg_attn_shape &s, const zwg_batch &b, uint64_t ws_c
         const uint64_t target = (uint64_t)(s.causal ? causal_target : ZWG_FLASH_BLOCKS_PER_CU) * kNumCUs;
         tau = w_max;
         if (s.causal || units < target)
-            tau = std::min(w_max, std::max<uint64_t>(ZWG_FLASH_MIN_CHUNK_TILES, ceil_div(tiles, target)));
+            tau = std::min(w_max, std::max<uint64_t>(dense_math == ZWG_DENSE_FP32 ? 1 : ZWG_FLASH_MIN_CHUNK_TILES,
+                                                     ceil_div(tiles, target)));
     }
     if (units > kMaxSplitUnitsHint) tau = w_max;
     uint64_t chunks = split_bound(w_max, tau);
