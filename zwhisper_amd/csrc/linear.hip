@@ -200,6 +200,13 @@ constexpr int q8p_waves() { return MT == 1 ? ZWG_Q8P_WAVES_32 : ZWG_Q8P_WAVES; }
 #ifndef ZWG_Q8P_SPLIT_BELOW
 #define ZWG_Q8P_SPLIT_BELOW 128
 #endif
+// workgroups a split call is split up to (within its k chunks).  Only the Qwen2.5-1.5B down
+// projection (k = 8960, 35-way at 512) reaches it; its decode step measured 2163 / 2048 / 1960 /
+// 1964 / 1963 us at 128 / 192 / 256 / 512 / 1024: the partial sums' traffic (13.8 MB each way per
+// layer at 512) costs nothing that fewer splits would win back
+#ifndef ZWG_Q8P_SPLIT_TARGET
+#define ZWG_Q8P_SPLIT_TARGET 512
+#endif
 
 
 template <int MT>
@@ -230,7 +237,7 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g)
     const uint64_t part_off = (xcvt_bytes + 255) / 256 * 256;
     if (part_off > ctx->workspace_bytes) return fail(ctx, "workspace too small for this linear call");
     int n_split = 1;
-    if (split_k) n_split = (int)std::min<int64_t>(n_chunks, (512 + gx - 1) / gx);
+    if (split_k) n_split = (int)std::min<int64_t>(n_chunks, (ZWG_Q8P_SPLIT_TARGET + gx - 1) / gx);
     while (n_split > 1 && part_off + (uint64_t)n_split * m * n_tot * 4 > ctx->workspace_bytes) --n_split;
     a.chunks_per_split = (n_chunks + n_split - 1) / n_split;
     n_split = (n_chunks + a.chunks_per_split - 1) / a.chunks_per_split; // no empty splits
