@@ -970,7 +970,7 @@ def run_extra(name: str, torch, ctx, args, threads: int) -> dict:
         res["workload"] = wl.name
         res["description"] = wl.spec.description + "; as llm.prompt feeds it: 8 calls of 256 rows over growing caches"
         res["calls_per_step"] = wl.calls
-        res["roofline"]["traffic"] = None
+        res["roofline"]["traffic"] = traffic_for(wl.name)
         if not args.no_parity:
             res["parity"] = wl.parity(x3=True)
         res["cpu_baseline_note"] = "the qwen05_prefill line's cpu_baseline times the oracle in this same 8 x 256 form"
