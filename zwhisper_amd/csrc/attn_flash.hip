@@ -17,6 +17,8 @@
 // so each lane reads D/2 contiguous floats of its key row and keeps D/2 query values in VGPRs.
 //
 // Scores are pre-scaled by f32(1/sqrt(d)) * log2(e) (folded into Q) so softmax uses exp2.
+#include <type_traits>
+
 #include "attn_kernels.hpp"
 
 namespace zwg {
@@ -85,21 +87,9 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
     const int wave_hi = min(k_end, a.causal ? diag + q_wave_last + 1 : n_kv);
     const int wave_full = min(k_end, a.causal ? diag + q_wave + 1 : n_kv);
 
+    // this lane's query, pre-scaled into log2 units (loaded after the first tile's K and V loads
+    // are issued, so the three wait out one memory latency)
     float qreg[HD];
-    if (q_valid) {
-        const f32x4 *src = reinterpret_cast<const f32x4 *>(qp + (int64_t)query * a.q_stride + half * HD);
-#pragma unroll
-        for (int i = 0; i < HD / 4; ++i) {
-            const f32x4 t = src[i];
-            qreg[4 * i + 0] = t[0] * a.scale_log2;
-            qreg[4 * i + 1] = t[1] * a.scale_log2;
-            qreg[4 * i + 2] = t[2] * a.scale_log2;
-            qreg[4 * i + 3] = t[3] * a.scale_log2;
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < HD; ++i) qreg[i] = 0.f;
-    }
 
     f32x16 o[NDB];
 #pragma unroll
@@ -110,57 +100,76 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
     // Tile staging.  K runs two tiles ahead of the tile being finished and V one tile ahead,
     // so that in iteration t the MFMAs of S(t+1) (from K(t+1)) can overlap the softmax of
     // tile t, and the LDS buffers read in an iteration (K(t+1), V(t)) are never the ones
-    // written in it (K(t+2), V(t+1)): one barrier per tile suffices.
-    f32x4 kr[LD], vr[LD];
+    // written in it (K(t+2), V(t+1)): one barrier per tile suffices.  Each thread holds what it
+    // stores as 16-byte quads: four dims of one key for K (row-major K: one 16-byte load;
+    // transposed K: four coalesced dword loads, one per dim row) and four keys of one dim for V^T
+    // (four coalesced dword loads, one per key row), each stored with one 16-byte LDS write.
+    // Loads go through buffer descriptors (no branches, offsets as a per-lane base plus a
+    // wave-uniform part): V and row-major K end at the item's last key row, so a key at or past
+    // n_kv reads 0; transposed K ends at the last dim row's n_kv-th column, and a key past n_kv
+    // in an earlier dim row reads that row's padding (finite by the reference's contract,
+    // src/ops.zig:477-492) -- masked out of the scores either way.
+    constexpr int NG = D / 32;    // quads per thread per tile, per tensor
+    constexpr int VTPD = 256 / D; // V: threads per dim
+    static_assert(NG == LD, "each thread stages D/32 quads of each tile");
+    f32x4 kr[NG], vr[NG];
+    const int k_key = tid % BN, k_dq = tid / BN;   // transposed K: key, first dim quad
+    const int v_dim = tid % D, v_kq = tid / D;     // V: dim, first key quad
+    auto k_dim = [&](int g) { return 4 * (k_dq + 8 * g); };   // transposed K: quads k_dq, k_dq + 8, ..
+    auto v_key = [&](int g) { return 4 * (v_kq + VTPD * g); }; // V: quads v_kq, v_kq + VTPD, ..
+    const uint32_t row_b = (uint32_t)a.kv_stride * 4u;
+    const uint32_t kv_span = n_kv > 0 ? (uint32_t)(n_kv - 1) * row_b + 4u * D : 0u;
+    const uint32_t kt_span = n_kv > 0 ? (uint32_t)((D - 1) * a.kt_stride + n_kv) * 4u : 0u;
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(kp), 0, (int)(KT ? kt_span : kv_span), 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(vp), 0, (int)kv_span, 0x00020000);
+    const uint32_t kt_row_b = (uint32_t)a.kt_stride * 4u;
+    const uint32_t k_base = KT ? (uint32_t)k_dim(0) * kt_row_b + 4u * (uint32_t)k_key
+                               : (uint32_t)(tid / (D / 4)) * row_b + 16u * (uint32_t)(tid % (D / 4));
+    const uint32_t v_base = (uint32_t)v_key(0) * row_b + 4u * (uint32_t)v_dim;
     auto load_k = [&](int k0) {
 #pragma unroll
-        for (int i = 0; i < LD; ++i) {
-            const int f = tid + 256 * i;
+        for (int g = 0; g < NG; ++g) {
             if (KT) {
-                const int dim = f / (BN / 4);
-                const int gk = k0 + 4 * (f % (BN / 4));
-                kr[i] = gk < n_kv ? *reinterpret_cast<const f32x4 *>(kp + (int64_t)dim * a.kt_stride + gk)
-                                  : (f32x4){0};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    kr[g][j] = __builtin_bit_cast(
+                        float, __builtin_amdgcn_raw_buffer_load_b32(
+                                   krs, (int)k_base, (int)((uint32_t)k0 * 4u + (uint32_t)(32 * g + j) * kt_row_b), 0));
             } else {
-                const int gk = k0 + f / (D / 4);
-                kr[i] = gk < n_kv ? *reinterpret_cast<const f32x4 *>(kp + (int64_t)gk * a.kv_stride + 4 * (f % (D / 4)))
-                                  : (f32x4){0};
+                kr[g] = __builtin_bit_cast(
+                    f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                               krs, (int)k_base, (int)((uint32_t)(k0 + (1024 / D) * g) * row_b), 0));
             }
         }
     };
     auto load_v = [&](int k0) {
 #pragma unroll
-        for (int i = 0; i < LD; ++i) {
-            const int f = tid + 256 * i;
-            const int gv = k0 + f / (D / 4);
-            vr[i] = gv < n_kv ? *reinterpret_cast<const f32x4 *>(vp + (int64_t)gv * a.kv_stride + 4 * (f % (D / 4)))
-                              : (f32x4){0};
-        }
+        for (int g = 0; g < NG; ++g)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                vr[g][j] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(
+                               vrs, (int)v_base, (int)((uint32_t)(k0 + 4 * VTPD * g + j) * row_b), 0));
     };
     auto store_k = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < LD; ++i) {
-            const int f = tid + 256 * i;
+        for (int g = 0; g < NG; ++g) {
+            int key, dim;
             if (KT) {
-                const int dim = f / (BN / 4);
-                const int key = 4 * (f % (BN / 4));
-#pragma unroll
-                for (int j = 0; j < 4; ++j) Ks[buf][(key + j) * KS + dim] = kr[i][j];
+                key = k_key;
+                dim = k_dim(g);
             } else {
-                const int key = f / (D / 4);
-                *reinterpret_cast<f32x4 *>(&Ks[buf][key * KS + 4 * (f % (D / 4))]) = kr[i];
+                const int f = tid + 256 * g;
+                key = f / (D / 4);
+                dim = 4 * (f % (D / 4));
             }
+            *reinterpret_cast<f32x4 *>(&Ks[buf][key * KS + dim]) = kr[g];
         }
     };
     auto store_v = [&](int buf) {
 #pragma unroll
-        for (int i = 0; i < LD; ++i) {
-            const int f = tid + 256 * i;
-            const int key = f / (D / 4);
-            const int dim = 4 * (f % (D / 4));
-#pragma unroll
-            for (int j = 0; j < 4; ++j) Vt[buf][(dim + j) * VS + key] = vr[i][j];
-        }
+        for (int g = 0; g < NG; ++g) *reinterpret_cast<f32x4 *>(&Vt[buf][v_dim * VS + v_key(g)]) = vr[g];
     };
     // S^T tile = K . Q^T (32 keys x 32 queries) from the K buffer
     auto qk = [&](int buf) {
@@ -194,7 +203,7 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
         float mt = sc[0];
 #pragma unroll
         for (int r = 1; r < 16; ++r) mt = fmaxf(mt, sc[r]);
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        mt = lane_pair_max(mt);
         if (__any(mt > m_run + ZWG_RESCALE_SLACK)) {
             const float m_new = fmaxf(m_run, mt);
             const float alpha = m_run == -INFINITY ? 0.f : exp2_fast(m_run - m_new);
@@ -266,6 +275,22 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
     if (n_tiles > 0) {
         load_k(k_begin);
         load_v(k_begin);
+    }
+    if (q_valid) {
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(qp + (int64_t)query * a.q_stride + half * HD);
+#pragma unroll
+        for (int i = 0; i < HD / 4; ++i) {
+            const f32x4 t = src[i];
+            qreg[4 * i + 0] = t[0] * a.scale_log2;
+            qreg[4 * i + 1] = t[1] * a.scale_log2;
+            qreg[4 * i + 2] = t[2] * a.scale_log2;
+            qreg[4 * i + 3] = t[3] * a.scale_log2;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < HD; ++i) qreg[i] = 0.f;
+    }
+    if (n_tiles > 0) {
         store_k(0);
         store_v(0);
         if (n_tiles > 1) load_k(k_begin + BN);
@@ -275,31 +300,42 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
     if (n_tiles > 1) store_k(1);
     __syncthreads();
 
-    for (int t = 0; t < n_tiles; ++t) {
+    // one tile: t's buffer parity is a compile-time constant (the loop runs two tiles per turn),
+    // so LDS addresses are immediate offsets and the score registers alternate between s_cur and
+    // s_b without copies
+    auto step = [&](auto parity, int t, f32x16 &s_this, f32x16 &s_next) {
+        constexpr int cur = decltype(parity)::value, nxt = cur ^ 1;
         const int k0 = k_begin + t * BN;
         if (t + 2 < n_tiles) load_k(k0 + 2 * BN);
         if (t + 1 < n_tiles) load_v(k0 + BN);
         const bool need_cur = wave_needs(k0);
         const bool need_next = t + 1 < n_tiles && wave_needs(k0 + BN);
-        f32x16 s_next = (f32x16){0};
-        if (need_cur) mask_and_max(s_cur, k0);
+        if (need_cur) mask_and_max(s_this, k0);
         if (need_cur && need_next) {
             // the MFMAs of the next tile's scores and this tile's exponentials are independent:
             // issued in one block, the VALU work runs while the MFMA pipe is busy
-            s_next = qk_exp((t + 1) & 1, s_cur);
+            s_next = qk_exp(nxt, s_this);
         } else if (need_cur) {
-            exp_sum(s_cur);
+            exp_sum(s_this);
         } else if (need_next) {
-            s_next = qk((t + 1) & 1);
+            s_next = qk(nxt);
         }
-        if (need_cur) pv(s_cur, t & 1);
-        if (t + 2 < n_tiles) store_k(t & 1);
-        if (t + 1 < n_tiles) store_v((t + 1) & 1);
+        if (need_cur) pv(s_this, cur);
+        if (t + 2 < n_tiles) store_k(cur);
+        if (t + 1 < n_tiles) store_v(nxt);
         __syncthreads();
-        s_cur = s_next;
+    };
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    f32x16 s_b = (f32x16){0};
+    int t = 0;
+    for (; t + 1 < n_tiles; t += 2) {
+        step(P0{}, t, s_cur, s_b);
+        step(P1{}, t + 1, s_b, s_cur);
     }
+    if (t < n_tiles) step(P0{}, t, s_cur, s_b);
 
-    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    const float l_tot = lane_pair_sum(l_run);
     if (!q_valid) return;
     // lane holds dims db*32 + 8*g + 4*half + {0..3} in registers 4g..4g+3 of o[db]
     if (n_chunks == 1) { // an unsplit unit writes its rows itself; the merge pass skips them

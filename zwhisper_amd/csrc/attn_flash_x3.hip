@@ -91,26 +91,6 @@ __device__ __forceinline__ void split4(const f32x4 &x, f16x4 &hi, f16x4 &lo) {
     lo = __builtin_bit_cast(f16x4, l);
 }
 
-// max / sum over lanes l and l ^ 32 (the two halves of a query's keys): v_permlane32_swap
-// exchanges lanes 32..63 of its first register with lanes 0..31 of its second, so with x in both
-// the two hold x of lanes 0..31 and of lanes 32..63 in every lane -- no LDS round trip.  Issued
-// as inline asm: this compiler's __builtin_amdgcn_permlane32_swap returns the first register for
-// both results.  The s_nop gives the two wait states the instruction needs after a VALU write of
-// its operands.
-__device__ __forceinline__ f32x2 lane_halves(float x) {
-    float a = x, b = x;
-    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-    return (f32x2){a, b};
-}
-__device__ __forceinline__ float lane_pair_max(float x) {
-    const f32x2 h = lane_halves(x);
-    return fmaxf(h[0], h[1]);
-}
-__device__ __forceinline__ float lane_pair_sum(float x) {
-    const f32x2 h = lane_halves(x);
-    return h[0] + h[1];
-}
-
 // K tile element (key, dim): rows of D f16, 16-byte chunk c stored at c ^ (key / (128 / D))
 // mod (D / 8): the rows sharing LDS banks within a 16-lane read phase land in different chunks.
 template <int D>

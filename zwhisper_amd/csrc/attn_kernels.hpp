@@ -170,4 +170,26 @@ hipError_t launch_pad_kt(const float *src, float *dst, int n_batch, int n_head_k
 hipError_t launch_unpad_rows(const float *src, float *dst, int n_batch, int rows, int segs, int d, int D, int64_t drs,
                              int64_t dbs, hipStream_t stream);
 
+typedef float lane_f32x2 __attribute__((ext_vector_type(2)));
+
+// max / sum over lanes l and l ^ 32 (the two halves of a query's keys): v_permlane32_swap
+// exchanges lanes 32..63 of its first register with lanes 0..31 of its second, so with x in both
+// the two hold x of lanes 0..31 and of lanes 32..63 in every lane -- no LDS round trip.  Issued
+// as inline asm: this compiler's __builtin_amdgcn_permlane32_swap returns the first register for
+// both results.  The s_nop gives the two wait states the instruction needs after a VALU write of
+// its operands.
+__device__ __forceinline__ lane_f32x2 lane_halves(float x) {
+    float a = x, b = x;
+    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return (lane_f32x2){a, b};
+}
+__device__ __forceinline__ float lane_pair_max(float x) {
+    const lane_f32x2 h = lane_halves(x);
+    return fmaxf(h[0], h[1]);
+}
+__device__ __forceinline__ float lane_pair_sum(float x) {
+    const lane_f32x2 h = lane_halves(x);
+    return h[0] + h[1];
+}
+
 } // namespace zwg
