@@ -235,6 +235,30 @@ def test_ragged_lengths_edge_cases(torch, ctx, kt):
         check(got[i], ref, f"ragged item n_kv={L} ({'kt' if kt else 'row-major'})")
 
 
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("n_q", [1, 150])
+def test_kt_padding_never_reaches_the_output(torch, request, mode, n_q):
+    """A transposed cache's columns past n_kv (and cache rows past n_kv of V) hold NaN: the kernels
+    read the padding but mask every key past n_kv by selection, so the result is the f64 closed
+    form of the first n_kv keys.  (The reference asks for finite padding, src/ops.zig:477-492;
+    this holds beyond that contract.)  Dense (n_q = 150, both modes, causal) and decode (n_q = 1)."""
+    ctx = mode_ctx(request, mode)
+    n_kv, cap, h, hkv, d = 700, 1024, 6, 2, 64
+    q = W.normal(21, n_q * h * d).reshape(n_q, h * d)
+    kl = W.normal(22, n_kv * hkv * d).reshape(n_kv, hkv, d)
+    v = W.normal(23, n_kv * hkv * d).reshape(n_kv, hkv * d)
+    kt = np.full((hkv, d, cap), np.nan, np.float32)
+    kt[:, :, :n_kv] = np.transpose(kl, (1, 2, 0))
+    vpad = np.full((cap, hkv * d), np.nan, np.float32)
+    vpad[:n_kv] = v
+    sh = AttnShape(n_q, n_kv, h, hkv, d, h * d, hkv * d, h * d, True, cap)
+    out = torch.empty(n_q * h * d, device="cuda")
+    ctx.attention_dev(dev(torch, q), dev(torch, kt), dev(torch, vpad), sh, out)
+    torch.cuda.synchronize()
+    ref = naive.attention_f64(q, kt, v, sh)
+    check(out.cpu().numpy(), ref, f"NaN padding n_q={n_q} ({mode})", x3=mode == "x3" and n_q > 1)
+
+
 def test_split_and_unsplit_agree(torch):
     """A context too small for split partials runs every call unsplit; results must agree."""
     import zwhisper_amd as z
