@@ -1,15 +1,15 @@
 """CPU check of the x3 dense mode's tolerance bar (max abs 5e-5, normwise relative 3e-5).
 
 The x3 kernel (zwhisper_amd/csrc/attn_flash_x3.hip) computes each f32 product a.b as
-ah.bh + ah.bl + al.bh with x = xh + xl split into 16-bit terms: f16 for Q (pre-scaled by
-log2(e)/sqrt(d)) and K, bf16 for P and V, f32 accumulation, softmax in exp2 units.  This test
-emulates that arithmetic in numpy (terms in f64, so it models the splits, not the MFMA
+ah.bh + ah.bl + al.bh with x = xh + xl, xh = f16(x), xl = f16(x - xh), for Q (pre-scaled by
+log2(e)/sqrt(d)), K, P and V, with f32 accumulation and the softmax in exp2 units.  This test
+emulates that arithmetic in numpy (products summed in f64, so it models the splits, not the MFMA
 accumulation order) and checks two things against the f64 closed form:
 
-* the full three-term form sits well inside the bar (it measures ~2e-6);
-* dropping any one of the six products fails the bar.  The Q.K^T cross terms are the telling
-  ones: without qh.kl or ql.kh the error is ~1e-4, inside the reference's f32 bar (2e-4 abs,
-  1e-3 relative) but outside the x3 bar, so only the tighter bar pins that part of the split.
+* the full three-term form sits well inside the bar (it measures ~1e-7, as the kernel does);
+* dropping any one of the six products fails the bar.  The four cross terms are the telling
+  ones: without any one of them the error is 5e-5 to 2e-4, inside the reference's f32 bar
+  (2e-4 abs, 1e-3 relative) but outside the x3 bar, so only the tighter bar pins the split.
 """
 from __future__ import annotations
 
@@ -20,39 +20,30 @@ TOL_ABS_X3 = 5e-5
 TOL_REL_X3 = 3e-5
 TOL_ABS_F32 = 2e-4
 TOL_REL_F32 = 1e-3
-QK_TERMS = ("qh.kh", "qh.kl", "ql.kh")
-PV_TERMS = ("ph.vh", "ph.vl", "pl.vh")
+HI_TERMS = ("qh.kh", "ph.vh")
+CROSS_TERMS = ("qh.kl", "ql.kh", "ph.vl", "pl.vh")
 
 
-def _bf16(x: np.ndarray) -> np.ndarray:
-    """Round f32 to bf16 (nearest, ties to even), returned as f32."""
-    u = np.asarray(x, np.float32).view(np.uint32).astype(np.uint64)
-    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
-    return u.astype(np.uint32).view(np.float32)
-
-
-def _split(x: np.ndarray, kind: str) -> tuple[np.ndarray, np.ndarray]:
+def _split(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """x = hi + lo in f16 terms (returned as f32; f16 subnormals kept, as the MFMA keeps them)."""
     x = np.asarray(x, np.float32)
-    if kind == "f16":
-        hi = x.astype(np.float16).astype(np.float32)
-        return hi, (x - hi).astype(np.float16).astype(np.float32)
-    hi = _bf16(x)
-    return hi, _bf16(x - hi)
+    hi = x.astype(np.float16).astype(np.float32)
+    return hi, (x - hi).astype(np.float16).astype(np.float32)
 
 
 def x3_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, drop: str | None = None) -> np.ndarray:
     """One head of x3 attention (non-causal), optionally without one of the six products."""
     d = q.shape[1]
     c = np.float32(np.float32(1.0) / np.sqrt(np.float32(d))) * np.float32(np.log2(np.e))
-    qh, ql = _split(q.astype(np.float32) * c, "f16")
-    kh, kl = _split(k, "f16")
+    qh, ql = _split(q.astype(np.float32) * c)
+    kh, kl = _split(k)
     mm = lambda a, b: a.astype(np.float64) @ b.astype(np.float64)
     qk = {"qh.kh": mm(qh, kh.T), "qh.kl": mm(qh, kl.T), "ql.kh": mm(ql, kh.T)}
     s = sum(t for name, t in qk.items() if name != drop).astype(np.float32)
     p = np.exp2(s - s.max(axis=1, keepdims=True)).astype(np.float32)
     l = p.astype(np.float64).sum(axis=1, keepdims=True)
-    ph, pl = _split(p, "bf16")
-    vh, vl = _split(v, "bf16")
+    ph, pl = _split(p)
+    vh, vl = _split(v)
     pv = {"ph.vh": mm(ph, vh), "ph.vl": mm(ph, vl), "pl.vh": mm(pl, vh)}
     return (sum(t for name, t in pv.items() if name != drop) / l).astype(np.float32)
 
@@ -78,30 +69,32 @@ def head(request):
     return q, k, v, attention_f64(q, k, v)
 
 
-def test_bf16_rounding():
-    # bf16 keeps 8 significand bits: 1 + 2^-8 is a tie (to even: 1), 1 + 3 * 2^-8 a tie (to
-    # even: 1 + 2^-6), 1 + 2^-9 rounds down; the sign survives; a subnormal keeps its top bits
-    x = np.array([1.0, 1.0 + 2.0**-8, 1.0 + 3 * 2.0**-8, 1.0 + 2.0**-9, -(1.0 + 2.0**-7), 2.0**-130], np.float32)
-    want = np.array([1.0, 1.0, 1.0 + 2.0**-6, 1.0, -(1.0 + 2.0**-7), 2.0**-130], np.float32)
-    assert np.array_equal(_bf16(x), want)
+def test_split_is_exact_to_22_bits():
+    # magnitudes 2^-3 .. 2^15, where both terms are normal f16 numbers
+    rng = np.random.default_rng(1)
+    x = (rng.choice([-1.0, 1.0], 4096) * 2.0 ** rng.uniform(-3, 15, 4096)).astype(np.float32)
+    hi, lo = _split(x)
+    assert np.array_equal(hi, x.astype(np.float16).astype(np.float32))
+    rel = np.abs((hi.astype(np.float64) + lo) - x) / np.abs(x)
+    assert rel.max() <= 2.0**-21, rel.max()
 
 
 def test_full_form_within_bar(head):
     q, k, v, ref = head
     err, rel = _errors(x3_attention(q, k, v), ref)
-    assert err <= TOL_ABS_X3 / 10 and rel <= TOL_REL_X3 / 3, (err, rel)
+    assert err <= TOL_ABS_X3 / 10 and rel <= TOL_REL_X3 / 10, (err, rel)
 
 
-@pytest.mark.parametrize("drop", QK_TERMS + PV_TERMS)
+@pytest.mark.parametrize("drop", HI_TERMS + CROSS_TERMS)
 def test_dropped_product_fails_bar(head, drop):
     q, k, v, ref = head
     err, rel = _errors(x3_attention(q, k, v, drop), ref)
     assert err > TOL_ABS_X3 or rel > TOL_REL_X3, (drop, err, rel)
 
 
-@pytest.mark.parametrize("drop", ("qh.kl", "ql.kh"))
-def test_qk_cross_terms_escape_f32_bar(head, drop):
-    """Why x3 has its own bar: these two mistakes pass the reference's f32 bar."""
+@pytest.mark.parametrize("drop", CROSS_TERMS)
+def test_cross_terms_escape_f32_bar(head, drop):
+    """Why x3 has its own bar: each of these mistakes passes the reference's f32 bar."""
     q, k, v, ref = head
     err, rel = _errors(x3_attention(q, k, v, drop), ref)
     assert err <= TOL_ABS_F32 and rel <= TOL_REL_F32, (drop, err, rel)
