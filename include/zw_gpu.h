@@ -20,7 +20,7 @@
  *   - dense (encoder / prefill) kernel, ZWG_DENSE_X3 (the default, below): f32 operands split into
  *     f16 hi + lo terms (22 significand bits), three f16 MFMA products per product, f32
  *     accumulation.  Its own bar on N(0,1) inputs: max abs 5e-5 and normwise relative 3e-5
- *     (measured at most 8.4e-7 and 2.6e-7 on the Whisper / Qwen2 workloads); with scores spread
+ *     (measured at most 8.4e-7 abs and 1.3e-6 relative on the Whisper / Qwen2 workloads); with scores spread
  *     36x wider it measures 4.5e-5, inside the f32 bar.
  *   - dense kernel, ZWG_DENSE_FP32: fp32 MFMA (v_mfma_f32_32x32x2_f32) throughout; the f32 bar.
  * The absolute bars are for values of order one: an output row is a weighted mean of value rows,
