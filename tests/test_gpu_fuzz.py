@@ -16,7 +16,7 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 SENTINEL = -3.5
-N_CASES = 48
+N_CASES = 200
 
 
 @pytest.fixture(scope="module")
