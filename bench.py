@@ -7,9 +7,11 @@
 A step is one pass of the attention path over one batch of synthetic input, already resident
 in HBM.  The headline line (one JSON object on stdout) is workload 2, Whisper base.en encoder
 self-attention over 16 windows x 1500 frames (8 heads x 64, K transposed), in TFLOP/s of
-algorithmic work (4*d*H per visible (q, k) pair, src/bench.zig:76).  The other four workloads
-are measured too (unless --only) and reported under "workloads" in the same line, each with its
-own roofline: 16-bit MFMA (2.5 PFLOP/s, f16 and bf16 alike) for the dense ones, whose kernel
+algorithmic work (4*d*H per visible (q, k) pair, src/bench.zig:76).  stdout carries only that
+line, a few KB.  The other four workloads are measured too (unless --only): the headline line lists
+each under "workloads" with its value, step time and roofline fraction, and stderr carries every
+workload's full record, one "[bench-record] {...}" line each (src/bench.zig:51-78 likewise prints
+one short line per measurement).  Each has its own roofline: 16-bit MFMA (2.5 PFLOP/s, f16 and bf16 alike) for the dense ones, whose kernel
 computes each f32 product as three 16-bit products of hi/lo-split operands (ceiling: a third of
 that peak), HBM (8 TB/s) for the decode ones.  Unless --only, the three dense workloads are also
 run on the fp32-MFMA kernel ("*_fp32mfma", fp32 peak 157.3 TFLOP/s).  Every attention workload
@@ -773,6 +775,7 @@ def time_workload(wl, steps: int, warmup: int) -> dict:
 
 
 SETTLE_S = 0.3  # untimed continuous load before the sustained-rate steps
+TRAFFIC_SOURCE: dict = {}  # traffic_source(), set once in main()
 
 
 def sustained(r: dict, work: float, unit: str, peak: float, products: int = 1) -> dict:
@@ -868,15 +871,50 @@ def cpu_baseline(number: int, threads: int, decode_pool: bool = True, one_call: 
             "seconds": best}
 
 
-def traffic_for(workload_name: str):
-    """HBM bytes per launch from the committed rocprofv3 counter summary, if one exists."""
-    path = os.path.join(ROOT, "profiles", "traffic.json")
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def kernel_sources_sha() -> str:
+    """SHA-256 (first 16 hex digits) of the kernel sources (zwhisper_amd/csrc/*), in name order:
+    the traffic figures of profiles/traffic.json record the sources they were measured on."""
+    import hashlib
+
+    h = hashlib.sha256()
+    csrc = os.path.join(ROOT, "zwhisper_amd", "csrc")
+    for name in sorted(os.listdir(csrc)):
+        if name.endswith((".hip", ".hpp")):
+            h.update(name.encode())
+            with open(os.path.join(csrc, name), "rb") as f:
+                h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def _traffic_table() -> dict:
     try:
-        with open(path) as f:
-            data = json.load(f)
-        return data.get(workload_name)
+        with open(TRAFFIC_JSON) as f:
+            return json.load(f)
     except (OSError, ValueError):
-        return None
+        return {}
+
+
+def traffic_for(workload_name: str):
+    """HBM bytes per step from the committed rocprofv3 counter summary, if one exists.  The
+    figure is not measured in this run (counters need a run of their own under rocprofv3 --pmc);
+    traffic_source() says where it comes from and whether the kernels have changed since."""
+    return _traffic_table().get(workload_name)
+
+
+def traffic_source() -> dict:
+    """Where roofline.traffic comes from: profiles/traffic.json, two rocprofv3 --pmc passes
+    (FETCH_SIZE, WRITE_SIZE) scaled by a device-copy calibration, measured on the kernel sources
+    whose hash it records; `current` says whether those are the sources that ran here."""
+    cal = _traffic_table().get("_calibration", {})
+    measured = cal.get("sources_sha")
+    now = kernel_sources_sha()
+    return {"file": "profiles/traffic.json", "measured_in_this_run": False,
+            "counters": "rocprofv3 --pmc FETCH_SIZE (x%.3f) + WRITE_SIZE (x%.3f), separate passes"
+                        % (cal.get("fetch_factor", float("nan")), cal.get("write_factor", float("nan"))),
+            "sources_sha_measured": measured, "sources_sha_now": now, "current": measured == now}
 
 
 DENSE_DTYPE = ("x3: f32 inputs split into 16-bit hi + lo terms (f16 for Q.K^T and for P.V), three 16-bit MFMA "
@@ -944,6 +982,11 @@ def _attention_line(wl: Workload, r: dict, dense_math: int) -> dict:
 
 
 def _say(name: str, res: dict, peak_name: str) -> None:
+    """One summary line and the workload's full record (one JSON object) on stderr.  stdout carries
+    only the final headline line."""
+    roof = res.get("roofline", {})
+    if roof.get("traffic") is not None:
+        roof["traffic_source"] = TRAFFIC_SOURCE
     cpu = res.get("cpu_baseline")
     par = res.get("parity")
     print(f"[bench] {name}: {res['value']:.2f} {res['unit']} ({res['ms_per_step']:.4f} ms/step, kernels "
@@ -952,6 +995,8 @@ def _say(name: str, res: dict, peak_name: str) -> None:
              if "sustained" in res else "")
           + (f", parity max abs {par['max_abs']:.2e} rel {par['normwise_rel']:.2e}" if par else "")
           + (f", cpu {cpu['value']:.3f} {cpu['unit']} on {cpu['cores']} threads" if cpu else ""),
+          file=sys.stderr, flush=True)
+    print("[bench-record] " + json.dumps({"workload": name, **{k: v for k, v in res.items() if k != "workload"}}),
           file=sys.stderr, flush=True)
 
 
@@ -1103,6 +1148,8 @@ def main() -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "launches": 5}), flush=True)
         return 0
+    global TRAFFIC_SOURCE
+    TRAFFIC_SOURCE = traffic_source()
     host = host_cpus()
     threads = host_threads()
     print(f"[bench] host: {host['cpu_model']}, nproc {host['nproc']}, CPUs for this job {host['cpus']}, "
@@ -1202,15 +1249,23 @@ def main() -> int:
         "rate": head["rate"],
         "kernel_ms_median": head["kernel_ms_median"],
         "parity": head.get("parity"),
-        "host": host,
+        "host": {k: host[k] for k in ("cpu_model", "nproc", "cpus")},
         "cpu_baseline": head.get("cpu_baseline"),
-        **({"cpu_baseline_all_threads": head["cpu_baseline_all_threads"]} if "cpu_baseline_all_threads" in head else {}),
-        **({"dropin_host_buffers": head["dropin_host_buffers"]} if "dropin_host_buffers" in head else {}),
-        "workloads": {r["workload"]: {k: v for k, v in r.items() if k not in ("workload",)}
-                      for n, r in results.items() if n != args.workload},
+        # the other workloads, one short entry each; their full records are the "[bench-record]"
+        # lines on stderr
+        "workloads": {r["workload"]: _brief(r) for n, r in results.items() if n != args.workload},
     }
-    print(json.dumps(line), flush=True)
+    print(json.dumps(line, separators=(",", ":")), flush=True)
     return 0
+
+
+def _brief(res: dict) -> dict:
+    """A workload's entry on the headline line: value, step time and roofline fraction."""
+    out = {"value": round(res["value"], 4), "unit": res["unit"], "ms_per_step": round(res["ms_per_step"], 5),
+           "frac": round(res["roofline"]["frac"], 4), "bound": res["roofline"]["bound"]}
+    if "parity" in res and res["parity"] is not None:
+        out["parity_ok"] = res["parity"]["within_bar"]
+    return out
 
 
 if __name__ == "__main__":
