@@ -242,6 +242,30 @@ def test_noalloc_refuses_beyond_its_scratch_before_the_device():
     assert "static scratch" in _lib.last_error(None)
 
 
+@pytest.mark.parametrize("dense_math", [0, 1])
+def test_dense_k_v_spans_beyond_2gib_are_refused_in_both_modes(dense_math):
+    """Both dense kernels (x3 and fp32) address an item's K/V rows with 32-bit buffer offsets, so a
+    call whose rows span 2 GiB or more is refused with that reason before any device work: an
+    unsplit (512 units) non-causal call with a 1 GiB row stride, through the entry point that
+    needs no context."""
+    import ctypes
+
+    n_q = 128 * 512
+    sh = AttnShape(n_q, 2, 1, 1, 64, 64, 1 << 28, 64, False, None)
+    assert z.plan(sh).max_chunks == 1 and z.plan(sh).kernel == 1
+    c = sh.to_c()
+    fake = 1 << 20  # an aligned, never dereferenced address
+    rc = _lib.lib().zwg_attention_batch_noalloc(fake, fake, fake, ctypes.byref(c), None, fake, dense_math, None)
+    assert rc == _lib.ZWG_ERROR
+    assert "2 GiB" in _lib.last_error(None)
+    # the transposed-K span of one KV head: d rows of kt_stride columns
+    sh = AttnShape(n_q, 2, 1, 1, 64, 64, 64, 64, False, 1 << 23)
+    c = sh.to_c()
+    rc = _lib.lib().zwg_attention_batch_noalloc(fake, fake, fake, ctypes.byref(c), None, fake, dense_math, None)
+    assert rc == _lib.ZWG_ERROR
+    assert "transposed K rows" in _lib.last_error(None)
+
+
 def test_zig_binding_declares_the_whole_header():
     """zig/gpu.zig (the binding a maintainer drops into src/gpu.zig; no Zig toolchain here to
     compile it) declares every function of include/zw_gpu.h, and its extern structs carry the C

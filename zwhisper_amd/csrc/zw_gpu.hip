@@ -126,13 +126,14 @@ int run_kernels(zwg_ctx *ctx, const Exec &x, const float *q, const float *k, con
                  (unsigned long long)p.ws_bytes, (unsigned long long)x.ws_bytes, x.ws_name);
         return fail(ctx, buf);
     }
-    // the row-major decode kernel and the x3 dense kernel address one item's K/V rows (and the
-    // dense kernel one KV head's K^T rows) with 32-bit byte offsets
-    const bool dense_x3 = p.kernel == 1 && x.dense_math != ZWG_DENSE_FP32;
-    if ((p.kernel == 2 && !s.kt_stride) || dense_x3) {
-        if (s.n_kv > 0 && ((s.n_kv - 1 + (dense_x3 ? 32 : 0)) * s.kv_stride + s.d) * sizeof(float) > 0x7fffffffull)
+    // the row-major decode kernel and both dense kernels (x3 and fp32) address one item's K/V rows
+    // (and the dense kernels one KV head's K^T rows) through buffer descriptors with 32-bit byte
+    // offsets; the dense kernels' tile loads reach up to 32 rows past the last key
+    const bool dense = p.kernel == 1;
+    if ((p.kernel == 2 && !s.kt_stride) || dense) {
+        if (s.n_kv > 0 && ((s.n_kv - 1 + (dense ? 32 : 0)) * s.kv_stride + s.d) * sizeof(float) > 0x7fffffffull)
             return fail(ctx, "K/V rows of one batch item must span less than 2 GiB");
-        if (dense_x3 && s.kt_stride && (s.d * s.kt_stride + 32) * sizeof(float) > 0x7fffffffull)
+        if (dense && s.kt_stride && (s.d * s.kt_stride + 32) * sizeof(float) > 0x7fffffffull)
             return fail(ctx, "the transposed K rows of one KV head must span less than 2 GiB");
     }
 
