@@ -293,33 +293,69 @@ class Workload:
                 "bar": bar, "within_bar": err <= bar["max_abs"] and rel <= bar["normwise_rel"]}
 
     def dropin(self, reps: int = 3) -> dict:
-        """The host-pointer drop-in (zwg_attention_ex, what the unchanged src/encoder.zig:167 call
-        binds): one synchronous call per window on pageable host buffers, H2D of q/k/v, the kernels
-        and D2H of out, timed on the host clock.  Includes PCIe: never the headline value."""
+        """The host-pointer drop-in (zwg_attention_ex), what the unchanged callers bind: one
+        synchronous call per window or sequence on pageable host buffers, H2D of q/k/v (the spans
+        the reference reads), the kernels and D2H of out, timed on the host clock.
+          encoders: src/encoder.zig:167, one call per window;
+          decoder step: src/decoder.zig:184 (self, the window's cache rows 0..n_kv) and :191 (cross,
+            the window's 1500 encoder rows), two calls per window;
+          LLM decode step: src/llm.zig:191-202, one call per sequence over its transposed cache
+            (n_ctx columns) and its V rows 0..n_kv.
+        Includes PCIe: never the headline value."""
+        from zwhisper_amd.ops import AttnShape
+
         w, n = self.spec, self.number
-        assert n in (1, 2)
-        calls = []
-        for i in range(w.n_items):
-            calls.append((np.ascontiguousarray(self.host["q"][i]).reshape(-1),
-                          np.ascontiguousarray(self.host["k"][i]).reshape(-1),
-                          np.ascontiguousarray(self.host["v"][i]).reshape(-1),
-                          np.zeros(w.n_q * w.n_head * w.d, np.float32)))
+        h = self.host
+        calls = []  # (q, k, v, shape, out, device output row to compare with)
+        if n in (1, 2):
+            for i in range(w.n_items):
+                calls.append((np.ascontiguousarray(h["q"][i]).reshape(-1), np.ascontiguousarray(h["k"][i]).reshape(-1),
+                              np.ascontiguousarray(h["v"][i]).reshape(-1), self.shape,
+                              np.zeros(w.n_q * w.n_head * w.d, np.float32), ("out", i)))
+        elif n == 3:
+            ns = w.n_head * w.d
+            for i in range(w.n_items):
+                L = int(self.lengths[i])
+                sh = AttnShape(1, L, w.n_head, w.n_head, w.d, ns, ns, ns, True, None)
+                calls.append((h["qs"][i].copy(), np.ascontiguousarray(h["ks"][i, :L]).reshape(-1),
+                              np.ascontiguousarray(h["vs"][i, :L]).reshape(-1), sh, np.zeros(ns, np.float32),
+                              ("os", i)))
+                calls.append((h["qc"][i].copy(), np.ascontiguousarray(h["kc"][i]).reshape(-1),
+                              np.ascontiguousarray(h["vc"][i]).reshape(-1), self.shape_cross, np.zeros(ns, np.float32),
+                              ("oc", i)))
+        else:
+            ns, kvw, cap = w.n_head * w.d, w.n_head_kv * w.d, w.n_kv_cap
+            for i in range(w.n_items):
+                L = int(self.lengths[i])
+                sh = AttnShape(1, L, w.n_head, w.n_head_kv, w.d, ns, kvw, ns, True, cap)
+                calls.append((h["q"][i].copy(), np.ascontiguousarray(h["k"][i]).reshape(-1),
+                              np.ascontiguousarray(h["v"][i, :L]).reshape(-1), sh, np.zeros(ns, np.float32),
+                              ("out", i)))
 
         def run():
-            for q, k, v, out in calls:
-                self.ctx.attention_ex_host(q, k, v, self.shape, out)
+            for q, k, v, sh, out, _ in calls:
+                self.ctx.attention_ex_host(q, k, v, sh, out)
 
         best, mean, runs = time_cpu(run, reps)
         self.torch.cuda.synchronize()
-        dev_out = self.sets[self.last % len(self.sets)]["out"].cpu().numpy()
-        diff = max(float(np.abs(out - dev_out[i].reshape(-1)).max()) for i, (_, _, _, out) in enumerate(calls))
-        moved = sum(q.nbytes + k.nbytes + v.nbytes + out.nbytes for q, k, v, out in calls)
-        return {"value": self.work / best / 1e12, "unit": "TFLOP/s", "ms_per_step": 1e3 * best,
-                "ms_per_step_mean": 1e3 * mean, "calls_per_step": w.n_items, "pcie_bytes_per_step": moved,
-                "max_abs_vs_device_line": diff,
-                "note": "zwg_attention_ex per window on pageable host buffers (H2D q/k/v + kernels + D2H out), "
-                        "synchronous; best of " + f"{runs} runs; a one-window call plans its own key split, so it "
-                        "can round differently from the batched device call"}
+        s = self.sets[self.last % len(self.sets)]
+        dev = {key: s[key].cpu().numpy() for key in {c[5][0] for c in calls}}
+        diff = max(float(np.abs(out - dev[key][i].reshape(-1)).max()) for _, _, _, _, out, (key, i) in calls)
+        moved = sum(q.nbytes + k.nbytes + v.nbytes + out.nbytes for q, k, v, _, out, _ in calls)
+        per = "window" if n in (1, 2, 3) else "sequence"
+        res = {"ms_per_step": 1e3 * best, "ms_per_step_mean": 1e3 * mean, "calls_per_step": len(calls),
+               "pcie_bytes_per_step": moved, "max_abs_vs_device_line": diff,
+               "note": f"zwg_attention_ex per {per}" + (" (self and cross)" if n == 3 else "") +
+                       " on pageable host buffers (H2D q/k/v + kernels + D2H out), synchronous; best of "
+                       f"{runs} runs; a one-{per} call plans its own key split, so it can round differently "
+                       "from the batched device call"}
+        if w.bound == "mfma":
+            res.update({"value": self.work / best / 1e12, "unit": "TFLOP/s"})
+        else:
+            res.update({"value": self.work / best / 1e9, "unit": "GB/s",
+                        "tokens_per_s": w.n_items / best, "note_value": "the step's algorithmic bytes (the "
+                        "device line's) over the drop-in's wall time; PCIe moves pcie_bytes_per_step"})
+        return res
 
     def free(self):
         self.sets = []
@@ -1182,7 +1218,7 @@ def main() -> int:
         res["roofline"]["traffic"] = traffic_for(spec.name if dm == z.DENSE_X3 else spec.name + "_fp32mfma")
         if not args.no_parity:
             res["parity"] = wl.parity(x3=dm == z.DENSE_X3)
-        if not args.only and n in (1, 2) and dm == z.DENSE_X3:
+        if not args.only and dm == z.DENSE_X3 and n != 4:
             res["dropin_host_buffers"] = wl.dropin()
         if not args.no_cpu:
             res["cpu_baseline"] = cpu_baseline(n, threads)

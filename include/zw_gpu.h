@@ -38,7 +38,7 @@ extern "C" {
 
 #define ZWG_OK 0
 #define ZWG_ERROR 2
-#define ZWG_VERSION 1
+#define ZWG_VERSION 2
 
 typedef struct zwg_ctx zwg_ctx;
 
@@ -111,6 +111,14 @@ typedef struct zwg_limits {
                                  linear k splits); default 256 MiB */
     uint32_t dense_math;      /* ZWG_DENSE_X3 (0, default) or ZWG_DENSE_FP32 */
     uint32_t reserved;        /* must be 0 */
+    uint64_t staging_bytes;   /* bytes of each staging buffer: the host-pointer calls' device copies
+                                 of q, k, v and out, the zero-padded copies of calls whose head dim
+                                 has no kernel of its own, and the pinned host copy of results with
+                                 gaps between rows.  Non-zero: all are allocated here, like the
+                                 reference's scratch sized at load (src/ops.zig:545-560), and a call
+                                 that would need more is refused, so no call allocates.  0 (default):
+                                 each grows on the first call that needs more (that call allocates
+                                 and waits for the context's stream). */
 } zwg_limits;
 
 /* How a call will run (zwg_plan): which kernel, how the keys are split. */
@@ -134,7 +142,10 @@ const char *zwg_last_error(const zwg_ctx *ctx);
  * in use.  A context starts on a stream of its own; zwg_get_stream right after zwg_open
  * returns it, to switch back later.  Every call of a context uses the same workspace, so a
  * switch orders the new stream after the work already queued on the old one (an event recorded
- * on the old stream, waited on by the new); calls issued on one stream run in issue order. */
+ * on the old stream, waited on by the new); calls issued on one stream run in issue order.
+ * The old stream must still exist at the switch (the event is recorded on it): switch the
+ * context away from a caller's stream before destroying that stream, as for any HIP call, a
+ * call that names a destroyed stream is undefined. */
 int zwg_set_stream(zwg_ctx *ctx, void *hip_stream);
 void *zwg_get_stream(const zwg_ctx *ctx);
 /* Wait for all work queued on the context's stream. */
@@ -170,9 +181,8 @@ int zwg_attention_batch_dev(zwg_ctx *ctx, const float *q, const float *k, const 
 
 /*
  * zwg_attention_batch_dev without a context and without any device allocation.  No counterpart in
- * the reference (its attention never allocates: the caller passes scratch, src/ops.zig:1-2,
- * :562); this is for callers that cannot call hipMalloc -- code under HIP graph capture, tight
- * serving loops, harnesses that forbid allocation.  It runs on the calling thread's current
+ * the reference; it is for callers that cannot call hipMalloc -- code under HIP graph capture,
+ * tight serving loops, harnesses that forbid allocation.  It runs on the calling thread's current
  * device and on `hip_stream` (NULL: the null stream), with the dense arithmetic `dense_math`, and
  * plans and computes exactly as a context opened with the default workspace (same kernels, same
  * key splits, same results).  batch may be NULL (one item).

@@ -30,7 +30,7 @@ def gpu_present() -> bool:
 def test_library_is_built_and_loads():
     assert os.path.exists(_lib.LIB_PATH), "run `python -m zwhisper_amd.build` first"
     L = _lib.lib()
-    assert L.zwg_version() == 1
+    assert L.zwg_version() == 2
 
 
 def test_every_declared_symbol_is_exported():
@@ -63,6 +63,7 @@ def test_struct_layout_matches_header():
     assert ctypes.sizeof(_lib.ShapeC) == 9 * 8 + 2 * 4
     assert ctypes.sizeof(_lib.BatchC) == 6 * 8
     assert ctypes.sizeof(_lib.PlanC) == 2 * 4 + 4 * 8
+    assert ctypes.sizeof(_lib.LimitsC) == 8 + 2 * 4 + 8
 
 
 def S(n_q, n_kv, h, hkv, d, causal, kt=None, qs=None, kvs=None, os_=None):

@@ -44,6 +44,7 @@ pub const Limits = extern struct {
     workspace_bytes: u64 = 0,
     dense_math: u32 = DENSE_X3,
     reserved: u32 = 0,
+    staging_bytes: u64 = 0,
 };
 
 pub const PlanInfo = extern struct {

@@ -52,7 +52,8 @@ class BatchC(ctypes.Structure):
 
 
 class LimitsC(ctypes.Structure):
-    _fields_ = [("workspace_bytes", _u64), ("dense_math", ctypes.c_uint32), ("reserved", ctypes.c_uint32)]
+    _fields_ = [("workspace_bytes", _u64), ("dense_math", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
+                ("staging_bytes", _u64)]
 
 
 class PlanC(ctypes.Structure):

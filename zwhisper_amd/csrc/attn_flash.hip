@@ -341,13 +341,16 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
     if (n_chunks == 1) { // an unsplit unit writes its rows itself; the merge pass skips them
         const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
         float *op = a.out + item * a.out_bstride + (int64_t)query * a.out_stride + head * D;
+        bool bad = false;
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 f32x4 w = {o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv};
                 *reinterpret_cast<f32x4 *>(op + db * 32 + 8 * g + 4 * half) = w;
+                bad |= any_nonfinite4(w[0], w[1], w[2], w[3]);
             }
+        if (a.nonfinite && bad) *a.nonfinite = 1u;
     } else {
         const int64_t slot = row_index(a, item, head, query) * a.max_chunks + chunk;
         float *po = a.part_o + slot * D;
@@ -449,7 +452,9 @@ __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
     }
     const float inv = L > 0.f ? 1.f / L : 0.f;
     float *op = a.out + item * a.out_bstride + (int64_t)query * a.out_stride + head * D + 4 * g;
-    *reinterpret_cast<float4 *>(op) = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    const float4 w = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+    *reinterpret_cast<float4 *>(op) = w;
+    if (a.nonfinite && any_nonfinite4(w.x, w.y, w.z, w.w)) *a.nonfinite = 1u;
 }
 
 hipError_t launch_flash(const AttnArgs &a, int d, hipStream_t stream, int *grid_blocks) {

@@ -426,13 +426,16 @@ void flash_x3_kernel(AttnArgs a) {
     if (n_chunks == 1) {
         const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
         float *op = a.out + item * a.out_bstride + (int64_t)query * a.out_stride + head * D;
+        bool bad = false;
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 f32x4 w = {o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv};
                 *reinterpret_cast<f32x4 *>(op + db * 32 + 8 * g + 4 * half) = w;
+                bad |= any_nonfinite4(w[0], w[1], w[2], w[3]);
             }
+        if (a.nonfinite && bad) *a.nonfinite = 1u;
     } else {
         const int64_t slot = row_index(a, item, head, query) * a.max_chunks + chunk;
         float *po = a.part_o + slot * D;

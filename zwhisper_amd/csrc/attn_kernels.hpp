@@ -33,7 +33,17 @@ struct AttnArgs {
     int64_t live_blocks;   // dense, heavy_first == 2: workgroups of the grid (dense_live_unit)
     float *part_o;      // [row][max_chunks][d]   unnormalised sum of p*v
     float *part_ml;     // [row][max_chunks][2]   (running max in log2 units, sum of p)
+    // when set, the kernels that write `out` (the dense kernels' unsplit rows and the merge) store
+    // 1 here if any value they write is an infinity or a NaN
+    uint32_t *nonfinite;
 };
+
+// True when any of the four values is an infinity or a NaN.
+__device__ __forceinline__ bool any_nonfinite4(float x, float y, float z, float w) {
+    const uint32_t e = 0x7f800000u;
+    return ((__builtin_bit_cast(uint32_t, x) & e) == e) | ((__builtin_bit_cast(uint32_t, y) & e) == e) |
+           ((__builtin_bit_cast(uint32_t, z) & e) == e) | ((__builtin_bit_cast(uint32_t, w) & e) == e);
+}
 
 // Rows of a call are numbered ((item * n_head + head) * n_q + query).
 __host__ __device__ inline int64_t row_index(const AttnArgs &a, int item, int head, int query) {

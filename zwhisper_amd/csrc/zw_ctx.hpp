@@ -27,6 +27,8 @@ struct zwg_ctx {
     // work on the next touches it
     hipEvent_t switch_event = nullptr;
     float *workspace = nullptr;
+    // device word the kernels set when they write a non-finite result (host drop-in only)
+    uint32_t *nonfinite_flag = nullptr;
     uint32_t dense_math = ZWG_DENSE_X3; // products of the dense kernel (zwg_set_dense_math)
     uint64_t workspace_bytes = 0;
     // device staging: q, k, v, out of the host-pointer calls (0-3), and the zero-padded q, k, v, out
@@ -36,6 +38,9 @@ struct zwg_ctx {
     // pinned host staging for results whose rows are not contiguous in the caller's buffer
     float *host_stage = nullptr;
     uint64_t host_stage_bytes = 0;
+    // zwg_limits.staging_bytes was set: every staging buffer was allocated at zwg_open and a call
+    // that needs more is refused instead of growing it
+    bool fixed_staging = false;
     std::vector<ZwgChild> children;
     std::string err;
 };

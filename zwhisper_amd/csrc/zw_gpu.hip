@@ -31,6 +31,12 @@ int fail_hip(zwg_ctx *ctx, const char *what, hipError_t e) {
 int ensure_stage(zwg_ctx *ctx, int i, uint64_t bytes) {
     bytes = std::max<uint64_t>(bytes, 256);
     if (ctx->stage_bytes[i] >= bytes) return ZWG_OK;
+    if (ctx->fixed_staging) {
+        char buf[200];
+        snprintf(buf, sizeof buf, "this call needs %llu bytes of staging, more than the context's staging_bytes (%llu)",
+                 (unsigned long long)bytes, (unsigned long long)ctx->stage_bytes[i]);
+        return fail(ctx, buf);
+    }
     hipError_t e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) return fail_hip(ctx, "hipStreamSynchronize", e);
     if (ctx->stage[i]) {
@@ -57,6 +63,13 @@ int download_rows(zwg_ctx *ctx, float *dst, const float *src, uint64_t n_rows, u
         return ZWG_OK;
     }
     const uint64_t span = ((n_rows - 1) * stride + cols) * F;
+    if (ctx->host_stage_bytes < span && ctx->fixed_staging) {
+        char buf[200];
+        snprintf(buf, sizeof buf,
+                 "this call's result needs %llu bytes of pinned host staging, more than the context's staging_bytes "
+                 "(%llu)", (unsigned long long)span, (unsigned long long)ctx->host_stage_bytes);
+        return fail(ctx, buf);
+    }
     if (ctx->host_stage_bytes < span) {
         e = hipStreamSynchronize(ctx->stream);
         if (e != hipSuccess) return fail_hip(ctx, "hipStreamSynchronize", e);
@@ -107,6 +120,7 @@ struct Exec {
     uint32_t dense_math;
     uint64_t plan_cap; // workspace bytes the planner may use (>= ws_bytes: a bigger plan is refused)
     const char *ws_name;
+    uint32_t *nonfinite = nullptr; // device flag set by the kernels on a non-finite result, or null
 };
 
 Exec ctx_exec(const zwg_ctx *ctx) {
@@ -169,6 +183,7 @@ int run_kernels(zwg_ctx *ctx, const Exec &x, const float *q, const float *k, con
     const uint64_t n_rows = b.n_batch * s.n_head * s.n_q;
     a.part_ml = x.ws;
     a.part_o = x.ws + (p.max_chunks > 1 ? part_o_offset(n_rows, (uint64_t)p.max_chunks) : 0);
+    a.nonfinite = x.nonfinite;
 
     hipError_t e = hipSuccess;
     if (x.device >= 0) e = hipSetDevice(x.device);
@@ -250,20 +265,6 @@ int run(zwg_ctx *ctx, const Exec &x, const float *q, const float *k, const float
     return ZWG_OK;
 }
 
-// True when any of the n_rows rows of `cols` floats at `stride` holds an infinity or a NaN.
-bool any_non_finite(const float *p, uint64_t n_rows, uint64_t cols, uint64_t stride) {
-    uint32_t bad = 0;
-    for (uint64_t r = 0; r < n_rows; ++r) {
-        const float *row = p + r * stride;
-        for (uint64_t c = 0; c < cols; ++c) {
-            uint32_t bits;
-            std::memcpy(&bits, row + c, sizeof bits);
-            bad |= (uint32_t)((bits & 0x7f800000u) == 0x7f800000u);
-        }
-    }
-    return bad != 0;
-}
-
 } // namespace
 
 extern "C" {
@@ -338,6 +339,41 @@ int zwg_open(int device, const zwg_limits *limits, zwg_ctx **out) {
         return fail_hip(nullptr, "hipMalloc (workspace)", e);
     }
     ctx->workspace = static_cast<float *>(ws);
+    void *flag = nullptr;
+    e = hipMalloc(&flag, 256);
+    if (e != hipSuccess) {
+        (void)hipFree(ws);
+        (void)hipEventDestroy(ctx->switch_event);
+        (void)hipStreamDestroy(ctx->own_stream);
+        delete ctx;
+        return fail_hip(nullptr, "hipMalloc (flag)", e);
+    }
+    ctx->nonfinite_flag = static_cast<uint32_t *>(flag);
+    if (limits && limits->staging_bytes) {
+        // every staging buffer at its fixed size now: no later call allocates
+        const uint64_t sb = std::max<uint64_t>(limits->staging_bytes, 256);
+        for (int i = 0; i < 8 && e == hipSuccess; ++i) {
+            void *p = nullptr;
+            e = hipMalloc(&p, sb);
+            if (e == hipSuccess) {
+                ctx->stage[i] = static_cast<float *>(p);
+                ctx->stage_bytes[i] = sb;
+            }
+        }
+        if (e == hipSuccess) {
+            void *p = nullptr;
+            e = hipHostMalloc(&p, sb, hipHostMallocDefault);
+            if (e == hipSuccess) {
+                ctx->host_stage = static_cast<float *>(p);
+                ctx->host_stage_bytes = sb;
+            }
+        }
+        ctx->fixed_staging = true;
+        if (e != hipSuccess) {
+            zwg_close(ctx);
+            return fail_hip(nullptr, "allocating the staging buffers (zwg_limits.staging_bytes)", e);
+        }
+    }
     *out = ctx;
     return ZWG_OK;
 }
@@ -361,6 +397,7 @@ void zwg_close(zwg_ctx *ctx) {
         if (s) (void)hipFree(s);
     if (ctx->host_stage) (void)hipHostFree(ctx->host_stage);
     if (ctx->workspace) (void)hipFree(ctx->workspace);
+    if (ctx->nonfinite_flag) (void)hipFree(ctx->nonfinite_flag);
     if (ctx->switch_event) (void)hipEventDestroy(ctx->switch_event);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
@@ -429,10 +466,18 @@ int zwg_attention_ex(zwg_ctx *ctx, const float *q, const float *k, const float *
     if (e != hipSuccess) return fail_hip(ctx, "hipMemcpyAsync (upload)", e);
     const zwg_batch one{1, 0, 0, 0, 0, nullptr};
     Exec x = ctx_exec(ctx);
+    // the kernels that write out set this flag on a non-finite value (read back with the result)
+    x.nonfinite = ctx->nonfinite_flag;
+    e = hipMemsetAsync(ctx->nonfinite_flag, 0, sizeof(uint32_t), ctx->stream);
+    if (e != hipSuccess) return fail_hip(ctx, "hipMemsetAsync (flag)", e);
     Plan p;
     int rc = run(ctx, x, ctx->stage[0], ctx->stage[1], ctx->stage[2], s, one, ctx->stage[3], &p);
     if (rc != ZWG_OK) return rc;
-    // copy back only each row's n_head*d columns: out's other columns stay the caller's
+    uint32_t nonfinite = 0;
+    e = hipMemcpyAsync(&nonfinite, ctx->nonfinite_flag, sizeof nonfinite, hipMemcpyDeviceToHost, ctx->stream);
+    if (e != hipSuccess) return fail_hip(ctx, "hipMemcpyAsync (flag)", e);
+    // copy back only each row's n_head*d columns: out's other columns stay the caller's (waits for
+    // the stream, so the flag has arrived too)
     rc = download_rows(ctx, out, ctx->stage[3], s.n_q, hd, s.out_stride);
     if (rc != ZWG_OK) return rc;
     // The x3 dense kernel needs keys (and scaled queries) within f16 range; outside it the rows
@@ -440,7 +485,8 @@ int zwg_attention_ex(zwg_ctx *ctx, const float *q, const float *k, const float *
     // input (src/ops.zig:562-590), so a non-finite result of the x3 kernel is computed again on
     // the fp32-MFMA kernel, which has no range condition (and reproduces any NaN or infinity the
     // inputs themselves carry).
-    if (p.kernel == 1 && x.dense_math != ZWG_DENSE_FP32 && any_non_finite(out, s.n_q, hd, s.out_stride)) {
+    if (p.kernel == 1 && x.dense_math != ZWG_DENSE_FP32 && nonfinite) {
+        x.nonfinite = nullptr;
         x.dense_math = ZWG_DENSE_FP32;
         rc = run(ctx, x, ctx->stage[0], ctx->stage[1], ctx->stage[2], s, one, ctx->stage[3]);
         if (rc != ZWG_OK) return rc;

@@ -102,12 +102,14 @@ def plan(sh: AttnShape, n_batch: int = 1, workspace_bytes: int = 0) -> _lib.Plan
 class Context:
     """One library context (zwg_ctx): a device, a workspace, staging buffers."""
 
-    def __init__(self, device: int = 0, workspace_bytes: int = 0, dense_math: int = 0):
-        """dense_math: _lib.DENSE_X3 (0, default) or _lib.DENSE_FP32, the dense kernel's arithmetic."""
+    def __init__(self, device: int = 0, workspace_bytes: int = 0, dense_math: int = 0, staging_bytes: int = 0):
+        """dense_math: _lib.DENSE_X3 (0, default) or _lib.DENSE_FP32, the dense kernel's arithmetic.
+        staging_bytes: non-zero allocates every staging buffer at this size now, and calls that
+        would need more are refused (zwg_limits.staging_bytes)."""
         L = _lib.lib()
         self._L = L
         h = ctypes.c_void_p()
-        lim = _lib.LimitsC(workspace_bytes, dense_math, 0)
+        lim = _lib.LimitsC(workspace_bytes, dense_math, 0, staging_bytes)
         rc = L.zwg_open(device, ctypes.byref(lim), ctypes.byref(h))
         if rc != _lib.ZWG_OK:
             raise ZwgError(_lib.last_error(None))
