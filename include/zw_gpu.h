@@ -98,7 +98,10 @@ typedef struct zwg_batch {
  *     in magnitude (f16 range): a larger key gives NaN in the rows that see it, a larger value NaN
  *     in its own output column (head, dimension) of the rows whose 32-row group loads its 32-key
  *     tile -- never a silently wrong finite result
- *     (zwg_attention_ex then recomputes the call in ZWG_DENSE_FP32).
+ *     (zwg_attention_ex then recomputes the call in ZWG_DENSE_FP32).  Small values: the split's
+ *     low terms of values below 2^-3 are f16 subnormals, so the error has an absolute floor near
+ *     2^-25 rather than staying relative; results whose largest |value| is below 2^-9 can miss
+ *     the x3 relative bar (zwg_attention_ex recomputes those in ZWG_DENSE_FP32 too).
  *   ZWG_DENSE_FP32: fp32 MFMA (v_mfma_f32_32x32x2_f32) throughout, no range condition.
  * The decode kernels are f32 FMA in either mode.
  */
@@ -156,10 +159,12 @@ int zwg_set_dense_math(zwg_ctx *ctx, uint32_t mode);
 /*
  * Drop-in for ops.attentionEx (src/ops.zig:562): host pointers, synchronous — `out` holds the
  * result on return, and only each query row's n_head*d columns are written, as in the
- * reference.  Stages q/k/v through device buffers the context keeps (grown on first need).
- * It keeps the reference's contract for any finite input: when the x3 dense kernel's result
- * holds a non-finite value (a key, value or scaled query beyond f16 range), the call is computed
- * again on the fp32-MFMA kernel, which has no range condition.
+ * reference.  Stages q/k/v through device buffers the context keeps (grown on first need, or
+ * fixed at zwg_open: zwg_limits.staging_bytes).  It keeps the reference's contract for any
+ * finite input: the kernels record the largest |value| they write on the device, and when the
+ * x3 dense kernel's result holds a non-finite value (a key, value or scaled query beyond f16
+ * range) or is smaller than 2^-9 throughout (below the x3 error floor's reach), the call is
+ * computed again on the fp32-MFMA kernel, which has neither condition.
  */
 int zwg_attention_ex(zwg_ctx *ctx, const float *q, const float *k, const float *v, const zwg_attn_shape *shape,
                      float *out);

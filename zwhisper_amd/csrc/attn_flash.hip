@@ -336,35 +336,37 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
     if (t < n_tiles) step(P0{}, t, s_cur, s_b);
 
     const float l_tot = lane_pair_sum(l_run);
-    if (!q_valid) return;
     // lane holds dims db*32 + 8*g + 4*half + {0..3} in registers 4g..4g+3 of o[db]
     if (n_chunks == 1) { // an unsplit unit writes its rows itself; the merge pass skips them
-        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-        float *op = a.out + item * a.out_bstride + (int64_t)query * a.out_stride + head * D;
-        bool bad = false;
+        uint32_t big = 0;
+        if (q_valid) {
+            const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+            float *op = a.out + item * a.out_bstride + (int64_t)query * a.out_stride + head * D;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+            for (int db = 0; db < NDB; ++db)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                f32x4 w = {o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv};
-                *reinterpret_cast<f32x4 *>(op + db * 32 + 8 * g + 4 * half) = w;
-                bad |= any_nonfinite4(w[0], w[1], w[2], w[3]);
-            }
-        if (a.nonfinite && bad) *a.nonfinite = 1u;
-    } else {
-        const int64_t slot = row_index(a, item, head, query) * a.max_chunks + chunk;
-        float *po = a.part_o + slot * D;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                f32x4 w = {o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2], o[db][4 * g + 3]};
-                *reinterpret_cast<f32x4 *>(po + db * 32 + 8 * g + 4 * half) = w;
-            }
-        if (half == 0) {
-            a.part_ml[2 * slot] = m_run;
-            a.part_ml[2 * slot + 1] = l_tot;
+                for (int g = 0; g < 4; ++g) {
+                    f32x4 w = {o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv};
+                    *reinterpret_cast<f32x4 *>(op + db * 32 + 8 * g + 4 * half) = w;
+                    big = max(max(big, max(abs_bits(w[0]), abs_bits(w[1]))), max(abs_bits(w[2]), abs_bits(w[3])));
+                }
         }
+        if (a.out_max) out_max_record(a, big); // every lane of the wave takes part
+        return;
+    }
+    if (!q_valid) return;
+    const int64_t slot = row_index(a, item, head, query) * a.max_chunks + chunk;
+    float *po = a.part_o + slot * D;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            f32x4 w = {o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2], o[db][4 * g + 3]};
+            *reinterpret_cast<f32x4 *>(po + db * 32 + 8 * g + 4 * half) = w;
+        }
+    if (half == 0) {
+        a.part_ml[2 * slot] = m_run;
+        a.part_ml[2 * slot + 1] = l_tot;
     }
 }
 
@@ -373,88 +375,94 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
 // one thread per (row, 4 dims).  MAXC > 0: the call has at most MAXC splits per row.
 template <int D, int MAXC>
 __global__ __launch_bounds__(256) void combine_kernel(AttnArgs a) {
-    constexpr int G4 = D / 4;
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t n_rows = (int64_t)a.n_batch * a.n_head * a.n_q;
-    const int64_t row = t / G4;
-    if (row >= n_rows) return;
-    const int g = (int)(t - row * G4);
-    const int query = (int)(row % a.n_q);
-    const int64_t ih = row / a.n_q;
-    const int head = (int)(ih % a.n_head);
-    const int item = (int)(ih / a.n_head);
-    const float2 *ml = reinterpret_cast<const float2 *>(a.part_ml) + row * a.max_chunks;
-    const float4 *po = reinterpret_cast<const float4 *>(a.part_o + row * a.max_chunks * D) + g;
-    const int q_end = min((query / a.rows_per_unit + 1) * a.rows_per_unit, a.n_q);
-    auto row_chunks = [&](int n_kv) {
-        const int kv_hi = a.causal ? max(0, n_kv - a.n_q + q_end) : n_kv;
-        int chunk_keys;
-        return unit_split(kv_hi, a.split_tile, a.chunk_len, a.max_chunks, &chunk_keys);
-    };
-    // With one key count for every item the row's chunk count is known at once: rows the
-    // attention kernel finished (one chunk) load nothing, and the others load their own slots
-    // only.  With per-item counts in device memory, every slot of the row (c < max_chunks, all
-    // inside the workspace) is loaded before the count arrives, so the partials' round trip
-    // overlaps that of the count; slots past the row's chunk count are discarded below by
-    // selection (they may hold anything).
-    const int known_chunks = a.n_kv_item ? 0 : row_chunks(a.n_kv);
-    if (known_chunks == 1) return; // written by the attention kernel
-    const int last_slot = (known_chunks ? known_chunks : a.max_chunks) - 1;
-    float2 mlr[MAXC > 0 ? MAXC : 1];
-    float4 vr[MAXC > 0 ? MAXC : 1];
-    if (MAXC > 0) {
+    // the merge of one (row, 4 dims); returns the largest |value| written as its bit pattern, or 0
+    auto merge = [&]() -> uint32_t {
+        constexpr int G4 = D / 4;
+        const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+        const int64_t n_rows = (int64_t)a.n_batch * a.n_head * a.n_q;
+        const int64_t row = t / G4;
+        if (row >= n_rows) return 0u;
+        const int g = (int)(t - row * G4);
+        const int query = (int)(row % a.n_q);
+        const int64_t ih = row / a.n_q;
+        const int head = (int)(ih % a.n_head);
+        const int item = (int)(ih / a.n_head);
+        const float2 *ml = reinterpret_cast<const float2 *>(a.part_ml) + row * a.max_chunks;
+        const float4 *po = reinterpret_cast<const float4 *>(a.part_o + row * a.max_chunks * D) + g;
+        const int q_end = min((query / a.rows_per_unit + 1) * a.rows_per_unit, a.n_q);
+        auto row_chunks = [&](int n_kv) {
+            const int kv_hi = a.causal ? max(0, n_kv - a.n_q + q_end) : n_kv;
+            int chunk_keys;
+            return unit_split(kv_hi, a.split_tile, a.chunk_len, a.max_chunks, &chunk_keys);
+        };
+        // With one key count for every item the row's chunk count is known at once: rows the
+        // attention kernel finished (one chunk) load nothing, and the others load their own slots
+        // only.  With per-item counts in device memory, every slot of the row (c < max_chunks, all
+        // inside the workspace) is loaded before the count arrives, so the partials' round trip
+        // overlaps that of the count; slots past the row's chunk count are discarded below by
+        // selection (they may hold anything).
+        const int known_chunks = a.n_kv_item ? 0 : row_chunks(a.n_kv);
+        if (known_chunks == 1) return 0u; // written by the attention kernel
+        const int last_slot = (known_chunks ? known_chunks : a.max_chunks) - 1;
+        float2 mlr[MAXC > 0 ? MAXC : 1];
+        float4 vr[MAXC > 0 ? MAXC : 1];
+        if (MAXC > 0) {
 #pragma unroll
-        for (int c = 0; c < MAXC; ++c) { // slots past the last reload it: no branches
-            const int cc = min(c, last_slot);
-            mlr[c] = ml[cc];
-            vr[c] = po[(int64_t)cc * G4];
+            for (int c = 0; c < MAXC; ++c) { // slots past the last reload it: no branches
+                const int cc = min(c, last_slot);
+                mlr[c] = ml[cc];
+                vr[c] = po[(int64_t)cc * G4];
+            }
         }
-    }
-    const int n_chunks = known_chunks ? known_chunks : row_chunks(item_kv(a, item));
-    if (n_chunks == 1) return; // written by the attention kernel
+        const int n_chunks = known_chunks ? known_chunks : row_chunks(item_kv(a, item));
+        if (n_chunks == 1) return 0u; // written by the attention kernel
 
-    float M = -INFINITY, L = 0.f;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (MAXC > 0) {
-        // merged from registers: the row's first n_chunks slots only
+        float M = -INFINITY, L = 0.f;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (MAXC > 0) {
+            // merged from registers: the row's first n_chunks slots only
 #pragma unroll
-        for (int c = 0; c < MAXC; ++c)
-            if (c < n_chunks) M = fmaxf(M, mlr[c].x);
-        if (M != -INFINITY) {
+            for (int c = 0; c < MAXC; ++c)
+                if (c < n_chunks) M = fmaxf(M, mlr[c].x);
+            if (M != -INFINITY) {
 #pragma unroll
-            for (int c = 0; c < MAXC; ++c) {
-                if (c >= n_chunks) continue;
-                const float w = exp2_fast(mlr[c].x - M); // 0 for a split that saw no key of this row
-                L += w * mlr[c].y;
-                acc.x += w * vr[c].x;
-                acc.y += w * vr[c].y;
-                acc.z += w * vr[c].z;
-                acc.w += w * vr[c].w;
+                for (int c = 0; c < MAXC; ++c) {
+                    if (c >= n_chunks) continue;
+                    const float w = exp2_fast(mlr[c].x - M); // 0 for a split that saw no key of this row
+                    L += w * mlr[c].y;
+                    acc.x += w * vr[c].x;
+                    acc.y += w * vr[c].y;
+                    acc.z += w * vr[c].z;
+                    acc.w += w * vr[c].w;
+                }
+            }
+        } else {
+            // two passes whose loads do not depend on each other, so they are all in flight at once
+#pragma unroll 8
+            for (int c = 0; c < n_chunks; ++c) M = fmaxf(M, ml[c].x);
+            if (M != -INFINITY) {
+#pragma unroll 8
+                for (int c = 0; c < n_chunks; ++c) {
+                    const float2 m_l = ml[c];
+                    const float4 v = po[(int64_t)c * G4];
+                    const float w = exp2_fast(m_l.x - M);
+                    L += w * m_l.y;
+                    acc.x += w * v.x;
+                    acc.y += w * v.y;
+                    acc.z += w * v.z;
+                    acc.w += w * v.w;
+                }
             }
         }
-    } else {
-        // two passes whose loads do not depend on each other, so they are all in flight at once
-#pragma unroll 8
-        for (int c = 0; c < n_chunks; ++c) M = fmaxf(M, ml[c].x);
-        if (M != -INFINITY) {
-#pragma unroll 8
-            for (int c = 0; c < n_chunks; ++c) {
-                const float2 m_l = ml[c];
-                const float4 v = po[(int64_t)c * G4];
-                const float w = exp2_fast(m_l.x - M);
-                L += w * m_l.y;
-                acc.x += w * v.x;
-                acc.y += w * v.y;
-                acc.z += w * v.z;
-                acc.w += w * v.w;
-            }
-        }
-    }
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    float *op = a.out + item * a.out_bstride + (int64_t)query * a.out_stride + head * D + 4 * g;
-    const float4 w = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
-    *reinterpret_cast<float4 *>(op) = w;
-    if (a.nonfinite && any_nonfinite4(w.x, w.y, w.z, w.w)) *a.nonfinite = 1u;
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        float *op = a.out + item * a.out_bstride + (int64_t)query * a.out_stride + head * D + 4 * g;
+        const float4 w = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
+        *reinterpret_cast<float4 *>(op) = w;
+        return max(max(abs_bits(w.x), abs_bits(w.y)), max(abs_bits(w.z), abs_bits(w.w)));
+    };
+    const uint32_t big = merge();
+    if (a.out_max) out_max_record(a, big); // every lane of the wave takes part
+
 }
 
 hipError_t launch_flash(const AttnArgs &a, int d, hipStream_t stream, int *grid_blocks) {

@@ -421,35 +421,37 @@ void flash_x3_kernel(AttnArgs a) {
     if (t < n_tiles) step(P0{}, t, s_cur, s_b);
 
     const float l_tot = lane_pair_sum(l_run);
-    if (!q_valid) return;
     // lane holds dims db*32 + 8*g + 4*half + {0..3} in registers 4g..4g+3 of o[db]
-    if (n_chunks == 1) {
-        const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-        float *op = a.out + item * a.out_bstride + (int64_t)query * a.out_stride + head * D;
-        bool bad = false;
+    if (n_chunks == 1) { // an unsplit unit writes its rows itself; the merge pass skips them
+        uint32_t big = 0;
+        if (q_valid) {
+            const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+            float *op = a.out + item * a.out_bstride + (int64_t)query * a.out_stride + head * D;
 #pragma unroll
-        for (int db = 0; db < NDB; ++db)
+            for (int db = 0; db < NDB; ++db)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                f32x4 w = {o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv};
-                *reinterpret_cast<f32x4 *>(op + db * 32 + 8 * g + 4 * half) = w;
-                bad |= any_nonfinite4(w[0], w[1], w[2], w[3]);
-            }
-        if (a.nonfinite && bad) *a.nonfinite = 1u;
-    } else {
-        const int64_t slot = row_index(a, item, head, query) * a.max_chunks + chunk;
-        float *po = a.part_o + slot * D;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                f32x4 w = {o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2], o[db][4 * g + 3]};
-                *reinterpret_cast<f32x4 *>(po + db * 32 + 8 * g + 4 * half) = w;
-            }
-        if (half == 0) {
-            a.part_ml[2 * slot] = m_run;
-            a.part_ml[2 * slot + 1] = l_tot;
+                for (int g = 0; g < 4; ++g) {
+                    f32x4 w = {o[db][4 * g] * inv, o[db][4 * g + 1] * inv, o[db][4 * g + 2] * inv, o[db][4 * g + 3] * inv};
+                    *reinterpret_cast<f32x4 *>(op + db * 32 + 8 * g + 4 * half) = w;
+                    big = max(max(big, max(abs_bits(w[0]), abs_bits(w[1]))), max(abs_bits(w[2]), abs_bits(w[3])));
+                }
         }
+        if (a.out_max) out_max_record(a, big); // every lane of the wave takes part
+        return;
+    }
+    if (!q_valid) return;
+    const int64_t slot = row_index(a, item, head, query) * a.max_chunks + chunk;
+    float *po = a.part_o + slot * D;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            f32x4 w = {o[db][4 * g], o[db][4 * g + 1], o[db][4 * g + 2], o[db][4 * g + 3]};
+            *reinterpret_cast<f32x4 *>(po + db * 32 + 8 * g + 4 * half) = w;
+        }
+    if (half == 0) {
+        a.part_ml[2 * slot] = m_run;
+        a.part_ml[2 * slot + 1] = l_tot;
     }
 }
 

@@ -33,16 +33,21 @@ struct AttnArgs {
     int64_t live_blocks;   // dense, heavy_first == 2: workgroups of the grid (dense_live_unit)
     float *part_o;      // [row][max_chunks][d]   unnormalised sum of p*v
     float *part_ml;     // [row][max_chunks][2]   (running max in log2 units, sum of p)
-    // when set, the kernels that write `out` (the dense kernels' unsplit rows and the merge) store
-    // 1 here if any value they write is an infinity or a NaN
-    uint32_t *nonfinite;
+    // when set, the kernels that write `out` (the dense kernels' unsplit rows and the merge) raise
+    // this word to the largest |value| they write, as its f32 bit pattern (out_max_record): an
+    // infinity or a NaN gives a pattern of 0x7f800000 or more
+    uint32_t *out_max;
 };
 
-// True when any of the four values is an infinity or a NaN.
-__device__ __forceinline__ bool any_nonfinite4(float x, float y, float z, float w) {
-    const uint32_t e = 0x7f800000u;
-    return ((__builtin_bit_cast(uint32_t, x) & e) == e) | ((__builtin_bit_cast(uint32_t, y) & e) == e) |
-           ((__builtin_bit_cast(uint32_t, z) & e) == e) | ((__builtin_bit_cast(uint32_t, w) & e) == e);
+// |x| as its bit pattern: for non-negative floats the unsigned order is the float order, and
+// NaNs and infinities lie above every finite value.
+__device__ __forceinline__ uint32_t abs_bits(float x) { return __builtin_bit_cast(uint32_t, x) & 0x7fffffffu; }
+
+// Raise *a.out_max to the wave's largest abs_bits `m` (one atomic per wave).
+__device__ __forceinline__ void out_max_record(const AttnArgs &a, uint32_t m) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, off));
+    if ((threadIdx.x & 63) == 0) atomicMax(a.out_max, m);
 }
 
 // Rows of a call are numbered ((item * n_head + head) * n_q + query).

@@ -27,8 +27,8 @@ struct zwg_ctx {
     // work on the next touches it
     hipEvent_t switch_event = nullptr;
     float *workspace = nullptr;
-    // device word the kernels set when they write a non-finite result (host drop-in only)
-    uint32_t *nonfinite_flag = nullptr;
+    // device word the kernels raise to the largest |out| they write (host drop-in only)
+    uint32_t *out_max_word = nullptr;
     uint32_t dense_math = ZWG_DENSE_X3; // products of the dense kernel (zwg_set_dense_math)
     uint64_t workspace_bytes = 0;
     // device staging: q, k, v, out of the host-pointer calls (0-3), and the zero-padded q, k, v, out

@@ -120,7 +120,7 @@ struct Exec {
     uint32_t dense_math;
     uint64_t plan_cap; // workspace bytes the planner may use (>= ws_bytes: a bigger plan is refused)
     const char *ws_name;
-    uint32_t *nonfinite = nullptr; // device flag set by the kernels on a non-finite result, or null
+    uint32_t *out_max = nullptr; // device word the kernels raise to the largest |out| they write, or null
 };
 
 Exec ctx_exec(const zwg_ctx *ctx) {
@@ -183,7 +183,7 @@ int run_kernels(zwg_ctx *ctx, const Exec &x, const float *q, const float *k, con
     const uint64_t n_rows = b.n_batch * s.n_head * s.n_q;
     a.part_ml = x.ws;
     a.part_o = x.ws + (p.max_chunks > 1 ? part_o_offset(n_rows, (uint64_t)p.max_chunks) : 0);
-    a.nonfinite = x.nonfinite;
+    a.out_max = x.out_max;
 
     hipError_t e = hipSuccess;
     if (x.device >= 0) e = hipSetDevice(x.device);
@@ -348,7 +348,7 @@ int zwg_open(int device, const zwg_limits *limits, zwg_ctx **out) {
         delete ctx;
         return fail_hip(nullptr, "hipMalloc (flag)", e);
     }
-    ctx->nonfinite_flag = static_cast<uint32_t *>(flag);
+    ctx->out_max_word = static_cast<uint32_t *>(flag);
     if (limits && limits->staging_bytes) {
         // every staging buffer at its fixed size now: no later call allocates
         const uint64_t sb = std::max<uint64_t>(limits->staging_bytes, 256);
@@ -397,7 +397,7 @@ void zwg_close(zwg_ctx *ctx) {
         if (s) (void)hipFree(s);
     if (ctx->host_stage) (void)hipHostFree(ctx->host_stage);
     if (ctx->workspace) (void)hipFree(ctx->workspace);
-    if (ctx->nonfinite_flag) (void)hipFree(ctx->nonfinite_flag);
+    if (ctx->out_max_word) (void)hipFree(ctx->out_max_word);
     if (ctx->switch_event) (void)hipEventDestroy(ctx->switch_event);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
@@ -466,27 +466,33 @@ int zwg_attention_ex(zwg_ctx *ctx, const float *q, const float *k, const float *
     if (e != hipSuccess) return fail_hip(ctx, "hipMemcpyAsync (upload)", e);
     const zwg_batch one{1, 0, 0, 0, 0, nullptr};
     Exec x = ctx_exec(ctx);
-    // the kernels that write out set this flag on a non-finite value (read back with the result)
-    x.nonfinite = ctx->nonfinite_flag;
-    e = hipMemsetAsync(ctx->nonfinite_flag, 0, sizeof(uint32_t), ctx->stream);
-    if (e != hipSuccess) return fail_hip(ctx, "hipMemsetAsync (flag)", e);
+    // the kernels that write out raise this word to the largest |value| they write (read back with
+    // the result)
+    x.out_max = ctx->out_max_word;
+    e = hipMemsetAsync(ctx->out_max_word, 0, sizeof(uint32_t), ctx->stream);
+    if (e != hipSuccess) return fail_hip(ctx, "hipMemsetAsync (result maximum)", e);
     Plan p;
     int rc = run(ctx, x, ctx->stage[0], ctx->stage[1], ctx->stage[2], s, one, ctx->stage[3], &p);
     if (rc != ZWG_OK) return rc;
-    uint32_t nonfinite = 0;
-    e = hipMemcpyAsync(&nonfinite, ctx->nonfinite_flag, sizeof nonfinite, hipMemcpyDeviceToHost, ctx->stream);
-    if (e != hipSuccess) return fail_hip(ctx, "hipMemcpyAsync (flag)", e);
+    uint32_t out_max = 0;
+    e = hipMemcpyAsync(&out_max, ctx->out_max_word, sizeof out_max, hipMemcpyDeviceToHost, ctx->stream);
+    if (e != hipSuccess) return fail_hip(ctx, "hipMemcpyAsync (result maximum)", e);
     // copy back only each row's n_head*d columns: out's other columns stay the caller's (waits for
-    // the stream, so the flag has arrived too)
+    // the stream, so the maximum has arrived too)
     rc = download_rows(ctx, out, ctx->stage[3], s.n_q, hd, s.out_stride);
     if (rc != ZWG_OK) return rc;
-    // The x3 dense kernel needs keys (and scaled queries) within f16 range; outside it the rows
-    // that see such a key come out NaN.  The reference gives finite results for any finite
-    // input (src/ops.zig:562-590), so a non-finite result of the x3 kernel is computed again on
-    // the fp32-MFMA kernel, which has no range condition (and reproduces any NaN or infinity the
-    // inputs themselves carry).
-    if (p.kernel == 1 && x.dense_math != ZWG_DENSE_FP32 && nonfinite) {
-        x.nonfinite = nullptr;
+    // The reference gives finite, f32-accurate results for any finite input (src/ops.zig:562-590).
+    // The x3 dense kernel meets that when its result is finite and not tiny; otherwise the call is
+    // computed again on the fp32-MFMA kernel (which reproduces any NaN or infinity the inputs
+    // themselves carry):
+    //  - keys (and scaled queries) beyond f16 range make the rows that see them NaN;
+    //  - the f16 split of V (and of P) has an absolute error floor near 2^-25 (the spacing of f16
+    //    subnormals, where the low terms of values below 2^-3 land): a result whose largest |value|
+    //    is below 2^-9 could miss the x3 bar (3e-5 normwise) relative to it.
+    constexpr uint32_t kX3SmallResult = 0x3b000000u; // 2^-9
+    const bool x3_off_range = out_max >= 0x7f800000u || out_max < kX3SmallResult;
+    if (p.kernel == 1 && x.dense_math != ZWG_DENSE_FP32 && x3_off_range) {
+        x.out_max = nullptr;
         x.dense_math = ZWG_DENSE_FP32;
         rc = run(ctx, x, ctx->stage[0], ctx->stage[1], ctx->stage[2], s, one, ctx->stage[3]);
         if (rc != ZWG_OK) return rc;
