@@ -49,12 +49,14 @@ typedef struct zwg_ctx zwg_ctx;
  * [n_head_kv][d][kt_stride] (keys along the last axis, as the LLM's cache, src/llm.zig:27).
  * causal: query i sees keys j <= n_kv - n_q + i (src/ops.zig:466), so n_kv >= n_q is required.
  *
- * Limits of this build (checked; ZWG_ERROR otherwise): d a multiple of 4 up to 128 (the
+ * Limits of this build (checked; ZWG_ERROR otherwise): d a multiple of 4 up to 1024 (the
  * reference takes any d % V == 0, V = 8 or 16); q_stride, kv_stride, out_stride and kt_stride
  * multiples of 4; q, k, v, out 16-byte aligned; n_q, n_kv and n_head below 2^30; n_head * n_batch
- * below 2^31.  The kernels are built for d = 32, 64 and 128; any other d runs on the kernels of
- * the next of them over zero-padded copies of q, k, v and out that the context keeps (one more
- * read and write of each tensor per call; same results up to f32 rounding).
+ * below 2^31.  The MFMA and split-K kernels are built for d = 32, 64 and 128; any other d up to
+ * 128 runs on the kernels of the next of them over zero-padded copies of q, k, v and out that the
+ * context keeps (one more read and write of each tensor per call; same results up to f32
+ * rounding); d above 128 runs on a plain f32 kernel, one wavefront per query row, unsplit (no
+ * model zwhisper runs has such a head dim: it keeps the drop-in whole, untuned).
  * Device buffers: with kt_stride, the last transposed row is read in 16-byte groups, so k must
  * hold (n_head_kv*d - 1)*kt_stride + round_up(n_kv, 4) floats -- no more than the reference
  * itself reads (round_up(n_kv, V) columns of every row, src/ops.zig:529-530).
@@ -126,7 +128,8 @@ typedef struct zwg_limits {
 
 /* How a call will run (zwg_plan): which kernel, how the keys are split. */
 typedef struct zwg_plan_info {
-    uint32_t kernel;        /* 1 = dense MFMA flash kernel, 2 = split-K streaming decode kernel */
+    uint32_t kernel;        /* 1 = dense MFMA flash kernel, 2 = split-K streaming decode kernel,
+                               3 = f32 kernel for head dims above 128 */
     uint32_t rows_per_unit; /* query rows one work unit covers (q-block, or heads x queries) */
     uint64_t chunk_len;     /* keys per split (a multiple of the kernel's key tile) */
     uint64_t max_chunks;    /* splits of the longest row; 1 = no combine pass */
@@ -197,7 +200,7 @@ int zwg_attention_batch_dev(zwg_ctx *ctx, const float *q, const float *k, const 
  * between calls (every partial a merge reads is written by the same call first).  All calls on
  * one GPU share that array: calls that overlap in time on one GPU (different streams, or threads)
  * race on it and give wrong results; calls on one stream run in order and are safe.  Head dims
- * other than 32, 64 and 128 need the padded copies of a context and are refused here.
+ * up to 128 other than 32, 64 and 128 need the padded copies of a context and are refused here.
  */
 #define ZWG_NOALLOC_SCRATCH_BYTES (64ull << 20)
 int zwg_attention_batch_noalloc(const float *q, const float *k, const float *v, const zwg_attn_shape *shape,

@@ -44,7 +44,7 @@ int main() {
         s.n_kv = big ? rng() % (1ull << 31) : pick({0, 1, 5, 17, 90, 255, 256, 257, 448, 1500, 2048, 4096, 32768});
         s.n_head_kv = pick({1, 2, 4, 8});
         s.n_head = s.n_head_kv * pick({1, 2, 6, 7});
-        s.d = pick({0, 4, 16, 32, 48, 64, 100, 128, 132});
+        s.d = pick({0, 4, 16, 32, 48, 64, 100, 128, 132, 256, 1024, 1028});
         s.causal = rng() % 2;
         const uint64_t hd = s.n_head * s.d, kvd = s.n_head_kv * s.d;
         s.q_stride = hd + 4 * (rng() % 3);
@@ -63,7 +63,13 @@ int main() {
         }
         ++accepted;
         const Plan p = make_plan(s, b, cap, mode);
-        CHECK(p.kernel == 1 || p.kernel == 2, "kernel %d", p.kernel);
+        CHECK(p.kernel == 1 || p.kernel == 2 || p.kernel == 3, "kernel %d", p.kernel);
+        if (p.kernel == 3) { // head dims above 128: one wavefront per row, unsplit
+            CHECK(s.d > 128 && p.max_chunks == 1 && p.ws_bytes == 0, "f32 kernel plan");
+            CHECK(p.grid_blocks == ceil_div(b.n_batch * s.n_head * s.n_q, 4), "f32 kernel grid");
+            continue;
+        }
+        CHECK(s.d <= 128, "head dims above 128 take the f32 kernel");
         CHECK(p.split_tile > 0 && p.chunk_len > 0 && p.chunk_len % p.split_tile == 0, "chunk_len %d tile %d", p.chunk_len,
               p.split_tile);
         CHECK(p.max_chunks >= 1 && (uint64_t)p.max_chunks <= kMaxChunks, "max_chunks %d", p.max_chunks);

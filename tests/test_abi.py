@@ -74,7 +74,7 @@ def S(n_q, n_kv, h, hkv, d, causal, kt=None, qs=None, kvs=None, os_=None):
     S(1500, 1500, 6, 6, 64, False, kt=1504), S(1, 448, 12, 12, 64, True), S(2048, 2048, 14, 2, 64, True, kt=2048),
     S(1, 4096, 12, 2, 128, True, kt=4096), S(20, 20, 12, 12, 32, False), S(0, 0, 1, 1, 64, False),
     S(3, 0, 2, 2, 64, False), S(2, 3, 2, 2, 48, False), S(2, 3, 2, 2, 16, False), S(5, 9, 4, 2, 4, True, kt=12),
-    S(7, 7, 2, 1, 100, False),
+    S(7, 7, 2, 1, 100, False), S(3, 5, 2, 1, 132, True), S(3, 5, 2, 2, 256, False), S(1, 9, 1, 1, 1024, False),
 ])
 def test_check_shape_accepts(sh):
     z.check_shape(sh)
@@ -82,7 +82,8 @@ def test_check_shape_accepts(sh):
 
 @pytest.mark.parametrize("sh,msg", [
     (S(2, 3, 2, 2, 50, False), "head dim"),
-    (S(2, 3, 2, 2, 132, False), "head dim"),
+    (S(2, 3, 2, 2, 1028, False), "head dim"),
+    (S(2, 3, 2, 2, 134, False), "head dim"),
     (S(2, 3, 2, 2, 0, False), "head dim"),
     (S(2, 3, 3, 2, 64, False), "multiple of n_head_kv"),
     (S(2, 3, 0, 1, 64, False), "multiple of n_head_kv"),
@@ -108,6 +109,15 @@ def test_reserved_field_must_be_zero():
 
 # ---------------------------------------------------------------------------------------------
 # planning (which kernel, how keys are split)
+
+
+def test_plan_picks_the_f32_kernel_above_128():
+    """Head dims above the built kernels' 128 run on the plain f32 kernel, one wavefront per query
+    row, unsplit, with no workspace."""
+    for sh, nb in ((S(1500, 1500, 2, 2, 256, False), 1), (S(1, 300, 8, 2, 192, True, kt=304), 4)):
+        p = z.plan(sh, nb)
+        assert p.kernel == 3 and p.max_chunks == 1 and p.workspace_bytes == 0
+        assert p.grid_blocks == -(-nb * sh.n_head * sh.n_q // 4)
 
 
 def test_plan_picks_decode_for_few_rows_per_kv_head():

@@ -8,7 +8,10 @@ the x3 bar (max abs 5e-5, normwise relative 3e-5) for dense calls of an x3 conte
 (2e-4, 1e-3) otherwise.  Covered: the dense kernel in both modes with row-major and transposed
 keys, causal GQA and non-causal; the decode kernels over row-major and transposed caches with
 per-item key counts; output columns outside each head's d left untouched; the allocation-free
-entry point's refusal of such d.
+entry point's refusal of such d.  Head dims above 128 (up to 1024) run on a plain f32 kernel
+(zwhisper_amd/csrc/attn_generic.hip) in either dense mode, held to the f32 bar: dense and decode
+shapes, row-major and transposed keys, per-item key counts, the host drop-in and the
+allocation-free entry point (which needs no padded copies for them).
 """
 from __future__ import annotations
 
@@ -150,3 +153,80 @@ def test_head_dim_noalloc_refused(torch):
     t = torch.zeros(4096, device="cuda")
     with pytest.raises(z.ZwgError, match="head dims other than 32, 64 and 128"):
         z.ops.attention_batch_noalloc(t, t, t, sh, t)
+
+
+BIG_DIMS = [132, 192, 256, 516, 1024]
+
+
+@pytest.mark.parametrize("d", BIG_DIMS)
+@pytest.mark.parametrize("kind", ["enc_rowmajor", "enc_kt", "prefill_gqa_kt", "decode_rowmajor", "decode_gqa_kt"])
+def test_head_dim_above_128(torch, d, kind):
+    import zwhisper_amd as z
+    from zwhisper_amd.ops import AttnShape
+
+    rng = np.random.default_rng(3000 + d)
+    n_q, n_kv, h, hk, causal, kt = {
+        "enc_rowmajor": (70, 130, 3, 3, False, False),
+        "enc_kt": (70, 130, 2, 2, False, True),
+        "prefill_gqa_kt": (90, 150, 6, 2, True, True),
+        "decode_rowmajor": (1, 333, 4, 4, True, False),
+        "decode_gqa_kt": (1, 400, 8, 2, True, True),
+    }[kind]
+    q, k, v, (qs, kvs, os_, kts) = make(rng, n_q, n_kv, h, hk, d, kt)
+    sh = AttnShape(n_q, n_kv, h, hk, d, qs, kvs, os_, causal, kts)
+    assert z.plan(sh).kernel == 3
+    with z.Context(0) as c:
+        out = torch.full((n_q * os_,), SENTINEL, dtype=torch.float32, device="cuda")
+        c.attention_dev(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(), sh, out)
+        torch.cuda.synchronize()
+    check(out.cpu().numpy(), q, k, v, sh, False, f"{kind} d={d}")
+
+
+@pytest.mark.parametrize("kt", [False, True])
+def test_head_dim_above_128_batch_per_item_lengths(torch, kt):
+    """A batch of decode steps with their own key counts (0 included) at d = 256."""
+    import zwhisper_amd as z
+    from zwhisper_amd.ops import AttnShape
+
+    d = 256
+    rng = np.random.default_rng(99)
+    n_items, cap, h, hk = 4, 300, 4, 2
+    lengths = np.array([1, 77, 300, 0], np.int32)
+    items = [make(rng, 1, cap, h, hk, d, kt) for _ in range(n_items)]
+    qs, kvs, os_, kts = items[0][3]
+    sh = AttnShape(1, cap, h, hk, d, qs, kvs, os_, True, kts)
+    q = np.stack([it[0] for it in items])
+    k = np.stack([it[1] for it in items])
+    v = np.stack([it[2] for it in items])
+    with z.Context(0) as c:
+        out = torch.full((n_items, os_), SENTINEL, dtype=torch.float32, device="cuda")
+        c.attention_batch_dev(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(), sh,
+                              out, n_items, q[0].size, k[0].size, v[0].size, os_, torch.from_numpy(lengths).cuda())
+        torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    for i, L in enumerate(lengths):
+        shi = AttnShape(1, int(L), h, hk, d, qs, kvs, os_, True, kts)
+        if L == 0:
+            assert np.all(got[i, : h * d] == 0.0) and np.all(got[i, h * d:] == np.float32(SENTINEL))
+            continue
+        check(got[i], q[i], k[i], v[i], shi, False, f"item {i} n_kv={L} d={d} kt={kt}")
+
+
+def test_head_dim_above_128_dropin_and_noalloc(torch):
+    """d = 192 through the host drop-in, and through the allocation-free entry point, which needs
+    no padded copies for head dims above 128."""
+    import zwhisper_amd as z
+    from zwhisper_amd.ops import AttnShape
+
+    rng = np.random.default_rng(7)
+    q, k, v, (qs, kvs, os_, kts) = make(rng, 50, 80, 4, 2, 192, False)
+    sh = AttnShape(50, 80, 4, 2, 192, qs, kvs, os_, True, kts)
+    out = np.full(50 * os_, SENTINEL, np.float32)
+    with z.Context(0) as c:
+        c.attention_ex_host(q, k, v, sh, out)
+    check(out, q, k, v, sh, False, "host drop-in d=192")
+    dev_out = torch.full((50 * os_,), SENTINEL, dtype=torch.float32, device="cuda")
+    z.ops.attention_batch_noalloc(torch.from_numpy(q).cuda(), torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda(),
+                                  sh, dev_out)
+    torch.cuda.synchronize()
+    assert np.array_equal(dev_out.cpu().numpy(), out), "the allocation-free entry point differs from the drop-in"

@@ -177,6 +177,9 @@ hipError_t launch_flash(const AttnArgs &a, int d, hipStream_t stream, int *grid_
 hipError_t launch_flash_x3(const AttnArgs &a, int d, hipStream_t stream, int *grid_blocks);
 hipError_t launch_decode(const AttnArgs &a, int d, int rows, hipStream_t stream, int *grid_blocks);
 hipError_t launch_combine(const AttnArgs &a, int d, hipStream_t stream);
+// head dims above 128 (attn_generic.hip): any d % 4 == 0 up to kGenericMaxD, f32 on the VALU
+constexpr int kGenericMaxD = 1024;
+hipError_t launch_generic(const AttnArgs &a, int d, hipStream_t stream);
 // head dims without kernels of their own (attn_pad.hip): zero-padded copies to the next built dim
 hipError_t launch_pad_rows(const float *src, float *dst, int n_batch, int rows, int segs, int d, int D, int64_t srs,
                            int64_t sbs, const int32_t *n_rows_item, hipStream_t stream);

@@ -52,15 +52,19 @@ constexpr uint64_t kMaxSplitUnitsHint = 1ull << 22;
 #define ZWG_FLASH32_CAUSAL_BLOCKS_PER_CU 6 // ... the same for the fp32 dense kernel (ZWG_DENSE_FP32)
 #endif
 
+// Largest head dim: the built kernels take 32, 64 and 128 (other dims up to 128 on zero-padded
+// copies); above 128 a plain f32 kernel (attn_generic.hip) takes any multiple of 4 up to this.
+constexpr int kMaxHeadDim = 1024;
+
 // Shape rules: the reference's asserts (src/ops.zig:564, :568; causal needs n_kv >= n_q,
 // src/ops.zig:534) plus this build's limits.
 inline std::string check_shape(const zwg_attn_shape &s) {
     const uint64_t lim = 1ull << 30; // keeps every key and row index, plus a tile, within int32
     char buf[256];
     if (s.reserved != 0) return "shape.reserved must be 0";
-    if (s.d == 0 || s.d % 4 != 0 || s.d > 128) {
-        snprintf(buf, sizeof buf, "head dim d=%llu unsupported (this build: multiples of 4 up to 128)",
-                 (unsigned long long)s.d);
+    if (s.d == 0 || s.d % 4 != 0 || s.d > (uint64_t)kMaxHeadDim) {
+        snprintf(buf, sizeof buf, "head dim d=%llu unsupported (this build: multiples of 4 up to %d)",
+                 (unsigned long long)s.d, kMaxHeadDim);
         return buf;
     }
     if (s.n_head == 0 || s.n_head_kv == 0 || s.n_head % s.n_head_kv != 0) {
@@ -93,10 +97,10 @@ inline std::string check_batch(const zwg_attn_shape &s, const zwg_batch &b) {
 
 // The head dim the kernels run at: d itself for the built dims 32, 64 and 128, else the next
 // of them, over zero-padded copies of the tensors (attn_pad.hip).
-inline uint64_t kernel_d(uint64_t d) { return d <= 32 ? 32 : d <= 64 ? 64 : 128; }
+inline uint64_t kernel_d(uint64_t d) { return d <= 32 ? 32 : d <= 64 ? 64 : d <= 128 ? 128 : d; }
 
 struct Plan {
-    int kernel = 0; // 1 flash, 2 decode
+    int kernel = 0; // 1 flash, 2 decode, 3 generic (head dims above 128)
     int rows_per_unit = 0;
     int split_tile = 0;
     int chunk_len = 0;
@@ -132,6 +136,16 @@ inline Plan make_plan(const zwg_attn_shape &s, const zwg_batch &b, uint64_t ws_c
     const uint64_t group = s.n_head / s.n_head_kv;
     const uint64_t n_rows_total = b.n_batch * s.n_head * s.n_q;
     uint64_t tile = 0, tau = 1, w_max = 1, units = 0;
+    if (s.d > 128) {
+        // one wavefront per query row, no key split (attn_generic.hip)
+        p.kernel = 3;
+        p.rows_per_unit = 1;
+        p.split_tile = 64;
+        p.chunk_len = 64;
+        p.max_chunks = 1;
+        p.grid_blocks = ceil_div(n_rows_total, 4);
+        return p;
+    }
     if (s.n_q * group <= (uint64_t)zwg::kDecodeMaxRows) {
         p.kernel = 2;
         p.rows_per_unit = (int)s.n_q;

@@ -192,6 +192,8 @@ int run_kernels(zwg_ctx *ctx, const Exec &x, const float *q, const float *k, con
     if (p.kernel == 1)
         e = x.dense_math == ZWG_DENSE_FP32 ? zwg::launch_flash(a, (int)s.d, x.stream, &blocks)
                                             : zwg::launch_flash_x3(a, (int)s.d, x.stream, &blocks);
+    else if (p.kernel == 3)
+        e = zwg::launch_generic(a, (int)s.d, x.stream);
     else
         e = zwg::launch_decode(a, (int)s.d, (int)(s.n_q * a.group), x.stream, &blocks);
     if (e != hipSuccess) return fail_hip(ctx, "attention kernel launch", e);
@@ -217,7 +219,7 @@ int run(zwg_ctx *ctx, const Exec &x, const float *q, const float *k, const float
     // f32(1/sqrt(d)) as the reference computes it (src/ops.zig:531), of the caller's d
     const float scale = 1.0f / std::sqrt((float)s.d);
     const uint64_t D = kernel_d(s.d);
-    if (D == s.d) return run_kernels(ctx, x, q, k, v, s, b, out, plan_out, scale);
+    if (D == s.d) return run_kernels(ctx, x, q, k, v, s, b, out, plan_out, scale); // built dims, and above 128
     if (!ctx)
         return fail(nullptr, "head dims other than 32, 64 and 128 run over zero-padded copies, which need a context "
                              "(zwg_attention_batch_dev)");
