@@ -327,3 +327,30 @@ def test_split_calls_in_graph_replays(torch, ctx):
                 assert np.array_equal(captured[j].cpu().numpy(), eager[j]), f"replay {rep}, call {j}"
             step(other768, other3072)  # eager calls between replays
             torch.cuda.synchronize()
+
+
+# Unsplit calls of 128-255 workgroups (resident weights): each workgroup's waves form two groups,
+# each over half of the stages of 128 k, summed through LDS.  Shapes: the Qwen2.5-1.5B MLP gate
+# (m = 64 and 33, two m-tiles), a 32-row call (one m-tile, x split in the stream kernel), and k
+# whose stage count is odd or leaves the second group one stage (k = 416: 4 stages, the last
+# partial; k = 384: 3 stages; k = 288: 3 stages, the last a quarter).
+TWO_GROUP_CASES = [(64, 1536, 17920), (33, 416, 16400), (32, 384, 9000), (17, 8960, 9000), (1, 288, 12000)]
+
+
+@pytest.mark.parametrize("m,k,n", TWO_GROUP_CASES)
+def test_two_stage_groups(torch, ctx, m, k, n):
+    x, w, b = inputs(m * 5 + n + k, m, k, n)
+    xd, bd = torch.from_numpy(x).cuda(), torch.from_numpy(b).cuda()
+    ref = ref64(x, w, b)
+    with w.resident(ctx) as rw:
+        outs = []
+        for _ in range(2):
+            out = torch.full((m, n), float("nan"), device="cuda")
+            ctx.linear_q8w_dev(xd, m, rw, bd, out)
+            torch.cuda.synchronize()
+            outs.append(out.cpu().numpy())
+    err = float(np.abs(outs[0] - ref).max())
+    bar = 2e-5 * np.sqrt(k)
+    print(f"two stage groups q8 {m}x{k}x{n}: max abs {err:.2e} (bar {bar:.1e})", flush=True)
+    assert np.all(np.isfinite(outs[0])) and err <= bar
+    assert np.array_equal(outs[0], outs[1])

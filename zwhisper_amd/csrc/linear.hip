@@ -207,6 +207,11 @@ constexpr int q8p_waves() { return MT == 1 ? ZWG_Q8P_WAVES_32 : ZWG_Q8P_WAVES; }
 #ifndef ZWG_Q8P_SPLIT_TARGET
 #define ZWG_Q8P_SPLIT_TARGET 512
 #endif
+// unsplit calls of fewer workgroups than this run two stage groups per workgroup (each over half
+// of k, summed through LDS at the end)
+#ifndef ZWG_Q8P_KS_BELOW
+#define ZWG_Q8P_KS_BELOW 256
+#endif
 
 
 template <int MT>
@@ -259,8 +264,15 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g)
         if (e != hipSuccess) return fail_hip(ctx, "linear (int8) x preparation launch", e);
     }
     dim3 grid((unsigned)gx, (unsigned)n_split);
-    if (XS) zwg_lin::linear_q8p_stream_kernel<MT, 1, kQ8pWaves, true><<<grid, 64 * kQ8pWaves, 0, ctx->stream>>>(a, g, xcvt);
-    else zwg_lin::linear_q8p_stream_kernel<MT, 1, kQ8pWaves, false><<<grid, 64 * kQ8pWaves, 0, ctx->stream>>>(a, g, xcvt);
+    // unsplit calls of too few workgroups to fill the chip: two stage groups per workgroup
+    const bool two_groups = n_split == 1 && gx < ZWG_Q8P_KS_BELOW && n_chunks > 1;
+    if (two_groups) {
+        if (XS) zwg_lin::linear_q8p_stream_kernel<MT, 1, kQ8pWaves, true, 2><<<grid, 128 * kQ8pWaves, 0, ctx->stream>>>(a, g, xcvt);
+        else zwg_lin::linear_q8p_stream_kernel<MT, 1, kQ8pWaves, false, 2><<<grid, 128 * kQ8pWaves, 0, ctx->stream>>>(a, g, xcvt);
+    } else {
+        if (XS) zwg_lin::linear_q8p_stream_kernel<MT, 1, kQ8pWaves, true><<<grid, 64 * kQ8pWaves, 0, ctx->stream>>>(a, g, xcvt);
+        else zwg_lin::linear_q8p_stream_kernel<MT, 1, kQ8pWaves, false><<<grid, 64 * kQ8pWaves, 0, ctx->stream>>>(a, g, xcvt);
+    }
     e = hipGetLastError();
     if (e != hipSuccess) return fail_hip(ctx, "linear (int8 stream) kernel launch", e);
     if (n_split > 1) {

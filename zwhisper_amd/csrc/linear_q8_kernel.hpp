@@ -341,11 +341,19 @@ __global__ __launch_bounds__(256) void linear_q8_pack_kernel(const int8_t *q, co
 constexpr int kQ8StageBlocks = 4;
 constexpr int kQ8StageK = kQ8StageBlocks * kQ8Block;
 
-template <int MT, int S, int NW, bool XS>
-__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
+// KS = 2: the workgroup's waves form two groups of NW, each over the same slabs and half of the
+// workgroup's stages (contiguous, each half a whole number of 2-stage turns), with x buffers of
+// their own; at the end the second group adds its sums into the first's through LDS (in that
+// order, so the result is the two halves' sums added once, as a 2-way k split would add them) and
+// the first stores.  For calls whose weight rows give too few workgroups for the chip and are not
+// split: each wave then walks half the stages, and two waves share each SIMD, with no partial
+// sums in memory and no second launch.
+template <int MT, int S, int NW, bool XS, int KS = 1>
+__global__ __launch_bounds__(64 * NW * KS) __attribute__((amdgpu_waves_per_eu(2)))
 void linear_q8p_stream_kernel(Q8Args a, Q8Group grp, const _Float16 *xcvt) {
+    static_assert(KS == 1 || KS == 2, "one or two stage groups");
     constexpr int NB = kQ8StageBlocks;
-    constexpr int NT = 64 * NW;
+    constexpr int NT = 64 * NW;                   // threads of one stage group
     constexpr int SLABS = NW * S;                 // slabs of 32 weight rows per workgroup (NW waves)
     constexpr int PIECES = NB * MT * 4;           // 1 KB pieces of an x stage
     constexpr int XL = PIECES / NW;               // pieces each wave copies (XS = false)
@@ -353,7 +361,7 @@ void linear_q8p_stream_kernel(Q8Args a, Q8Group grp, const _Float16 *xcvt) {
     constexpr int STAGE_HALVES = PIECES * 512;
     constexpr int XQ = XS ? MT * 32 * kQ8StageK / 4 / NT : 1; // 16-byte x loads per thread (XS = true)
     static_assert(!XS || XQ * 4 * NT == MT * 32 * kQ8StageK, "every thread loads whole quads of the x stage");
-    __shared__ __align__(16) _Float16 xs[2][STAGE_HALVES];
+    __shared__ __align__(16) _Float16 xs_all[KS][2][STAGE_HALVES];
 
     // this workgroup's weight set and its index within the set
     const int set = q8_group_of_block(grp, (int)blockIdx.x);
@@ -364,14 +372,24 @@ void linear_q8p_stream_kernel(Q8Args a, Q8Group grp, const _Float16 *xcvt) {
     a.out = q8_pick(grp.out, set);
     a.part = q8_pick(grp.part, set);
 
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // uniform: the LDS DMA base is per wave
+    const int lane = threadIdx.x & 63;
+    const int wave_all = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6); // uniform: the LDS DMA base is per wave
+    const int kg = wave_all / NW;            // stage group
+    const int wave = wave_all - kg * NW;     // wave within the group: its slabs
+    const int tid = (int)threadIdx.x - kg * NT; // thread within the group
+    _Float16(&xs)[2][STAGE_HALVES] = xs_all[kg];
     const int r32 = lane & 31, g = lane >> 5;
     const int slab0 = bx * SLABS + wave * S; // this wave's first slab
     const int split = blockIdx.y;
     const int n_stages = (a.k + NB * kQ8Block - 1) / (NB * kQ8Block);
-    const int t_begin = split * a.chunks_per_split * 2;
-    const int t_end = min(t_begin + a.chunks_per_split * 2, n_stages);
+    const int w_begin = split * a.chunks_per_split * 2;
+    const int w_end = min(w_begin + a.chunks_per_split * 2, n_stages);
+    // this group's stages (whole 2-stage turns for the first group, so both groups run as many
+    // turns and meet the same barriers)
+    const int half = KS == 1 ? w_end - w_begin : ((w_end - w_begin + 3) / 4) * 2;
+    const int t_begin = min(w_begin + kg * half, w_end);
+    const int t_end = KS == 1 ? w_end : min(t_begin + half, w_end);
+    const int turns = (half + 1) / 2; // 2-stage loop turns, the same in every group
 
     // XS: x [m][k] f32, rows past m read as 0 (range), columns past k get an out-of-range offset;
     // otherwise the call's split x chunks
@@ -497,7 +515,7 @@ void linear_q8p_stream_kernel(Q8Args a, Q8Group grp, const _Float16 *xcvt) {
     f32x4 scA[S], scB[S];
     constexpr int LOADS = S * (NB + 1); // weight and scale loads of one stage, issued after its x
     issue(t_begin, 0, xr, wqA, scA);
-    for (int t = t_begin; t < t_end; t += 2) {
+    for (int turn = 0, t = t_begin; turn < turns; ++turn, t += 2) {
         // stage t (set A, buffer 0)
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(q8_vmcnt(LOADS));
@@ -506,7 +524,7 @@ void linear_q8p_stream_kernel(Q8Args a, Q8Group grp, const _Float16 *xcvt) {
         __builtin_amdgcn_sched_barrier(0);
         issue(t + 1, 1, xr, wqB, scB);
         __builtin_amdgcn_sched_barrier(0);
-        compute(0, wqA, scA);
+        if (KS == 1 || t < t_end) compute(0, wqA, scA); // the second group's may be empty
         // stage t + 1 (set B, buffer 1); a no-op past the end (its loads returned zeros)
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(q8_vmcnt(LOADS));
@@ -518,6 +536,29 @@ void linear_q8p_stream_kernel(Q8Args a, Q8Group grp, const _Float16 *xcvt) {
         if (t + 1 < t_end) compute(1, wqB, scB);
     }
     __builtin_amdgcn_s_waitcnt(q8_vmcnt(0)); // the last, out-of-range prefetch
+    if constexpr (KS == 2) {
+        // the second group's sums into the first's, through the (now free) x buffers: lane-major
+        // per (wave, m-tile, slab, register), conflict-free
+        float *red = reinterpret_cast<float *>(&xs_all[0][0][0]);
+        static_assert(NW * MT * S * 16 * 64 * 4 <= (int)sizeof(xs_all), "the sums fit in the x buffers");
+        __syncthreads(); // every wave is past its last compute
+        if (kg == 1) {
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int s = 0; s < S; ++s)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) red[(((wave * MT + i) * S + s) * 16 + r) * 64 + lane] = acc[i][s][r];
+        }
+        __syncthreads();
+        if (kg == 1) return;
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int s = 0; s < S; ++s)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][s][r] += red[(((wave * MT + i) * S + s) * 16 + r) * 64 + lane];
+    }
 
     float *dst = a.n_split > 1 ? a.part + (int64_t)split * a.m * a.n : a.out;
 #pragma unroll
