@@ -374,9 +374,9 @@ void linear_q8p_stream_kernel(Q8Args a, Q8Group grp, const _Float16 *xcvt) {
 
     const int lane = threadIdx.x & 63;
     const int wave_all = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6); // uniform: the LDS DMA base is per wave
-    const int kg = wave_all / NW;            // stage group
-    const int wave = wave_all - kg * NW;     // wave within the group: its slabs
-    const int tid = (int)threadIdx.x - kg * NT; // thread within the group
+    const int kg = KS == 1 ? 0 : wave_all / NW;                    // stage group
+    const int wave = KS == 1 ? wave_all : wave_all - kg * NW;      // wave within the group: its slabs
+    const int tid = KS == 1 ? (int)threadIdx.x : (int)threadIdx.x - kg * NT; // thread within the group
     _Float16(&xs)[2][STAGE_HALVES] = xs_all[kg];
     const int r32 = lane & 31, g = lane >> 5;
     const int slab0 = bx * SLABS + wave * S; // this wave's first slab
@@ -515,7 +515,7 @@ void linear_q8p_stream_kernel(Q8Args a, Q8Group grp, const _Float16 *xcvt) {
     f32x4 scA[S], scB[S];
     constexpr int LOADS = S * (NB + 1); // weight and scale loads of one stage, issued after its x
     issue(t_begin, 0, xr, wqA, scA);
-    for (int turn = 0, t = t_begin; turn < turns; ++turn, t += 2) {
+    for (int turn = 0, t = t_begin; KS == 1 ? t < t_end : turn < turns; ++turn, t += 2) {
         // stage t (set A, buffer 0)
         __builtin_amdgcn_sched_barrier(0);
         __builtin_amdgcn_s_waitcnt(q8_vmcnt(LOADS));
