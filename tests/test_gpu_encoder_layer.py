@@ -186,3 +186,57 @@ def test_encoder_layer(torch, ctx, ora, n_windows, n_ctx, ns, n_head):
         err = float(np.max(np.abs(got[win] - ref)))
         print(f"encoder layer {n_ctx}x{ns} window {win}: max abs {err:.2e}", flush=True)
         assert np.all(np.isfinite(got[win])) and err <= 2e-4
+
+
+def composed_layer(torch, ctx, xd, n_windows, n_ctx, ns, n_head, wd):
+    """The layer from the library's public calls with q | k | v as f32 rows (the path without tile
+    images): layer norm, the three projections into one [rows][3 ns] buffer, batched attention
+    through its strides, then the o-projection and MLP with their fused epilogues."""
+    from zwhisper_amd import _lib
+    from zwhisper_amd.ops import AttnShape
+
+    rows = n_windows * n_ctx
+    a = torch.empty((rows, ns), device="cuda")
+    b = torch.empty((rows, 3 * ns), device="cuda")
+    ctx.layer_norm_dev(xd, rows, ns, wd["attn_ln_w"], wd["attn_ln_b"], 1e-5, a)
+    flat = b.view(-1)
+    ctx.linear_epi_dev(a, rows, ns, wd["q_w"], wd["q_b"], ns, flat, _lib.EPI_NONE, out_stride=3 * ns)
+    ctx.linear_epi_dev(a, rows, ns, wd["k_w"], None, ns, flat[ns:], _lib.EPI_NONE, out_stride=3 * ns)
+    ctx.linear_epi_dev(a, rows, ns, wd["v_w"], wd["v_b"], ns, flat[2 * ns:], _lib.EPI_NONE, out_stride=3 * ns)
+    sh = AttnShape(n_ctx, n_ctx, n_head, n_head, ns // n_head, 3 * ns, 3 * ns, ns, False)
+    ctx.attention_batch_dev(flat, flat[ns:], flat[2 * ns:], sh, a, n_windows, n_ctx * 3 * ns, n_ctx * 3 * ns,
+                            n_ctx * 3 * ns, n_ctx * ns)
+    ctx.linear_epi_dev(a, rows, ns, wd["o_w"], wd["o_b"], ns, xd, _lib.EPI_ADD)
+    ctx.layer_norm_dev(xd, rows, ns, wd["mlp_ln_w"], wd["mlp_ln_b"], 1e-5, a)
+    h = torch.empty((rows, 4 * ns), device="cuda")
+    ctx.linear_epi_dev(a, rows, ns, wd["mlp0_w"], wd["mlp0_b"], 4 * ns, h, _lib.EPI_GELU)
+    ctx.linear_epi_dev(h, rows, 4 * ns, wd["mlp1_w"], wd["mlp1_b"], ns, xd, _lib.EPI_ADD)
+
+
+# (windows, frames, n_state, heads): base.en and tiny.en windows (1500 frames: the last 32-key tile
+# holds 28 keys), head dim 128 with a last tile of 4 keys, whole tiles only, and 70 frames (not a
+# multiple of 4: no images, the f32 path)
+IMAGE_SHAPES = [(2, 1500, 512, 8), (1, 1500, 384, 6), (2, 68, 256, 2), (3, 64, 128, 2), (2, 70, 128, 2)]
+
+
+@pytest.mark.parametrize("n_windows,n_ctx,ns,n_head", IMAGE_SHAPES)
+def test_encoder_layer_images_match_f32_rows(torch, ctx, n_windows, n_ctx, ns, n_head):
+    """In the x3 mode the layer's K and V projections write tile images that attention copies into
+    LDS as they are; the f16 terms are the ones attention would form from f32 rows, so the layer
+    equals the composed f32-row layer bit for bit (the scratch is filled with NaN first, so an
+    unwritten padding key would show)."""
+    import zwhisper_amd as z
+
+    rng = np.random.default_rng(ns + n_ctx)
+    wd = {kk: dev(torch, v) for kk, v in layer_weights(rng, ns).items()}
+    x = rng.standard_normal((n_windows, n_ctx, ns)).astype(np.float32)
+    got = dev(torch, x)
+    scratch = torch.full((z.ops.encoder_layer_scratch(n_windows * n_ctx, ns),), float("nan"), device="cuda")
+    ctx.encoder_layer_dev(got, n_windows, n_ctx, ns, n_head, wd, scratch)
+    ref = dev(torch, x)
+    composed_layer(torch, ctx, ref, n_windows, n_ctx, ns, n_head, wd)
+    torch.cuda.synchronize()
+    print(f"encoder layer images {n_windows}x{n_ctx}x{ns}/{n_head}: max abs diff "
+          f"{float((got - ref).abs().max()):.2e}", flush=True)
+    assert bool(torch.isfinite(got).all())
+    assert torch.equal(got, ref)

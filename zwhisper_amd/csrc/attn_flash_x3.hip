@@ -32,6 +32,7 @@
 #include <type_traits>
 
 #include "attn_kernels.hpp"
+#include "kv_image.hpp"
 
 namespace zwg {
 
@@ -91,26 +92,27 @@ __device__ __forceinline__ void split4(const f32x4 &x, f16x4 &hi, f16x4 &lo) {
     lo = __builtin_bit_cast(f16x4, l);
 }
 
-// K tile element (key, dim): rows of D f16, 16-byte chunk c stored at c ^ (key / (128 / D))
-// mod (D / 8): the rows sharing LDS banks within a 16-lane read phase land in different chunks.
+// LDS tile layouts (kv_image.hpp): K [key][dim] and V^T [dim][key position], XOR-swizzled
 template <int D>
-__device__ __forceinline__ int k_at(int key, int dim) {
-    constexpr int C = D / 8, R = 128 / D > 0 ? 128 / D : 1;
-    return key * D + ((((dim >> 3) ^ ((key / R) & (C - 1))) << 3) | (dim & 7));
-}
-// V^T tile position of a key: bits 2 and 3 swapped (keys 4..7 <-> 8..11 of every 16)
-__device__ __forceinline__ int v_pos(int key) { return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1); }
-// V^T tile element (dim, pos): rows of 32 f16 (64 bytes, 4 chunks), chunk c at c ^ ((dim >> 2) & 3)
-__device__ __forceinline__ int v_at(int dim, int pos) {
-    return dim * kFlashBN + ((((pos >> 3) ^ ((dim >> 2) & 3)) << 3) | (pos & 7));
-}
+__device__ __forceinline__ int k_at(int key, int dim) { return zwg_img::k_at<D>(key, dim); }
+__device__ __forceinline__ int v_pos(int key) { return zwg_img::v_pos(key); }
+__device__ __forceinline__ int v_at(int dim, int pos) { return zwg_img::v_at(dim, pos); }
+
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt in bits 3:0 and 15:14,
+// expcnt 6:4 and lgkmcnt 11:8 left at their maxima)
+constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
 } // namespace
 
-// d = 128 needs just over 256 VGPRs unconstrained; capping it there keeps two waves per SIMD
-template <int D, bool KT>
+// d = 128 needs just over 256 VGPRs unconstrained; capping it there keeps two waves per SIMD.
+// PL: K and V come as tile images (kv_image.hpp: a.k_img, a.v_img), copied into LDS by the
+// buffer loads' LDS mode with no registers and no split; a.k and a.v are not read.
+// (PL at d = 64 needs 145 VGPRs, three waves per SIMD; capped at 128 for a fourth it spills and
+// measured no faster.)
+template <int D, bool KT, bool PL = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 ? 2 : 1)))
 void flash_x3_kernel(AttnArgs a) {
+    static_assert(!PL || (!KT && D >= 64), "tile images: row-major K, whole 4 KB planes");
     constexpr int BM = kFlashBM;
     constexpr int BN = kFlashBN;
     constexpr int NKS = D / 16;  // k-steps of the QK product
@@ -198,6 +200,31 @@ void flash_x3_kernel(AttnArgs a) {
     const uint32_t k_base = KT ? (uint32_t)k_dim(0) * kt_row_b + 4u * (uint32_t)k_key
                                : (uint32_t)(tid / (D / 4)) * row_b + 16u * (uint32_t)(tid % (D / 4));
     const uint32_t v_base = (uint32_t)v_key(0) * row_b + 4u * (uint32_t)v_dim;
+    // PL: this (item, KV head)'s images; wave w copies bytes [1024 w, 1024 w + 1024) of every 4 KB
+    // piece of a tile's planes, lane l 16 of them
+    constexpr int PIECES = 32 * D * 2 / 4096; // 4 KB pieces of one plane
+    constexpr int IMG_LOADS = 2 * PIECES;     // copies per wave per tile of K (or of V)
+    const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+    const int64_t img_ih = (int64_t)item * a.n_head_kv + hk;
+    const uint32_t img_bytes = PL ? (uint32_t)a.img_tiles * (uint32_t)zwg_img::block_halves(D) * 2u : 0u;
+    const __amdgpu_buffer_rsrc_t kimg = __builtin_amdgcn_make_buffer_rsrc(
+        PL ? const_cast<_Float16 *>(a.k_img + zwg_img::block_offset(img_ih, a.img_tiles, 0, D)) : nullptr, 0,
+        (int)img_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t vimg = __builtin_amdgcn_make_buffer_rsrc(
+        PL ? const_cast<_Float16 *>(a.v_img + zwg_img::block_offset(img_ih, a.img_tiles, 0, D)) : nullptr, 0,
+        (int)img_bytes, 0x00020000);
+    auto copy_tile = [&](__amdgpu_buffer_rsrc_t src, int k0, _Float16 *hi_dst, _Float16 *lo_dst) {
+        const uint32_t t_off = (uint32_t)(k0 / BN) * (uint32_t)zwg_img::block_halves(D) * 2u;
+#pragma unroll
+        for (int pl = 0; pl < 2; ++pl)
+#pragma unroll
+            for (int c = 0; c < PIECES; ++c) {
+                const int in_plane = c * 4096 + wave_u * 1024; // bytes
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    src, (__attribute__((address_space(3))) void *)((pl ? lo_dst : hi_dst) + in_plane / 2), 16,
+                    (int)(t_off + (uint32_t)(pl * 32 * D * 2 + in_plane) + 16u * (uint32_t)lane), 0, 0, 0);
+            }
+    };
     auto load_k = [&](int k0) {
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
@@ -348,7 +375,13 @@ void flash_x3_kernel(AttnArgs a) {
 
     const int n_tiles = k_end > k_begin ? (k_end - k_begin + BN - 1) / BN : 0;
     f32x16 s_cur = (f32x16){0};
-    if (n_tiles > 0) {
+    if constexpr (PL) {
+        if (n_tiles > 0) {
+            copy_tile(vimg, k_begin, Vh[0], Vl[0]);
+            copy_tile(kimg, k_begin, Kh[0], Kl[0]);
+        }
+        if (n_tiles > 1) copy_tile(kimg, k_begin + BN, Kh[1], Kl[1]);
+    } else if (n_tiles > 0) {
         load_k(k_begin);
         load_v(k_begin);
     }
@@ -377,15 +410,17 @@ void flash_x3_kernel(AttnArgs a) {
             split8(qv, qh[j], ql[j]);
         }
     }
-    if (n_tiles > 0) {
+    if constexpr (PL) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    } else if (n_tiles > 0) {
         store_k(0);
         store_v(0);
         if (n_tiles > 1) load_k(k_begin + BN);
     }
     __syncthreads();
     if (n_tiles > 0 && wave_needs(k_begin)) s_cur = qk(0);
-    if (n_tiles > 1) store_k(1);
-    __syncthreads();
+    if (!PL && n_tiles > 1) store_k(1);
+    __syncthreads(); // PL: every wave is done with tile 0's K before tile 2 is copied over it
 
     // one tile: t's buffer parity is a compile-time constant (the loop runs two tiles per turn),
     // so LDS addresses are immediate offsets and the score registers alternate between sa and sb
@@ -393,8 +428,15 @@ void flash_x3_kernel(AttnArgs a) {
     auto step = [&](auto parity, int t, f32x16 &s_cur, f32x16 &s_next) {
         constexpr int cur = decltype(parity)::value, nxt = cur ^ 1;
         const int k0 = k_begin + t * BN;
-        if (t + 2 < n_tiles) load_k(k0 + 2 * BN);
-        if (t + 1 < n_tiles) load_v(k0 + BN);
+        if constexpr (PL) {
+            // V of tile t + 1 over tile t - 1's (read by the last step's P.V), K of tile t + 2
+            // over tile t's (read by the last step's scores)
+            if (t + 1 < n_tiles) copy_tile(vimg, k0 + BN, Vh[nxt], Vl[nxt]);
+            if (t + 2 < n_tiles) copy_tile(kimg, k0 + 2 * BN, Kh[cur], Kl[cur]);
+        } else {
+            if (t + 2 < n_tiles) load_k(k0 + 2 * BN);
+            if (t + 1 < n_tiles) load_v(k0 + BN);
+        }
         const bool need_cur = wave_needs(k0);
         const bool need_next = t + 1 < n_tiles && wave_needs(k0 + BN);
         if (need_cur) mask_and_max(s_cur, k0);
@@ -406,8 +448,14 @@ void flash_x3_kernel(AttnArgs a) {
             s_next = qk(nxt);
         }
         if (need_cur) pv(s_cur, cur);
-        if (t + 2 < n_tiles) store_k(cur);
-        if (t + 1 < n_tiles) store_v(nxt);
+        if constexpr (PL) {
+            // tile t + 1's K (copied a step ago) and V in LDS; tile t + 2's K may still be on its way
+            if (t + 2 < n_tiles) __builtin_amdgcn_s_waitcnt(vmcnt_only(IMG_LOADS));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+        } else {
+            if (t + 2 < n_tiles) store_k(cur);
+            if (t + 1 < n_tiles) store_v(nxt);
+        }
         __syncthreads();
     };
     using P0 = std::integral_constant<int, 0>;
@@ -456,6 +504,17 @@ void flash_x3_kernel(AttnArgs a) {
 }
 
 hipError_t launch_flash_x3(const AttnArgs &a, int d, hipStream_t stream, int *grid_blocks) {
+    if (a.k_img) { // tile images: row-major, d 64 or 128
+        const int n_qblocks = (a.n_q + kFlashBM - 1) / kFlashBM;
+        const int64_t blocks =
+            a.heavy_first == 2 ? a.live_blocks : (int64_t)a.max_chunks * n_qblocks * a.n_batch * a.n_head;
+        if (blocks > 0x7fffffffll || a.kt_stride || !a.v_img) return hipErrorInvalidValue;
+        if (grid_blocks) *grid_blocks = (int)blocks;
+        if (d == 64) flash_x3_kernel<64, false, true><<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(a);
+        else if (d == 128) flash_x3_kernel<128, false, true><<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(a);
+        else return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
     const int n_qblocks = (a.n_q + kFlashBM - 1) / kFlashBM;
     const int64_t blocks = a.heavy_first == 2 ? a.live_blocks : (int64_t)a.max_chunks * n_qblocks * a.n_batch * a.n_head;
     if (blocks > 0x7fffffffll) return hipErrorInvalidValue;

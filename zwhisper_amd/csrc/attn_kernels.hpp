@@ -37,6 +37,11 @@ struct AttnArgs {
     // this word to the largest |value| they write, as its f32 bit pattern (out_max_record): an
     // infinity or a NaN gives a pattern of 0x7f800000 or more
     uint32_t *out_max;
+    // the dense x3 kernel only: K and V as tile images (kv_image.hpp) of img_tiles 32-key tiles per
+    // (item, KV head), in place of k and v; null otherwise
+    const _Float16 *k_img;
+    const _Float16 *v_img;
+    int32_t img_tiles;
 };
 
 // |x| as its bit pattern: for non-negative floats the unsigned order is the float order, and

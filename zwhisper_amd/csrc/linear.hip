@@ -337,6 +337,48 @@ int run_linear(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void 
     return w_type == ZWG_W_Q8 ? run_tiled<zwg_lin::kWQ8>(ctx, a) : run_tiled<zwg_lin::kWF16>(ctx, a);
 }
 
+} // namespace
+
+int zwg_host::linear_f16_image(zwg_ctx *ctx, const float *x, uint64_t rows, uint64_t k, const void *w,
+                               const float *bias, uint64_t n, void *img, int kind, uint64_t n_ctx, uint64_t d) {
+    const std::string msg = check_linear(rows, k, ZWG_W_F16, n);
+    if (!msg.empty()) return fail(ctx, msg);
+    if (kind != 1 && kind != 2) return fail(ctx, "image kind must be 1 (K) or 2 (V)");
+    if ((d != 64 && d != 128) || n % d || n_ctx == 0 || n_ctx % 4 || rows % n_ctx)
+        return fail(ctx, "tile images need head dim 64 or 128, n a multiple of it and whole items of n_ctx % 4 == 0 keys");
+    if (rows == 0) return ZWG_OK;
+    const uint64_t tiles_per = (n_ctx + 31) / 32;
+    if ((rows / n_ctx) * (n / d) * tiles_per * 64 * d > 0x7fffffffffffull) return fail(ctx, "images too large");
+    const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (!x || !w || !img) return fail(ctx, "null x, w or image");
+    if (!al16(x) || !al16(w) || !al16(img)) return fail(ctx, "x, w and the image must be 16-byte aligned");
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
+    LinearArgs a{};
+    a.x = x;
+    a.w = w;
+    a.bias = bias;
+    a.ldx = (int64_t)k;
+    a.ldw = (int64_t)k;
+    a.m = (int32_t)rows;
+    a.n = (int32_t)n;
+    a.k = (int32_t)k;
+    a.nb = (int32_t)(k / 32);
+    a.img = static_cast<_Float16 *>(img);
+    a.img_kind = kind;
+    a.img_ctx = (int32_t)n_ctx;
+    a.img_d = (int32_t)d;
+    a.img_heads = (int32_t)(n / d);
+    a.img_tiles = (int32_t)tiles_per;
+    a.k_split = (int32_t)k; // never split: the image epilogue is the unsplit kernel's
+    const TileChoice tc = choose_tile<zwg_lin::kWF16>(rows, n);
+    e = launch_tiled<zwg_lin::kWF16>(a, tc, 1, ctx->stream);
+    if (e != hipSuccess) return fail_hip(ctx, "linear (image) kernel launch", e);
+    return ZWG_OK;
+}
+
+namespace {
+
 // Host-pointer form: stages x (slot 0), the weights (slot 1), the scales and bias (slot 2) and
 // out (slot 3) through the context, then waits.
 int run_linear_host(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void *w, uint32_t w_type,

@@ -39,6 +39,7 @@
 #include <stdint.h>
 
 #include "elementwise.hpp"
+#include "kv_image.hpp"
 
 namespace zwg_lin {
 
@@ -70,6 +71,11 @@ struct LinearArgs {
     // part[s][m][n]; a second kernel adds the splits in order, then bias and epilogue
     int32_t k_split;
     float *part;
+    // img_kind 1 (K) or 2 (V): the outputs go to `img` as tile images (kv_image.hpp) instead of to
+    // out -- rows are (item, key) with img_ctx keys per item (a multiple of 4), columns (head, dim)
+    // with img_d dims per head, img_tiles tiles per (item, head); no k split, no epilogue
+    _Float16 *img;
+    int32_t img_kind, img_ctx, img_d, img_heads, img_tiles;
 };
 
 // Eight int8 (two dwords) to eight exact f16: the biased byte b + 128 is placed under the
@@ -311,6 +317,29 @@ __global__ __launch_bounds__(128 * NWN) void linear_mfma_kernel(LinearArgs a) {
     compute((n_k - 1) & 1);
 
     // epilogue: register r of lane l is out[8 (r / 4) + 4 (l / 32) + r % 4][l % 32] of its tile
+    if constexpr (!KSPLIT && !Q8) {
+        if (a.img_kind) { // registers 4g .. 4g + 3: four consecutive rows (keys) of one column
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+                const int col = n0 + wn * WN + j * 32 + r32;
+                if (col >= a.n) continue;
+                const float bj = a.bias ? a.bias[col] : 0.f;
+                const int h = col / a.img_d, dim = col - h * a.img_d;
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int row0 = m0 + wm * WM + i * 32 + 8 * g + 4 * (lane >> 5);
+                        if (row0 >= a.m) continue;
+                        const f32x4 v = {acc[i][j][4 * g] + bj, acc[i][j][4 * g + 1] + bj, acc[i][j][4 * g + 2] + bj,
+                                         acc[i][j][4 * g + 3] + bj};
+                        zwg_img::store_quad(a.img, a.img_kind, row0, h, dim, v, a.img_ctx, a.img_d, a.img_heads,
+                                            a.img_tiles);
+                    }
+            }
+            return;
+        }
+    }
     float *part = KSPLIT ? a.part + (int64_t)split * a.m * a.n : nullptr;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {

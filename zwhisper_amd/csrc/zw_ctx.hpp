@@ -57,6 +57,14 @@ int ensure_stage(zwg_ctx *ctx, int i, uint64_t bytes);
 // the rows are contiguous, else one copy of the whole span into pinned staging and row copies on
 // the host.
 int download_rows(zwg_ctx *ctx, float *dst, const float *src, uint64_t n_rows, uint64_t cols, uint64_t stride);
+// The encoder layer's K/V path (kv_image.hpp): the f16 linear layer writing K (kind 1) or V
+// (kind 2) tile images in place of f32 rows -- rows = items * n_ctx (n_ctx % 4 == 0), n = heads * d
+// (d 64 or 128) -- and the dense x3 attention reading them (q, out and the shape as for
+// zwg_attention_batch_dev, row-major K; img_tiles = ceil(n_kv / 32)).
+int linear_f16_image(zwg_ctx *ctx, const float *x, uint64_t rows, uint64_t k, const void *w, const float *bias,
+                     uint64_t n, void *img, int kind, uint64_t n_ctx, uint64_t d);
+int attention_images_dev(zwg_ctx *ctx, const float *q, const void *k_img, const void *v_img, uint64_t img_tiles,
+                         const zwg_attn_shape &s, const zwg_batch &b, float *out);
 // Register / unregister an object made from ctx (see ZwgChild).
 void add_child(zwg_ctx *ctx, void *obj, void (*detach)(void *));
 void remove_child(zwg_ctx *ctx, void *obj);

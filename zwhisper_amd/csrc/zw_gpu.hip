@@ -121,6 +121,10 @@ struct Exec {
     uint64_t plan_cap; // workspace bytes the planner may use (>= ws_bytes: a bigger plan is refused)
     const char *ws_name;
     uint32_t *out_max = nullptr; // device word the kernels raise to the largest |out| they write, or null
+    // K and V as tile images (the encoder layer's projections write them), read by the dense x3
+    // kernel in place of k and v
+    const _Float16 *k_img = nullptr, *v_img = nullptr;
+    uint64_t img_tiles = 0;
 };
 
 Exec ctx_exec(const zwg_ctx *ctx) {
@@ -144,7 +148,15 @@ int run_kernels(zwg_ctx *ctx, const Exec &x, const float *q, const float *k, con
     // (and the dense kernels one KV head's K^T rows) through buffer descriptors with 32-bit byte
     // offsets; the dense kernels' tile loads reach up to 32 rows past the last key
     const bool dense = p.kernel == 1;
-    if ((p.kernel == 2 && !s.kt_stride) || dense) {
+    if (x.k_img) {
+        if (!dense || x.dense_math != ZWG_DENSE_X3 || s.kt_stride || (s.d != 64 && s.d != 128) ||
+            x.img_tiles != (s.n_kv + 31) / 32 || b.n_kv_dev)
+            return fail(ctx, "tile images are read by the dense x3 kernel only (row-major K, d 64 or 128, "
+                             "all items at n_kv keys)");
+        if (b.n_batch * s.n_head_kv * x.img_tiles * 64 * s.d * 2 > 0xffffffffffffull ||
+            x.img_tiles * 64 * s.d * 2 > 0x7fffffffull)
+            return fail(ctx, "tile images too large");
+    } else if ((p.kernel == 2 && !s.kt_stride) || dense) {
         if (s.n_kv > 0 && ((s.n_kv - 1 + (dense ? 32 : 0)) * s.kv_stride + s.d) * sizeof(float) > 0x7fffffffull)
             return fail(ctx, "K/V rows of one batch item must span less than 2 GiB");
         if (dense && s.kt_stride && (s.d * s.kt_stride + 32) * sizeof(float) > 0x7fffffffull)
@@ -184,6 +196,9 @@ int run_kernels(zwg_ctx *ctx, const Exec &x, const float *q, const float *k, con
     a.part_ml = x.ws;
     a.part_o = x.ws + (p.max_chunks > 1 ? part_o_offset(n_rows, (uint64_t)p.max_chunks) : 0);
     a.out_max = x.out_max;
+    a.k_img = x.k_img;
+    a.v_img = x.v_img;
+    a.img_tiles = (int32_t)x.img_tiles;
 
     hipError_t e = hipSuccess;
     if (x.device >= 0) e = hipSetDevice(x.device);
@@ -268,6 +283,17 @@ int run(zwg_ctx *ctx, const Exec &x, const float *q, const float *k, const float
 }
 
 } // namespace
+
+int zwg_host::attention_images_dev(zwg_ctx *ctx, const float *q, const void *k_img, const void *v_img,
+                                   uint64_t img_tiles, const zwg_attn_shape &s, const zwg_batch &b, float *out) {
+    if (!ctx) return fail(nullptr, "null context");
+    if (!k_img || !v_img) return fail(ctx, "null tile image");
+    Exec x = ctx_exec(ctx);
+    x.k_img = static_cast<const _Float16 *>(k_img);
+    x.v_img = static_cast<const _Float16 *>(v_img);
+    x.img_tiles = img_tiles;
+    return run(ctx, x, q, static_cast<const float *>(k_img), static_cast<const float *>(v_img), s, b, out);
+}
 
 extern "C" {
 
