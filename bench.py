@@ -20,15 +20,15 @@ the bar of the arithmetic that ran.  The two encoder workloads also carry "dropi
 the host-pointer drop-in (zwg_attention_ex, H2D + kernels + D2H per window), which includes PCIe
 and is never the headline value.
 
-Timing: W untimed warm-up steps, then exactly K steps bracketed by torch.cuda.synchronize() and
-by one pair of HIP events on the stream the kernels run on; the events' elapsed time over K is
-the kernel time used for the roofline (kernel_ms_mean).  K further steps, each between its own
-pair of events, give kernel_ms_median and kernel_ms_min.  Decode workloads rotate between two copies of their
-inputs so no step finds its K/V in the 256 MB last-level cache left by the previous one.
-The card raises its clocks over the first tens of milliseconds of continuous load, so the K timed
-steps after a few warm-up steps include part of that ramp.  After them, each workload keeps running
-untimed for 0.3 s and K more steps are timed with one event pair: "sustained" reports that device
-time per step and its roofline fraction, the rate a serving loop sees.  It is never "value".
+Timing: the card raises its clocks over the first tens of milliseconds of continuous load, so
+each workload runs W untimed warm-up steps, K "cold" steps timed with one event pair (reported
+as `cold`, the rate while the clocks ramp; never the value), untimed steps for 0.3 s, and then
+exactly K steps bracketed by torch.cuda.synchronize() and by one pair of HIP events on the stream
+the kernels run on: their wall time gives ms_per_step and `value`, the events' elapsed time over
+K the kernel time used for the roofline (kernel_ms_mean) -- the rate a serving loop under steady
+load sees.  K further steps, each between its own pair of events, give kernel_ms_median and
+kernel_ms_min.  Decode workloads rotate between two copies of their inputs so no step finds its
+K/V in the 256 MB last-level cache left by the previous one.
 The CPU baseline is the C restatement of the reference's multithreaded attention (oracle/),
 timed on this host's cores on a bounded sample of the same workload, on CPUs - 1 threads (the
 reference's default pool) over the CPUs this job may use (affinity, cgroup quota and
@@ -759,38 +759,30 @@ def q8_workloads(torch, ctx):
 
 
 def time_workload(wl, steps: int, warmup: int) -> dict:
-    """W warm-up steps, then exactly K timed steps bracketed by torch.cuda.synchronize(), with one
-    pair of HIP events on the stream the kernels run on around the K steps: kernel_ms_mean is
-    their elapsed time over K, the device time per step with nothing inserted between the steps.
-    Afterwards (outside the timed region) K more steps each bracketed by their own events give the
-    per-step median and minimum; an event pair between launches adds a short gap, so those run a
-    little above the mean."""
+    """The card raises its clocks over the first tens of milliseconds of continuous load, so steps
+    timed right after a few warm-up steps measure part of that ramp.  Order: W warm-up steps; K
+    "cold" steps timed with one event pair (reported as `cold`, never as the value); untimed steps
+    for SETTLE_S; then exactly K timed steps bracketed by torch.cuda.synchronize(), with one pair
+    of HIP events on the stream the kernels run on around them: the wall time gives ms_per_step
+    (and `value`), the events kernel_ms_mean, the device time per step with nothing inserted
+    between the steps.  Afterwards (outside the timed region) K more steps each bracketed by their
+    own events give the per-step median and minimum; an event pair between launches adds a short
+    gap, so those run a little above the mean."""
     torch = wl.torch
-    for i in range(warmup):
-        wl.step(i)
-    torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    i = 0
+    for _ in range(warmup):
+        wl.step(i)
+        i += 1
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    e0.record(stream)
-    for i in range(steps):
-        wl.step(warmup + i)
-    e1.record(stream)
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    c0.record(stream)
+    for _ in range(steps):
+        wl.step(i)
+        i += 1
+    c1.record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    kernel_ms_mean = e0.elapsed_time(e1) / steps
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    for i in range(steps):
-        ev[i][0].record(stream)
-        wl.step(warmup + steps + i)
-        ev[i][1].record(stream)
-    torch.cuda.synchronize()
-    kms = [a.elapsed_time(b) for a, b in ev]
-    # Sustained rate, after everything above and outside the reported figures: the card raises its
-    # clocks over the first tens of milliseconds of continuous load, so a short run measures part of
-    # that ramp.  Steps keep running untimed for SETTLE_S, then K more are timed with one event pair.
-    i = warmup + 2 * steps
+    cold_ms = c0.elapsed_time(c1) / steps
     t_settle = time.perf_counter()
     while time.perf_counter() - t_settle < SETTLE_S:
         for _ in range(16):
@@ -798,31 +790,42 @@ def time_workload(wl, steps: int, warmup: int) -> dict:
             i += 1
         torch.cuda.synchronize()
     settle_s = time.perf_counter() - t_settle
-    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    s0.record(stream)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(stream)
     for _ in range(steps):
         wl.step(i)
         i += 1
-    s1.record(stream)
+    e1.record(stream)
     torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms_mean = e0.elapsed_time(e1) / steps
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for k in range(steps):
+        ev[k][0].record(stream)
+        wl.step(i)
+        i += 1
+        ev[k][1].record(stream)
+    torch.cuda.synchronize()
+    kms = [a.elapsed_time(b) for a, b in ev]
     return {"wall_s": wall, "ms_per_step": 1e3 * wall / steps, "kernel_ms_mean": kernel_ms_mean,
             "kernel_ms_min": float(np.min(kms)), "kernel_ms_median": float(np.median(kms)),
-            "sustained_kernel_ms": s0.elapsed_time(s1) / steps, "settle_s": settle_s}
+            "cold_kernel_ms": cold_ms, "settle_s": settle_s}
 
 
-SETTLE_S = 0.3  # untimed continuous load before the sustained-rate steps
+SETTLE_S = 0.3  # untimed continuous load between the cold steps and the timed steps
 TRAFFIC_SOURCE: dict = {}  # traffic_source(), set once in main()
 
 
-def sustained(r: dict, work: float, unit: str, peak: float, products: int = 1) -> dict:
-    """The sustained-rate record of a workload (reported beside `value`, never as it): device time
-    per step of K steps timed after SETTLE_S of untimed continuous load, and the roofline fraction
-    at that time."""
+def cold(r: dict, work: float, unit: str, peak: float, products: int = 1) -> dict:
+    """The cold-start record of a workload (reported beside `value`, never as it): device time per
+    step of the K steps timed right after the W warm-up steps, before the clocks settle."""
     scale = 1e12 if unit == "TFLOP/s" else 1e9
-    achieved = work / (r["sustained_kernel_ms"] * 1e-3)
-    out = {"kernel_ms_per_step": r["sustained_kernel_ms"], "achieved": achieved / scale, "unit": unit,
-           "frac": achieved / peak, "settle_s": r["settle_s"],
-           "note": "device time per step after the clocks settle under continuous load; not the timed steps"}
+    achieved = work / (r["cold_kernel_ms"] * 1e-3)
+    out = {"kernel_ms_per_step": r["cold_kernel_ms"], "achieved": achieved / scale, "unit": unit,
+           "frac": achieved / peak,
+           "note": "device time per step of K steps right after the W warm-up steps, while the clocks ramp"}
     if products > 1:
         out["issued_frac"] = products * achieved / peak
     return out
@@ -1006,15 +1009,15 @@ def _attention_line(wl: Workload, r: dict, dense_math: int) -> dict:
         unit = "GB/s"
         dtype = "f32"
     if spec.bound == "mfma":
-        sus = sustained(r, per_step, "TFLOP/s", PEAK_MFMA_F16 if dense_math == 0 else PEAK_MFMA_F32,
+        cold_rec = cold(r, per_step, "TFLOP/s", PEAK_MFMA_F16 if dense_math == 0 else PEAK_MFMA_F32,
                         3 if dense_math == 0 else 1)
     else:
-        sus = sustained(r, per_step, "GB/s", PEAK_HBM)
+        cold_rec = cold(r, per_step, "GB/s", PEAK_HBM)
     return {"workload": spec.name, "description": spec.description, "value": value, "unit": unit,
             "rate": step_rate(wl.number, r["ms_per_step"]), "ms_per_step": r["ms_per_step"],
             "kernel_ms_mean": r["kernel_ms_mean"], "kernel_ms_median": r["kernel_ms_median"],
             "kernel_ms_min": r["kernel_ms_min"], "algorithmic_work_per_step": per_step, "dtype": dtype,
-            "roofline": roof, "sustained": sus}
+            "roofline": roof, "cold": cold_rec, "settle_s": r["settle_s"]}
 
 
 def _say(name: str, res: dict, peak_name: str) -> None:
@@ -1027,8 +1030,8 @@ def _say(name: str, res: dict, peak_name: str) -> None:
     par = res.get("parity")
     print(f"[bench] {name}: {res['value']:.2f} {res['unit']} ({res['ms_per_step']:.4f} ms/step, kernels "
           f"{res['kernel_ms_mean']:.4f} ms, {100 * res['roofline']['frac']:.1f}% of {peak_name})"
-          + (f", sustained {res['sustained']['kernel_ms_per_step']:.4f} ms ({100 * res['sustained']['frac']:.1f}%)"
-             if "sustained" in res else "")
+          + (f", cold {res['cold']['kernel_ms_per_step']:.4f} ms ({100 * res['cold']['frac']:.1f}%)"
+             if "cold" in res else "")
           + (f", parity max abs {par['max_abs']:.2e} rel {par['normwise_rel']:.2e}" if par else "")
           + (f", cpu {cpu['value']:.3f} {cpu['unit']} on {cpu['cores']} threads" if cpu else ""),
           file=sys.stderr, flush=True)
@@ -1088,7 +1091,7 @@ def run_extra(name: str, torch, ctx, args, threads: int) -> dict:
                "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": PEAK_MFMA_F16 / 1e12,
                             "unit": "TFLOP/s", "frac": achieved / PEAK_MFMA_F16, "traffic": traffic_for(wl.name),
                             "note": "two f16 MFMAs per f32 x f16 product: the kernels' ceiling is frac 0.5"},
-               "sustained": sustained(r, wl.work, "TFLOP/s", PEAK_MFMA_F16, 2)}
+               "cold": cold(r, wl.work, "TFLOP/s", PEAK_MFMA_F16, 2)}
         if not args.no_cpu:
             res["cpu_baseline"] = wl.cpu_baseline(threads)
         wl.free()
@@ -1111,7 +1114,7 @@ def run_extra(name: str, torch, ctx, args, threads: int) -> dict:
                             "note": "peak = the layer's flops over the time they take at their own peaks: "
                                     "projections at half the f16 MFMA peak, attention at a third of the 16-bit MFMA "
                                     "peak"},
-               "sustained": sustained(r, wl.work, "TFLOP/s", peak)}
+               "cold": cold(r, wl.work, "TFLOP/s", peak)}
         if not args.no_cpu:
             res["cpu_baseline"] = wl.cpu_baseline(threads)
         wl.free()
@@ -1132,7 +1135,7 @@ def run_extra(name: str, torch, ctx, args, threads: int) -> dict:
                         "f16 terms, block sums scaled in f32)",
                "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                             "frac": achieved / PEAK_HBM, "traffic": traffic_for(wl.name)},
-               "sustained": sustained(r, wl.work, "GB/s", PEAK_HBM)}
+               "cold": cold(r, wl.work, "GB/s", PEAK_HBM)}
         if not args.no_cpu:
             res["cpu_baseline"] = wl.cpu_baseline(threads)
         wl.free()
@@ -1281,7 +1284,7 @@ def main() -> int:
                    "n_head": spec.n_head, "n_head_kv": spec.n_head_kv, "head_dim": spec.d, "causal": spec.causal,
                    "k_layout": "transposed" if spec.kt else "row-major", "parallelism": "single GPU"},
         "roofline": head["roofline"],
-        "sustained": head["sustained"],
+        "cold": head["cold"],
         "rate": head["rate"],
         "kernel_ms_median": head["kernel_ms_median"],
         "parity": head.get("parity"),
