@@ -27,7 +27,8 @@ struct zwg_ctx {
     // work on the next touches it
     hipEvent_t switch_event = nullptr;
     float *workspace = nullptr;
-    // device word the kernels raise to the largest |out| they write (host drop-in only)
+    // device words the kernels raise to the largest |out| they write (host drop-in only;
+    // zwg::kOutMaxSlots slots 128 bytes apart)
     uint32_t *out_max_word = nullptr;
     uint32_t dense_math = ZWG_DENSE_X3; // products of the dense kernel (zwg_set_dense_math)
     uint64_t workspace_bytes = 0;

@@ -120,7 +120,7 @@ struct Exec {
     uint32_t dense_math;
     uint64_t plan_cap; // workspace bytes the planner may use (>= ws_bytes: a bigger plan is refused)
     const char *ws_name;
-    uint32_t *out_max = nullptr; // device word the kernels raise to the largest |out| they write, or null
+    uint32_t *out_max = nullptr; // device words the kernels raise to the largest |out| they write, or null
     // K and V as tile images (the encoder layer's projections write them), read by the dense x3
     // kernel in place of k and v
     const _Float16 *k_img = nullptr, *v_img = nullptr;
@@ -368,7 +368,7 @@ int zwg_open(int device, const zwg_limits *limits, zwg_ctx **out) {
     }
     ctx->workspace = static_cast<float *>(ws);
     void *flag = nullptr;
-    e = hipMalloc(&flag, 256);
+    e = hipMalloc(&flag, zwg::kOutMaxBytes);
     if (e != hipSuccess) {
         (void)hipFree(ws);
         (void)hipEventDestroy(ctx->switch_event);
@@ -494,21 +494,23 @@ int zwg_attention_ex(zwg_ctx *ctx, const float *q, const float *k, const float *
     if (e != hipSuccess) return fail_hip(ctx, "hipMemcpyAsync (upload)", e);
     const zwg_batch one{1, 0, 0, 0, 0, nullptr};
     Exec x = ctx_exec(ctx);
-    // the kernels that write out raise this word to the largest |value| they write (read back with
-    // the result)
+    // the kernels that write out raise these words to the largest |value| they write (read back
+    // with the result)
     x.out_max = ctx->out_max_word;
-    e = hipMemsetAsync(ctx->out_max_word, 0, sizeof(uint32_t), ctx->stream);
+    e = hipMemsetAsync(ctx->out_max_word, 0, zwg::kOutMaxBytes, ctx->stream);
     if (e != hipSuccess) return fail_hip(ctx, "hipMemsetAsync (result maximum)", e);
     Plan p;
     int rc = run(ctx, x, ctx->stage[0], ctx->stage[1], ctx->stage[2], s, one, ctx->stage[3], &p);
     if (rc != ZWG_OK) return rc;
-    uint32_t out_max = 0;
-    e = hipMemcpyAsync(&out_max, ctx->out_max_word, sizeof out_max, hipMemcpyDeviceToHost, ctx->stream);
+    uint32_t slots[zwg::kOutMaxSlots * zwg::kOutMaxStride];
+    e = hipMemcpyAsync(slots, ctx->out_max_word, sizeof slots, hipMemcpyDeviceToHost, ctx->stream);
     if (e != hipSuccess) return fail_hip(ctx, "hipMemcpyAsync (result maximum)", e);
     // copy back only each row's n_head*d columns: out's other columns stay the caller's (waits for
     // the stream, so the maximum has arrived too)
     rc = download_rows(ctx, out, ctx->stage[3], s.n_q, hd, s.out_stride);
     if (rc != ZWG_OK) return rc;
+    uint32_t out_max = 0;
+    for (int i = 0; i < zwg::kOutMaxSlots; ++i) out_max = std::max(out_max, slots[i * zwg::kOutMaxStride]);
     // The reference gives finite, f32-accurate results for any finite input (src/ops.zig:562-590).
     // The x3 dense kernel meets that when its result is finite and not tiny; otherwise the call is
     // computed again on the fp32-MFMA kernel (which reproduces any NaN or infinity the inputs
