@@ -149,3 +149,41 @@ def test_linear_errors(torch, ctx):
         ctx.linear_dev(t, 2, 12, w, None, 2, t)
     with pytest.raises(z.ZwgError, match="float16"):
         ctx.linear_dev(t, 2, 8, t, None, 2, t)
+
+
+# Large calls run 64 x 256 (or 128 x 256) tiles, small ones 64 x 64; every tile shape accumulates
+# each output over k in the same order (stages of 32 k in order, per 16-k step the hi then the lo
+# product), so a row computed in a large unsplit call equals the same row computed in a small
+# unsplit call bit for bit.  Shapes: the base.en projections' width, an n with a partial column
+# tile, m and n tails with 3 stages of k, and 5 stages.
+TILE_CASES = [(16384, 256, 512), (12000, 448, 768), (8193, 96, 1040), (16400, 160, 256)]
+
+
+@pytest.mark.parametrize("m,k,n", TILE_CASES)
+def test_large_and_small_calls_agree_bitwise(torch, ctx, m, k, n):
+    from zwhisper_amd import _lib
+
+    x, w, b = inputs(m + k + n, m, k, n)
+    xd, wd, bd = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda(), torch.from_numpy(b).cuda()
+    big = torch.full((m, n), float("nan"), device="cuda")
+    ctx.linear_epi_dev(xd, m, k, wd, bd, n, big, _lib.EPI_NONE)
+    gel = torch.full((m, n), float("nan"), device="cuda")
+    ctx.linear_epi_dev(xd, m, k, wd, bd, n, gel, _lib.EPI_GELU)
+    wide = torch.full((m, 2 * n), 7.0, device="cuda")
+    ctx.linear_epi_dev(xd, m, k, wd, bd, n, wide.view(-1)[n:], _lib.EPI_NONE, out_stride=2 * n)
+    torch.cuda.synchronize()
+    got = big.cpu().numpy()
+    ref = ref64(x, w, b)
+    err = float(np.abs(got - ref).max())
+    print(f"linear {m}x{k}x{n}: max abs {err:.2e}", flush=True)
+    assert np.all(np.isfinite(got)) and err <= 2e-5 * np.sqrt(k)
+    ref_g = big.clone()
+    ctx.gelu_dev(ref_g)
+    torch.cuda.synchronize()
+    assert torch.equal(gel, ref_g)
+    assert torch.equal(wide[:, n:], big) and bool((wide[:, :n] == 7.0).all())
+    for r0, r1 in ((0, 64), (m - 61, m), (4999, 5130)):
+        small = torch.full((r1 - r0, n), float("nan"), device="cuda")
+        ctx.linear_epi_dev(xd[r0:r1].contiguous(), r1 - r0, k, wd, bd, n, small, _lib.EPI_NONE)
+        torch.cuda.synchronize()
+        assert torch.equal(small, big[r0:r1]), (r0, r1)
