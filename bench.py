@@ -45,8 +45,11 @@ HBM roofline and oracle/kv.py's update timed beside it, and the six linear layer
 encoder layer over the 16 windows ("base_enc_linear_x16", f16 weights on f16 MFMA) with the
 oracle's ops.linear timed beside it, and three decode steps' linear layers over int8 block
 weights (HBM-bound; "qwen15_logits_q8_x64", "qwen15_decode_q8_linear_x64",
-"small_dec_q8_linear_x32") with the oracle's ops.linear over Q8 timed beside them, and one whole
-base.en encoder layer over the 16 windows ("base_enc_layer_x16") with the oracle's layer beside it.
+"small_dec_q8_linear_x32") with the oracle's ops.linear over Q8 timed beside them, two decode
+steps' q/k/v projections with the new K/V rows written into the device caches by the projections
+themselves ("small_dec_qkv_cache_x32", "qwen15_qkv_cache_x64", with the unfused projections +
+append timed beside them), and one whole base.en encoder layer over the 16 windows
+("base_enc_layer_x16") with the oracle's layer beside it.
 
 Each attention workload also carries "rate": windows/s for the encoders, tokens/s for the decoder
 step, the prefill and the LLM decode step, at wall time per step.  The prefill's CPU baseline runs
@@ -738,8 +741,117 @@ class Q8LinearWorkload:
         self.x = self.out = self.sets = self.raw = None
 
 
+class QkvCacheWorkload:
+    """A decode step's q/k/v projections and cache writes over all layers, int8 resident weights:
+    per layer one zwg_linear_q8w_qkv_kv_dev (the projections with the cache append in their final
+    store: q rotated and written out, k and v rotated and scattered into the device cache at each
+    sequence's position), replayed as one HIP graph per step.  Beside it the record times the same
+    step as the two calls it replaces, zwg_linear_q8w_group_dev into rows and zwg_kv_append_batch,
+    per layer ("unfused"): one launch more per layer.  Algorithmic bytes per layer: the three weight
+    sets (int8, f32 block scales, biases), x read, q written, and the k and v rows written into the
+    cache."""
+
+    def __init__(self, name: str, description: str, torch, ctx, m: int, k: int, n_layer: int, n_head: int,
+                 n_head_kv: int, d: int, kt: bool, rope: float, n_ctx: int, biases):
+        import zwhisper_amd as z
+        from zwhisper_amd import _lib
+
+        self.name, self.description = name, description
+        self.torch, self.ctx, self.m, self.k, self.n_layer = torch, ctx, m, k, n_layer
+        g = torch.Generator(device="cuda").manual_seed(0x0909)
+        ns = (n_head * d, n_head_kv * d, n_head_kv * d)
+        self.layers = []
+        self.raw = None
+        for li in range(n_layer):
+            rs, bs = [], []
+            for n, hb in zip(ns, biases):
+                q = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda", generator=g)
+                sc = torch.rand(n, k // 32, device="cuda", generator=g) * (2.0 / 127 / np.sqrt(k))
+                rs.append(z.Q8(q, sc, n, k).resident(ctx))
+                bs.append(torch.randn(n, device="cuda", generator=g) if hb else None)
+                if li == 0:
+                    self.raw = (self.raw or []) + [(q.cpu().numpy(), sc.cpu().numpy(),
+                                                    None if bs[-1] is None else bs[-1].cpu().numpy())]
+            self.layers.append((rs, bs))
+        self.kv = z.KVCache(ctx, n_layer, m, n_ctx, n_head_kv, d, _lib.KV_KT if kt else _lib.KV_ROW, rope)
+        self.x = torch.randn(m, k, device="cuda", generator=g)
+        self.q = torch.empty(m, n_head * d, device="cuda")
+        self.k_rows = torch.empty(m, n_head_kv * d, device="cuda")
+        self.v_rows = torch.empty(m, n_head_kv * d, device="cuda")
+        self.pos = torch.randint(0, n_ctx, (m,), dtype=torch.int32, device="cuda", generator=g)
+        self.n_head, self.rope = n_head, rope
+        self.work = float(n_layer * (sum(n * k + n * k // 32 * 4 + (n * 4 if hb else 0) for n, hb in zip(ns, biases))
+                                     + m * k * 4 + m * ns[0] * 4 + 2 * m * ns[1] * 4))
+        self.graphs = {}
+        for mode in ("fused", "unfused"):
+            self._run(mode)
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                self._run(mode)
+            self.graphs[mode] = gr
+        torch.cuda.synchronize()
+
+    def _run(self, mode: str):
+        for li, (rs, bs) in enumerate(self.layers):
+            if mode == "fused":
+                self.ctx.linear_q8w_qkv_kv_dev(self.x, self.m, rs, bs, self.q, self.kv, li, 0, self.pos)
+            else:
+                self.ctx.linear_q8w_group_dev(self.x, self.m, rs, bs, [self.q, self.k_rows, self.v_rows])
+                self.kv.append_batch(li, 0, self.pos, self.k_rows, self.v_rows,
+                                     q=self.q if self.rope > 0 else None, n_head=self.n_head,
+                                     q_stride=self.q.shape[1])
+
+    def step(self, i: int):
+        self.graphs["fused"].replay()
+
+    def extra_record(self, steps: int) -> dict:
+        """The unfused step (group call + append per layer), timed as the fused one."""
+        torch = self.torch
+        for _ in range(5):
+            self.graphs["unfused"].replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            self.graphs["unfused"].replay()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        return {"unfused": {"kernel_ms_per_step": ms, "launches_per_layer": 3,
+                            "note": "zwg_linear_q8w_group_dev into rows + zwg_kv_append_batch per layer, the "
+                                    "same HIP-graph replay; the fused call takes 2 launches per layer"}}
+
+    def cpu_baseline(self, threads: int) -> dict:
+        """The oracle's ops.linear over Q8 (oracle/attn_oracle.c) for one layer's q, k and v."""
+        import oracle
+
+        x = self.x.cpu().numpy()
+        outs = [np.zeros(self.m * q.shape[0], np.float32) for q, _, _ in self.raw]
+        o = oracle.Oracle(threads)
+
+        def run():
+            for (q, sc, b), out in zip(self.raw, outs):
+                o.linear_q8(x, self.m, self.k, q, sc, b, q.shape[0], out=out)
+
+        best, mean, runs = time_cpu(run, 3)
+        o.close()
+        return {"value": self.work / self.n_layer / best / 1e9, "unit": "GB/s", "cores": o.threads, "kind": "port",
+                "sample": "layer 0's q, k and v projections (the cache rows' copy not included); "
+                          "oracle/attn_oracle.c ora_linear_q8; " + cpu_timing(best, mean, runs), "seconds": best}
+
+    def free(self):
+        self.graphs = None
+        for rs, _ in self.layers or []:
+            for w in rs:
+                w.close()
+        if self.kv is not None:
+            self.kv.close()
+        self.layers = self.kv = self.x = self.q = self.raw = None
+
+
 def q8_workloads(torch, ctx):
-    """(name, constructor) of the three int8 decode-step measurements."""
+    """(name, constructor) of the int8 decode-step measurements."""
     qwen_layer = [(1536, 1536, True), (1536, 256, True), (1536, 256, True), (1536, 1536, False),
                   (1536, 8960, False), (1536, 8960, False), (8960, 1536, False)]  # src/llm.zig:179-207
     whisper_layer = [(768, 768, True), (768, 768, False), (768, 768, True), (768, 768, True),
@@ -756,6 +868,16 @@ def q8_workloads(torch, ctx):
         "12 layers and the 51864-token logits (97 linear layers in 73 calls: q/k/v grouped), int8 block weights",
         torch, ctx, 32, whisper_layer * 12 + [(768, 51864, False)], copies=2, cpu_layers=8,
         groups=[3, 1, 1, 1, 1, 1] * 12 + [1])
+    yield "small_dec_qkv_cache_x32", lambda: QkvCacheWorkload(
+        "small_dec_qkv_cache_x32", "Whisper small.en decoder step, 32 windows: self-attention q/k/v projections "
+        "of all 12 layers with the new k and v rows written into the row-major device caches "
+        "(src/decoder.zig:181-183), int8 block weights", torch, ctx, 32, 768, 12, 12, 12, 64, False, 0.0, 448,
+        (True, False, True))
+    yield "qwen15_qkv_cache_x64", lambda: QkvCacheWorkload(
+        "qwen15_qkv_cache_x64", "Qwen2.5-1.5B decode step, 64 sequences: q/k/v projections of all 28 layers, "
+        "q and k rotated (base 1e6), k scattered into the transposed device cache and v into its rows "
+        "(src/llm.zig:179-190), int8 block weights", torch, ctx, 64, 1536, 28, 12, 2, 128, True, 1e6, 4096,
+        (True, True, True))
 
 
 def time_workload(wl, steps: int, warmup: int) -> dict:
@@ -1041,7 +1163,8 @@ def _say(name: str, res: dict, peak_name: str) -> None:
 
 EXTRAS = ("qwen05_prefill_8x256", "small_dec_kv_append_x32", "qwen15_kv_append_x64", "qwen05_prefill_kv_append",
           "base_enc_linear_x16",
-          "base_enc_layer_x16", "qwen15_logits_q8_x64", "qwen15_decode_q8_linear_x64", "small_dec_q8_linear_x32")
+          "base_enc_layer_x16", "qwen15_logits_q8_x64", "qwen15_decode_q8_linear_x64", "small_dec_q8_linear_x32",
+          "small_dec_qkv_cache_x32", "qwen15_qkv_cache_x64")
 
 
 def run_extra(name: str, torch, ctx, args, threads: int) -> dict:
@@ -1136,6 +1259,8 @@ def run_extra(name: str, torch, ctx, args, threads: int) -> dict:
                "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                             "frac": achieved / PEAK_HBM, "traffic": traffic_for(wl.name)},
                "cold": cold(r, wl.work, "GB/s", PEAK_HBM)}
+        if hasattr(wl, "extra_record"):
+            res.update(wl.extra_record(args.steps))
         if not args.no_cpu:
             res["cpu_baseline"] = wl.cpu_baseline(threads)
         wl.free()

@@ -383,6 +383,26 @@ int zwg_linear_q8w_group_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t 
                              const float *const *bias, float *const *out);
 
 /*
+ * A decode step's q/k/v projections with the cache append in their final store: the projections
+ * of zwg_linear_q8w_group_dev over w[0] (q: n_head * d rows), w[1] and w[2] (k, v: n_head_kv * d
+ * rows of kv), bias[0..2] (each NULL or 16-byte aligned; bias itself may be NULL), then what
+ * zwg_kv_append_batch(kv, layer, seq0, m, pos_dev, k, v, q_out, n_head, n_head * d) does with them:
+ * with the cache's rotary tables q and k rotated at their token's position; q written to q_out
+ * [m][n_head * d]; token i's k and v written into sequence seq0 + i's cache at pos_dev[i] (k
+ * transposed for ZWG_KV_KT); a position outside [0, n_ctx) writes no cache rows and leaves q
+ * unrotated.  q_out and the caches equal those two calls' bit for bit whenever the group call
+ * splits k (its m <= 64 calls of fewer than 128 workgroups, which include the Whisper and Qwen2
+ * decode steps' q/k/v); this call always splits, so the rows never go through memory unsummed.
+ * m <= 64 (one row per sequence), k above 256.  As the reference, whose decoder writes the k and v
+ * projections straight into its cache rows (src/decoder.zig:181-183) and whose Qwen2 step rotates
+ * and scatters them (src/llm.zig:179-190): one launch fewer per layer than projections + append.
+ * Device pointers, asynchronous.
+ */
+int zwg_linear_q8w_qkv_kv_dev(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *const *w,
+                              const float *const *bias, float *q_out, zwg_kv *kv, uint64_t layer, uint64_t seq0,
+                              const int32_t *pos_dev);
+
+/*
  * Row-wise and elementwise ops around the projections, device pointers, asynchronous:
  * ops.layerNormEps (src/ops.zig:388-395; ops.layerNorm is eps = 1e-5, BERT uses 1e-12):
  * out[i] = (x[i] - mean) / sqrt(var + eps) * w + b per row of x [m][n]; ops.gelu (src/ops.zig:

@@ -147,6 +147,8 @@ pub extern "zwgpu" fn zwg_linear_q8w_epi_dev(ctx: *Ctx, x: [*]const f32, m: u64,
     bias: ?[*]const f32, out: [*]f32, epilogue: u32) c_int;
 pub extern "zwgpu" fn zwg_linear_q8w_group_dev(ctx: *Ctx, x: [*]const f32, m: u64, n_w: u32,
     w: [*]const *const Q8w, bias: ?[*]const ?[*]const f32, out: [*]const [*]f32) c_int;
+pub extern "zwgpu" fn zwg_linear_q8w_qkv_kv_dev(ctx: *Ctx, x: [*]const f32, m: u64, w: [*]const *const Q8w,
+    bias: ?[*]const ?[*]const f32, q_out: [*]f32, kv: *Kv, layer: u64, seq0: u64, pos_dev: [*]const i32) c_int;
 
 // ---- layer norm, GELU, add, a whole encoder layer
 

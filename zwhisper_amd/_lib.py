@@ -187,6 +187,9 @@ def lib() -> ctypes.CDLL:
     L.zwg_linear_q8w_group_dev.restype = c_int
     L.zwg_linear_q8w_group_dev.argtypes = [vp, _fp, _u64, ctypes.c_uint32, ctypes.POINTER(vp), ctypes.POINTER(_fp),
                                            ctypes.POINTER(_fp)]
+    L.zwg_linear_q8w_qkv_kv_dev.restype = c_int
+    L.zwg_linear_q8w_qkv_kv_dev.argtypes = [vp, _fp, _u64, ctypes.POINTER(vp), ctypes.POINTER(_fp), _fp, vp, _u64,
+                                            _u64, vp]
     L.zwg_linear_epi_dev.restype = c_int
     L.zwg_linear_epi_dev.argtypes = [vp, _fp, _u64, _u64, vp, ctypes.c_uint32, _fp, _u64, _fp, _u64, ctypes.c_uint32]
     L.zwg_layer_norm_dev.restype = c_int

@@ -23,17 +23,6 @@
 
 using namespace zwg_host;
 
-struct zwg_kv {
-    zwg_ctx *ctx = nullptr;
-    zwg_kv_desc desc{};
-    uint64_t kvw = 0;     // n_head_kv * d
-    uint64_t per_seq = 0; // floats of one (layer, sequence) K or V cache: n_ctx * kvw
-    float *k = nullptr;   // [layer][sequence][per_seq]
-    float *v = nullptr;
-    float *cos = nullptr; // [n_ctx][d/2] rotary tables when rope_base > 0
-    float *sin = nullptr;
-};
-
 namespace {
 
 constexpr int kAppendThreads = 256;

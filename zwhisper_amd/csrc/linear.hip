@@ -214,8 +214,11 @@ constexpr int q8p_waves() { return MT == 1 ? ZWG_Q8P_WAVES_32 : ZWG_Q8P_WAVES; }
 #endif
 
 
+// kvs (a q/k/v group, sets 0, 1, 2): the split sum stores into q_out and the KV cache
+// (linear_split_sum_qkv_kernel), so the call is always split, in two at least.
 template <int MT>
-int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g) {
+int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
+                  const zwg_lin::Q8KvStore *kvs = nullptr) {
     constexpr int kQ8pWaves = q8p_waves<MT>();
     zwg_lin::Q8Args a = base;
     const uint64_t m = (uint64_t)a.m;
@@ -243,7 +246,12 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g)
     if (part_off > ctx->workspace_bytes) return fail(ctx, "workspace too small for this linear call");
     int n_split = 1;
     if (split_k) n_split = (int)std::min<int64_t>(n_chunks, (ZWG_Q8P_SPLIT_TARGET + gx - 1) / gx);
+    if (kvs) {
+        if (n_chunks < 2) return fail(ctx, "the cache-writing q/k/v call needs k above 256 (its sum is a k split)");
+        n_split = std::max(n_split, 2);
+    }
     while (n_split > 1 && part_off + (uint64_t)n_split * m * n_tot * 4 > ctx->workspace_bytes) --n_split;
+    if (kvs && n_split < 2) return fail(ctx, "workspace too small for this q/k/v call's partial sums");
     a.chunks_per_split = (n_chunks + n_split - 1) / n_split;
     n_split = (n_chunks + a.chunks_per_split - 1) / a.chunks_per_split; // no empty splits
     a.n_split = n_split;
@@ -275,7 +283,18 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g)
     }
     e = hipGetLastError();
     if (e != hipSuccess) return fail_hip(ctx, "linear (int8 stream) kernel launch", e);
-    if (n_split > 1) {
+    if (kvs) {
+        const int64_t threads = (int64_t)m * (kvs->n_head + 2 * kvs->n_head_kv) * (kvs->d / 8);
+        const int bs = small_block(threads);
+        if (kvs->d == 64)
+            zwg_lin::linear_split_sum_qkv_kernel<64><<<blocks_for(threads, bs), bs, 0, ctx->stream>>>(g, *kvs, a.m, n_split);
+        else if (kvs->d == 128)
+            zwg_lin::linear_split_sum_qkv_kernel<128><<<blocks_for(threads, bs), bs, 0, ctx->stream>>>(g, *kvs, a.m, n_split);
+        else
+            zwg_lin::linear_split_sum_qkv_kernel<32><<<blocks_for(threads, bs), bs, 0, ctx->stream>>>(g, *kvs, a.m, n_split);
+        e = hipGetLastError();
+        if (e != hipSuccess) return fail_hip(ctx, "q/k/v cache split-sum kernel launch", e);
+    } else if (n_split > 1) {
         const int64_t elems = (int64_t)(m * n_tot);
         const int bs = small_block(elems);
         zwg_lin::linear_split_sum_group_kernel<<<blocks_for(elems, bs), bs, 0, ctx->stream>>>(
@@ -445,7 +464,8 @@ void detach_q8w(void *obj) {
 // The token-step path (m <= 64) over n_w resident weight sets sharing x and k (checked by the
 // callers).
 int run_q8w_token_step(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t n_w, const zwg_q8w *const *w,
-                       const float *const *bias, float *const *out, uint32_t epi) {
+                       const float *const *bias, float *const *out, uint32_t epi,
+                       const zwg_lin::Q8KvStore *kvs = nullptr) {
     zwg_lin::Q8Args a{};
     a.x = x;
     a.m = (int32_t)m;
@@ -460,9 +480,9 @@ int run_q8w_token_step(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t n_w, c
         g.n_slabs[j] = w[j]->n_slabs;
         g.n[j] = (int32_t)w[j]->n;
         g.bias[j] = bias ? bias[j] : nullptr;
-        g.out[j] = out[j];
+        g.out[j] = out ? out[j] : nullptr;
     }
-    return m > 32 ? run_q8p_group<2>(ctx, a, g) : run_q8p_group<1>(ctx, a, g);
+    return m > 32 ? run_q8p_group<2>(ctx, a, g, kvs) : run_q8p_group<1>(ctx, a, g, kvs);
 }
 
 int run_linear_q8w(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, const float *bias, float *out,
@@ -614,6 +634,48 @@ int zwg_linear_q8w_group_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t 
     const hipError_t e = hipSetDevice(ctx->device);
     if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
     return run_q8w_token_step(ctx, x, m, n_w, w, bias, out, zwg_ew::kEpiNone);
+}
+
+int zwg_linear_q8w_qkv_kv_dev(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *const *w,
+                              const float *const *bias, float *q_out, zwg_kv *kv, uint64_t layer, uint64_t seq0,
+                              const int32_t *pos_dev) {
+    if (!ctx) return fail(nullptr, "null context");
+    if (!w || !kv) return fail(ctx, "null weight array or cache");
+    if (kv->ctx != ctx) return fail(ctx, "the cache belongs to another context (or its context is closed)");
+    const zwg_kv_desc &d = kv->desc;
+    const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    for (int j = 0; j < 3; ++j) {
+        if (!w[j]) return fail(ctx, "null weights");
+        if (!w[j]->ctx) return fail(ctx, kQ8wClosed);
+        if (w[j]->k != w[0]->k) return fail(ctx, "q, k and v weights must share k");
+        const std::string msg = check_linear(m, w[j]->k, ZWG_W_Q8, w[j]->n);
+        if (!msg.empty()) return fail(ctx, msg);
+        if (bias && bias[j] && !al16(bias[j])) return fail(ctx, "biases must be 16-byte aligned");
+    }
+    if (w[1]->n != kv->kvw || w[2]->n != kv->kvw) return fail(ctx, "k and v weights must have n_head_kv * d rows");
+    if (w[0]->n % d.d || (w[0]->n / d.d) % d.n_head_kv) return fail(ctx, "q weights must have n_head * d rows, n_head a multiple of n_head_kv");
+    if (layer >= d.n_layer) return fail(ctx, "kv layer out of range");
+    if (m > 64) return fail(ctx, "the cache-writing q/k/v call takes at most 64 tokens (one decode step)");
+    if (seq0 + m > d.n_seq) return fail(ctx, "kv sequences out of range");
+    if (m == 0) return ZWG_OK;
+    if (!x || !al16(x) || !q_out || !al16(q_out) || !pos_dev) return fail(ctx, "x, q_out (16-byte aligned) and pos_dev must be non-null");
+    const hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
+    zwg_lin::Q8KvStore kvs{};
+    kvs.q_out = q_out;
+    kvs.k_cache = kv->k + layer * d.n_seq * kv->per_seq;
+    kvs.v_cache = kv->v + layer * d.n_seq * kv->per_seq;
+    kvs.cos = kv->cos;
+    kvs.sin = kv->sin;
+    kvs.pos_dev = pos_dev;
+    kvs.per_seq = (int64_t)kv->per_seq;
+    kvs.seq0 = (int32_t)seq0;
+    kvs.n_ctx = (int32_t)d.n_ctx;
+    kvs.n_head = (int32_t)(w[0]->n / d.d);
+    kvs.n_head_kv = (int32_t)d.n_head_kv;
+    kvs.kt = d.layout == ZWG_KV_KT;
+    kvs.d = (int32_t)d.d;
+    return run_q8w_token_step(ctx, x, m, 3, w, bias, nullptr, zwg_ew::kEpiNone, &kvs);
 }
 
 int zwg_linear_epi_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void *w, uint32_t w_type,

@@ -642,4 +642,98 @@ __global__ __launch_bounds__(256) void linear_split_sum_group_kernel(Q8Group grp
     zwg_ew::epilogue_store(&q8_pick(grp.out, set)[le], s, epi);
 }
 
+// The q/k/v group's split sum with the cache append fused into its stores (set 0 q, 1 k, 2 v of a
+// Q8Group; n = heads * D).  Where the split sum writes rows and kv_append_kernel then reads them
+// back, this kernel takes the same sums -- the splits added in split order, then the bias -- and
+// does what the append does with them:
+//   - q and k at their token's position get NeoX rotary positions (pairs (j, j + D/2), rounded
+//     product by product as the reference does, src/llm.zig:221-238) when the cache has tables;
+//   - q is written to q_out; k into the key cache, transposed ([head][dim][n_ctx]) or as a row; v
+//     as a row; a token whose position is outside [0, n_ctx) writes no cache rows and an unrotated q.
+// So the caches and q equal, bit for bit, the group call into rows followed by zwg_kv_append_batch.
+// A thread takes one (token, set, head, 4 dims j .. j+3) and the 4 dims j + D/2 .. of the pair.
+struct Q8KvStore {
+    float *q_out;           // [m][n_head * D]
+    float *k_cache;         // the layer's caches: token i's sequence seq0 + i at + (seq0 + i) * per_seq
+    float *v_cache;
+    const float *cos;       // [n_ctx][D/2], or nullptr: no rotary positions
+    const float *sin;
+    const int32_t *pos_dev; // [m] positions
+    int64_t per_seq;
+    int32_t seq0, n_ctx, n_head, n_head_kv, kt;
+    int32_t d; // the kernel's D (host side: which instantiation)
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void linear_split_sum_qkv_kernel(Q8Group grp, Q8KvStore kv, int32_t m,
+                                                                  int32_t n_split) {
+#pragma clang fp contract(off) // the rotation rounds each product and sum, as the reference does
+    constexpr int HALF = D / 2, QH = D / 8; // pair quads per head
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int per_tok = (kv.n_head + 2 * kv.n_head_kv) * QH;
+    if (e >= (int64_t)m * per_tok) return;
+    const int i = (int)(e / per_tok);
+    int u = (int)(e - (int64_t)i * per_tok);
+    const int set = u < kv.n_head * QH ? 0 : u < (kv.n_head + kv.n_head_kv) * QH ? 1 : 2;
+    u -= set == 0 ? 0 : set == 1 ? kv.n_head * QH : (kv.n_head + kv.n_head_kv) * QH;
+    const int h = u / QH, j = 4 * (u - h * QH);
+    const int32_t n = q8_pick(grp.n, set);
+    const int64_t mn = (int64_t)m * n;
+    const float *part = q8_pick(grp.part, set) + (int64_t)i * n + h * D + j;
+    const float *bias = q8_pick(grp.bias, set);
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    f4 lo = {0, 0, 0, 0}, hi = {0, 0, 0, 0};
+    for (int q0 = 0; q0 < n_split; q0 += kSumBatch) { // as linear_split_sum_group_kernel: loads first
+        f4 vl[kSumBatch], vh[kSumBatch];
+#pragma unroll
+        for (int t = 0; t < kSumBatch; ++t)
+            if (q0 + t < n_split) {
+                vl[t] = *reinterpret_cast<const f4 *>(part + (q0 + t) * mn);
+                vh[t] = *reinterpret_cast<const f4 *>(part + (q0 + t) * mn + HALF);
+            }
+#pragma unroll
+        for (int t = 0; t < kSumBatch; ++t)
+            if (q0 + t < n_split) {
+                lo = q0 + t == 0 ? vl[t] : lo + vl[t];
+                hi = q0 + t == 0 ? vh[t] : hi + vh[t];
+            }
+    }
+    if (bias) {
+        const f4 bl = *reinterpret_cast<const f4 *>(bias + h * D + j);
+        const f4 bh = *reinterpret_cast<const f4 *>(bias + h * D + j + HALF);
+        lo += bl;
+        hi += bh;
+    }
+    const int p = kv.pos_dev[i];
+    const bool live = p >= 0 && p < kv.n_ctx;
+    if (set < 2 && kv.cos && live) {
+        const f4 c = *reinterpret_cast<const f4 *>(kv.cos + (int64_t)p * HALF + j);
+        const f4 s = *reinterpret_cast<const f4 *>(kv.sin + (int64_t)p * HALF + j);
+        const f4 x0 = lo, x1 = hi;
+        lo = x0 * c - x1 * s;
+        hi = x0 * s + x1 * c;
+    }
+    if (set == 0) {
+        float *qr = kv.q_out + (int64_t)i * kv.n_head * D + h * D + j;
+        *reinterpret_cast<f4 *>(qr) = lo;
+        *reinterpret_cast<f4 *>(qr + HALF) = hi;
+        return;
+    }
+    if (!live) return;
+    const int kvw = kv.n_head_kv * D;
+    const int64_t seq = (int64_t)(kv.seq0 + i) * kv.per_seq;
+    if (set == 1 && kv.kt) {
+        float *kc = kv.k_cache + seq + (int64_t)(h * D + j) * kv.n_ctx + p;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            kc[(int64_t)t * kv.n_ctx] = lo[t];
+            kc[(int64_t)(t + HALF) * kv.n_ctx] = hi[t];
+        }
+        return;
+    }
+    float *row = (set == 1 ? kv.k_cache : kv.v_cache) + seq + (int64_t)p * kvw + h * D + j;
+    *reinterpret_cast<f4 *>(row) = lo;
+    *reinterpret_cast<f4 *>(row + HALF) = hi;
+}
+
 } // namespace zwg_lin

@@ -46,6 +46,19 @@ struct zwg_ctx {
     std::string err;
 };
 
+// A device-resident KV cache (zwg_kv_create, kv_cache.hip); the q/k/v projections with the cache
+// append fused into their final store (linear.hip) write into it too.
+struct zwg_kv {
+    zwg_ctx *ctx = nullptr;
+    zwg_kv_desc desc{};
+    uint64_t kvw = 0;     // n_head_kv * d
+    uint64_t per_seq = 0; // floats of one (layer, sequence) K or V cache: n_ctx * kvw
+    float *k = nullptr;   // [layer][sequence][per_seq]
+    float *v = nullptr;
+    float *cos = nullptr; // [n_ctx][d/2] rotary tables when rope_base > 0
+    float *sin = nullptr;
+};
+
 namespace zwg_host {
 
 // Record `msg` as the last error (of ctx, and of this thread) and return ZWG_ERROR.

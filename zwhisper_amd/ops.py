@@ -248,6 +248,34 @@ class Context:
         oa = (_lib._fp * n_w)(*[self._dev_ptr(o, "out") for o in outs])
         self._check(self._L.zwg_linear_q8w_group_dev(self._h, self._dev_ptr(x, "x"), m, n_w, wa, ba, oa))
 
+    def linear_q8w_qkv_kv_dev(self, x, m: int, ws, biases, q_out, kv: "KVCache", layer: int, seq0: int,
+                              pos_dev) -> None:
+        """A decode step's q/k/v projections (resident weights ws = (q, k, v)) with the cache append
+        fused into their store: q (rotated when the cache has rotary tables) to q_out, k and v into
+        kv's rows of sequences seq0 .. seq0 + m - 1 at the positions of pos_dev (a CUDA int32
+        tensor of m entries) -- zwg_linear_q8w_qkv_kv_dev."""
+        import torch
+
+        if len(ws) != 3 or (biases is not None and len(biases) != 3):
+            raise ZwgError("three weight sets (q, k, v), and three biases or None")
+        for w in ws:
+            if not isinstance(w, Q8Resident):
+                raise ZwgError("weights must be Q8Resident (Q8.resident)")
+        if x.numel() < m * ws[0].k or q_out.numel() < m * ws[0].n:
+            raise ZwgError("a tensor is shorter than m, n and k need")
+        if not pos_dev.is_cuda or pos_dev.dtype != torch.int32 or pos_dev.numel() < m:
+            raise ZwgError("pos_dev must be a CUDA int32 tensor with m entries")
+        bias_list = list(biases) if biases is not None else [None] * 3
+        for w, b in zip(ws, bias_list):
+            if b is not None and b.numel() < w.n:
+                raise ZwgError("a bias is shorter than n")
+        self._bind_torch_stream()
+        wa = (ctypes.c_void_p * 3)(*[w.handle for w in ws])
+        ba = (_lib._fp * 3)(*[self._dev_ptr(b, "bias") for b in bias_list])
+        self._check(self._L.zwg_linear_q8w_qkv_kv_dev(self._h, self._dev_ptr(x, "x"), m, wa, ba,
+                                                      self._dev_ptr(q_out, "q_out"), kv._h, layer, seq0,
+                                                      pos_dev.data_ptr()))
+
     def linear_epi_dev(self, x, m: int, k: int, w, bias, n: int, out, epilogue: int, out_stride: int = 0) -> None:
         """linear_dev with an epilogue (_lib.EPI_NONE / EPI_GELU / EPI_ADD) and an output row stride."""
         import torch
