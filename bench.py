@@ -850,6 +850,216 @@ class QkvCacheWorkload:
         self.layers = self.kv = self.x = self.q = self.raw = None
 
 
+class DecoderStepWorkload:
+    """The Whisper text decoder's token step on the device (zwg_decoder_step_dev: Decoder.forward,
+    src/decoder.zig:165-205, one new token in each of m windows decoded in lockstep): embeddings,
+    every layer's self-attention over the window's cache (k and v rows written at its position),
+    cross-attention over its n_audio_ctx cross K/V, MLP, then the final norm and the logits over
+    the vocabulary.  Random int8 block weights of the model's shapes, resident; the cross caches
+    filled once by zwg_decoder_set_audio_dev from a random encoder output (setAudio, timed once
+    and reported beside); window w decodes at position n_kv_w - 1 with the small.en step's seeded
+    self lengths (n_kv ~ U[1, 448]).  A step is one replay of a HIP graph of the call.
+
+    Algorithmic bytes per step: every layer's int8 weights, block scales, biases and norms read
+    once, the token embedding once (the logits' weights), each window's self K/V rows 0..pos and
+    its cross K/V read once per layer and its new k and v rows written, the positional rows read
+    and the logits written.  Beside it the record times the same step composed of the separate
+    calls ("unfused": layer norms, q/k/v + cache, attention, int8 linears with their epilogues),
+    which gives the same results bit for bit."""
+
+    dtype = ("f32 (projections: f32 x int8 block weights on f16 MFMA, x split into two f16 terms; attention: "
+             "f32 FMA decode kernels)")
+
+    def __init__(self, name: str, description: str, torch, ctx, m: int = 32, n_layer: int = 12, ns: int = 768,
+                 n_head: int = 12, n_vocab: int = 51864, n_tctx: int = 448, n_actx: int = 1500):
+        import zwhisper_amd as z
+        from zwhisper_amd.workloads import kv_lengths
+
+        self.name, self.description = name, description
+        self.torch, self.ctx, self.m, self.ns, self.H = torch, ctx, m, ns, n_head
+        self.n_layer, self.n_vocab, self.n_tctx, self.n_actx = n_layer, n_vocab, n_tctx, n_actx
+        g = torch.Generator(device="cuda").manual_seed(0x0A0A)
+
+        def q8(n, k):
+            q = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda", generator=g)
+            sc = torch.rand(n, k // 32, device="cuda", generator=g) * (2.0 / 127 / np.sqrt(k))
+            return z.Q8(q, sc, n, k)
+
+        def vec(n, base=0.0):
+            return base + 0.1 * torch.randn(n, device="cuda", generator=g)
+
+        layers = []
+        for _ in range(n_layer):
+            w = {nm: q8(ns, ns) for nm in ("q_w", "k_w", "v_w", "o_w", "cq_w", "ck_w", "cv_w", "co_w")}
+            w["mlp0_w"], w["mlp1_w"] = q8(4 * ns, ns), q8(ns, 4 * ns)
+            for nm in ("q_b", "v_b", "o_b", "cq_b", "cv_b", "co_b", "mlp1_b"):
+                w[nm] = vec(ns)
+            w["mlp0_b"] = vec(4 * ns)
+            for ln in ("attn_ln", "cross_ln", "mlp_ln"):
+                w[ln + "_w"], w[ln + "_b"] = vec(ns, 1.0), vec(ns)
+            layers.append(w)
+        te = q8(n_vocab, ns)
+        pe = 0.5 * torch.randn(n_tctx, ns, device="cuda", generator=g)
+        self.dec = z.Decoder(ctx, te, pe, vec(ns, 1.0), vec(ns), layers, n_head, n_tctx, n_actx, m)
+        self.host = None  # host copies for the CPU baseline: one window's weights and cross K/V
+        self._host_src = (te, pe, layers)
+        enc = torch.randn(m, n_actx, ns, device="cuda", generator=g)
+        self.dec.set_audio(enc, m, 0)  # first call: kernels loaded
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        self.dec.set_audio(enc, m, 0)
+        e1.record()
+        torch.cuda.synchronize()
+        self.set_audio_ms = e0.elapsed_time(e1)
+        self.enc0 = enc[0].cpu().numpy()
+        n_kv = kv_lengths(3)[:m].astype(np.int64)
+        self.pos = torch.from_numpy((n_kv - 1).astype(np.int32)).cuda()
+        self.tok = torch.randint(0, n_vocab, (m,), dtype=torch.int32, device="cuda", generator=g)
+        self.logits = torch.empty(m, n_vocab, device="cuda")
+        wb = sum(w.n * w.k * 1.125 for lw in layers for nm, w in lw.items() if nm not in ("ck_w", "cv_w")
+                 and isinstance(w, z.Q8))
+        vb = 4.0 * sum(t.numel() for lw in layers for nm, t in lw.items() if not isinstance(t, z.Q8)
+                       and nm not in ("cv_b",))
+        kvb = 4.0 * ns * n_layer * (2 * float(n_kv.sum()) + 2 * m * n_actx + 2 * m)
+        self.work = float(wb + vb + te.n * te.k * 1.125 + kvb + 4.0 * m * ns * 2 + 4.0 * m * n_vocab)
+        self.n_kv = n_kv
+        # the unfused step: the separate calls over the same weights, its own caches (cross K/V by
+        # the same projections of the same encoder output)
+        self.self_kv = z.KVCache(ctx, n_layer, m, n_tctx, n_head, ns // n_head)
+        self.cross_kv = z.KVCache(ctx, n_layer, m, n_actx, n_head, ns // n_head)
+        for li, L in enumerate(self.dec.layer_refs):
+            k, v = self.cross_kv.ptrs(li, 0)
+            ctx.linear_q8w_dev(enc, m * n_actx, L["ck_w"], None, k)
+            ctx.linear_q8w_dev(enc, m * n_actx, L["cv_w"], L["cv_b"], v)
+        del enc
+        self.X, self.A, self.Q, self.T = (torch.empty(m, ns, device="cuda") for _ in range(4))
+        self.Hd = torch.empty(m, 4 * ns, device="cuda")
+        # the embedding rows te.row(tok) + pe[pos], f32 products and sums as the fused kernel's
+        tl = self.tok.long()
+        self.E = te.q[tl].float() * te.scales[tl].repeat_interleave(32, dim=1) + pe[self.pos.long()]
+        self.n_kv_t = (self.pos + 1).to(torch.int32)
+        self.graphs = {}
+        for mode in ("fused", "unfused"):
+            self._run(mode)
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                self._run(mode)
+            self.graphs[mode] = gr
+        torch.cuda.synchronize()
+
+    def _run(self, mode: str):
+        import zwhisper_amd as z
+        from zwhisper_amd import _lib
+
+        if mode == "fused":
+            self.dec.step(self.tok, self.pos, self.logits, 0)
+            return
+        ctx, dec, m, ns, H = self.ctx, self.dec, self.m, self.ns, self.H
+        X, A, Q, T, Hd = self.X, self.A, self.Q, self.T, self.Hd
+        X.copy_(self.E)
+        L0 = dec.layer_refs[0]
+        ctx.layer_norm_dev(X, m, ns, L0["attn_ln_w"], L0["attn_ln_b"], 1e-5, A)
+        sh_s = z.AttnShape(1, self.n_tctx, H, H, ns // H, ns, ns, ns, False)
+        sh_c = z.AttnShape(1, self.n_actx, H, H, ns // H, ns, ns, ns, False)
+        ps, pc = self.self_kv.info.seq_stride, self.cross_kv.info.seq_stride
+        for li, L in enumerate(dec.layer_refs):
+            ctx.linear_q8w_qkv_kv_dev(A, m, [L["q_w"], L["k_w"], L["v_w"]], [L["q_b"], None, L["v_b"]], Q,
+                                      self.self_kv, li, 0, self.pos)
+            k, v = self.self_kv.ptrs(li, 0)
+            ctx.attention_batch_dev(Q, k, v, sh_s, T, m, ns, ps, ps, ns, self.n_kv_t)
+            ctx.linear_q8w_epi_dev(T, m, L["o_w"], L["o_b"], X, _lib.EPI_ADD)
+            ctx.layer_norm_dev(X, m, ns, L["cross_ln_w"], L["cross_ln_b"], 1e-5, A)
+            ctx.linear_q8w_dev(A, m, L["cq_w"], L["cq_b"], Q)
+            k, v = self.cross_kv.ptrs(li, 0)
+            ctx.attention_batch_dev(Q, k, v, sh_c, T, m, ns, pc, pc, ns)
+            ctx.linear_q8w_epi_dev(T, m, L["co_w"], L["co_b"], X, _lib.EPI_ADD)
+            ctx.layer_norm_dev(X, m, ns, L["mlp_ln_w"], L["mlp_ln_b"], 1e-5, A)
+            ctx.linear_q8w_epi_dev(A, m, L["mlp0_w"], L["mlp0_b"], Hd, _lib.EPI_GELU)
+            ctx.linear_q8w_epi_dev(Hd, m, L["mlp1_w"], L["mlp1_b"], X, _lib.EPI_ADD)
+            last = li + 1 == self.n_layer
+            ctx.layer_norm_dev(X, m, ns, dec.ln_w if last else dec.layer_refs[li + 1]["attn_ln_w"],
+                               dec.ln_b if last else dec.layer_refs[li + 1]["attn_ln_b"], 1e-5, A)
+        ctx.linear_q8w_dev(A, m, dec.te, None, self.logits_u)
+
+    @property
+    def logits_u(self):
+        if not hasattr(self, "_lu"):
+            self._lu = self.torch.empty_like(self.logits)
+        return self._lu
+
+    def step(self, i: int):
+        self.graphs["fused"].replay()
+
+    def extra_record(self, steps: int) -> dict:
+        """The unfused step timed as the fused one, the bit-for-bit check of the two, tokens/s and
+        the setAudio time."""
+        torch = self.torch
+        for _ in range(5):
+            self.graphs["unfused"].replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            self.graphs["unfused"].replay()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        self.graphs["fused"].replay()
+        torch.cuda.synchronize()
+        same = bool(torch.equal(self.logits, self.logits_u))
+        return {"unfused": {"kernel_ms_per_step": ms, "logits_equal_bitwise": same,
+                            "note": "the same step as separate calls (layer norms, q/k/v + cache, attention, "
+                                    "int8 linears with add / GELU epilogues), one HIP-graph replay per step"},
+                "tokens_per_step": self.m,
+                "set_audio_ms": self.set_audio_ms,
+                "set_audio_note": f"cross K/V of {self.m} windows x {self.n_layer} layers from the encoder output "
+                                  f"({self.m} x {self.n_actx} rows x 2 projections per layer), one call"}
+
+    def cpu_baseline(self, threads: int) -> dict:
+        """The oracle's Decoder.forward (Oracle.decoder_forward: ops.linear over Q8, layerNorm, gelu,
+        attention, the reference's steps) for one window's token, all layers and the logits."""
+        import oracle
+
+        te, pe, layers = self._host_src
+        w0 = 0
+        hl = [{nm: ((t.q.cpu().numpy(), t.scales.cpu().numpy()) if hasattr(t, "scales") else t.cpu().numpy())
+               for nm, t in lw.items()} for lw in layers]
+        dec = {"te": (te.q.cpu().numpy(), te.scales.cpu().numpy()), "pe": pe.cpu().numpy(),
+               "ln_w": self.dec.ln_w.cpu().numpy(), "ln_b": self.dec.ln_b.cpu().numpy(), "n_head": self.H,
+               "layers": hl}
+        o = oracle.Oracle(threads)
+        cross = o.decoder_set_audio(self.enc0, self.n_actx, self.ns, hl)
+        cache = {"k": np.zeros((self.n_layer, self.n_tctx, self.ns), np.float32),
+                 "v": np.zeros((self.n_layer, self.n_tctx, self.ns), np.float32),
+                 "ck": np.stack([c[0] for c in cross]), "cv": np.stack([c[1] for c in cross])}
+        pos = int(self.n_kv[w0]) - 1
+        tok = int(self.tok[w0].item())
+
+        def run():
+            o.decoder_forward(dec, cache, tok, pos)
+
+        best, mean, runs = time_cpu(run, 3)
+        o.close()
+        # one window's token: all the weights, and that window's own cache rows
+        kv_all = 4.0 * self.ns * self.n_layer * (2 * float(self.n_kv.sum()) + 2 * self.m * self.n_actx + 2 * self.m)
+        kv_one = 4.0 * self.ns * self.n_layer * (2 * (pos + 1) + 2 * self.n_actx + 2)
+        work1 = self.work - kv_all - 4.0 * self.m * (2 * self.ns + self.n_vocab) + kv_one + 4.0 * (2 * self.ns + self.n_vocab)
+        return {"value": 1.0 / best, "unit": "tokens/s", "cores": o.threads, "kind": "port",
+                "bytes_per_token": work1, "gb_per_s": work1 / best / 1e9,
+                "sample": f"one window's token (position {pos}) through all {self.n_layer} layers and the logits, "
+                          "as the reference decodes a window; oracle Decoder.forward over oracle/attn_oracle.c; "
+                          + cpu_timing(best, mean, runs), "seconds": best}
+
+    def free(self):
+        self.graphs = None
+        self.dec.close()
+        self.self_kv.close()
+        self.cross_kv.close()
+        self.dec = self.self_kv = self.cross_kv = self._host_src = None
+
+
 def q8_workloads(torch, ctx):
     """(name, constructor) of the int8 decode-step measurements."""
     qwen_layer = [(1536, 1536, True), (1536, 256, True), (1536, 256, True), (1536, 1536, False),
@@ -873,6 +1083,10 @@ def q8_workloads(torch, ctx):
         "of all 12 layers with the new k and v rows written into the row-major device caches "
         "(src/decoder.zig:181-183), int8 block weights", torch, ctx, 32, 768, 12, 12, 12, 64, False, 0.0, 448,
         (True, False, True))
+    yield "small_dec_step_x32", lambda: DecoderStepWorkload(
+        "small_dec_step_x32", "Whisper small.en decoder token step, 32 windows in lockstep (src/decoder.zig:165-205): "
+        "embeddings, 12 layers of self-attention over each window's cache (n_kv ~ U[1, 448]), cross-attention over "
+        "1500 audio frames and MLP, int8 block weights, then the 51864-token logits", torch, ctx)
     yield "qwen15_qkv_cache_x64", lambda: QkvCacheWorkload(
         "qwen15_qkv_cache_x64", "Qwen2.5-1.5B decode step, 64 sequences: q/k/v projections of all 28 layers, "
         "q and k rotated (base 1e6), k scattered into the transposed device cache and v into its rows "
@@ -1164,7 +1378,7 @@ def _say(name: str, res: dict, peak_name: str) -> None:
 EXTRAS = ("qwen05_prefill_8x256", "small_dec_kv_append_x32", "qwen15_kv_append_x64", "qwen05_prefill_kv_append",
           "base_enc_linear_x16",
           "base_enc_layer_x16", "qwen15_logits_q8_x64", "qwen15_decode_q8_linear_x64", "small_dec_q8_linear_x32",
-          "small_dec_qkv_cache_x32", "qwen15_qkv_cache_x64")
+          "small_dec_qkv_cache_x32", "qwen15_qkv_cache_x64", "small_dec_step_x32")
 
 
 def run_extra(name: str, torch, ctx, args, threads: int) -> dict:
@@ -1254,13 +1468,15 @@ def run_extra(name: str, torch, ctx, args, threads: int) -> dict:
                "ms_per_step": r["ms_per_step"], "kernel_ms_mean": r["kernel_ms_mean"],
                "kernel_ms_median": r["kernel_ms_median"], "kernel_ms_min": r["kernel_ms_min"],
                "algorithmic_work_per_step": wl.work,
-               "dtype": "f32 activations x int8 block weights, f32 accumulation (f16 MFMA, x split into two "
+               "dtype": getattr(wl, "dtype", None) or "f32 activations x int8 block weights, f32 accumulation (f16 MFMA, x split into two "
                         "f16 terms, block sums scaled in f32)",
                "roofline": {"bound": "hbm", "achieved": achieved / 1e9, "peak": PEAK_HBM / 1e9, "unit": "GB/s",
                             "frac": achieved / PEAK_HBM, "traffic": traffic_for(wl.name)},
                "cold": cold(r, wl.work, "GB/s", PEAK_HBM)}
         if hasattr(wl, "extra_record"):
             res.update(wl.extra_record(args.steps))
+        if "tokens_per_step" in res:
+            res["tokens_per_s"] = res["tokens_per_step"] / (r["ms_per_step"] * 1e-3)
         if not args.no_cpu:
             res["cpu_baseline"] = wl.cpu_baseline(threads)
         wl.free()

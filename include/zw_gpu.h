@@ -442,6 +442,74 @@ uint64_t zwg_encoder_layer_scratch(uint64_t n_rows, uint64_t n_state);
 int zwg_encoder_layer_dev(zwg_ctx *ctx, float *x, uint64_t n_windows, uint64_t n_ctx, uint64_t n_state,
                           uint64_t n_head, const zwg_enc_layer *w, float *scratch);
 
+/*
+ * The Whisper text decoder on the device: Decoder.setAudio (src/decoder.zig:151-159) and
+ * Decoder.forward (src/decoder.zig:165-205) for a batch of windows decoded in lockstep, one new
+ * token per window per step.  The weights are the tensors src/decoder.zig:96-131 loads: int8
+ * block matrices as resident zwg_q8w [out][in], f32 device vectors for norms and biases (a NULL
+ * bias adds nothing).  The windows are the sequences of two zwg_kv caches, both ZWG_KV_ROW with
+ * n_head_kv = n_head, d = n_state / n_head (32, 64 or 128) and no rotary positions: self_kv with
+ * n_ctx = n_text_ctx (the reference's cache_k / cache_v, src/decoder.zig:39-40), cross_kv with
+ * n_ctx = n_audio_ctx (cross_k / cross_v, :41-42); both hold at least n_layer layers.
+ * n_state: a multiple of 4, above 256 and at most 2048.
+ */
+typedef struct zwg_dec_layer {
+    const float *attn_ln_w, *attn_ln_b; /* [n_state] */
+    const zwg_q8w *q_w;                 /* [n_state][n_state] */
+    const float *q_b;
+    const zwg_q8w *k_w; /* no bias */
+    const zwg_q8w *v_w;
+    const float *v_b;
+    const zwg_q8w *o_w;
+    const float *o_b;
+    const float *cross_ln_w, *cross_ln_b;
+    const zwg_q8w *cq_w;
+    const float *cq_b;
+    const zwg_q8w *ck_w; /* no bias; used by zwg_decoder_set_audio_dev */
+    const zwg_q8w *cv_w;
+    const float *cv_b;
+    const zwg_q8w *co_w;
+    const float *co_b;
+    const float *mlp_ln_w, *mlp_ln_b;
+    const zwg_q8w *mlp0_w; /* [4 n_state][n_state] */
+    const float *mlp0_b;
+    const zwg_q8w *mlp1_w; /* [n_state][4 n_state] */
+    const float *mlp1_b;
+} zwg_dec_layer;
+
+typedef struct zwg_decoder {
+    uint64_t n_vocab, n_state, n_head, n_layer;
+    const zwg_q8w *te;           /* token embedding [n_vocab][n_state], also the logits' weights */
+    const float *pe;             /* positional embedding [n_text_ctx][n_state] */
+    const float *ln_w, *ln_b;    /* the final layer norm */
+    const zwg_dec_layer *layers; /* host array of n_layer */
+    zwg_kv *self_kv;
+    zwg_kv *cross_kv;
+} zwg_decoder;
+
+/* setAudio for windows seq0 .. seq0 + n_windows - 1: enc [n_windows][n_audio_ctx][n_state] (the
+ * encoder's output, device) projected by every layer's ck_w and cv_w (+ cv_b) straight into the
+ * windows' cross caches.  Asynchronous. */
+int zwg_decoder_set_audio_dev(zwg_ctx *ctx, const zwg_decoder *dec, const float *enc, uint64_t n_windows,
+                              uint64_t seq0);
+
+/* Floats of scratch a step over m windows needs (the reference's x, x_ln, q, attn and hidden
+ * buffers, src/decoder.zig:57-63, and the self-attention key counts). */
+uint64_t zwg_decoder_scratch(uint64_t m, uint64_t n_state);
+
+/* forward for windows seq0 .. seq0 + m - 1 (m <= 64), window i taking token tokens[i] at
+ * position pos[i] (its n_past; tokens, pos: device int32 [m]): embeddings, every layer (its k and
+ * v rows written into the self cache at pos[i], self-attention over the window's pos[i] + 1
+ * cached keys, cross-attention over all n_audio_ctx keys), the final layer norm and the logits
+ * [m][n_vocab] = ln(x) . te^T.  A position outside [0, n_text_ctx) writes no cache rows and its
+ * window's logits are meaningless; a token outside [0, n_vocab) embeds as a zero row.  The work
+ * the reference does, fused where it saves launches (layer norms into the residual projections'
+ * split sums, the cache writes into the q/k/v projections'), with results equal bit for bit to
+ * the same step composed of zwg_layer_norm_dev, zwg_linear_q8w_qkv_kv_dev,
+ * zwg_attention_batch_dev and zwg_linear_q8w_epi_dev calls.  Asynchronous. */
+int zwg_decoder_step_dev(zwg_ctx *ctx, const zwg_decoder *dec, const int32_t *tokens, const int32_t *pos, uint64_t m,
+                         uint64_t seq0, float *logits, float *scratch);
+
 int zwg_version(void); /* ZWG_VERSION */
 
 #ifdef __cplusplus

@@ -285,6 +285,51 @@ class Oracle:
         x += self.linear_f16(h, n_ctx, 4 * ns, w["mlp1_w"], w["mlp1_b"], ns).reshape(n_ctx, ns)
         return x
 
+    def decoder_set_audio(self, enc, n_audio_ctx: int, n_state: int, layers) -> list:
+        """Decoder.setAudio (src/decoder.zig:151-159) for one window: per layer (cross_k, cross_v)
+        [n_audio_ctx][n_state] = enc . ck^T and enc . cv^T + cv_b.  Matrices are (q, scales) pairs
+        of gemm.Q8 (int8 [n][k], f32 [n][k / 32])."""
+        ns = n_state
+        out = []
+        for w in layers:
+            ck = self.linear_q8(enc, n_audio_ctx, ns, *w["ck_w"], None, ns).reshape(n_audio_ctx, ns)
+            cv = self.linear_q8(enc, n_audio_ctx, ns, *w["cv_w"], w["cv_b"], ns).reshape(n_audio_ctx, ns)
+            out.append((ck, cv))
+        return out
+
+    def decoder_forward(self, dec: dict, cache: dict, token: int, pos: int) -> np.ndarray:
+        """Decoder.forward (src/decoder.zig:165-205) for one window and one token at position pos
+        (n_past), as the reference runs it: x = te.row(token) + pe[pos] (src/gemm.zig:257-265,
+        ops.add); per layer the pre-norm self-attention over the cache (k and v rows written at pos,
+        then attention causal over pos + 1 keys), the cross-attention over the window's cross K/V
+        and the MLP, each added to x; then the final layer norm and logits = ln(x) . te^T.
+        dec: {"te": (q, scales) [n_vocab][n_state], "pe", "ln_w", "ln_b", "n_head", "layers": [dict
+        of the layer's tensors, matrices as (q, scales)]}; cache: {"k", "v": [n_layer][n_ctx][ns],
+        "ck", "cv": [n_layer][n_audio_ctx][ns]} (k and v updated at row pos).  Returns the logits."""
+        te_q, te_s = dec["te"]
+        n_vocab, ns = te_q.shape
+        H = dec["n_head"]
+        lin = lambda a, w, b, n, k: self.linear_q8(a, 1, k, *w, b, n)  # noqa: E731
+        row = te_q[token].astype(np.float32).reshape(-1, Q8_BLOCK) * te_s[token].astype(np.float32)[:, None]
+        x = (row.reshape(-1) + dec["pe"][pos]).astype(np.float32)
+        n_audio = cache["ck"].shape[1]
+        for li, w in enumerate(dec["layers"]):
+            xl = self.layer_norm(x, 1, ns, w["attn_ln_w"], w["attn_ln_b"])
+            q = lin(xl, w["q_w"], w["q_b"], ns, ns)
+            cache["k"][li][pos] = lin(xl, w["k_w"], None, ns, ns)
+            cache["v"][li][pos] = lin(xl, w["v_w"], w["v_b"], ns, ns)
+            att = self.attention(q, cache["k"][li][:pos + 1], cache["v"][li][:pos + 1], 1, pos + 1, ns, H, True)
+            x = x + lin(att, w["o_w"], w["o_b"], ns, ns)
+            xl = self.layer_norm(x, 1, ns, w["cross_ln_w"], w["cross_ln_b"])
+            q = lin(xl, w["cq_w"], w["cq_b"], ns, ns)
+            att = self.attention(q, cache["ck"][li], cache["cv"][li], 1, n_audio, ns, H, False)
+            x = x + lin(att, w["co_w"], w["co_b"], ns, ns)
+            xl = self.layer_norm(x, 1, ns, w["mlp_ln_w"], w["mlp_ln_b"])
+            h = self.gelu(lin(xl, w["mlp0_w"], w["mlp0_b"], 4 * ns, ns))
+            x = x + lin(h, w["mlp1_w"], w["mlp1_b"], ns, 4 * ns)
+        xl = self.layer_norm(x, 1, ns, dec["ln_w"], dec["ln_b"])
+        return self.linear_q8(xl, 1, ns, te_q, te_s, None, n_vocab)
+
     def attention(self, q, k, v, n_q, n_kv, n_state, n_head, causal, out=None) -> np.ndarray:
         """ops.attention (src/ops.zig:593-605)."""
         q = np.ascontiguousarray(q, dtype=np.float32).reshape(-1)

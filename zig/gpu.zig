@@ -177,6 +177,53 @@ pub extern "zwgpu" fn zwg_encoder_layer_scratch(n_rows: u64, n_state: u64) u64;
 pub extern "zwgpu" fn zwg_encoder_layer_dev(ctx: *Ctx, x: [*]f32, n_windows: u64, n_ctx: u64, n_state: u64,
     n_head: u64, w: *const EncLayer, scratch: [*]f32) c_int;
 
+// ---- the Whisper text decoder: setAudio and forward for windows decoded in lockstep
+
+pub const DecLayer = extern struct {
+    attn_ln_w: [*]const f32,
+    attn_ln_b: [*]const f32,
+    q_w: *const Q8w,
+    q_b: ?[*]const f32,
+    k_w: *const Q8w,
+    v_w: *const Q8w,
+    v_b: ?[*]const f32,
+    o_w: *const Q8w,
+    o_b: ?[*]const f32,
+    cross_ln_w: [*]const f32,
+    cross_ln_b: [*]const f32,
+    cq_w: *const Q8w,
+    cq_b: ?[*]const f32,
+    ck_w: *const Q8w,
+    cv_w: *const Q8w,
+    cv_b: ?[*]const f32,
+    co_w: *const Q8w,
+    co_b: ?[*]const f32,
+    mlp_ln_w: [*]const f32,
+    mlp_ln_b: [*]const f32,
+    mlp0_w: *const Q8w,
+    mlp0_b: ?[*]const f32,
+    mlp1_w: *const Q8w,
+    mlp1_b: ?[*]const f32,
+};
+pub const Decoder = extern struct {
+    n_vocab: u64,
+    n_state: u64,
+    n_head: u64,
+    n_layer: u64,
+    te: *const Q8w,
+    pe: [*]const f32,
+    ln_w: [*]const f32,
+    ln_b: [*]const f32,
+    layers: [*]const DecLayer,
+    self_kv: *Kv,
+    cross_kv: *Kv,
+};
+pub extern "zwgpu" fn zwg_decoder_set_audio_dev(ctx: *Ctx, dec: *const Decoder, enc: [*]const f32, n_windows: u64,
+    seq0: u64) c_int;
+pub extern "zwgpu" fn zwg_decoder_scratch(m: u64, n_state: u64) u64;
+pub extern "zwgpu" fn zwg_decoder_step_dev(ctx: *Ctx, dec: *const Decoder, tokens: [*]const i32, pos: [*]const i32,
+    m: u64, seq0: u64, logits: [*]f32, scratch: [*]f32) c_int;
+
 // ---- the calling thread's context
 
 /// One context per thread that calls into ops (the zw_* handles are per thread too,

@@ -73,6 +73,31 @@ class EncLayerC(ctypes.Structure):
         "mlp0_b", "mlp1_w", "mlp1_b")]
 
 
+DEC_LAYER_FIELDS = ("attn_ln_w", "attn_ln_b", "q_w", "q_b", "k_w", "v_w", "v_b", "o_w", "o_b", "cross_ln_w",
+                    "cross_ln_b", "cq_w", "cq_b", "ck_w", "cv_w", "cv_b", "co_w", "co_b", "mlp_ln_w", "mlp_ln_b",
+                    "mlp0_w", "mlp0_b", "mlp1_w", "mlp1_b")
+
+
+class DecLayerC(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_void_p) for name in DEC_LAYER_FIELDS]
+
+
+class DecoderC(ctypes.Structure):
+    _fields_ = [
+        ("n_vocab", _u64),
+        ("n_state", _u64),
+        ("n_head", _u64),
+        ("n_layer", _u64),
+        ("te", ctypes.c_void_p),
+        ("pe", ctypes.c_void_p),
+        ("ln_w", ctypes.c_void_p),
+        ("ln_b", ctypes.c_void_p),
+        ("layers", ctypes.POINTER(DecLayerC)),
+        ("self_kv", ctypes.c_void_p),
+        ("cross_kv", ctypes.c_void_p),
+    ]
+
+
 class KVDescC(ctypes.Structure):
     _fields_ = [
         ("n_layer", _u64),
@@ -202,6 +227,12 @@ def lib() -> ctypes.CDLL:
     L.zwg_encoder_layer_scratch.argtypes = [_u64, _u64]
     L.zwg_encoder_layer_dev.restype = c_int
     L.zwg_encoder_layer_dev.argtypes = [vp, _fp, _u64, _u64, _u64, _u64, ctypes.POINTER(EncLayerC), _fp]
+    L.zwg_decoder_set_audio_dev.restype = c_int
+    L.zwg_decoder_set_audio_dev.argtypes = [vp, ctypes.POINTER(DecoderC), _fp, _u64, _u64]
+    L.zwg_decoder_scratch.restype = _u64
+    L.zwg_decoder_scratch.argtypes = [_u64, _u64]
+    L.zwg_decoder_step_dev.restype = c_int
+    L.zwg_decoder_step_dev.argtypes = [vp, ctypes.POINTER(DecoderC), vp, vp, _u64, _u64, _fp, _fp]
     for name in ("zwg_linear_q8", "zwg_linear_q8_dev"):
         getattr(L, name).restype = c_int
         getattr(L, name).argtypes = [vp, _fp, _u64, _u64, vp, _fp, _fp, _u64, _fp]

@@ -26,13 +26,8 @@ namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kNormRegs = 8; // float4 per lane held in registers: rows up to 64 * 4 * 8 = 2048
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
+using zwg_ew::kNormRegs;
+using zwg_ew::wave_sum;
 
 // 4 waves per workgroup, one row per wave.
 __global__ __launch_bounds__(256) void layer_norm_kernel(const float *x, const float *w, const float *b, float *out,
@@ -46,39 +41,12 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(const float *x, const f
     const float fn = (float)n;
     if (n4 <= 64 * kNormRegs) {
         f32x4 v[kNormRegs];
-        float s = 0.f;
 #pragma unroll
         for (int i = 0; i < kNormRegs; ++i) {
             const int c = lane + 64 * i;
             v[i] = c < n4 ? reinterpret_cast<const f32x4 *>(xr)[c] : (f32x4){0.f, 0.f, 0.f, 0.f};
-            s += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
         }
-        const float mean = wave_sum(s) / fn;
-        float q = 0.f;
-#pragma unroll
-        for (int i = 0; i < kNormRegs; ++i) {
-            const int c = lane + 64 * i;
-            if (c < n4) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const float d = v[i][e] - mean;
-                    q = __builtin_fmaf(d, d, q);
-                }
-            }
-        }
-        const float inv = 1.0f / sqrtf(wave_sum(q) / fn + eps);
-#pragma unroll
-        for (int i = 0; i < kNormRegs; ++i) {
-            const int c = lane + 64 * i;
-            if (c < n4) {
-                const f32x4 wv = reinterpret_cast<const f32x4 *>(w)[c];
-                const f32x4 bv = reinterpret_cast<const f32x4 *>(b)[c];
-                f32x4 o;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = __builtin_fmaf((v[i][e] - mean) * inv, wv[e], bv[e]);
-                reinterpret_cast<f32x4 *>(orow)[c] = o;
-            }
-        }
+        zwg_ew::layer_norm_regs<kNormRegs>(v, lane, n4, w, b, eps, orow);
         return;
     }
     float s = 0.f;

@@ -34,6 +34,58 @@ __device__ __forceinline__ void epilogue_store(float *p, float v, uint32_t epi) 
     *p = v;
 }
 
+typedef float ew_f32x4 __attribute__((ext_vector_type(4)));
+
+// float4 per lane a row held in registers may take: rows up to 64 * 4 * 8 = 2048 floats
+constexpr int kNormRegs = 8;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// ops.layerNormEps (src/ops.zig:355-381) of one row of n = 4 n4 floats held by one wave: lane l
+// holds float4 c = l + 64 i in v[i] (R >= ceil(n4 / 64); zeros past n4).  mean = sum / n, var =
+// sum((x - mean)^2) / n (the reference's two passes), inv = 1 / sqrt(var + eps), out = fma((x -
+// mean) * inv, w, b).  The sums are reduced across the wave by butterfly, so their rounding order
+// differs from the reference's 16-lane vector order (a few f32 ulps).  Every kernel that normalises
+// a row goes through this function, so a fused norm equals the separate one bit for bit.
+template <int R>
+__device__ __forceinline__ void layer_norm_regs(const ew_f32x4 (&v)[R], int lane, int n4, const float *w,
+                                                const float *b, float eps, float *orow) {
+    const float fn = (float)(4 * n4);
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < R; ++i) s += (v[i][0] + v[i][1]) + (v[i][2] + v[i][3]);
+    const float mean = wave_sum(s) / fn;
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int c = lane + 64 * i;
+        if (c < n4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float d = v[i][e] - mean;
+                q = __builtin_fmaf(d, d, q);
+            }
+        }
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(q) / fn + eps);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int c = lane + 64 * i;
+        if (c < n4) {
+            const ew_f32x4 wv = reinterpret_cast<const ew_f32x4 *>(w)[c];
+            const ew_f32x4 bv = reinterpret_cast<const ew_f32x4 *>(b)[c];
+            ew_f32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = __builtin_fmaf((v[i][e] - mean) * inv, wv[e], bv[e]);
+            reinterpret_cast<ew_f32x4 *>(orow)[c] = o;
+        }
+    }
+}
+
 } // namespace zwg_ew
 
 namespace zwg_host {

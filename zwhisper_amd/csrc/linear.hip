@@ -214,11 +214,47 @@ constexpr int q8p_waves() { return MT == 1 ? ZWG_Q8P_WAVES_32 : ZWG_Q8P_WAVES; }
 #endif
 
 
+// Row kernels of n <= 2048 floats (a wave per row, n / 256 float4 per lane, rounded up)
+template <template <int> class K, typename... Args>
+hipError_t launch_rows(int32_t n, int32_t m, hipStream_t stream, Args... args) {
+    const int R = (n / 4 + 63) / 64;
+    const dim3 grid((unsigned)((m + 3) / 4)), block(256);
+    switch (R) {
+    case 1: K<1>::launch(grid, block, stream, args...); break;
+    case 2: K<2>::launch(grid, block, stream, args...); break;
+    case 3: K<3>::launch(grid, block, stream, args...); break;
+    case 4: K<4>::launch(grid, block, stream, args...); break;
+    case 5: K<5>::launch(grid, block, stream, args...); break;
+    case 6: K<6>::launch(grid, block, stream, args...); break;
+    case 7: K<7>::launch(grid, block, stream, args...); break;
+    case 8: K<8>::launch(grid, block, stream, args...); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+template <int R>
+struct AddLnRows {
+    static void launch(dim3 g, dim3 b, hipStream_t st, const float *part, const float *bias, zwg_lin::Q8ResLn r,
+                       int32_t m, int32_t n, int32_t n_split) {
+        zwg_lin::linear_split_sum_add_ln_kernel<R><<<g, b, 0, st>>>(part, bias, r, m, n, n_split);
+    }
+};
+template <int R>
+struct EmbedLnRows {
+    static void launch(dim3 g, dim3 b, hipStream_t st, zwg_lin::Q8Packed te, int32_t n_vocab, const int32_t *tok,
+                       const float *pe, const int32_t *pos, int32_t pe_rows, int32_t m, int32_t n, float *x,
+                       zwg_lin::Q8ResLn r) {
+        zwg_lin::q8p_embed_ln_kernel<R><<<g, b, 0, st>>>(te, n_vocab, tok, pe, pos, pe_rows, m, n, x, r);
+    }
+};
+
 // kvs (a q/k/v group, sets 0, 1, 2): the split sum stores into q_out and the KV cache
-// (linear_split_sum_qkv_kernel), so the call is always split, in two at least.
+// (linear_split_sum_qkv_kernel), so the call is always split, in two at least.  resln (one set,
+// n <= 2048): the split sum adds into the residual stream and normalises the rows
+// (linear_split_sum_add_ln_kernel), likewise always split.
 template <int MT>
 int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
-                  const zwg_lin::Q8KvStore *kvs = nullptr) {
+                  const zwg_lin::Q8KvStore *kvs = nullptr, const zwg_lin::Q8ResLn *resln = nullptr) {
     constexpr int kQ8pWaves = q8p_waves<MT>();
     zwg_lin::Q8Args a = base;
     const uint64_t m = (uint64_t)a.m;
@@ -246,12 +282,12 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
     if (part_off > ctx->workspace_bytes) return fail(ctx, "workspace too small for this linear call");
     int n_split = 1;
     if (split_k) n_split = (int)std::min<int64_t>(n_chunks, (ZWG_Q8P_SPLIT_TARGET + gx - 1) / gx);
-    if (kvs) {
-        if (n_chunks < 2) return fail(ctx, "the cache-writing q/k/v call needs k above 256 (its sum is a k split)");
+    if (kvs || resln) {
+        if (n_chunks < 2) return fail(ctx, "the fused split-sum calls need k above 256 (their sum is a k split)");
         n_split = std::max(n_split, 2);
     }
     while (n_split > 1 && part_off + (uint64_t)n_split * m * n_tot * 4 > ctx->workspace_bytes) --n_split;
-    if (kvs && n_split < 2) return fail(ctx, "workspace too small for this q/k/v call's partial sums");
+    if ((kvs || resln) && n_split < 2) return fail(ctx, "workspace too small for this call's partial sums");
     a.chunks_per_split = (n_chunks + n_split - 1) / n_split;
     n_split = (n_chunks + a.chunks_per_split - 1) / a.chunks_per_split; // no empty splits
     a.n_split = n_split;
@@ -294,6 +330,10 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
             zwg_lin::linear_split_sum_qkv_kernel<32><<<blocks_for(threads, bs), bs, 0, ctx->stream>>>(g, *kvs, a.m, n_split);
         e = hipGetLastError();
         if (e != hipSuccess) return fail_hip(ctx, "q/k/v cache split-sum kernel launch", e);
+    } else if (resln) {
+        e = launch_rows<AddLnRows>(g.n[0], a.m, ctx->stream, (const float *)g.part[0], g.bias[0], *resln, a.m, g.n[0],
+                                   n_split);
+        if (e != hipSuccess) return fail_hip(ctx, "split-sum + residual + layer norm kernel launch", e);
     } else if (n_split > 1) {
         const int64_t elems = (int64_t)(m * n_tot);
         const int bs = small_block(elems);
@@ -465,7 +505,7 @@ void detach_q8w(void *obj) {
 // callers).
 int run_q8w_token_step(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t n_w, const zwg_q8w *const *w,
                        const float *const *bias, float *const *out, uint32_t epi,
-                       const zwg_lin::Q8KvStore *kvs = nullptr) {
+                       const zwg_lin::Q8KvStore *kvs = nullptr, const zwg_lin::Q8ResLn *resln = nullptr) {
     zwg_lin::Q8Args a{};
     a.x = x;
     a.m = (int32_t)m;
@@ -482,7 +522,7 @@ int run_q8w_token_step(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t n_w, c
         g.bias[j] = bias ? bias[j] : nullptr;
         g.out[j] = out ? out[j] : nullptr;
     }
-    return m > 32 ? run_q8p_group<2>(ctx, a, g, kvs) : run_q8p_group<1>(ctx, a, g, kvs);
+    return m > 32 ? run_q8p_group<2>(ctx, a, g, kvs, resln) : run_q8p_group<1>(ctx, a, g, kvs, resln);
 }
 
 int run_linear_q8w(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, const float *bias, float *out,
@@ -517,6 +557,91 @@ int run_linear_q8w(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, c
 }
 
 } // namespace
+
+int zwg_host::linear_q8w_qkv_kv(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *const *w,
+                                const float *const *bias, float *q_out, zwg_kv *kv, uint64_t layer, uint64_t seq0,
+                                const int32_t *pos_dev, int32_t *n_kv_out) {
+    if (!ctx) return fail(nullptr, "null context");
+    if (!w || !kv) return fail(ctx, "null weight array or cache");
+    if (kv->ctx != ctx) return fail(ctx, "the cache belongs to another context (or its context is closed)");
+    const zwg_kv_desc &d = kv->desc;
+    const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    for (int j = 0; j < 3; ++j) {
+        if (!w[j]) return fail(ctx, "null weights");
+        if (!w[j]->ctx) return fail(ctx, kQ8wClosed);
+        if (w[j]->k != w[0]->k) return fail(ctx, "q, k and v weights must share k");
+        const std::string msg = check_linear(m, w[j]->k, ZWG_W_Q8, w[j]->n);
+        if (!msg.empty()) return fail(ctx, msg);
+        if (bias && bias[j] && !al16(bias[j])) return fail(ctx, "biases must be 16-byte aligned");
+    }
+    if (w[1]->n != kv->kvw || w[2]->n != kv->kvw) return fail(ctx, "k and v weights must have n_head_kv * d rows");
+    if (w[0]->n % d.d || (w[0]->n / d.d) % d.n_head_kv) return fail(ctx, "q weights must have n_head * d rows, n_head a multiple of n_head_kv");
+    if (layer >= d.n_layer) return fail(ctx, "kv layer out of range");
+    if (m > 64) return fail(ctx, "the cache-writing q/k/v call takes at most 64 tokens (one decode step)");
+    if (seq0 + m > d.n_seq) return fail(ctx, "kv sequences out of range");
+    if (m == 0) return ZWG_OK;
+    if (!x || !al16(x) || !q_out || !al16(q_out) || !pos_dev) return fail(ctx, "x, q_out (16-byte aligned) and pos_dev must be non-null");
+    const hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
+    zwg_lin::Q8KvStore kvs{};
+    kvs.q_out = q_out;
+    kvs.k_cache = kv->k + layer * d.n_seq * kv->per_seq;
+    kvs.v_cache = kv->v + layer * d.n_seq * kv->per_seq;
+    kvs.cos = kv->cos;
+    kvs.sin = kv->sin;
+    kvs.pos_dev = pos_dev;
+    kvs.n_kv_out = n_kv_out;
+    kvs.per_seq = (int64_t)kv->per_seq;
+    kvs.seq0 = (int32_t)seq0;
+    kvs.n_ctx = (int32_t)d.n_ctx;
+    kvs.n_head = (int32_t)(w[0]->n / d.d);
+    kvs.n_head_kv = (int32_t)d.n_head_kv;
+    kvs.kt = d.layout == ZWG_KV_KT;
+    kvs.d = (int32_t)d.d;
+    return run_q8w_token_step(ctx, x, m, 3, w, bias, nullptr, zwg_ew::kEpiNone, &kvs);
+}
+
+// x += xin . W^T + bias and ln_out = layerNorm(x) (ln_w, ln_b, eps) for a decode step's rows
+// (m <= 64, n <= 2048): one stream launch and linear_split_sum_add_ln_kernel; a call too short to
+// split k (k <= 256) runs the add epilogue and the layer norm as two launches, with the same results.
+int zwg_host::linear_q8w_add_ln(zwg_ctx *ctx, const float *xin, uint64_t m, const zwg_q8w *w, const float *bias,
+                                float *x, const float *ln_w, const float *ln_b, float eps, float *ln_out) {
+    if (!w || !w->ctx) return fail(ctx, w ? kQ8wClosed : "null weights");
+    const std::string msg = check_linear(m, w->k, ZWG_W_Q8, w->n);
+    if (!msg.empty()) return fail(ctx, msg);
+    if (m == 0) return ZWG_OK;
+    const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (m > 64 || w->n % 4 || w->n > 2048) return fail(ctx, "the fused residual + layer norm call takes m <= 64 and n <= 2048, n % 4 == 0");
+    if (!xin || !x || !ln_w || !ln_b || !ln_out || !al16(xin) || !al16(x) || !al16(ln_w) || !al16(ln_b) ||
+        !al16(ln_out) || (bias && !al16(bias)))
+        return fail(ctx, "null or unaligned buffer (all 16-byte aligned)");
+    if (w->n_chunks < 2) {
+        const int rc = run_linear_q8w(ctx, xin, m, w, bias, x, zwg_ew::kEpiAdd);
+        return rc != ZWG_OK ? rc : layer_norm(ctx, x, m, w->n, ln_w, ln_b, eps, ln_out);
+    }
+    zwg_lin::Q8ResLn r{x, ln_w, ln_b, ln_out, eps};
+    float *outs[1] = {x};
+    return run_q8w_token_step(ctx, xin, m, 1, &w, &bias, outs, zwg_ew::kEpiAdd, nullptr, &r);
+}
+
+// x[i] = te.row(tok[i]) + pe[pos[i]] and ln_out[i] = layerNorm(x[i]) (q8p_embed_ln_kernel).
+int zwg_host::q8w_embed_ln(zwg_ctx *ctx, const zwg_q8w *te, const int32_t *tok, const float *pe, const int32_t *pos,
+                           uint64_t pe_rows, uint64_t m, float *x, const float *ln_w, const float *ln_b, float eps,
+                           float *ln_out) {
+    if (!te || !te->ctx) return fail(ctx, te ? kQ8wClosed : "null weights");
+    if (m == 0) return ZWG_OK;
+    const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (te->k % 4 || te->k > 2048 || m > 0x7fffffffull || pe_rows > 0x7fffffffull)
+        return fail(ctx, "embedding rows of at most 2048 floats, a multiple of 4");
+    if (!tok || !pos || !x || !ln_w || !ln_b || !ln_out || (pe_rows && !pe) || !al16(x) || !al16(ln_w) ||
+        !al16(ln_b) || !al16(ln_out) || (pe && !al16(pe)))
+        return fail(ctx, "null or unaligned buffer (all 16-byte aligned)");
+    zwg_lin::Q8Packed tp{te->q, te->scales, te->n_slabs, te->n_chunks};
+    zwg_lin::Q8ResLn r{nullptr, ln_w, ln_b, ln_out, eps};
+    const hipError_t e = launch_rows<EmbedLnRows>((int32_t)te->k, (int32_t)m, ctx->stream, tp, (int32_t)te->n, tok, pe,
+                                                  pos, (int32_t)pe_rows, (int32_t)m, (int32_t)te->k, x, r);
+    return e == hipSuccess ? ZWG_OK : fail_hip(ctx, "token embedding kernel launch", e);
+}
 
 extern "C" {
 
@@ -640,42 +765,7 @@ int zwg_linear_q8w_qkv_kv_dev(zwg_ctx *ctx, const float *x, uint64_t m, const zw
                               const float *const *bias, float *q_out, zwg_kv *kv, uint64_t layer, uint64_t seq0,
                               const int32_t *pos_dev) {
     if (!ctx) return fail(nullptr, "null context");
-    if (!w || !kv) return fail(ctx, "null weight array or cache");
-    if (kv->ctx != ctx) return fail(ctx, "the cache belongs to another context (or its context is closed)");
-    const zwg_kv_desc &d = kv->desc;
-    const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-    for (int j = 0; j < 3; ++j) {
-        if (!w[j]) return fail(ctx, "null weights");
-        if (!w[j]->ctx) return fail(ctx, kQ8wClosed);
-        if (w[j]->k != w[0]->k) return fail(ctx, "q, k and v weights must share k");
-        const std::string msg = check_linear(m, w[j]->k, ZWG_W_Q8, w[j]->n);
-        if (!msg.empty()) return fail(ctx, msg);
-        if (bias && bias[j] && !al16(bias[j])) return fail(ctx, "biases must be 16-byte aligned");
-    }
-    if (w[1]->n != kv->kvw || w[2]->n != kv->kvw) return fail(ctx, "k and v weights must have n_head_kv * d rows");
-    if (w[0]->n % d.d || (w[0]->n / d.d) % d.n_head_kv) return fail(ctx, "q weights must have n_head * d rows, n_head a multiple of n_head_kv");
-    if (layer >= d.n_layer) return fail(ctx, "kv layer out of range");
-    if (m > 64) return fail(ctx, "the cache-writing q/k/v call takes at most 64 tokens (one decode step)");
-    if (seq0 + m > d.n_seq) return fail(ctx, "kv sequences out of range");
-    if (m == 0) return ZWG_OK;
-    if (!x || !al16(x) || !q_out || !al16(q_out) || !pos_dev) return fail(ctx, "x, q_out (16-byte aligned) and pos_dev must be non-null");
-    const hipError_t e = hipSetDevice(ctx->device);
-    if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
-    zwg_lin::Q8KvStore kvs{};
-    kvs.q_out = q_out;
-    kvs.k_cache = kv->k + layer * d.n_seq * kv->per_seq;
-    kvs.v_cache = kv->v + layer * d.n_seq * kv->per_seq;
-    kvs.cos = kv->cos;
-    kvs.sin = kv->sin;
-    kvs.pos_dev = pos_dev;
-    kvs.per_seq = (int64_t)kv->per_seq;
-    kvs.seq0 = (int32_t)seq0;
-    kvs.n_ctx = (int32_t)d.n_ctx;
-    kvs.n_head = (int32_t)(w[0]->n / d.d);
-    kvs.n_head_kv = (int32_t)d.n_head_kv;
-    kvs.kt = d.layout == ZWG_KV_KT;
-    kvs.d = (int32_t)d.d;
-    return run_q8w_token_step(ctx, x, m, 3, w, bias, nullptr, zwg_ew::kEpiNone, &kvs);
+    return linear_q8w_qkv_kv(ctx, x, m, w, bias, q_out, kv, layer, seq0, pos_dev, nullptr);
 }
 
 int zwg_linear_epi_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t k, const void *w, uint32_t w_type,

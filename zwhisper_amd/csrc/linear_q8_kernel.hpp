@@ -659,6 +659,7 @@ struct Q8KvStore {
     const float *cos;       // [n_ctx][D/2], or nullptr: no rotary positions
     const float *sin;
     const int32_t *pos_dev; // [m] positions
+    int32_t *n_kv_out;      // or nullptr: [m] keys each sequence's cache then holds, pos + 1 (0 off the cache)
     int64_t per_seq;
     int32_t seq0, n_ctx, n_head, n_head_kv, kt;
     int32_t d; // the kernel's D (host side: which instantiation)
@@ -706,6 +707,7 @@ __global__ __launch_bounds__(256) void linear_split_sum_qkv_kernel(Q8Group grp, 
     }
     const int p = kv.pos_dev[i];
     const bool live = p >= 0 && p < kv.n_ctx;
+    if (kv.n_kv_out && set == 0 && h == 0 && j == 0) kv.n_kv_out[i] = live ? p + 1 : 0;
     if (set < 2 && kv.cos && live) {
         const f4 c = *reinterpret_cast<const f4 *>(kv.cos + (int64_t)p * HALF + j);
         const f4 s = *reinterpret_cast<const f4 *>(kv.sin + (int64_t)p * HALF + j);
@@ -734,6 +736,115 @@ __global__ __launch_bounds__(256) void linear_split_sum_qkv_kernel(Q8Group grp, 
     float *row = (set == 1 ? kv.k_cache : kv.v_cache) + seq + (int64_t)p * kvw + h * D + j;
     *reinterpret_cast<f4 *>(row) = lo;
     *reinterpret_cast<f4 *>(row + HALF) = hi;
+}
+
+// A one-set call's split sum added to the residual stream and normalised, for the decoder blocks'
+// ops.linear + ops.add + next ops.layerNorm (src/decoder.zig:185-188, :192-195, :200 with the
+// next block's :178): row i of x += sum over splits (in split order) of part[s][i] + bias -- as
+// linear_split_sum_group_kernel with the add epilogue forms it -- then ln_out[i] = layerNorm(x[i])
+// through zwg_ew::layer_norm_regs, as layer_norm_kernel computes it.  So x and ln_out equal the
+// split sum and the layer-norm launch bit for bit.  One wave per row of n <= 256 R floats; the
+// loads of B splits at a time are issued before their adds.
+struct Q8ResLn {
+    float *x; // [m][n] residual stream, updated in place
+    const float *ln_w, *ln_b;
+    float *ln_out; // [m][n]
+    float eps;
+};
+
+template <int R>
+__global__ __launch_bounds__(256) void linear_split_sum_add_ln_kernel(const float *part, const float *bias, Q8ResLn r,
+                                                                     int32_t m, int32_t n, int32_t n_split) {
+#pragma clang fp contract(off)
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    constexpr int B = R == 1 ? 16 : R == 2 ? 12 : R == 3 ? 8 : R == 4 ? 6 : 4;
+    const int lane = threadIdx.x & 63;
+    const int row = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (row >= m) return;
+    const int n4 = n >> 2;
+    const int64_t step = (int64_t)m * n4; // float4s of one split
+    const f4 *p = reinterpret_cast<const f4 *>(part) + (int64_t)row * n4;
+    f4 s[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) s[i] = (f4){0.f, 0.f, 0.f, 0.f};
+    for (int q0 = 0; q0 < n_split; q0 += B) {
+        f4 t[B][R];
+#pragma unroll
+        for (int j = 0; j < B; ++j)
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const int c = lane + 64 * i;
+                if (q0 + j < n_split && c < n4) t[j][i] = p[(q0 + j) * step + c];
+            }
+#pragma unroll
+        for (int j = 0; j < B; ++j)
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const int c = lane + 64 * i;
+                if (q0 + j < n_split && c < n4) s[i] = q0 + j == 0 ? t[j][i] : s[i] + t[j][i];
+            }
+    }
+    zwg_ew::ew_f32x4 v[R];
+    f4 *xr = reinterpret_cast<f4 *>(r.x + (int64_t)row * n);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int c = lane + 64 * i;
+        if (c < n4) {
+            f4 val = s[i];
+            if (bias) val = val + reinterpret_cast<const f4 *>(bias)[c];
+            const f4 nx = xr[c] + val;
+            xr[c] = nx;
+            v[i] = nx;
+        } else {
+            v[i] = (zwg_ew::ew_f32x4){0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    zwg_ew::layer_norm_regs<R>(v, lane, n4, r.ln_w, r.ln_b, r.eps, r.ln_out + (int64_t)row * n);
+}
+
+// A decode step's token embeddings from the packed int8 token embedding (the tied output
+// projection): x[i] = te.row(tok[i]) + pe[pos[i]] -- gemm.Q8.row (src/gemm.zig:257-265, q * scale
+// in f32) then ops.add (src/decoder.zig:171-174) -- and ln_out[i] = layerNorm(x[i]) (the first
+// block's attn_ln, src/decoder.zig:178) through zwg_ew::layer_norm_regs.  A token outside
+// [0, n_vocab) gives a zero embedding row; a position outside [0, pe_rows) adds no position row.
+// One wave per row of n <= 256 R floats; a lane's float4 is 4 bytes of one 16-byte lane piece of
+// its block's tile (Q8Packed).
+template <int R>
+__global__ __launch_bounds__(256) void q8p_embed_ln_kernel(Q8Packed te, int32_t n_vocab, const int32_t *tok,
+                                                          const float *pe, const int32_t *pos, int32_t pe_rows,
+                                                          int32_t m, int32_t n, float *x, Q8ResLn r) {
+#pragma clang fp contract(off)
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const int lane = threadIdx.x & 63;
+    const int row = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    if (row >= m) return;
+    const int n4 = n >> 2;
+    const int t = tok[row], ps = pos[row];
+    const bool t_ok = t >= 0 && t < n_vocab, p_ok = ps >= 0 && ps < pe_rows;
+    const int slab = t_ok ? t >> 5 : 0, r32 = t & 31;
+    const int nbp = te.n_chunks * kQ8ChunkBlocks;
+    zwg_ew::ew_f32x4 v[R];
+    f4 *xr = reinterpret_cast<f4 *>(x + (int64_t)row * n);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int c = lane + 64 * i;
+        f4 val = {0.f, 0.f, 0.f, 0.f};
+        if (c < n4) {
+            if (t_ok) {
+                const int k0 = 4 * c, b = k0 >> 5;
+                const uint32_t w4 = *reinterpret_cast<const uint32_t *>(
+                    te.q + (((int64_t)slab * nbp + b) * 64 + r32 + 32 * ((k0 & 31) >> 4)) * 16 + (k0 & 15));
+                const float sc =
+                    te.scales[(((int64_t)slab * te.n_chunks + (b >> 3)) * 32 + r32) * kQ8ChunkBlocks + (b & 7)];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) val[e] = (float)(int8_t)(uint8_t)(w4 >> (8 * e)) * sc;
+            }
+            if (p_ok) val = val + reinterpret_cast<const f4 *>(pe + (int64_t)ps * n)[c];
+            xr[c] = val;
+        }
+        v[i] = val;
+    }
+    zwg_ew::layer_norm_regs<R>(v, lane, n4, r.ln_w, r.ln_b, r.eps, r.ln_out + (int64_t)row * n);
 }
 
 } // namespace zwg_lin

@@ -218,10 +218,12 @@ class Context:
                                               self._dev_ptr(out, "out")))
 
     def linear_q8w_dev(self, x, m: int, w: "Q8Resident", bias, out) -> None:
-        """out[m][w.n] = x[m][w.k] . W^T (+ bias) over resident packed int8 weights: CUDA float32 tensors."""
+        """out[m][w.n] = x[m][w.k] . W^T (+ bias) over resident packed int8 weights: CUDA float32 tensors
+        (out may be a raw device address, e.g. a KVCache's rows)."""
         if not isinstance(w, Q8Resident):
             raise ZwgError("w must be a Q8Resident (Q8.resident)")
-        if x.numel() < m * w.k or out.numel() < m * w.n or (bias is not None and bias.numel() < w.n):
+        if x.numel() < m * w.k or (not isinstance(out, int) and out.numel() < m * w.n) or (
+                bias is not None and bias.numel() < w.n):
             raise ZwgError("a tensor is shorter than m, n and k need")
         self._bind_torch_stream()
         self._check(self._L.zwg_linear_q8w_dev(self._h, self._dev_ptr(x, "x"), m, w.handle,
@@ -468,6 +470,101 @@ class KVCache:
         v = np.empty(self.n_ctx * self.kvw, np.float32)
         self.ctx._check(self._L.zwg_kv_read(self._h, layer, seq, k.ctypes.data, v.ctypes.data))
         return k, v
+
+
+class Decoder:
+    """The Whisper text decoder on the device (zwg_decoder_*), src/decoder.zig's Decoder for n_windows
+    windows decoded in lockstep: set_audio is Decoder.setAudio (src/decoder.zig:151-159) for a range
+    of windows, step is Decoder.forward (src/decoder.zig:165-205) with one token per window.
+
+    layers: one dict per layer mapping the zwg_dec_layer field names (_lib.DEC_LAYER_FIELDS) to a
+    Q8 (the matrices) or a float32 array / CUDA tensor (norms, biases; a bias may be None); te: Q8
+    [n_vocab][n_state]; pe [n_text_ctx][n_state], ln_w, ln_b [n_state].  The weights are made
+    resident and the self and cross caches allocated here; close() frees them."""
+
+    def __init__(self, ctx: Context, te: "Q8", pe, ln_w, ln_b, layers, n_head: int, n_text_ctx: int,
+                 n_audio_ctx: int, n_windows: int):
+        import torch
+
+        self.ctx = ctx
+        self._L = ctx._L
+        self.n_vocab, self.n_state, self.n_head, self.n_layer = te.n, te.k, n_head, len(layers)
+        self.n_text_ctx, self.n_audio_ctx, self.n_windows = n_text_ctx, n_audio_ctx, n_windows
+        self._owned = []  # residents and caches, closed in reverse
+        self._keep = []   # device tensors the C structs point at
+
+        def vec(a):
+            if a is None:
+                return None
+            t = a if isinstance(a, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(a, np.float32))
+            t = t.to(device=f"cuda:{ctx.device}", dtype=torch.float32).contiguous()
+            self._keep.append(t)
+            return t.data_ptr()
+
+        def res(w):
+            r = w.resident(ctx)
+            self._owned.append(r)
+            return r.handle
+
+        d = self.n_state // n_head
+        self.te = te.resident(ctx)
+        self._owned.append(self.te)
+        c_layers = (_lib.DecLayerC * self.n_layer)()
+        # per layer, what each field points at: a Q8Resident, a CUDA tensor or None
+        self.layer_refs = []
+        for li, lw in enumerate(layers):
+            vals, refs = {}, {}
+            for name in _lib.DEC_LAYER_FIELDS:
+                v = lw.get(name)
+                vals[name] = res(v) if isinstance(v, Q8) else vec(v)
+                refs[name] = (self._owned[-1] if isinstance(v, Q8) else self._keep[-1]) if v is not None else None
+            c_layers[li] = _lib.DecLayerC(**vals)
+            self.layer_refs.append(refs)
+        self.self_kv = KVCache(ctx, self.n_layer, n_windows, n_text_ctx, n_head, d)
+        self.cross_kv = KVCache(ctx, self.n_layer, n_windows, n_audio_ctx, n_head, d)
+        self._owned += [self.self_kv, self.cross_kv]
+        self._layers = c_layers
+        pe_p, lnw_p, lnb_p = vec(pe), vec(ln_w), vec(ln_b)
+        self.pe, self.ln_w, self.ln_b = self._keep[-3:]
+        self.c = _lib.DecoderC(self.n_vocab, self.n_state, n_head, self.n_layer, self.te.handle, pe_p, lnw_p, lnb_p,
+                               c_layers, self.self_kv._h.value, self.cross_kv._h.value)
+        self.scratch = torch.empty(int(self._L.zwg_decoder_scratch(64, self.n_state)), device=f"cuda:{ctx.device}")
+
+    def set_audio(self, enc, n_windows: int, seq0: int = 0) -> None:
+        """Cross K/V of windows seq0 .. seq0 + n_windows - 1 from the encoder output enc
+        [n_windows][n_audio_ctx][n_state] (CUDA float32)."""
+        if enc.numel() < n_windows * self.n_audio_ctx * self.n_state:
+            raise ZwgError("enc is shorter than n_windows x n_audio_ctx x n_state")
+        self.ctx._bind_torch_stream()
+        self.ctx._check(self._L.zwg_decoder_set_audio_dev(self.ctx.handle, ctypes_byref(self.c),
+                                                          Context._dev_ptr(enc, "enc"), n_windows, seq0))
+
+    def step(self, tokens, pos, logits, seq0: int = 0) -> None:
+        """One token per window for windows seq0 .. seq0 + m - 1 (tokens, pos: CUDA int32 tensors of m
+        entries, pos the windows' n_past); logits [m][n_vocab] (CUDA float32) written."""
+        import torch
+
+        m = tokens.numel()
+        for name, t in (("tokens", tokens), ("pos", pos)):
+            if not t.is_cuda or t.dtype != torch.int32 or t.numel() != m:
+                raise ZwgError(f"{name} must be a CUDA int32 tensor of m entries")
+        if logits.numel() < m * self.n_vocab:
+            raise ZwgError("logits is shorter than m x n_vocab")
+        self.ctx._bind_torch_stream()
+        self.ctx._check(self._L.zwg_decoder_step_dev(self.ctx.handle, ctypes_byref(self.c), tokens.data_ptr(),
+                                                     pos.data_ptr(), m, seq0, Context._dev_ptr(logits, "logits"),
+                                                     Context._dev_ptr(self.scratch, "scratch")))
+
+    def close(self) -> None:
+        for o in reversed(self._owned):
+            o.close()
+        self._owned = []
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
 
 
 _tls = threading.local()
