@@ -494,7 +494,8 @@ int zwg_decoder_set_audio_dev(zwg_ctx *ctx, const zwg_decoder *dec, const float 
                               uint64_t seq0);
 
 /* Floats of scratch a step over m windows needs (the reference's x, x_ln, q, attn and hidden
- * buffers, src/decoder.zig:57-63, and the self-attention key counts). */
+ * buffers, src/decoder.zig:57-63, the cross-attention query's k-split partial sums and the
+ * self-attention key counts). */
 uint64_t zwg_decoder_scratch(uint64_t m, uint64_t n_state);
 
 /* forward for windows seq0 .. seq0 + m - 1 (m <= 64), window i taking token tokens[i] at
@@ -504,7 +505,8 @@ uint64_t zwg_decoder_scratch(uint64_t m, uint64_t n_state);
  * [m][n_vocab] = ln(x) . te^T.  A position outside [0, n_text_ctx) writes no cache rows and its
  * window's logits are meaningless; a token outside [0, n_vocab) embeds as a zero row.  The work
  * the reference does, fused where it saves launches (layer norms into the residual projections'
- * split sums, the cache writes into the q/k/v projections'), with results equal bit for bit to
+ * split sums, the cache writes into the q/k/v projections', the cross-attention query's split sum
+ * into the attention's query load), with results equal bit for bit to
  * the same step composed of zwg_layer_norm_dev, zwg_linear_q8w_qkv_kv_dev,
  * zwg_attention_batch_dev and zwg_linear_q8w_epi_dev calls.  Asynchronous. */
 int zwg_decoder_step_dev(zwg_ctx *ctx, const zwg_decoder *dec, const int32_t *tokens, const int32_t *pos, uint64_t m,

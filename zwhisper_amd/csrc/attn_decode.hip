@@ -101,7 +101,7 @@ __global__ __launch_bounds__(64) void decode_kt_kernel(AttnArgs a) {
         if (r < rows) {
             const int qi = r / G;
             const int head = hk * G + (r - qi * G);
-            val = a.q[item * a.q_bstride + (int64_t)qi * a.q_stride + head * D + p] * a.scale_log2;
+            val = load_q(a, item * a.q_bstride + (int64_t)qi * a.q_stride + head * D + p, head * D + p) * a.scale_log2;
         }
         q_s[r][p] = val;
     }
@@ -338,7 +338,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_rm_kernel(AttnArgs a) {
         if (r < rows) {
             const int qi = r / G;
             const int head = hk * G + (r - qi * G);
-            val = a.q[item * a.q_bstride + (int64_t)qi * a.q_stride + head * D + p] * a.scale_log2;
+            val = load_q(a, item * a.q_bstride + (int64_t)qi * a.q_stride + head * D + p, head * D + p) * a.scale_log2;
         }
         q_s[r][p] = val;
     }

@@ -127,22 +127,23 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
     const uint32_t k_base = KT ? (uint32_t)k_dim(0) * kt_row_b + 4u * (uint32_t)k_key
                                : (uint32_t)(tid / (D / 4)) * row_b + 16u * (uint32_t)(tid % (D / 4));
     const uint32_t v_base = (uint32_t)v_key(0) * row_b + 4u * (uint32_t)v_dim;
-    auto load_k = [&](int k0) {
+    auto load_k_to = [&](f32x4 (&dst)[NG], int k0) {
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
             if (KT) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    kr[g][j] = __builtin_bit_cast(
+                    dst[g][j] = __builtin_bit_cast(
                         float, __builtin_amdgcn_raw_buffer_load_b32(
                                    krs, (int)k_base, (int)((uint32_t)k0 * 4u + (uint32_t)(32 * g + j) * kt_row_b), 0));
             } else {
-                kr[g] = __builtin_bit_cast(
+                dst[g] = __builtin_bit_cast(
                     f32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                krs, (int)k_base, (int)((uint32_t)(k0 + (1024 / D) * g) * row_b), 0));
             }
         }
     };
+    auto load_k = [&](int k0) { load_k_to(kr, k0); };
     auto load_v = [&](int k0) {
 #pragma unroll
         for (int g = 0; g < NG; ++g)
@@ -272,10 +273,14 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
 
     const int n_tiles = k_end > k_begin ? (k_end - k_begin + BN - 1) / BN : 0;
     f32x16 s_cur = (f32x16){0};
+    // tile 1's K goes out with tile 0's K and V and the queries: the prologue waits out one memory
+    // round trip, not two
+    f32x4 kr1[NG];
     if (n_tiles > 0) {
         load_k(k_begin);
         load_v(k_begin);
     }
+    if (n_tiles > 1) load_k_to(kr1, k_begin + BN);
     if (q_valid) {
         const f32x4 *src = reinterpret_cast<const f32x4 *>(qp + (int64_t)query * a.q_stride + half * HD);
 #pragma unroll
@@ -293,7 +298,9 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(AttnArgs a) {
     if (n_tiles > 0) {
         store_k(0);
         store_v(0);
-        if (n_tiles > 1) load_k(k_begin + BN);
+        if (n_tiles > 1)
+#pragma unroll
+            for (int g = 0; g < NG; ++g) kr[g] = kr1[g];
     }
     __syncthreads();
     if (n_tiles > 0 && wave_needs(k_begin)) s_cur = qk(0);

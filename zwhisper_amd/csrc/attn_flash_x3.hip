@@ -225,22 +225,23 @@ void flash_x3_kernel(AttnArgs a) {
                     (int)(t_off + (uint32_t)(pl * 32 * D * 2 + in_plane) + 16u * (uint32_t)lane), 0, 0, 0);
             }
     };
-    auto load_k = [&](int k0) {
+    auto load_k_to = [&](f32x4 (&dst)[NG], int k0) {
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
             if (KT) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    kr[g][j] = __builtin_bit_cast(
+                    dst[g][j] = __builtin_bit_cast(
                         float, __builtin_amdgcn_raw_buffer_load_b32(
                                    krs, (int)k_base, (int)((uint32_t)k0 * 4u + (uint32_t)(32 * g + j) * kt_row_b), 0));
             } else {
-                kr[g] = __builtin_bit_cast(
+                dst[g] = __builtin_bit_cast(
                     f32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                krs, (int)k_base, (int)((uint32_t)(k0 + (1024 / D) * g) * row_b), 0));
             }
         }
     };
+    auto load_k = [&](int k0) { load_k_to(kr, k0); };
     auto load_v = [&](int k0) {
 #pragma unroll
         for (int g = 0; g < NG; ++g)
@@ -375,15 +376,21 @@ void flash_x3_kernel(AttnArgs a) {
 
     const int n_tiles = k_end > k_begin ? (k_end - k_begin + BN - 1) / BN : 0;
     f32x16 s_cur = (f32x16){0};
+    // tile 1's K goes out with tile 0's K and V and the queries, so the prologue waits out one
+    // memory round trip, not two (the loop then keeps its one-tile-ahead staging)
+    f32x4 kr1[NG];
     if constexpr (PL) {
         if (n_tiles > 0) {
             copy_tile(vimg, k_begin, Vh[0], Vl[0]);
             copy_tile(kimg, k_begin, Kh[0], Kl[0]);
         }
         if (n_tiles > 1) copy_tile(kimg, k_begin + BN, Kh[1], Kl[1]);
-    } else if (n_tiles > 0) {
-        load_k(k_begin);
-        load_v(k_begin);
+    } else {
+        if (n_tiles > 0) {
+            load_k(k_begin);
+            load_v(k_begin);
+        }
+        if (n_tiles > 1) load_k_to(kr1, k_begin + BN);
     }
     {
         // all of the row's loads go out together, then one wait
@@ -415,7 +422,9 @@ void flash_x3_kernel(AttnArgs a) {
     } else if (n_tiles > 0) {
         store_k(0);
         store_v(0);
-        if (n_tiles > 1) load_k(k_begin + BN);
+        if (n_tiles > 1)
+#pragma unroll
+            for (int g = 0; g < NG; ++g) kr[g] = kr1[g];
     }
     __syncthreads();
     if (n_tiles > 0 && wave_needs(k_begin)) s_cur = qk(0);

@@ -42,7 +42,23 @@ struct AttnArgs {
     const _Float16 *k_img;
     const _Float16 *v_img;
     int32_t img_tiles;
+    // the decode kernels only: when q_parts > 1, q holds the q_parts k-split partial sums of the
+    // queries' projection, q_part_stride floats apart, and a query value is their sum in split
+    // order plus q_bias[column] (load_q) -- the projection's split sum, taken in the q load
+    int32_t q_parts;
+    int64_t q_part_stride;
+    const float *q_bias;
 };
+
+// Query value at float offset `at` of a.q, column `col` of its row (head * d + dim): a.q[at], or
+// with q_parts > 1 the projection's split sum formed here, as linear_split_sum_group_kernel forms
+// it (partials added in split order, then the bias), so the value is the same bit for bit.
+__device__ __forceinline__ float load_q(const AttnArgs &a, int64_t at, int col) {
+    if (a.q_parts <= 1) return a.q[at];
+    float s = a.q[at];
+    for (int j = 1; j < a.q_parts; ++j) s = s + a.q[at + j * a.q_part_stride];
+    return a.q_bias ? s + a.q_bias[col] : s;
+}
 
 // |x| as its bit pattern: for non-negative floats the unsigned order is the float order, and
 // NaNs and infinities lie above every finite value.

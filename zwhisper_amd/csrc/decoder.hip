@@ -11,14 +11,14 @@
 //                                                     also writes the key counts pos + 1
 //     T = attention(Q, self cache[0 .. pos])           decode kernel (+ merge)
 //     X += o(T); A = cross_ln(X)                       stream + linear_split_sum_add_ln_kernel
-//     Q = cq(A)                                        stream + split sum
-//     T = attention(Q, cross cache)                    decode kernel (+ merge)
+//     T = attention(cq(A), cross cache)                stream (partials to P) + decode kernel, whose
+//                                                     q load adds the partials and bias (+ merge)
 //     X += co(T); A = mlp_ln(X)                        stream + linear_split_sum_add_ln_kernel
 //     H = gelu(mlp0(A))                                stream + split sum (GELU in its store)
 //     X += mlp1(H); A = next layer's attn_ln(X), or the final ln after the last layer
 //   logits = A . te^T                                  stream (unsplit)
 //
-// 13-15 launches per layer where the same step as separate calls (layer norm, q/k/v projections,
+// 12-14 launches per layer where the same step as separate calls (layer norm, q/k/v projections,
 // append, add) takes 19-21.  The fused launches form the same values in the same order as the
 // separate ones (the split sums in split order, the add, layer_norm_regs for every norm), so the
 // results are equal bit for bit.  The self-attention is the reference's causal call with one
@@ -36,6 +36,9 @@ using namespace zwg_host;
 namespace {
 
 constexpr float kLnEps = 1e-5f; // ops.layerNorm (src/ops.zig:342-344)
+// scratch: X, A, Q, T (m rows each), H (4 m rows), P (kMaxQParts m rows: the cross-attention
+// query's k-split partials), then the self-attention key counts
+constexpr int kMaxQParts = 8;
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -111,7 +114,9 @@ int zwg_decoder_set_audio_dev(zwg_ctx *ctx, const zwg_decoder *dec, const float 
     return ZWG_OK;
 }
 
-uint64_t zwg_decoder_scratch(uint64_t m, uint64_t n_state) { return 8 * m * n_state + (m + 3) / 4 * 4; }
+uint64_t zwg_decoder_scratch(uint64_t m, uint64_t n_state) {
+    return (8 + kMaxQParts) * m * n_state + (m + 3) / 4 * 4;
+}
 
 int zwg_decoder_step_dev(zwg_ctx *ctx, const zwg_decoder *dec, const int32_t *tokens, const int32_t *pos, uint64_t m,
                          uint64_t seq0, float *logits, float *scratch) {
@@ -145,8 +150,8 @@ int zwg_decoder_step_dev(zwg_ctx *ctx, const zwg_decoder *dec, const int32_t *to
     hipError_t e = hipSetDevice(ctx->device);
     if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
 
-    float *X = scratch, *A = X + m * ns, *Q = A + m * ns, *T = Q + m * ns, *Hd = T + m * ns;
-    int32_t *n_kv = reinterpret_cast<int32_t *>(Hd + 4 * m * ns);
+    float *X = scratch, *A = X + m * ns, *Q = A + m * ns, *T = Q + m * ns, *Hd = T + m * ns, *P = Hd + 4 * m * ns;
+    int32_t *n_kv = reinterpret_cast<int32_t *>(P + kMaxQParts * m * ns);
     zwg_kv *self = dec->self_kv, *cross = dec->cross_kv;
     int rc = q8w_embed_ln(ctx, dec->te, tokens, dec->pe, pos, self->desc.n_ctx, m, X, dec->layers[0].attn_ln_w,
                           dec->layers[0].attn_ln_b, kLnEps, A);
@@ -180,13 +185,17 @@ int zwg_decoder_step_dev(zwg_ctx *ctx, const zwg_decoder *dec, const int32_t *to
         if ((rc = zwg_attention_batch_dev(ctx, Q, self->k + s_at, self->v + s_at, &sh, &bt, T)) != ZWG_OK) return rc;
         if ((rc = linear_q8w_add_ln(ctx, T, m, L.o_w, L.o_b, X, L.cross_ln_w, L.cross_ln_b, kLnEps, A)) != ZWG_OK)
             return rc;
-        // cross-attention over the audio (src/decoder.zig:190-194)
-        if ((rc = zwg_linear_q8w_dev(ctx, A, m, L.cq_w, L.cq_b, Q)) != ZWG_OK) return rc;
+        // cross-attention over the audio (src/decoder.zig:190-194): the query projection's k-split
+        // partials go to P and the attention's q load adds them (and the bias)
+        int n_parts = 0;
+        if ((rc = linear_q8w_parts(ctx, A, m, L.cq_w, P, kMaxQParts, &n_parts)) != ZWG_OK) return rc;
         const uint64_t c_at = (l * cross->desc.n_seq + seq0) * cross->per_seq;
         sh.n_kv = cross->desc.n_ctx;
         bt.k_bstride = bt.v_bstride = cross->per_seq;
         bt.n_kv_dev = nullptr;
-        if ((rc = zwg_attention_batch_dev(ctx, Q, cross->k + c_at, cross->v + c_at, &sh, &bt, T)) != ZWG_OK) return rc;
+        if ((rc = attention_qparts_dev(ctx, P, n_parts, m * ns, L.cq_b, cross->k + c_at, cross->v + c_at, sh, bt,
+                                       T)) != ZWG_OK)
+            return rc;
         if ((rc = linear_q8w_add_ln(ctx, T, m, L.co_w, L.co_b, X, L.mlp_ln_w, L.mlp_ln_b, kLnEps, A)) != ZWG_OK)
             return rc;
         // mlp (src/decoder.zig:197-201), then the next block's attn_ln or the final ln (:203)

@@ -252,9 +252,17 @@ struct EmbedLnRows {
 // (linear_split_sum_qkv_kernel), so the call is always split, in two at least.  resln (one set,
 // n <= 2048): the split sum adds into the residual stream and normalises the rows
 // (linear_split_sum_add_ln_kernel), likewise always split.
+// po (one set): the partials go to po->part (at most po->max_parts splits, at least two) and no
+// split sum is launched; the split count is returned in po->n_split.
+struct Q8PartsOut {
+    float *part;
+    int max_parts;
+    int n_split;
+};
 template <int MT>
 int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
-                  const zwg_lin::Q8KvStore *kvs = nullptr, const zwg_lin::Q8ResLn *resln = nullptr) {
+                  const zwg_lin::Q8KvStore *kvs = nullptr, const zwg_lin::Q8ResLn *resln = nullptr,
+                  Q8PartsOut *po = nullptr) {
     constexpr int kQ8pWaves = q8p_waves<MT>();
     zwg_lin::Q8Args a = base;
     const uint64_t m = (uint64_t)a.m;
@@ -282,12 +290,13 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
     if (part_off > ctx->workspace_bytes) return fail(ctx, "workspace too small for this linear call");
     int n_split = 1;
     if (split_k) n_split = (int)std::min<int64_t>(n_chunks, (ZWG_Q8P_SPLIT_TARGET + gx - 1) / gx);
-    if (kvs || resln) {
+    if (kvs || resln || po) {
         if (n_chunks < 2) return fail(ctx, "the fused split-sum calls need k above 256 (their sum is a k split)");
         n_split = std::max(n_split, 2);
     }
-    while (n_split > 1 && part_off + (uint64_t)n_split * m * n_tot * 4 > ctx->workspace_bytes) --n_split;
-    if ((kvs || resln) && n_split < 2) return fail(ctx, "workspace too small for this call's partial sums");
+    if (po) n_split = std::min(n_split, po->max_parts);
+    else while (n_split > 1 && part_off + (uint64_t)n_split * m * n_tot * 4 > ctx->workspace_bytes) --n_split;
+    if ((kvs || resln || po) && n_split < 2) return fail(ctx, "too little room for this call's partial sums");
     a.chunks_per_split = (n_chunks + n_split - 1) / n_split;
     n_split = (n_chunks + a.chunks_per_split - 1) / a.chunks_per_split; // no empty splits
     a.n_split = n_split;
@@ -296,6 +305,10 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
     for (int j = 0; j < zwg_lin::kQ8MaxGroup; ++j) {
         g.part[j] = (j < g.count && n_split > 1) ? reinterpret_cast<float *>(ws + off) : nullptr;
         if (j < g.count) off += (uint64_t)n_split * m * (uint64_t)g.n[j] * 4;
+    }
+    if (po) {
+        g.part[0] = po->part;
+        po->n_split = n_split;
     }
     _Float16 *xcvt = XS ? nullptr : reinterpret_cast<_Float16 *>(ctx->workspace);
     hipError_t e;
@@ -330,6 +343,8 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
             zwg_lin::linear_split_sum_qkv_kernel<32><<<blocks_for(threads, bs), bs, 0, ctx->stream>>>(g, *kvs, a.m, n_split);
         e = hipGetLastError();
         if (e != hipSuccess) return fail_hip(ctx, "q/k/v cache split-sum kernel launch", e);
+    } else if (po) {
+        // the caller adds the partials (attention's q load)
     } else if (resln) {
         e = launch_rows<AddLnRows>(g.n[0], a.m, ctx->stream, (const float *)g.part[0], g.bias[0], *resln, a.m, g.n[0],
                                    n_split);
@@ -505,7 +520,8 @@ void detach_q8w(void *obj) {
 // callers).
 int run_q8w_token_step(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t n_w, const zwg_q8w *const *w,
                        const float *const *bias, float *const *out, uint32_t epi,
-                       const zwg_lin::Q8KvStore *kvs = nullptr, const zwg_lin::Q8ResLn *resln = nullptr) {
+                       const zwg_lin::Q8KvStore *kvs = nullptr, const zwg_lin::Q8ResLn *resln = nullptr,
+                       Q8PartsOut *po = nullptr) {
     zwg_lin::Q8Args a{};
     a.x = x;
     a.m = (int32_t)m;
@@ -522,7 +538,7 @@ int run_q8w_token_step(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t n_w, c
         g.bias[j] = bias ? bias[j] : nullptr;
         g.out[j] = out ? out[j] : nullptr;
     }
-    return m > 32 ? run_q8p_group<2>(ctx, a, g, kvs, resln) : run_q8p_group<1>(ctx, a, g, kvs, resln);
+    return m > 32 ? run_q8p_group<2>(ctx, a, g, kvs, resln, po) : run_q8p_group<1>(ctx, a, g, kvs, resln, po);
 }
 
 int run_linear_q8w(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, const float *bias, float *out,
@@ -622,6 +638,21 @@ int zwg_host::linear_q8w_add_ln(zwg_ctx *ctx, const float *xin, uint64_t m, cons
     zwg_lin::Q8ResLn r{x, ln_w, ln_b, ln_out, eps};
     float *outs[1] = {x};
     return run_q8w_token_step(ctx, xin, m, 1, &w, &bias, outs, zwg_ew::kEpiAdd, nullptr, &r);
+}
+
+int zwg_host::linear_q8w_parts(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, float *parts,
+                               int max_parts, int *n_split) {
+    if (!w || !w->ctx) return fail(ctx, w ? kQ8wClosed : "null weights");
+    const std::string msg = check_linear(m, w->k, ZWG_W_Q8, w->n);
+    if (!msg.empty()) return fail(ctx, msg);
+    const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (m == 0 || m > 64 || w->n_chunks < 2 || max_parts < 2 || w->n % 4)
+        return fail(ctx, "projection partials: 1 <= m <= 64, k above 256, n % 4 == 0, room for two splits");
+    if (!x || !parts || !n_split || !al16(x) || !al16(parts)) return fail(ctx, "null or unaligned buffer");
+    Q8PartsOut po{parts, max_parts, 0};
+    const int rc = run_q8w_token_step(ctx, x, m, 1, &w, nullptr, nullptr, zwg_ew::kEpiNone, nullptr, nullptr, &po);
+    *n_split = po.n_split;
+    return rc;
 }
 
 // x[i] = te.row(tok[i]) + pe[pos[i]] and ln_out[i] = layerNorm(x[i]) (q8p_embed_ln_kernel).

@@ -744,7 +744,7 @@ __global__ __launch_bounds__(256) void linear_split_sum_qkv_kernel(Q8Group grp, 
 // linear_split_sum_group_kernel with the add epilogue forms it -- then ln_out[i] = layerNorm(x[i])
 // through zwg_ew::layer_norm_regs, as layer_norm_kernel computes it.  So x and ln_out equal the
 // split sum and the layer-norm launch bit for bit.  One wave per row of n <= 256 R floats; the
-// loads of B splits at a time are issued before their adds.
+// residual row, the bias and the partials of B splits at a time are loaded before any add.
 struct Q8ResLn {
     float *x; // [m][n] residual stream, updated in place
     const float *ln_w, *ln_b;
@@ -757,13 +757,24 @@ __global__ __launch_bounds__(256) void linear_split_sum_add_ln_kernel(const floa
                                                                      int32_t m, int32_t n, int32_t n_split) {
 #pragma clang fp contract(off)
     typedef float f4 __attribute__((ext_vector_type(4)));
-    constexpr int B = R == 1 ? 16 : R == 2 ? 12 : R == 3 ? 8 : R == 4 ? 6 : 4;
+    constexpr int B = 48 / R < 16 ? 48 / R : 16; // splits whose loads go out together (B R float4 per lane)
     const int lane = threadIdx.x & 63;
     const int row = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
     if (row >= m) return;
     const int n4 = n >> 2;
     const int64_t step = (int64_t)m * n4; // float4s of one split
     const f4 *p = reinterpret_cast<const f4 *>(part) + (int64_t)row * n4;
+    // the residual row and the bias first: their loads share the partials' round trip
+    f4 *xr = reinterpret_cast<f4 *>(r.x + (int64_t)row * n);
+    f4 xo[R], bo[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int c = lane + 64 * i;
+        if (c < n4) {
+            xo[i] = xr[c];
+            bo[i] = bias ? reinterpret_cast<const f4 *>(bias)[c] : (f4){0.f, 0.f, 0.f, 0.f};
+        }
+    }
     f4 s[R];
 #pragma unroll
     for (int i = 0; i < R; ++i) s[i] = (f4){0.f, 0.f, 0.f, 0.f};
@@ -785,14 +796,13 @@ __global__ __launch_bounds__(256) void linear_split_sum_add_ln_kernel(const floa
             }
     }
     zwg_ew::ew_f32x4 v[R];
-    f4 *xr = reinterpret_cast<f4 *>(r.x + (int64_t)row * n);
 #pragma unroll
     for (int i = 0; i < R; ++i) {
         const int c = lane + 64 * i;
         if (c < n4) {
             f4 val = s[i];
-            if (bias) val = val + reinterpret_cast<const f4 *>(bias)[c];
-            const f4 nx = xr[c] + val;
+            if (bias) val = val + bo[i];
+            const f4 nx = xo[i] + val;
             xr[c] = nx;
             v[i] = nx;
         } else {

@@ -79,6 +79,15 @@ int linear_f16_image(zwg_ctx *ctx, const float *x, uint64_t rows, uint64_t k, co
                      uint64_t n, void *img, int kind, uint64_t n_ctx, uint64_t d);
 int attention_images_dev(zwg_ctx *ctx, const float *q, const void *k_img, const void *v_img, uint64_t img_tiles,
                          const zwg_attn_shape &s, const zwg_batch &b, float *out);
+// zwg_attention_batch_dev whose queries are the n_parts k-split partial sums of their projection
+// (part_stride floats apart) plus q_bias: the decode kernels add them in their q load.
+int attention_qparts_dev(zwg_ctx *ctx, const float *q_parts, int n_parts, uint64_t part_stride, const float *q_bias,
+                         const float *k, const float *v, const zwg_attn_shape &s, const zwg_batch &b, float *out);
+// A decode step's projection (m <= 64, k above 256) with its k-split partial sums left in
+// parts[n_split][m][n] (parts holds max_parts * m * n floats) and no split-sum launch; the
+// split count (2 .. max_parts) goes to *n_split.
+int linear_q8w_parts(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, float *parts, int max_parts,
+                     int *n_split);
 // zwg_linear_q8w_qkv_kv_dev with, when n_kv_out is set, each sequence's key count after the
 // append (pos + 1, 0 for a position off the cache) written to n_kv_out[m] by the same launch.
 int linear_q8w_qkv_kv(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *const *w, const float *const *bias,

@@ -125,6 +125,10 @@ struct Exec {
     // kernel in place of k and v
     const _Float16 *k_img = nullptr, *v_img = nullptr;
     uint64_t img_tiles = 0;
+    // q as q_parts k-split partials of its projection (AttnArgs::q_parts), decode kernels only
+    int32_t q_parts = 0;
+    int64_t q_part_stride = 0;
+    const float *q_bias = nullptr;
 };
 
 Exec ctx_exec(const zwg_ctx *ctx) {
@@ -156,6 +160,8 @@ int run_kernels(zwg_ctx *ctx, const Exec &x, const float *q, const float *k, con
         if (b.n_batch * s.n_head_kv * x.img_tiles * 64 * s.d * 2 > 0xffffffffffffull ||
             x.img_tiles * 64 * s.d * 2 > 0x7fffffffull)
             return fail(ctx, "tile images too large");
+    } else if (x.q_parts > 1 && p.kernel != 2) {
+        return fail(ctx, "queries as projection partials are read by the decode kernels only");
     } else if ((p.kernel == 2 && !s.kt_stride) || dense) {
         if (s.n_kv > 0 && ((s.n_kv - 1 + (dense ? 32 : 0)) * s.kv_stride + s.d) * sizeof(float) > 0x7fffffffull)
             return fail(ctx, "K/V rows of one batch item must span less than 2 GiB");
@@ -199,6 +205,9 @@ int run_kernels(zwg_ctx *ctx, const Exec &x, const float *q, const float *k, con
     a.k_img = x.k_img;
     a.v_img = x.v_img;
     a.img_tiles = (int32_t)x.img_tiles;
+    a.q_parts = x.q_parts;
+    a.q_part_stride = x.q_part_stride;
+    a.q_bias = x.q_bias;
 
     hipError_t e = hipSuccess;
     if (x.device >= 0) e = hipSetDevice(x.device);
@@ -293,6 +302,19 @@ int zwg_host::attention_images_dev(zwg_ctx *ctx, const float *q, const void *k_i
     x.v_img = static_cast<const _Float16 *>(v_img);
     x.img_tiles = img_tiles;
     return run(ctx, x, q, static_cast<const float *>(k_img), static_cast<const float *>(v_img), s, b, out);
+}
+
+int zwg_host::attention_qparts_dev(zwg_ctx *ctx, const float *q_parts, int n_parts, uint64_t part_stride,
+                                   const float *q_bias, const float *k, const float *v, const zwg_attn_shape &s,
+                                   const zwg_batch &b, float *out) {
+    if (!ctx) return fail(nullptr, "null context");
+    if (n_parts < 2 || part_stride > 0x7fffffffffffull) return fail(ctx, "q partials: at least two, bounded stride");
+    if (kernel_d(s.d) != s.d) return fail(ctx, "q partials need a head dim with kernels of its own (32, 64, 128)");
+    Exec x = ctx_exec(ctx);
+    x.q_parts = n_parts;
+    x.q_part_stride = (int64_t)part_stride;
+    x.q_bias = q_bias;
+    return run(ctx, x, q_parts, k, v, s, b, out);
 }
 
 extern "C" {
