@@ -51,12 +51,20 @@ struct AttnArgs {
 };
 
 // Query value at float offset `at` of a.q, column `col` of its row (head * d + dim): a.q[at], or
-// with q_parts > 1 the projection's split sum formed here, as linear_split_sum_group_kernel forms
-// it (partials added in split order, then the bias), so the value is the same bit for bit.
+// with q_parts > 1 (at most kMaxQParts) the projection's split sum formed here, as
+// linear_split_sum_group_kernel forms it (partials added in split order, then the bias), so the
+// value is the same bit for bit.  Every part's load goes out before the first add.
+constexpr int kMaxQParts = 8;
 __device__ __forceinline__ float load_q(const AttnArgs &a, int64_t at, int col) {
     if (a.q_parts <= 1) return a.q[at];
-    float s = a.q[at];
-    for (int j = 1; j < a.q_parts; ++j) s = s + a.q[at + j * a.q_part_stride];
+    float v[kMaxQParts];
+#pragma unroll
+    for (int j = 0; j < kMaxQParts; ++j)
+        if (j < a.q_parts) v[j] = a.q[at + j * a.q_part_stride];
+    float s = v[0];
+#pragma unroll
+    for (int j = 1; j < kMaxQParts; ++j)
+        if (j < a.q_parts) s = s + v[j];
     return a.q_bias ? s + a.q_bias[col] : s;
 }
 

@@ -38,7 +38,7 @@ namespace {
 constexpr float kLnEps = 1e-5f; // ops.layerNorm (src/ops.zig:342-344)
 // scratch: X, A, Q, T (m rows each), H (4 m rows), P (kMaxQParts m rows: the cross-attention
 // query's k-split partials), then the self-attention key counts
-constexpr int kMaxQParts = 8;
+constexpr int kMaxQParts = 8; // the decode kernels' load_q takes at most this many
 
 bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 

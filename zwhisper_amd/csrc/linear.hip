@@ -214,11 +214,14 @@ constexpr int q8p_waves() { return MT == 1 ? ZWG_Q8P_WAVES_32 : ZWG_Q8P_WAVES; }
 #endif
 
 
-// Row kernels of n <= 2048 floats (a wave per row, n / 256 float4 per lane, rounded up)
+// Row kernels of n <= 2048 floats (a wave per row, n / 256 float4 per lane, rounded up), one
+// wave per workgroup: a decode step's few rows then read their partials through as many CUs as
+// there are rows (four rows per workgroup put a 32-row step's 1.3 MB of partial loads through 8
+// CUs' load paths)
 template <template <int> class K, typename... Args>
 hipError_t launch_rows(int32_t n, int32_t m, hipStream_t stream, Args... args) {
     const int R = (n / 4 + 63) / 64;
-    const dim3 grid((unsigned)((m + 3) / 4)), block(256);
+    const dim3 grid((unsigned)m), block(64);
     switch (R) {
     case 1: K<1>::launch(grid, block, stream, args...); break;
     case 2: K<2>::launch(grid, block, stream, args...); break;

@@ -744,7 +744,8 @@ __global__ __launch_bounds__(256) void linear_split_sum_qkv_kernel(Q8Group grp, 
 // linear_split_sum_group_kernel with the add epilogue forms it -- then ln_out[i] = layerNorm(x[i])
 // through zwg_ew::layer_norm_regs, as layer_norm_kernel computes it.  So x and ln_out equal the
 // split sum and the layer-norm launch bit for bit.  One wave per row of n <= 256 R floats; the
-// residual row, the bias and the partials of B splits at a time are loaded before any add.
+// residual row, the bias and the partials of B splits at a time are loaded before any add.  One
+// one-wave workgroup per row.
 struct Q8ResLn {
     float *x; // [m][n] residual stream, updated in place
     const float *ln_w, *ln_b;
@@ -753,13 +754,13 @@ struct Q8ResLn {
 };
 
 template <int R>
-__global__ __launch_bounds__(256) void linear_split_sum_add_ln_kernel(const float *part, const float *bias, Q8ResLn r,
+__global__ __launch_bounds__(64) void linear_split_sum_add_ln_kernel(const float *part, const float *bias, Q8ResLn r,
                                                                      int32_t m, int32_t n, int32_t n_split) {
 #pragma clang fp contract(off)
     typedef float f4 __attribute__((ext_vector_type(4)));
     constexpr int B = 48 / R < 16 ? 48 / R : 16; // splits whose loads go out together (B R float4 per lane)
-    const int lane = threadIdx.x & 63;
-    const int row = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    const int lane = threadIdx.x;
+    const int row = (int)blockIdx.x; // one wave per workgroup, one row per wave
     if (row >= m) return;
     const int n4 = n >> 2;
     const int64_t step = (int64_t)m * n4; // float4s of one split
@@ -820,13 +821,13 @@ __global__ __launch_bounds__(256) void linear_split_sum_add_ln_kernel(const floa
 // One wave per row of n <= 256 R floats; a lane's float4 is 4 bytes of one 16-byte lane piece of
 // its block's tile (Q8Packed).
 template <int R>
-__global__ __launch_bounds__(256) void q8p_embed_ln_kernel(Q8Packed te, int32_t n_vocab, const int32_t *tok,
+__global__ __launch_bounds__(64) void q8p_embed_ln_kernel(Q8Packed te, int32_t n_vocab, const int32_t *tok,
                                                           const float *pe, const int32_t *pos, int32_t pe_rows,
                                                           int32_t m, int32_t n, float *x, Q8ResLn r) {
 #pragma clang fp contract(off)
     typedef float f4 __attribute__((ext_vector_type(4)));
-    const int lane = threadIdx.x & 63;
-    const int row = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    const int lane = threadIdx.x;
+    const int row = (int)blockIdx.x; // one wave per workgroup, one row per wave
     if (row >= m) return;
     const int n4 = n >> 2;
     const int t = tok[row], ps = pos[row];

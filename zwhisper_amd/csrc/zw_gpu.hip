@@ -308,7 +308,8 @@ int zwg_host::attention_qparts_dev(zwg_ctx *ctx, const float *q_parts, int n_par
                                    const float *q_bias, const float *k, const float *v, const zwg_attn_shape &s,
                                    const zwg_batch &b, float *out) {
     if (!ctx) return fail(nullptr, "null context");
-    if (n_parts < 2 || part_stride > 0x7fffffffffffull) return fail(ctx, "q partials: at least two, bounded stride");
+    if (n_parts < 2 || n_parts > zwg::kMaxQParts || part_stride > 0x7fffffffffffull)
+        return fail(ctx, "q partials: two to eight, bounded stride");
     if (kernel_d(s.d) != s.d) return fail(ctx, "q partials need a head dim with kernels of its own (32, 64, 128)");
     Exec x = ctx_exec(ctx);
     x.q_parts = n_parts;
