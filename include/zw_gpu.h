@@ -413,6 +413,13 @@ int zwg_layer_norm_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t n, con
                        float *out);
 int zwg_gelu_dev(zwg_ctx *ctx, float *x, uint64_t count);
 int zwg_add_dev(zwg_ctx *ctx, float *x, const float *y, uint64_t count);
+/* Qwen2's norm and MLP gate (src/llm.zig:178, :204-205): ops.rmsNorm (src/ops.zig:409-427),
+ * out[i] = x[i] / sqrt(sum(x[i]^2) / n + eps) * w per row of x [m][n]; ops.siluMul
+ * (src/ops.zig:429-439), gate = gate / (1 + e^-gate) * up in place (e^x the device's expf, the
+ * reference's expVec polynomial agreeing to a few f32 ulps).  n and count multiples of 4, buffers
+ * 16-byte aligned, device pointers, asynchronous. */
+int zwg_rms_norm_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t n, const float *w, float eps, float *out);
+int zwg_silu_mul_dev(zwg_ctx *ctx, float *gate, const float *up, uint64_t count);
 
 /*
  * One Whisper encoder layer (the loop body of Encoder.encode, src/encoder.zig:164-175) over
@@ -511,6 +518,58 @@ uint64_t zwg_decoder_scratch(uint64_t m, uint64_t n_state);
  * zwg_attention_batch_dev and zwg_linear_q8w_epi_dev calls.  Asynchronous. */
 int zwg_decoder_step_dev(zwg_ctx *ctx, const zwg_decoder *dec, const int32_t *tokens, const int32_t *pos, uint64_t m,
                          uint64_t seq0, float *logits, float *scratch);
+
+/*
+ * Qwen2's decode step on the device: Model.forward (src/llm.zig:169-216) with one new token in
+ * each of m sequences decoded in lockstep.  Weights as src/llm.zig:104-126 loads them: int8
+ * block matrices as resident zwg_q8w [out][in], f32 device vectors for norms and biases (a NULL
+ * bias adds nothing); `output` may be `embd` (tied).  The sequences are those of one zwg_kv,
+ * ZWG_KV_KT with n_head_kv, d = n_embd / n_head (32, 64 or 128) and the model's rotary base
+ * (qwen2.rope.freq_base), holding at least n_layer layers: the reference's cache_kt and cache_v
+ * (src/llm.zig:27-29).  n_embd a multiple of 4, above 256 and at most 4096; n_ff a multiple of 4.
+ */
+typedef struct zwg_llm_layer {
+    const float *attn_norm; /* [n_embd] */
+    const zwg_q8w *wq;      /* [n_embd][n_embd] */
+    const float *bq;
+    const zwg_q8w *wk; /* [n_head_kv * d][n_embd] */
+    const float *bk;
+    const zwg_q8w *wv;
+    const float *bv;
+    const zwg_q8w *wo; /* [n_embd][n_embd], no bias */
+    const float *ffn_norm;
+    const zwg_q8w *w_gate; /* [n_ff][n_embd] */
+    const zwg_q8w *w_up;
+    const zwg_q8w *w_down; /* [n_embd][n_ff] */
+} zwg_llm_layer;
+
+typedef struct zwg_llm {
+    uint64_t n_vocab, n_embd, n_head, n_head_kv, n_ff, n_layer;
+    float eps;         /* qwen2.attention.layer_norm_rms_epsilon (src/llm.zig:100) */
+    uint32_t reserved; /* must be 0 */
+    const zwg_q8w *embd;   /* [n_vocab][n_embd] */
+    const zwg_q8w *output; /* [n_vocab][n_embd] */
+    const float *output_norm;
+    const zwg_llm_layer *layers; /* host array of n_layer */
+    zwg_kv *kv;
+} zwg_llm;
+
+/* Floats of scratch a step over m sequences needs (the reference's x, h, q, attn, gate and up
+ * buffers, src/llm.zig:139-146, and the attention's key counts). */
+uint64_t zwg_llm_scratch(uint64_t m, uint64_t n_embd, uint64_t n_ff);
+
+/* forward for sequences seq0 .. seq0 + m - 1 (m <= 64), sequence i taking token tokens[i] at
+ * position pos[i] (its n_past; device int32 [m]): embedding, every layer (q and k rotated at
+ * pos[i], k scattered into the transposed cache and v into its rows, attention over the pos[i] +
+ * 1 cached keys, the SiLU-gated MLP), the output norm and the logits [m][n_vocab].  A position
+ * outside [0, n_ctx) writes no cache rows and its sequence's logits are meaningless; a token
+ * outside [0, n_vocab) embeds as a zero row.  The RMS norms are fused into the residual
+ * projections' split sums and the cache writes into the q/k/v projections', with results equal
+ * bit for bit to the same step composed of zwg_rms_norm_dev, zwg_linear_q8w_qkv_kv_dev,
+ * zwg_attention_batch_dev, zwg_linear_q8w_epi_dev, zwg_linear_q8w_group_dev and
+ * zwg_silu_mul_dev calls.  Asynchronous. */
+int zwg_llm_step_dev(zwg_ctx *ctx, const zwg_llm *lm, const int32_t *tokens, const int32_t *pos, uint64_t m,
+                     uint64_t seq0, float *logits, float *scratch);
 
 int zwg_version(void); /* ZWG_VERSION */
 

@@ -114,6 +114,10 @@ def lib():
         L.ora_layer_norm.argtypes = [ctypes.c_void_p, _fp, _c_size, _c_size, _fp, _fp, ctypes.c_float, _fp]
         L.ora_gelu.restype = None
         L.ora_gelu.argtypes = [ctypes.c_void_p, _fp, _c_size]
+        L.ora_rms_norm.restype = None
+        L.ora_rms_norm.argtypes = [_fp, _c_size, _c_size, _fp, ctypes.c_float, _fp]
+        L.ora_silu_mul.restype = None
+        L.ora_silu_mul.argtypes = [_fp, _fp, _c_size]
         L.ora_q8_quantize.restype = None
         L.ora_q8_quantize.argtypes = [_fp, _c_size, _c_size, ctypes.c_void_p, _fp]
         _lib = L
@@ -268,6 +272,25 @@ class Oracle:
         self._L.ora_gelu(self._pool, _ptr(y.reshape(-1)), y.size)
         return y
 
+    def rms_norm(self, x, m: int, n: int, w, eps: float) -> np.ndarray:
+        """ops.rmsNorm (src/ops.zig:409-427) of x [m][n]; returns out [m][n]."""
+        x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+        w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+        if x.size < m * n or w.size < n:
+            raise ValueError("x or w shorter than the shape needs")
+        out = np.empty(m * n, np.float32)
+        self._L.ora_rms_norm(_ptr(x), m, n, _ptr(w), eps, _ptr(out))
+        return out.reshape(m, n)
+
+    def silu_mul(self, gate, up) -> np.ndarray:
+        """ops.siluMul (src/ops.zig:435-439) on a copy of gate: gate / (1 + e^-gate) * up."""
+        g = np.ascontiguousarray(gate, dtype=np.float32).copy()
+        u = np.ascontiguousarray(up, dtype=np.float32).reshape(-1)
+        if u.size < g.size:
+            raise ValueError("up shorter than gate")
+        self._L.ora_silu_mul(_ptr(g.reshape(-1)), _ptr(u), g.size)
+        return g
+
     def encoder_layer(self, x, n_ctx: int, n_state: int, n_head: int, w: dict) -> np.ndarray:
         """One Whisper encoder layer (src/encoder.zig:164-175) on one window x [n_ctx][n_state] with f16
         weights (w: attn_ln_w/b, q_w/q_b, k_w, v_w/v_b, o_w/o_b, mlp_ln_w/b, mlp0_w/b, mlp1_w/b); returns
@@ -329,6 +352,46 @@ class Oracle:
             x = x + lin(h, w["mlp1_w"], w["mlp1_b"], ns, 4 * ns)
         xl = self.layer_norm(x, 1, ns, dec["ln_w"], dec["ln_b"])
         return self.linear_q8(xl, 1, ns, te_q, te_s, None, n_vocab)
+
+    def llm_forward(self, lm: dict, cache: dict, token: int, pos: int) -> np.ndarray:
+        """Model.forward (src/llm.zig:169-216) for one sequence and one token at position pos
+        (n_past), as the reference runs it: x = embd.row(token); per layer rmsNorm, q/k/v with
+        their biases, NeoX rotary positions on q and k, k scattered into the transposed cache and v
+        into its rows at pos (oracle/kv.py llm_append), attentionEx over the pos + 1 cached keys
+        (causal, kt_stride = n_ctx), o added into x, rmsNorm, the SiLU-gated MLP added into x; then
+        the output norm and logits = norm(x) . output^T.  lm: {"embd": (q, scales), "output": (q,
+        scales), "output_norm", "n_head", "n_head_kv", "eps", "cos", "sin", "layers": [dict of the
+        layer's tensors, matrices as (q, scales)]}; cache: {"kt": [n_layer][n_head_kv * d *
+        n_ctx], "v": [n_layer][n_ctx][n_head_kv * d]} (updated at pos).  Returns the logits."""
+        from types import SimpleNamespace
+
+        from . import kv as kvo
+
+        e_q, e_s = lm["embd"]
+        n_vocab, ne = e_q.shape
+        H, Hk, eps = lm["n_head"], lm["n_head_kv"], lm["eps"]
+        d = ne // H
+        kvw = Hk * d
+        n_ctx = cache["v"].shape[1]
+        lin = lambda a, w, b, n, k: self.linear_q8(a, 1, k, *w, b, n)  # noqa: E731
+        x = (e_q[token].astype(np.float32).reshape(-1, Q8_BLOCK) * e_s[token].astype(np.float32)[:, None]).reshape(-1)
+        for li, w in enumerate(lm["layers"]):
+            h = self.rms_norm(x, 1, ne, w["attn_norm"], eps)
+            q = lin(h, w["wq"], w.get("bq"), ne, ne)
+            k = lin(h, w["wk"], w.get("bk"), kvw, ne)
+            v = lin(h, w["wv"], w.get("bv"), kvw, ne)
+            kvo.llm_append(q, k, v, 1, pos, H, Hk, d, ne, cache["kt"][li], cache["v"][li], n_ctx, lm["cos"], lm["sin"])
+            sh = SimpleNamespace(n_q=1, n_kv=pos + 1, n_head=H, n_head_kv=Hk, d=d, q_stride=ne, kv_stride=kvw,
+                                 out_stride=ne, causal=True, kt_stride=n_ctx)
+            att = self.attention_ex(q, cache["kt"][li], cache["v"][li][:pos + 1], sh)
+            x = x + lin(att, w["wo"], None, ne, ne)
+            h = self.rms_norm(x, 1, ne, w["ffn_norm"], eps)
+            g = lin(h, w["w_gate"], None, w["w_gate"][0].shape[0], ne)
+            u = lin(h, w["w_up"], None, w["w_up"][0].shape[0], ne)
+            g = self.silu_mul(g, u)
+            x = x + lin(g, w["w_down"], None, ne, g.size)
+        h = self.rms_norm(x, 1, ne, lm["output_norm"], eps)
+        return self.linear_q8(h, 1, ne, *lm["output"], None, n_vocab)
 
     def attention(self, q, k, v, n_q, n_kv, n_state, n_head, causal, out=None) -> np.ndarray:
         """ops.attention (src/ops.zig:593-605)."""

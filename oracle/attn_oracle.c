@@ -28,6 +28,8 @@
  *   gemm.mc, nc ............ src/gemm.zig:27-28
  *   ops.layerNormEps ....... src/ops.zig:342-395, normRow :355-381 (ora_layer_norm)
  *   ops.gelu ............... src/ops.zig:310-340, geluScalar/geluVec :312-327 (ora_gelu)
+ *   ops.rmsNorm ............ src/ops.zig:409-427 (ora_rms_norm)
+ *   ops.siluMul ............ src/ops.zig:429-439, siluVec :429-432 (ora_silu_mul)
  *
  * V, the vector width, is 16 (the reference's value on AVX-512 hosts, src/gemm.zig:15-24):
  * it fixes the K padding (n_kv_pad), the column count of S and the split between
@@ -786,6 +788,47 @@ void ora_layer_norm(ora_pool *pool, const float *x, size_t m, size_t n, const fl
                     float *out) {
     norm_job j = {x, w, b, out, n, m, 64, eps};
     pool_parallel_for(pool, (m + 63) / 64, &j, norm_task);
+}
+
+/* ops.rmsNorm (src/ops.zig:409-427), serial as the reference runs it: per row the sum of squares
+ * in V lanes (fma), reduced, plus the scalar tail; inv = 1 / sqrt(ss / n + eps); out = row * inv
+ * * w, multiplied left to right. */
+void ora_rms_norm(const float *x, size_t m, size_t n, const float *w, float eps, float *out) {
+    for (size_t i = 0; i < m; ++i) {
+        const float *row = x + i * n;
+        float *o = out + i * n;
+        vf sv = (vf){0};
+        size_t j = 0;
+        for (; j + V <= n; j += V) {
+            const vf v = vload(row + j);
+            sv = v * v + sv;
+        }
+        float ss = hsum(sv);
+        for (; j < n; ++j) ss += row[j] * row[j];
+        const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+        j = 0;
+        for (; j + V <= n; j += V) {
+            const vf r = vload(row + j) * vsplat(inv);
+            vstore(o + j, r * vload(w + j));
+        }
+        for (; j < n; ++j) {
+            const float r = row[j] * inv;
+            o[j] = r * w[j];
+        }
+    }
+}
+
+/* ops.siluMul (src/ops.zig:429-439): gate = gate / (1 + expVec(-gate)) * up over V-wide vectors,
+ * the tail with exp; serial as the reference runs it. */
+__attribute__((optimize("fp-contract=off"))) void ora_silu_mul(float *gate, const float *up, size_t len) {
+    size_t i = 0;
+    const vf one = vsplat(1.0f);
+    for (; i + V <= len; i += V) {
+        const vf g = vload(gate + i);
+        const vf s = g / (one + exp_vec(-g));
+        vstore(gate + i, s * vload(up + i));
+    }
+    for (; i < len; ++i) gate[i] = gate[i] / (1.0f + expf(-gate[i])) * up[i];
 }
 
 /* geluScalar (src/ops.zig:312-315): std.math.tanh */

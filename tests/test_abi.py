@@ -293,5 +293,6 @@ def test_zig_binding_declares_the_whole_header():
 
     for zname, cstruct in (("Shape", _lib.ShapeC), ("Batch", _lib.BatchC), ("Limits", _lib.LimitsC),
                            ("PlanInfo", _lib.PlanC), ("KvDesc", _lib.KVDescC), ("KvInfo", _lib.KVInfoC),
-                           ("EncLayer", _lib.EncLayerC), ("DecLayer", _lib.DecLayerC), ("Decoder", _lib.DecoderC)):
+                           ("EncLayer", _lib.EncLayerC), ("DecLayer", _lib.DecLayerC), ("Decoder", _lib.DecoderC),
+                           ("LlmLayer", _lib.LlmLayerC), ("Llm", _lib.LlmC)):
         assert zig_fields(zname) == [f for f, _ in cstruct._fields_], zname

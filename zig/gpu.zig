@@ -224,6 +224,44 @@ pub extern "zwgpu" fn zwg_decoder_scratch(m: u64, n_state: u64) u64;
 pub extern "zwgpu" fn zwg_decoder_step_dev(ctx: *Ctx, dec: *const Decoder, tokens: [*]const i32, pos: [*]const i32,
     m: u64, seq0: u64, logits: [*]f32, scratch: [*]f32) c_int;
 
+// ---- Qwen2's norm, MLP gate and decode step
+
+pub extern "zwgpu" fn zwg_rms_norm_dev(ctx: *Ctx, x: [*]const f32, m: u64, n: u64, w: [*]const f32, eps: f32,
+    out: [*]f32) c_int;
+pub extern "zwgpu" fn zwg_silu_mul_dev(ctx: *Ctx, gate: [*]f32, up: [*]const f32, count: u64) c_int;
+pub const LlmLayer = extern struct {
+    attn_norm: [*]const f32,
+    wq: *const Q8w,
+    bq: ?[*]const f32,
+    wk: *const Q8w,
+    bk: ?[*]const f32,
+    wv: *const Q8w,
+    bv: ?[*]const f32,
+    wo: *const Q8w,
+    ffn_norm: [*]const f32,
+    w_gate: *const Q8w,
+    w_up: *const Q8w,
+    w_down: *const Q8w,
+};
+pub const Llm = extern struct {
+    n_vocab: u64,
+    n_embd: u64,
+    n_head: u64,
+    n_head_kv: u64,
+    n_ff: u64,
+    n_layer: u64,
+    eps: f32,
+    reserved: u32,
+    embd: *const Q8w,
+    output: *const Q8w,
+    output_norm: [*]const f32,
+    layers: [*]const LlmLayer,
+    kv: *Kv,
+};
+pub extern "zwgpu" fn zwg_llm_scratch(m: u64, n_embd: u64, n_ff: u64) u64;
+pub extern "zwgpu" fn zwg_llm_step_dev(ctx: *Ctx, lm: *const Llm, tokens: [*]const i32, pos: [*]const i32, m: u64,
+    seq0: u64, logits: [*]f32, scratch: [*]f32) c_int;
+
 // ---- the calling thread's context
 
 /// One context per thread that calls into ops (the zw_* handles are per thread too,

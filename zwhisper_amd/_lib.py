@@ -98,6 +98,31 @@ class DecoderC(ctypes.Structure):
     ]
 
 
+LLM_LAYER_FIELDS = ("attn_norm", "wq", "bq", "wk", "bk", "wv", "bv", "wo", "ffn_norm", "w_gate", "w_up", "w_down")
+
+
+class LlmLayerC(ctypes.Structure):
+    _fields_ = [(name, ctypes.c_void_p) for name in LLM_LAYER_FIELDS]
+
+
+class LlmC(ctypes.Structure):
+    _fields_ = [
+        ("n_vocab", _u64),
+        ("n_embd", _u64),
+        ("n_head", _u64),
+        ("n_head_kv", _u64),
+        ("n_ff", _u64),
+        ("n_layer", _u64),
+        ("eps", ctypes.c_float),
+        ("reserved", ctypes.c_uint32),
+        ("embd", ctypes.c_void_p),
+        ("output", ctypes.c_void_p),
+        ("output_norm", ctypes.c_void_p),
+        ("layers", ctypes.POINTER(LlmLayerC)),
+        ("kv", ctypes.c_void_p),
+    ]
+
+
 class KVDescC(ctypes.Structure):
     _fields_ = [
         ("n_layer", _u64),
@@ -227,6 +252,14 @@ def lib() -> ctypes.CDLL:
     L.zwg_encoder_layer_scratch.argtypes = [_u64, _u64]
     L.zwg_encoder_layer_dev.restype = c_int
     L.zwg_encoder_layer_dev.argtypes = [vp, _fp, _u64, _u64, _u64, _u64, ctypes.POINTER(EncLayerC), _fp]
+    L.zwg_rms_norm_dev.restype = c_int
+    L.zwg_rms_norm_dev.argtypes = [vp, _fp, _u64, _u64, _fp, ctypes.c_float, _fp]
+    L.zwg_silu_mul_dev.restype = c_int
+    L.zwg_silu_mul_dev.argtypes = [vp, _fp, _fp, _u64]
+    L.zwg_llm_scratch.restype = _u64
+    L.zwg_llm_scratch.argtypes = [_u64, _u64, _u64]
+    L.zwg_llm_step_dev.restype = c_int
+    L.zwg_llm_step_dev.argtypes = [vp, ctypes.POINTER(LlmC), vp, vp, _u64, _u64, _fp, _fp]
     L.zwg_decoder_set_audio_dev.restype = c_int
     L.zwg_decoder_set_audio_dev.argtypes = [vp, ctypes.POINTER(DecoderC), _fp, _u64, _u64]
     L.zwg_decoder_scratch.restype = _u64

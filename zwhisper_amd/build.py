@@ -25,7 +25,7 @@ CPP_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "test_attention.cpp")
 CPP_TEST_BIN = os.path.join(BUILD, "test_attention")
 
 SOURCES = ["zw_gpu.hip", "attn_flash.hip", "attn_flash_x3.hip", "attn_decode.hip", "attn_pad.hip", "attn_generic.hip", "kv_cache.hip", "linear.hip", "elementwise.hip",
-           "encoder_layer.hip", "decoder.hip"]
+           "encoder_layer.hip", "decoder.hip", "llm_step.hip"]
 HOST_SOURCES = ["zw_ops.cpp"]
 
 

@@ -86,9 +86,62 @@ __device__ __forceinline__ void layer_norm_regs(const ew_f32x4 (&v)[R], int lane
     }
 }
 
+// ops.rmsNorm (src/ops.zig:409-427) of one row held by one wave as for layer_norm_regs: ss = sum of
+// x^2 (each lane's fmas, then a butterfly sum across the wave), inv = 1 / sqrt(ss / n + eps), out
+// = x * inv * w, multiplied left to right.  Every kernel that RMS-normalises a row goes through
+// this function.
+template <int R>
+__device__ __forceinline__ void rms_norm_regs(const ew_f32x4 (&v)[R], int lane, int n4, const float *w, float eps,
+                                              float *orow) {
+    const float fn = (float)(4 * n4);
+    float q = 0.f;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int c = lane + 64 * i;
+        if (c < n4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) q = __builtin_fmaf(v[i][e], v[i][e], q);
+        }
+    }
+    const float inv = 1.0f / sqrtf(wave_sum(q) / fn + eps);
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const int c = lane + 64 * i;
+        if (c < n4) {
+            const ew_f32x4 wv = reinterpret_cast<const ew_f32x4 *>(w)[c];
+            ew_f32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+#pragma clang fp contract(off)
+                const float r = v[i][e] * inv;
+                o[e] = r * wv[e];
+            }
+            reinterpret_cast<ew_f32x4 *>(orow)[c] = o;
+        }
+    }
+}
+
+// The row norms of the fused kernels: layer norm (w, b) or RMS norm (w; b unused)
+constexpr int kNormLayer = 0, kNormRms = 1;
+template <int KIND, int R>
+__device__ __forceinline__ void norm_regs(const ew_f32x4 (&v)[R], int lane, int n4, const float *w, const float *b,
+                                          float eps, float *orow) {
+    if constexpr (KIND == kNormRms) rms_norm_regs<R>(v, lane, n4, w, eps, orow);
+    else layer_norm_regs<R>(v, lane, n4, w, b, eps, orow);
+}
+
+// ops.siluMul's element (src/ops.zig:429-439): gate / (1 + e^-gate) * up, rounded step by step in
+// that order (no contraction); e^x is the device's expf.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+#pragma clang fp contract(off)
+    const float s = g / (1.0f + expf(-g));
+    return s * u;
+}
+
 } // namespace zwg_ew
 
 namespace zwg_host {
 int layer_norm(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t n, const float *w, const float *b, float eps,
                float *out);
+int rms_norm(zwg_ctx *ctx, const float *x, uint64_t m, uint64_t n, const float *w, float eps, float *out);
 } // namespace zwg_host

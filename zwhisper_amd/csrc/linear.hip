@@ -218,36 +218,41 @@ constexpr int q8p_waves() { return MT == 1 ? ZWG_Q8P_WAVES_32 : ZWG_Q8P_WAVES; }
 // wave per workgroup: a decode step's few rows then read their partials through as many CUs as
 // there are rows (four rows per workgroup put a 32-row step's 1.3 MB of partial loads through 8
 // CUs' load paths)
-template <template <int> class K, typename... Args>
+constexpr int kMaxRowN = 4096; // the row kernels' widest row: 16 float4 per lane
+template <template <int, int> class K, int NORM, typename... Args>
 hipError_t launch_rows(int32_t n, int32_t m, hipStream_t stream, Args... args) {
     const int R = (n / 4 + 63) / 64;
     const dim3 grid((unsigned)m), block(64);
     switch (R) {
-    case 1: K<1>::launch(grid, block, stream, args...); break;
-    case 2: K<2>::launch(grid, block, stream, args...); break;
-    case 3: K<3>::launch(grid, block, stream, args...); break;
-    case 4: K<4>::launch(grid, block, stream, args...); break;
-    case 5: K<5>::launch(grid, block, stream, args...); break;
-    case 6: K<6>::launch(grid, block, stream, args...); break;
-    case 7: K<7>::launch(grid, block, stream, args...); break;
-    case 8: K<8>::launch(grid, block, stream, args...); break;
+    case 1: K<1, NORM>::launch(grid, block, stream, args...); break;
+    case 2: K<2, NORM>::launch(grid, block, stream, args...); break;
+    case 3: K<3, NORM>::launch(grid, block, stream, args...); break;
+    case 4: K<4, NORM>::launch(grid, block, stream, args...); break;
+    case 5: K<5, NORM>::launch(grid, block, stream, args...); break;
+    case 6: K<6, NORM>::launch(grid, block, stream, args...); break;
+    case 7: K<7, NORM>::launch(grid, block, stream, args...); break;
+    case 8: K<8, NORM>::launch(grid, block, stream, args...); break;
+    case 10: K<10, NORM>::launch(grid, block, stream, args...); break;
+    case 12: K<12, NORM>::launch(grid, block, stream, args...); break;
+    case 14: K<14, NORM>::launch(grid, block, stream, args...); break;
+    case 9: case 11: case 13: case 15: case 16: K<16, NORM>::launch(grid, block, stream, args...); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
-template <int R>
+template <int R, int NORM>
 struct AddLnRows {
     static void launch(dim3 g, dim3 b, hipStream_t st, const float *part, const float *bias, zwg_lin::Q8ResLn r,
                        int32_t m, int32_t n, int32_t n_split) {
-        zwg_lin::linear_split_sum_add_ln_kernel<R><<<g, b, 0, st>>>(part, bias, r, m, n, n_split);
+        zwg_lin::linear_split_sum_add_ln_kernel<R, NORM><<<g, b, 0, st>>>(part, bias, r, m, n, n_split);
     }
 };
-template <int R>
+template <int R, int NORM>
 struct EmbedLnRows {
     static void launch(dim3 g, dim3 b, hipStream_t st, zwg_lin::Q8Packed te, int32_t n_vocab, const int32_t *tok,
                        const float *pe, const int32_t *pos, int32_t pe_rows, int32_t m, int32_t n, float *x,
                        zwg_lin::Q8ResLn r) {
-        zwg_lin::q8p_embed_ln_kernel<R><<<g, b, 0, st>>>(te, n_vocab, tok, pe, pos, pe_rows, m, n, x, r);
+        zwg_lin::q8p_embed_ln_kernel<R, NORM><<<g, b, 0, st>>>(te, n_vocab, tok, pe, pos, pe_rows, m, n, x, r);
     }
 };
 
@@ -349,9 +354,12 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
     } else if (po) {
         // the caller adds the partials (attention's q load)
     } else if (resln) {
-        e = launch_rows<AddLnRows>(g.n[0], a.m, ctx->stream, (const float *)g.part[0], g.bias[0], *resln, a.m, g.n[0],
-                                   n_split);
-        if (e != hipSuccess) return fail_hip(ctx, "split-sum + residual + layer norm kernel launch", e);
+        e = resln->norm == zwg_ew::kNormRms
+                ? launch_rows<AddLnRows, zwg_ew::kNormRms>(g.n[0], a.m, ctx->stream, (const float *)g.part[0], g.bias[0],
+                                                           *resln, a.m, g.n[0], n_split)
+                : launch_rows<AddLnRows, zwg_ew::kNormLayer>(g.n[0], a.m, ctx->stream, (const float *)g.part[0],
+                                                             g.bias[0], *resln, a.m, g.n[0], n_split);
+        if (e != hipSuccess) return fail_hip(ctx, "split-sum + residual + norm kernel launch", e);
     } else if (n_split > 1) {
         const int64_t elems = (int64_t)(m * n_tot);
         const int bs = small_block(elems);
@@ -620,25 +628,29 @@ int zwg_host::linear_q8w_qkv_kv(zwg_ctx *ctx, const float *x, uint64_t m, const 
     return run_q8w_token_step(ctx, x, m, 3, w, bias, nullptr, zwg_ew::kEpiNone, &kvs);
 }
 
-// x += xin . W^T + bias and ln_out = layerNorm(x) (ln_w, ln_b, eps) for a decode step's rows
-// (m <= 64, n <= 2048): one stream launch and linear_split_sum_add_ln_kernel; a call too short to
-// split k (k <= 256) runs the add epilogue and the layer norm as two launches, with the same results.
+// x += xin . W^T + bias and ln_out = the norm of x (layer norm with ln_w, ln_b, or RMS norm with
+// ln_w; eps) for a decode step's rows (m <= 64, n <= 4096): one stream launch and
+// linear_split_sum_add_ln_kernel; a call too short to split k (k <= 256) runs the add epilogue and
+// the norm as two launches, with the same results.
 int zwg_host::linear_q8w_add_ln(zwg_ctx *ctx, const float *xin, uint64_t m, const zwg_q8w *w, const float *bias,
-                                float *x, const float *ln_w, const float *ln_b, float eps, float *ln_out) {
+                                float *x, const float *ln_w, const float *ln_b, float eps, float *ln_out, int norm) {
     if (!w || !w->ctx) return fail(ctx, w ? kQ8wClosed : "null weights");
     const std::string msg = check_linear(m, w->k, ZWG_W_Q8, w->n);
     if (!msg.empty()) return fail(ctx, msg);
     if (m == 0) return ZWG_OK;
     const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-    if (m > 64 || w->n % 4 || w->n > 2048) return fail(ctx, "the fused residual + layer norm call takes m <= 64 and n <= 2048, n % 4 == 0");
-    if (!xin || !x || !ln_w || !ln_b || !ln_out || !al16(xin) || !al16(x) || !al16(ln_w) || !al16(ln_b) ||
-        !al16(ln_out) || (bias && !al16(bias)))
+    if (m > 64 || w->n % 4 || w->n > (uint64_t)kMaxRowN)
+        return fail(ctx, "the fused residual + norm call takes m <= 64 and n <= 4096, n % 4 == 0");
+    const bool rms = norm == zwg_ew::kNormRms;
+    if (!xin || !x || !ln_w || (!rms && !ln_b) || !ln_out || !al16(xin) || !al16(x) || !al16(ln_w) ||
+        (ln_b && !al16(ln_b)) || !al16(ln_out) || (bias && !al16(bias)))
         return fail(ctx, "null or unaligned buffer (all 16-byte aligned)");
     if (w->n_chunks < 2) {
         const int rc = run_linear_q8w(ctx, xin, m, w, bias, x, zwg_ew::kEpiAdd);
-        return rc != ZWG_OK ? rc : layer_norm(ctx, x, m, w->n, ln_w, ln_b, eps, ln_out);
+        if (rc != ZWG_OK) return rc;
+        return rms ? rms_norm(ctx, x, m, w->n, ln_w, eps, ln_out) : layer_norm(ctx, x, m, w->n, ln_w, ln_b, eps, ln_out);
     }
-    zwg_lin::Q8ResLn r{x, ln_w, ln_b, ln_out, eps};
+    zwg_lin::Q8ResLn r{x, ln_w, ln_b, ln_out, eps, rms ? zwg_ew::kNormRms : zwg_ew::kNormLayer};
     float *outs[1] = {x};
     return run_q8w_token_step(ctx, xin, m, 1, &w, &bias, outs, zwg_ew::kEpiAdd, nullptr, &r);
 }
@@ -658,22 +670,27 @@ int zwg_host::linear_q8w_parts(zwg_ctx *ctx, const float *x, uint64_t m, const z
     return rc;
 }
 
-// x[i] = te.row(tok[i]) + pe[pos[i]] and ln_out[i] = layerNorm(x[i]) (q8p_embed_ln_kernel).
+// x[i] = te.row(tok[i]) + pe[pos[i]] and ln_out[i] = the norm of x[i] (q8p_embed_ln_kernel).
 int zwg_host::q8w_embed_ln(zwg_ctx *ctx, const zwg_q8w *te, const int32_t *tok, const float *pe, const int32_t *pos,
                            uint64_t pe_rows, uint64_t m, float *x, const float *ln_w, const float *ln_b, float eps,
-                           float *ln_out) {
+                           float *ln_out, int norm) {
     if (!te || !te->ctx) return fail(ctx, te ? kQ8wClosed : "null weights");
     if (m == 0) return ZWG_OK;
     const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-    if (te->k % 4 || te->k > 2048 || m > 0x7fffffffull || pe_rows > 0x7fffffffull)
-        return fail(ctx, "embedding rows of at most 2048 floats, a multiple of 4");
-    if (!tok || !pos || !x || !ln_w || !ln_b || !ln_out || (pe_rows && !pe) || !al16(x) || !al16(ln_w) ||
-        !al16(ln_b) || !al16(ln_out) || (pe && !al16(pe)))
+    if (te->k % 4 || te->k > (uint64_t)kMaxRowN || m > 0x7fffffffull || pe_rows > 0x7fffffffull)
+        return fail(ctx, "embedding rows of at most 4096 floats, a multiple of 4");
+    const bool rms = norm == zwg_ew::kNormRms;
+    if (!tok || !pos || !x || !ln_w || (!rms && !ln_b) || !ln_out || (pe_rows && !pe) || !al16(x) || !al16(ln_w) ||
+        (ln_b && !al16(ln_b)) || !al16(ln_out) || (pe && !al16(pe)))
         return fail(ctx, "null or unaligned buffer (all 16-byte aligned)");
     zwg_lin::Q8Packed tp{te->q, te->scales, te->n_slabs, te->n_chunks};
-    zwg_lin::Q8ResLn r{nullptr, ln_w, ln_b, ln_out, eps};
-    const hipError_t e = launch_rows<EmbedLnRows>((int32_t)te->k, (int32_t)m, ctx->stream, tp, (int32_t)te->n, tok, pe,
-                                                  pos, (int32_t)pe_rows, (int32_t)m, (int32_t)te->k, x, r);
+    zwg_lin::Q8ResLn r{nullptr, ln_w, ln_b, ln_out, eps, rms ? zwg_ew::kNormRms : zwg_ew::kNormLayer};
+    const hipError_t e =
+        rms ? launch_rows<EmbedLnRows, zwg_ew::kNormRms>((int32_t)te->k, (int32_t)m, ctx->stream, tp, (int32_t)te->n,
+                                                         tok, pe, pos, (int32_t)pe_rows, (int32_t)m, (int32_t)te->k, x, r)
+            : launch_rows<EmbedLnRows, zwg_ew::kNormLayer>((int32_t)te->k, (int32_t)m, ctx->stream, tp,
+                                                           (int32_t)te->n, tok, pe, pos, (int32_t)pe_rows, (int32_t)m,
+                                                           (int32_t)te->k, x, r);
     return e == hipSuccess ? ZWG_OK : fail_hip(ctx, "token embedding kernel launch", e);
 }
 

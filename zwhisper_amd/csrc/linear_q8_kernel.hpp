@@ -740,20 +740,22 @@ __global__ __launch_bounds__(256) void linear_split_sum_qkv_kernel(Q8Group grp, 
 
 // A one-set call's split sum added to the residual stream and normalised, for the decoder blocks'
 // ops.linear + ops.add + next ops.layerNorm (src/decoder.zig:185-188, :192-195, :200 with the
-// next block's :178): row i of x += sum over splits (in split order) of part[s][i] + bias -- as
-// linear_split_sum_group_kernel with the add epilogue forms it -- then ln_out[i] = layerNorm(x[i])
-// through zwg_ew::layer_norm_regs, as layer_norm_kernel computes it.  So x and ln_out equal the
-// split sum and the layer-norm launch bit for bit.  One wave per row of n <= 256 R floats; the
+// next block's :178) and Qwen2's + ops.rmsNorm (src/llm.zig:203-204, :206-207 with :178): row i
+// of x += sum over splits (in split order) of part[s][i] + bias -- as
+// linear_split_sum_group_kernel with the add epilogue forms it -- then ln_out[i] = the norm of
+// x[i] (NORM: zwg_ew::kNormLayer or kNormRms, through the functions layer_norm_kernel and
+// rms_norm_kernel use).  So x and ln_out equal the split sum and the norm launch bit for bit.  One wave per row of n <= 256 R floats; the
 // residual row, the bias and the partials of B splits at a time are loaded before any add.  One
 // one-wave workgroup per row.
 struct Q8ResLn {
     float *x; // [m][n] residual stream, updated in place
-    const float *ln_w, *ln_b;
+    const float *ln_w, *ln_b; // ln_b unused by the RMS norm
     float *ln_out; // [m][n]
     float eps;
+    int32_t norm; // zwg_ew::kNormLayer or kNormRms (host side: which instantiation)
 };
 
-template <int R>
+template <int R, int NORM>
 __global__ __launch_bounds__(64) void linear_split_sum_add_ln_kernel(const float *part, const float *bias, Q8ResLn r,
                                                                      int32_t m, int32_t n, int32_t n_split) {
 #pragma clang fp contract(off)
@@ -810,17 +812,18 @@ __global__ __launch_bounds__(64) void linear_split_sum_add_ln_kernel(const float
             v[i] = (zwg_ew::ew_f32x4){0.f, 0.f, 0.f, 0.f};
         }
     }
-    zwg_ew::layer_norm_regs<R>(v, lane, n4, r.ln_w, r.ln_b, r.eps, r.ln_out + (int64_t)row * n);
+    zwg_ew::norm_regs<NORM, R>(v, lane, n4, r.ln_w, r.ln_b, r.eps, r.ln_out + (int64_t)row * n);
 }
 
 // A decode step's token embeddings from the packed int8 token embedding (the tied output
 // projection): x[i] = te.row(tok[i]) + pe[pos[i]] -- gemm.Q8.row (src/gemm.zig:257-265, q * scale
-// in f32) then ops.add (src/decoder.zig:171-174) -- and ln_out[i] = layerNorm(x[i]) (the first
-// block's attn_ln, src/decoder.zig:178) through zwg_ew::layer_norm_regs.  A token outside
+// in f32) then ops.add (src/decoder.zig:171-174) -- and ln_out[i] = the norm of x[i] (the first
+// block's attn_ln, src/decoder.zig:178; for Qwen2, no position rows and the first block's RMS
+// norm, src/llm.zig:175-178).  A token outside
 // [0, n_vocab) gives a zero embedding row; a position outside [0, pe_rows) adds no position row.
 // One wave per row of n <= 256 R floats; a lane's float4 is 4 bytes of one 16-byte lane piece of
 // its block's tile (Q8Packed).
-template <int R>
+template <int R, int NORM>
 __global__ __launch_bounds__(64) void q8p_embed_ln_kernel(Q8Packed te, int32_t n_vocab, const int32_t *tok,
                                                           const float *pe, const int32_t *pos, int32_t pe_rows,
                                                           int32_t m, int32_t n, float *x, Q8ResLn r) {
@@ -855,7 +858,7 @@ __global__ __launch_bounds__(64) void q8p_embed_ln_kernel(Q8Packed te, int32_t n
         }
         v[i] = val;
     }
-    zwg_ew::layer_norm_regs<R>(v, lane, n4, r.ln_w, r.ln_b, r.eps, r.ln_out + (int64_t)row * n);
+    zwg_ew::norm_regs<NORM, R>(v, lane, n4, r.ln_w, r.ln_b, r.eps, r.ln_out + (int64_t)row * n);
 }
 
 } // namespace zwg_lin

@@ -1,0 +1,169 @@
+// Qwen2's decode step on the device (include/zw_gpu.h, zwg_llm_step_dev): Model.forward
+// (src/llm.zig:169-216) with one new token in each of m sequences decoded in lockstep, the caches
+// in HBM as one zwg_kv (transposed keys, rotary positions).
+//
+// A step over m sequences (X: residual stream, H: normalised rows, Q, T: attention in and out,
+// G, U: MLP gate and up rows -- the reference's x, h, q, attn, gate and up, src/llm.zig:139-146):
+//
+//   X = embd.row(tok); H = rmsNorm(X, attn_norm)      q8p_embed_ln_kernel (RMS), one launch
+//   per layer:
+//     Q = rope(q(H)); rope(k(H)) -> K^T cache, v(H) -> V cache at pos
+//                                                    stream + linear_split_sum_qkv_kernel, which
+//                                                    also writes the key counts pos + 1
+//     T = attention(Q, caches[0 .. pos])             decode kernel over transposed keys (+ merge)
+//     X += o(T); H = rmsNorm(X, ffn_norm)            stream + linear_split_sum_add_ln_kernel (RMS)
+//     G, U = gate(H), up(H)                          one grouped call
+//     G = silu(G) * U                                silu_mul_kernel
+//     X += down(G); H = next layer's attn_norm(X), or the output norm after the last layer
+//   logits = H . output^T
+//
+// The fused launches form the same values in the same order as the separate calls (the split
+// sums in split order, the residual add, zwg_ew::rms_norm_regs for every norm), so the results
+// are equal bit for bit.  The attention is the reference's causal call with one query, whose only
+// row sees every cached key: it runs non-causal over each sequence's own key count.
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "elementwise.hpp"
+#include "zw_ctx.hpp"
+#include "zw_gpu.h"
+
+using namespace zwg_host;
+
+namespace {
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+std::string check_q8(const zwg_q8w *w, uint64_t n, uint64_t k, const char *name) {
+    uint64_t wn = 0, wk = 0;
+    if (!w) return std::string("null weights ") + name;
+    if (zwg_q8w_shape(w, &wn, &wk) != ZWG_OK) return std::string("closed weights ") + name;
+    if (wn != n || wk != k)
+        return std::string("weights ") + name + " are " + std::to_string(wn) + " x " + std::to_string(wk) +
+               ", expected " + std::to_string(n) + " x " + std::to_string(k);
+    return "";
+}
+
+std::string check_vec(const float *p, bool required, const char *name) {
+    if (!p) return required ? std::string("null ") + name : "";
+    return aligned16(p) ? "" : std::string(name) + " must be 16-byte aligned";
+}
+
+std::string check_llm(const zwg_ctx *ctx, const zwg_llm &lm, uint64_t n_seq_needed) {
+    const uint64_t ne = lm.n_embd, H = lm.n_head, Hk = lm.n_head_kv;
+    if (!lm.layers || lm.n_layer == 0) return "a model needs n_layer >= 1 layers";
+    if (lm.reserved) return "reserved must be 0";
+    if (H == 0 || Hk == 0 || ne % H || H % Hk) return "n_embd must be a multiple of n_head, n_head of n_head_kv";
+    if (ne % 4 || ne <= 256 || ne > 4096) return "n_embd must be a multiple of 4, above 256 and at most 4096";
+    if (lm.n_ff == 0 || lm.n_ff % 4) return "n_ff must be a positive multiple of 4";
+    if (!(lm.eps >= 0.0f)) return "eps must be >= 0";
+    const uint64_t d = ne / H;
+    if (d != 32 && d != 64 && d != 128) return "head dim n_embd / n_head must be 32, 64 or 128";
+    const zwg_kv *kv = lm.kv;
+    if (!kv) return "null cache";
+    if (kv->ctx != ctx) return "the cache belongs to another context (or its context is closed)";
+    const zwg_kv_desc &k = kv->desc;
+    if (k.layout != ZWG_KV_KT || k.n_head_kv != Hk || k.d != d || !(k.rope_base > 0.0))
+        return "the cache must be ZWG_KV_KT with the model's n_head_kv, d = n_embd / n_head and rotary positions";
+    if (k.n_layer < lm.n_layer) return "the cache has fewer layers than the model";
+    if (k.n_seq < n_seq_needed) return "sequences out of range of the cache";
+    std::string msg = check_q8(lm.embd, lm.n_vocab, ne, "embd");
+    if (msg.empty()) msg = check_q8(lm.output, lm.n_vocab, ne, "output");
+    if (msg.empty()) msg = check_vec(lm.output_norm, true, "output_norm");
+    const uint64_t kvw = Hk * d;
+    for (uint64_t l = 0; l < lm.n_layer && msg.empty(); ++l) {
+        const zwg_llm_layer &L = lm.layers[l];
+        msg = check_q8(L.wq, ne, ne, "wq");
+        if (msg.empty()) msg = check_q8(L.wk, kvw, ne, "wk");
+        if (msg.empty()) msg = check_q8(L.wv, kvw, ne, "wv");
+        if (msg.empty()) msg = check_q8(L.wo, ne, ne, "wo");
+        if (msg.empty()) msg = check_q8(L.w_gate, lm.n_ff, ne, "w_gate");
+        if (msg.empty()) msg = check_q8(L.w_up, lm.n_ff, ne, "w_up");
+        if (msg.empty()) msg = check_q8(L.w_down, ne, lm.n_ff, "w_down");
+        if (msg.empty()) msg = check_vec(L.attn_norm, true, "attn_norm");
+        if (msg.empty()) msg = check_vec(L.ffn_norm, true, "ffn_norm");
+        const float *biases[3] = {L.bq, L.bk, L.bv};
+        for (int j = 0; j < 3 && msg.empty(); ++j) msg = check_vec(biases[j], false, "biases");
+    }
+    return msg;
+}
+
+} // namespace
+
+extern "C" {
+
+uint64_t zwg_llm_scratch(uint64_t m, uint64_t n_embd, uint64_t n_ff) {
+    return 4 * m * n_embd + 2 * m * n_ff + (m + 3) / 4 * 4;
+}
+
+int zwg_llm_step_dev(zwg_ctx *ctx, const zwg_llm *lm, const int32_t *tokens, const int32_t *pos, uint64_t m,
+                     uint64_t seq0, float *logits, float *scratch) {
+    if (!ctx) return fail(nullptr, "null context");
+    if (!lm) return fail(ctx, "null model");
+    if (m == 0) return ZWG_OK;
+    if (m > 64) return fail(ctx, "a decode step takes at most 64 sequences");
+    const std::string msg = check_llm(ctx, *lm, seq0 + m);
+    if (!msg.empty()) return fail(ctx, msg);
+    if (!tokens || !pos) return fail(ctx, "null tokens or pos");
+    if (!logits || !scratch || !aligned16(logits) || !aligned16(scratch))
+        return fail(ctx, "logits and scratch must be non-null and 16-byte aligned");
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
+
+    const uint64_t ne = lm->n_embd, nff = lm->n_ff, H = lm->n_head, Hk = lm->n_head_kv, d = ne / H;
+    const int rms = zwg_ew::kNormRms;
+    float *X = scratch, *Hn = X + m * ne, *Q = Hn + m * ne, *T = Q + m * ne, *G = T + m * ne, *U = G + m * nff;
+    int32_t *n_kv = reinterpret_cast<int32_t *>(U + m * nff);
+    zwg_kv *kv = lm->kv;
+    // src/llm.zig:175: embd.row, then the first block's attn_norm (:178)
+    int rc = q8w_embed_ln(ctx, lm->embd, tokens, nullptr, pos, 0, m, X, lm->layers[0].attn_norm, nullptr, lm->eps, Hn,
+                          rms);
+    if (rc != ZWG_OK) return rc;
+
+    // one query per sequence over its transposed key cache (src/llm.zig:191-202)
+    zwg_attn_shape sh{};
+    sh.n_q = 1;
+    sh.n_kv = kv->desc.n_ctx;
+    sh.n_head = H;
+    sh.n_head_kv = Hk;
+    sh.d = d;
+    sh.q_stride = ne;
+    sh.kv_stride = Hk * d;
+    sh.out_stride = ne;
+    sh.kt_stride = kv->desc.n_ctx;
+    sh.causal = 0;
+    zwg_batch bt{};
+    bt.n_batch = m;
+    bt.q_bstride = ne;
+    bt.k_bstride = kv->per_seq;
+    bt.v_bstride = kv->per_seq;
+    bt.out_bstride = ne;
+    bt.n_kv_dev = n_kv;
+
+    for (uint64_t l = 0; l < lm->n_layer; ++l) {
+        const zwg_llm_layer &L = lm->layers[l];
+        // src/llm.zig:179-190: q/k/v, rotary positions, the cache writes
+        const zwg_q8w *qkv[3] = {L.wq, L.wk, L.wv};
+        const float *qkv_b[3] = {L.bq, L.bk, L.bv};
+        if ((rc = linear_q8w_qkv_kv(ctx, Hn, m, qkv, qkv_b, Q, kv, l, seq0, pos, n_kv)) != ZWG_OK) return rc;
+        const uint64_t at = (l * kv->desc.n_seq + seq0) * kv->per_seq;
+        if ((rc = zwg_attention_batch_dev(ctx, Q, kv->k + at, kv->v + at, &sh, &bt, T)) != ZWG_OK) return rc;
+        // :203-204 and the ffn norm (:206)
+        if ((rc = linear_q8w_add_ln(ctx, T, m, L.wo, nullptr, X, L.ffn_norm, nullptr, lm->eps, Hn, rms)) != ZWG_OK)
+            return rc;
+        // :207-211: gate and up, SiLU-gated, down, then the next block's attn_norm or the output
+        // norm (:215)
+        const zwg_q8w *gu[2] = {L.w_gate, L.w_up};
+        float *gu_out[2] = {G, U};
+        if ((rc = zwg_linear_q8w_group_dev(ctx, Hn, m, 2, gu, nullptr, gu_out)) != ZWG_OK) return rc;
+        if ((rc = zwg_silu_mul_dev(ctx, G, U, m * nff)) != ZWG_OK) return rc;
+        const float *nw = l + 1 == lm->n_layer ? lm->output_norm : lm->layers[l + 1].attn_norm;
+        if ((rc = linear_q8w_add_ln(ctx, G, m, L.w_down, nullptr, X, nw, nullptr, lm->eps, Hn, rms)) != ZWG_OK)
+            return rc;
+    }
+    // the logits of every sequence's token (src/llm.zig:216)
+    return zwg_linear_q8w_dev(ctx, Hn, m, lm->output, nullptr, logits);
+}
+
+} // extern "C"

@@ -93,15 +93,15 @@ int linear_q8w_parts(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w,
 int linear_q8w_qkv_kv(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *const *w, const float *const *bias,
                       float *q_out, zwg_kv *kv, uint64_t layer, uint64_t seq0, const int32_t *pos_dev,
                       int32_t *n_kv_out);
-// A decode step's residual projection and the next layer norm: x += xin . W^T + bias, then
-// ln_out = layerNorm(x) (m <= 64, n <= 2048; linear.hip).
+// A decode step's residual projection and the next norm: x += xin . W^T + bias, then ln_out =
+// the norm of x (norm 0: layer norm, 1: RMS norm; m <= 64, n <= 4096; linear.hip).
 int linear_q8w_add_ln(zwg_ctx *ctx, const float *xin, uint64_t m, const zwg_q8w *w, const float *bias, float *x,
-                      const float *ln_w, const float *ln_b, float eps, float *ln_out);
-// Token embeddings from packed int8 rows plus positional rows, and their layer norm: x[i] =
-// te.row(tok[i]) + pe[pos[i]], ln_out[i] = layerNorm(x[i]) (n <= 2048; linear.hip).
+                      const float *ln_w, const float *ln_b, float eps, float *ln_out, int norm = 0);
+// Token embeddings from packed int8 rows plus positional rows (pe may be null), and their norm:
+// x[i] = te.row(tok[i]) + pe[pos[i]], ln_out[i] = the norm of x[i] (n <= 4096; linear.hip).
 int q8w_embed_ln(zwg_ctx *ctx, const zwg_q8w *te, const int32_t *tok, const float *pe, const int32_t *pos,
                  uint64_t pe_rows, uint64_t m, float *x, const float *ln_w, const float *ln_b, float eps,
-                 float *ln_out);
+                 float *ln_out, int norm = 0);
 // Register / unregister an object made from ctx (see ZwgChild).
 void add_child(zwg_ctx *ctx, void *obj, void (*detach)(void *));
 void remove_child(zwg_ctx *ctx, void *obj);

@@ -311,6 +311,22 @@ class Context:
         self._check(self._L.zwg_layer_norm_dev(self._h, self._dev_ptr(x, "x"), m, n, self._dev_ptr(w, "w"),
                                                self._dev_ptr(b, "b"), eps, self._dev_ptr(out, "out")))
 
+    def rms_norm_dev(self, x, m: int, n: int, w, eps: float, out) -> None:
+        """ops.rmsNorm (src/ops.zig:409-427) on CUDA float32 tensors."""
+        if x.numel() < m * n or out.numel() < m * n or w.numel() < n:
+            raise ZwgError("a tensor is shorter than m and n need")
+        self._bind_torch_stream()
+        self._check(self._L.zwg_rms_norm_dev(self._h, self._dev_ptr(x, "x"), m, n, self._dev_ptr(w, "w"), eps,
+                                             self._dev_ptr(out, "out")))
+
+    def silu_mul_dev(self, gate, up) -> None:
+        """ops.siluMul (src/ops.zig:435-439): gate = gate / (1 + e^-gate) * up, CUDA float32 tensors."""
+        if up.numel() < gate.numel():
+            raise ZwgError("up is shorter than gate")
+        self._bind_torch_stream()
+        self._check(self._L.zwg_silu_mul_dev(self._h, self._dev_ptr(gate, "gate"), self._dev_ptr(up, "up"),
+                                             gate.numel()))
+
     def gelu_dev(self, x) -> None:
         """ops.gelu (src/ops.zig:335-340) in place on a CUDA float32 tensor."""
         self._bind_torch_stream()
@@ -554,6 +570,91 @@ class Decoder:
         self.ctx._check(self._L.zwg_decoder_step_dev(self.ctx.handle, ctypes_byref(self.c), tokens.data_ptr(),
                                                      pos.data_ptr(), m, seq0, Context._dev_ptr(logits, "logits"),
                                                      Context._dev_ptr(self.scratch, "scratch")))
+
+    def close(self) -> None:
+        for o in reversed(self._owned):
+            o.close()
+        self._owned = []
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+class LLM:
+    """Qwen2's decode step on the device (zwg_llm_step_dev): src/llm.zig's Model.forward
+    (src/llm.zig:169-216) for n_seq sequences decoded in lockstep, one token per sequence per step.
+
+    layers: one dict per layer mapping the zwg_llm_layer field names (_lib.LLM_LAYER_FIELDS) to a
+    Q8 (the matrices) or a float32 array / CUDA tensor (norms, biases; a bias may be None); embd:
+    Q8 [n_vocab][n_embd]; output: Q8 or None (tied to embd); output_norm [n_embd].  The weights are
+    made resident and the cache (transposed keys, rotary base rope_base) allocated here; close()
+    frees them."""
+
+    def __init__(self, ctx: Context, embd: "Q8", output, output_norm, layers, n_head: int, n_head_kv: int,
+                 n_ff: int, n_ctx: int, n_seq: int, rope_base: float = 1e6, eps: float = 1e-6):
+        import torch
+
+        self.ctx = ctx
+        self._L = ctx._L
+        self.n_vocab, self.n_embd, self.n_head, self.n_head_kv = embd.n, embd.k, n_head, n_head_kv
+        self.n_ff, self.n_layer, self.n_ctx, self.n_seq, self.eps = n_ff, len(layers), n_ctx, n_seq, eps
+        self._owned, self._keep = [], []
+
+        def vec(a):
+            if a is None:
+                return None
+            t = a if isinstance(a, torch.Tensor) else torch.from_numpy(np.ascontiguousarray(a, np.float32))
+            t = t.to(device=f"cuda:{ctx.device}", dtype=torch.float32).contiguous()
+            self._keep.append(t)
+            return t.data_ptr()
+
+        def res(w):
+            r = w.resident(ctx)
+            self._owned.append(r)
+            return r.handle
+
+        self.embd = embd.resident(ctx)
+        self._owned.append(self.embd)
+        self.output = self.embd if output is None else output.resident(ctx)
+        if output is not None:
+            self._owned.append(self.output)
+        c_layers = (_lib.LlmLayerC * self.n_layer)()
+        self.layer_refs = []
+        for li, lw in enumerate(layers):
+            vals, refs = {}, {}
+            for name in _lib.LLM_LAYER_FIELDS:
+                v = lw.get(name)
+                vals[name] = res(v) if isinstance(v, Q8) else vec(v)
+                refs[name] = (self._owned[-1] if isinstance(v, Q8) else self._keep[-1]) if v is not None else None
+            c_layers[li] = _lib.LlmLayerC(**vals)
+            self.layer_refs.append(refs)
+        self.kv = KVCache(ctx, self.n_layer, n_seq, n_ctx, n_head_kv, self.n_embd // n_head, _lib.KV_KT, rope_base)
+        self._owned.append(self.kv)
+        self._layers = c_layers
+        on_p = vec(output_norm)
+        self.output_norm = self._keep[-1]
+        self.c = _lib.LlmC(self.n_vocab, self.n_embd, n_head, n_head_kv, n_ff, self.n_layer, eps, 0, self.embd.handle,
+                           self.output.handle, on_p, c_layers, self.kv._h.value)
+        self.scratch = torch.empty(int(self._L.zwg_llm_scratch(64, self.n_embd, n_ff)), device=f"cuda:{ctx.device}")
+
+    def step(self, tokens, pos, logits, seq0: int = 0) -> None:
+        """One token per sequence for sequences seq0 .. seq0 + m - 1 (tokens, pos: CUDA int32 tensors
+        of m entries, pos the sequences' n_past); logits [m][n_vocab] (CUDA float32) written."""
+        import torch
+
+        m = tokens.numel()
+        for name, t in (("tokens", tokens), ("pos", pos)):
+            if not t.is_cuda or t.dtype != torch.int32 or t.numel() != m:
+                raise ZwgError(f"{name} must be a CUDA int32 tensor of m entries")
+        if logits.numel() < m * self.n_vocab:
+            raise ZwgError("logits is shorter than m x n_vocab")
+        self.ctx._bind_torch_stream()
+        self.ctx._check(self._L.zwg_llm_step_dev(self.ctx.handle, ctypes_byref(self.c), tokens.data_ptr(),
+                                                 pos.data_ptr(), m, seq0, Context._dev_ptr(logits, "logits"),
+                                                 Context._dev_ptr(self.scratch, "scratch")))
 
     def close(self) -> None:
         for o in reversed(self._owned):
