@@ -1060,6 +1060,184 @@ class DecoderStepWorkload:
         self.dec = self.self_kv = self.cross_kv = self._host_src = None
 
 
+class LlmStepWorkload:
+    """Qwen2's decode step on the device (zwg_llm_step_dev: Model.forward, src/llm.zig:169-216, one
+    new token in each of m sequences decoded in lockstep): the embedding rows, every layer's RMS
+    norm, q/k/v projections with rotary positions and the cache writes (keys transposed), GQA
+    attention over each sequence's cached keys, the output projection, the SwiGLU MLP, then the
+    output norm and the logits over the vocabulary (tied to the embedding, as Qwen2.5-1.5B's).
+    Random int8 block weights of the model's shapes, resident; sequence s decodes at position
+    n_kv_s - 1 with the Qwen2.5-1.5B decode lengths (n_kv ~ U[1024, 4096]).  A step is one replay of
+    a HIP graph of the call.
+
+    Algorithmic bytes per step: every layer's int8 weights, block scales, biases and norms read
+    once, the output weights once, each sequence's embedding row, its K/V rows 0..pos read once
+    per layer and its new k and v rows written, and the logits written.  Beside it the record times
+    the same step composed of the separate calls ("unfused": RMS norms, q/k/v + cache, attention,
+    int8 linears with the add epilogue, the grouped gate/up call, SiLU-mul), which gives the same
+    results bit for bit."""
+
+    dtype = ("f32 (projections: f32 x int8 block weights on f16 MFMA, x split into two f16 terms; attention: "
+             "f32 FMA decode kernels over the transposed keys)")
+
+    def __init__(self, name: str, description: str, torch, ctx, m: int = 64, n_layer: int = 28, ne: int = 1536,
+                 n_head: int = 12, n_head_kv: int = 2, n_ff: int = 8960, n_vocab: int = 151936, n_ctx: int = 4096,
+                 rope_base: float = 1e6, eps: float = 1e-6):
+        import zwhisper_amd as z
+        from zwhisper_amd import _lib
+        from zwhisper_amd.workloads import kv_lengths
+
+        self.name, self.description = name, description
+        self.torch, self.ctx, self.m, self.ne, self.H, self.Hk = torch, ctx, m, ne, n_head, n_head_kv
+        self.n_layer, self.n_ff, self.n_vocab, self.n_ctx, self.eps = n_layer, n_ff, n_vocab, n_ctx, eps
+        d = ne // n_head
+        kvw = n_head_kv * d
+        g = torch.Generator(device="cuda").manual_seed(0x0B0B)
+
+        def q8(n, k):
+            q = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda", generator=g)
+            sc = torch.rand(n, k // 32, device="cuda", generator=g) * (2.0 / 127 / np.sqrt(k))
+            return z.Q8(q, sc, n, k)
+
+        def vec(n, base=0.0, scale=0.1):
+            return base + scale * torch.randn(n, device="cuda", generator=g)
+
+        layers = []
+        for _ in range(n_layer):
+            layers.append({"wq": q8(ne, ne), "wk": q8(kvw, ne), "wv": q8(kvw, ne), "wo": q8(ne, ne),
+                           "w_gate": q8(n_ff, ne), "w_up": q8(n_ff, ne), "w_down": q8(ne, n_ff),
+                           "bq": vec(ne, scale=0.3), "bk": vec(kvw, scale=0.3), "bv": vec(kvw),
+                           "attn_norm": vec(ne, 1.0), "ffn_norm": vec(ne, 1.0)})
+        embd = q8(n_vocab, ne)
+        output_norm = vec(ne, 1.0)
+        self.lm = z.LLM(ctx, embd, None, output_norm, layers, n_head, n_head_kv, n_ff, n_ctx, m, rope_base, eps)
+        self._host_src = (embd, output_norm, layers)
+        n_kv = kv_lengths(5)[:m].astype(np.int64)
+        self.n_kv = n_kv
+        self.pos = torch.from_numpy((n_kv - 1).astype(np.int32)).cuda()
+        self.tok = torch.randint(0, n_vocab, (m,), dtype=torch.int32, device="cuda", generator=g)
+        self.logits = torch.empty(m, n_vocab, device="cuda")
+        self._lu = torch.empty_like(self.logits)
+        wb = sum(w.n * w.k * 1.125 for lw in layers for w in lw.values() if isinstance(w, z.Q8))
+        vb = 4.0 * sum(t.numel() for lw in layers for t in lw.values() if not isinstance(t, z.Q8))
+        kvb = 4.0 * kvw * n_layer * (2 * float(n_kv.sum()) + 2 * m)
+        self.work = float(wb + vb + embd.n * embd.k * 1.125 + 4.0 * ne + m * ne * 1.125 + kvb + 4.0 * m * n_vocab)
+        # the unfused step: the separate calls over the same weights, its own cache
+        self.kv = z.KVCache(ctx, n_layer, m, n_ctx, n_head_kv, d, _lib.KV_KT, rope_base)
+        self.X, self.Hn, self.Q, self.T = (torch.empty(m, ne, device="cuda") for _ in range(4))
+        self.G, self.U = torch.empty(m, n_ff, device="cuda"), torch.empty(m, n_ff, device="cuda")
+        # the embedding rows embd.row(tok): f32 products as the fused kernel's
+        tl = self.tok.long()
+        self.E = embd.q[tl].float() * embd.scales[tl].repeat_interleave(32, dim=1)
+        self.n_kv_t = (self.pos + 1).to(torch.int32)
+        self.graphs = {}
+        for mode in ("fused", "unfused"):
+            self._run(mode)
+            torch.cuda.synchronize()
+            gr = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(gr):
+                self._run(mode)
+            self.graphs[mode] = gr
+        torch.cuda.synchronize()
+
+    def _run(self, mode: str):
+        import zwhisper_amd as z
+        from zwhisper_amd import _lib
+
+        if mode == "fused":
+            self.lm.step(self.tok, self.pos, self.logits, 0)
+            return
+        ctx, lm, m, ne, nff = self.ctx, self.lm, self.m, self.ne, self.n_ff
+        X, Hn, Q, T, G, U = self.X, self.Hn, self.Q, self.T, self.G, self.U
+        X.copy_(self.E)
+        ctx.rms_norm_dev(X, m, ne, lm.layer_refs[0]["attn_norm"], self.eps, Hn)
+        d = ne // self.H
+        sh = z.AttnShape(1, self.n_ctx, self.H, self.Hk, d, ne, self.Hk * d, ne, False, self.n_ctx)
+        ps = self.kv.info.seq_stride
+        for li, L in enumerate(lm.layer_refs):
+            ctx.linear_q8w_qkv_kv_dev(Hn, m, [L["wq"], L["wk"], L["wv"]], [L["bq"], L["bk"], L["bv"]], Q, self.kv, li,
+                                      0, self.pos)
+            k, v = self.kv.ptrs(li, 0)
+            ctx.attention_batch_dev(Q, k, v, sh, T, m, ne, ps, ps, ne, self.n_kv_t)
+            ctx.linear_q8w_epi_dev(T, m, L["wo"], None, X, _lib.EPI_ADD)
+            ctx.rms_norm_dev(X, m, ne, L["ffn_norm"], self.eps, Hn)
+            ctx.linear_q8w_group_dev(Hn, m, [L["w_gate"], L["w_up"]], None, [G, U])
+            ctx.silu_mul_dev(G, U)
+            ctx.linear_q8w_epi_dev(G, m, L["w_down"], None, X, _lib.EPI_ADD)
+            last = li + 1 == self.n_layer
+            ctx.rms_norm_dev(X, m, ne, lm.output_norm if last else lm.layer_refs[li + 1]["attn_norm"], self.eps, Hn)
+        ctx.linear_q8w_dev(Hn, m, lm.output, None, self._lu)
+
+    def step(self, i: int):
+        self.graphs["fused"].replay()
+
+    def extra_record(self, steps: int) -> dict:
+        """The unfused step timed as the fused one, the bit-for-bit check of the two and tokens/s."""
+        torch = self.torch
+        for _ in range(5):
+            self.graphs["unfused"].replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            self.graphs["unfused"].replay()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        self.graphs["fused"].replay()
+        torch.cuda.synchronize()
+        same = bool(torch.equal(self.logits, self._lu))
+        return {"unfused": {"kernel_ms_per_step": ms, "logits_equal_bitwise": same,
+                            "note": "the same step as separate calls (RMS norms, q/k/v + cache, attention, int8 "
+                                    "linears with the add epilogue, grouped gate/up, SiLU-mul), one HIP-graph "
+                                    "replay per step"},
+                "tokens_per_step": self.m}
+
+    def cpu_baseline(self, threads: int) -> dict:
+        """The oracle's Model.forward (Oracle.llm_forward: ops.linear over Q8, rmsNorm, the rotary
+        cache writes, attentionEx over the transposed cache, siluMul, the reference's steps) for
+        one sequence's token, all layers and the logits."""
+        import oracle
+        from oracle import kv as kvo
+
+        embd, output_norm, layers = self._host_src
+        d = self.ne // self.H
+        hl = [{nm: ((t.q.cpu().numpy(), t.scales.cpu().numpy()) if hasattr(t, "scales") else t.cpu().numpy())
+               for nm, t in lw.items()} for lw in layers]
+        e = (embd.q.cpu().numpy(), embd.scales.cpu().numpy())
+        cos, sin = kvo.rope_tables(self.n_ctx, d, 1e6)
+        lm = {"embd": e, "output": e, "output_norm": output_norm.cpu().numpy(), "n_head": self.H,
+              "n_head_kv": self.Hk, "eps": self.eps, "cos": cos, "sin": sin, "layers": hl}
+        cache = {"kt": np.zeros((self.n_layer, self.Hk * d * self.n_ctx), np.float32),
+                 "v": np.zeros((self.n_layer, self.n_ctx, self.Hk * d), np.float32)}
+        s0 = 0
+        pos = int(self.n_kv[s0]) - 1
+        tok = int(self.tok[s0].item())
+        o = oracle.Oracle(threads)
+
+        def run():
+            o.llm_forward(lm, cache, tok, pos)
+
+        best, mean, runs = time_cpu(run, 3)
+        o.close()
+        kvw = self.Hk * d
+        kv_all = 4.0 * kvw * self.n_layer * (2 * float(self.n_kv.sum()) + 2 * self.m)
+        kv_one = 4.0 * kvw * self.n_layer * (2 * (pos + 1) + 2)
+        per_seq = self.ne * 1.125 + 4.0 * self.n_vocab
+        work1 = self.work - kv_all - self.m * per_seq + kv_one + per_seq
+        return {"value": 1.0 / best, "unit": "tokens/s", "cores": o.threads, "kind": "port",
+                "bytes_per_token": work1, "gb_per_s": work1 / best / 1e9,
+                "sample": f"one sequence's token (position {pos}) through all {self.n_layer} layers and the logits, "
+                          "as the reference decodes a sequence; oracle Model.forward over oracle/attn_oracle.c; "
+                          + cpu_timing(best, mean, runs), "seconds": best}
+
+    def free(self):
+        self.graphs = None
+        self.lm.close()
+        self.kv.close()
+        self.lm = self.kv = self._host_src = None
+
+
 def q8_workloads(torch, ctx):
     """(name, constructor) of the int8 decode-step measurements."""
     qwen_layer = [(1536, 1536, True), (1536, 256, True), (1536, 256, True), (1536, 1536, False),
@@ -1092,6 +1270,11 @@ def q8_workloads(torch, ctx):
         "q and k rotated (base 1e6), k scattered into the transposed device cache and v into its rows "
         "(src/llm.zig:179-190), int8 block weights", torch, ctx, 64, 1536, 28, 12, 2, 128, True, 1e6, 4096,
         (True, True, True))
+    yield "qwen15_step_x64", lambda: LlmStepWorkload(
+        "qwen15_step_x64", "Qwen2.5-1.5B decode token step, 64 sequences in lockstep (src/llm.zig:169-216): "
+        "embeddings, 28 layers of RMS norm, q/k/v with rotary positions into the transposed cache, GQA attention "
+        "(12q/2kv x 128) over each sequence's cache (n_kv ~ U[1024, 4096]) and the SwiGLU MLP, int8 block weights, "
+        "then the 151936-token logits (tied output)", torch, ctx)
 
 
 def time_workload(wl, steps: int, warmup: int) -> dict:
@@ -1378,7 +1561,7 @@ def _say(name: str, res: dict, peak_name: str) -> None:
 EXTRAS = ("qwen05_prefill_8x256", "small_dec_kv_append_x32", "qwen15_kv_append_x64", "qwen05_prefill_kv_append",
           "base_enc_linear_x16",
           "base_enc_layer_x16", "qwen15_logits_q8_x64", "qwen15_decode_q8_linear_x64", "small_dec_q8_linear_x32",
-          "small_dec_qkv_cache_x32", "qwen15_qkv_cache_x64", "small_dec_step_x32")
+          "small_dec_qkv_cache_x32", "qwen15_qkv_cache_x64", "small_dec_step_x32", "qwen15_step_x64")
 
 
 def run_extra(name: str, torch, ctx, args, threads: int) -> dict:

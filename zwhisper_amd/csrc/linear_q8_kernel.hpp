@@ -815,6 +815,60 @@ __global__ __launch_bounds__(64) void linear_split_sum_add_ln_kernel(const float
     zwg_ew::norm_regs<NORM, R>(v, lane, n4, r.ln_w, r.ln_b, r.eps, r.ln_out + (int64_t)row * n);
 }
 
+// The same sums, residual add and norm with one thread per float4 column (R waves per row, n <=
+// 256 R floats): each thread has up to 24 of its column's splits in flight at once, where the
+// one-wave kernel walks R columns per lane in batches of 48 / R splits (the Qwen2.5-1.5B down
+// projection's 35 splits of 1536-float rows: 18 batches of loads one after another per wave).
+// The new row goes through LDS to the first wave, which normalises it with norm_regs exactly as
+// the one-wave kernel does (so the two give the same bits).
+template <int R, int NORM>
+__global__ __launch_bounds__(64 * R) void linear_split_sum_add_ln_wide_kernel(const float *part, const float *bias,
+                                                                              Q8ResLn r, int32_t m, int32_t n,
+                                                                              int32_t n_split) {
+#pragma clang fp contract(off)
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    constexpr int B = 24;
+    __shared__ f4 rowbuf[64 * R];
+    const int c = threadIdx.x; // this thread's float4 column
+    const int row = (int)blockIdx.x;
+    if (row >= m) return;
+    const int n4 = n >> 2;
+    const bool live = c < n4;
+    const int64_t step = (int64_t)m * n4;
+    const f4 *p = reinterpret_cast<const f4 *>(part) + (int64_t)row * n4 + c;
+    f4 *xr = reinterpret_cast<f4 *>(r.x + (int64_t)row * n);
+    f4 xo = {0.f, 0.f, 0.f, 0.f}, bo = {0.f, 0.f, 0.f, 0.f};
+    if (live) {
+        xo = xr[c];
+        if (bias) bo = reinterpret_cast<const f4 *>(bias)[c];
+    }
+    f4 s = {0.f, 0.f, 0.f, 0.f};
+    for (int q0 = 0; q0 < n_split; q0 += B) {
+        f4 t[B];
+#pragma unroll
+        for (int j = 0; j < B; ++j)
+            if (live && q0 + j < n_split) t[j] = p[(q0 + j) * step];
+#pragma unroll
+        for (int j = 0; j < B; ++j)
+            if (live && q0 + j < n_split) s = q0 + j == 0 ? t[j] : s + t[j];
+    }
+    f4 nx = {0.f, 0.f, 0.f, 0.f};
+    if (live) {
+        f4 val = s;
+        if (bias) val = val + bo;
+        nx = xo + val;
+        xr[c] = nx;
+    }
+    rowbuf[c] = nx;
+    __syncthreads();
+    if (c < 64) {
+        zwg_ew::ew_f32x4 v[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) v[i] = rowbuf[c + 64 * i];
+        zwg_ew::norm_regs<NORM, R>(v, c, n4, r.ln_w, r.ln_b, r.eps, r.ln_out + (int64_t)row * n);
+    }
+}
+
 // A decode step's token embeddings from the packed int8 token embedding (the tied output
 // projection): x[i] = te.row(tok[i]) + pe[pos[i]] -- gemm.Q8.row (src/gemm.zig:257-265, q * scale
 // in f32) then ops.add (src/decoder.zig:171-174) -- and ln_out[i] = the norm of x[i] (the first
