@@ -555,7 +555,8 @@ typedef struct zwg_llm {
 } zwg_llm;
 
 /* Floats of scratch a step over m sequences needs (the reference's x, h, q, attn, gate and up
- * buffers, src/llm.zig:139-146, and the attention's key counts). */
+ * buffers, src/llm.zig:139-146, the attention's key counts and the ffn-normed rows split into f16
+ * halves for the gate/up projections). */
 uint64_t zwg_llm_scratch(uint64_t m, uint64_t n_embd, uint64_t n_ff);
 
 /* forward for sequences seq0 .. seq0 + m - 1 (m <= 64), sequence i taking token tokens[i] at

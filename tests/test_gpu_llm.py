@@ -174,6 +174,38 @@ def test_step_bit_exact_with_composed_calls(torch, ctx, ne, H, Hk, nff):
                     assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1]), (step, li, s)
 
 
+@pytest.mark.parametrize("m", [40, 64])
+def test_step_bit_exact_33_to_64_rows(torch, ctx, m):
+    """33..64 sequences take the 64-row kernels, and (n_ff 8192: the gate/up call streams a split
+    x) the o projection's sum kernel splits the ffn-normed rows for it, zero rows past m
+    included."""
+    import zwhisper_amd as z
+    from zwhisper_amd import _lib
+
+    rng = np.random.default_rng(m)
+    ne, H, Hk, nff, n_layer, n_vocab, n_ctx = 384, 6, 2, 8192, 2, 300, 16
+    print(f"llm step n_embd={ne} heads {H}/{Hk} n_ff={nff} layers={n_layer} sequences {m}", flush=True)
+    mdl = model(rng, ne, H, Hk, nff, n_layer, n_vocab)
+    with contextlib.ExitStack() as st:
+        lm = st.enter_context(make_llm(z, ctx, mdl, H, Hk, nff, n_ctx, m))
+        kv = st.enter_context(z.KVCache(ctx, n_layer, m, n_ctx, Hk, ne // H, _lib.KV_KT, 1e6))
+        start = rng.integers(0, n_ctx - 2, m)
+        start[3] = -1
+        la = torch.empty(m, n_vocab, device="cuda")
+        lb = torch.empty(m, n_vocab, device="cuda")
+        for step in range(2):
+            pos = np.where(start >= 0, start + step, -1).astype(np.int32)
+            tok = rng.integers(0, n_vocab, m).astype(np.int32)
+            lm.step(torch.from_numpy(tok).cuda(), torch.from_numpy(pos).cuda(), la, 0)
+            composed_step(torch, ctx, lm, kv, mdl["embd"], H, Hk, tok, pos, 0, lb)
+            torch.cuda.synchronize()
+            assert torch.equal(la, lb), step
+            for li in range(n_layer):
+                for s in (0, 5, m - 1):
+                    a, b = lm.kv.read(li, s), kv.read(li, s)
+                    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1]), (step, li, s)
+
+
 def test_step_against_oracle(torch, ctx):
     import oracle
     import zwhisper_amd as z

@@ -51,9 +51,10 @@ __device__ __forceinline__ float wave_sum(float v) {
 // mean) * inv, w, b).  The sums are reduced across the wave by butterfly, so their rounding order
 // differs from the reference's 16-lane vector order (a few f32 ulps).  Every kernel that normalises
 // a row goes through this function, so a fused norm equals the separate one bit for bit.
+// copy: nullptr, or a second destination of the output float4s (same index as in orow).
 template <int R>
 __device__ __forceinline__ void layer_norm_regs(const ew_f32x4 (&v)[R], int lane, int n4, const float *w,
-                                                const float *b, float eps, float *orow) {
+                                                const float *b, float eps, float *orow, ew_f32x4 *copy = nullptr) {
     const float fn = (float)(4 * n4);
     float s = 0.f;
 #pragma unroll
@@ -82,6 +83,7 @@ __device__ __forceinline__ void layer_norm_regs(const ew_f32x4 (&v)[R], int lane
 #pragma unroll
             for (int e = 0; e < 4; ++e) o[e] = __builtin_fmaf((v[i][e] - mean) * inv, wv[e], bv[e]);
             reinterpret_cast<ew_f32x4 *>(orow)[c] = o;
+            if (copy) copy[c] = o;
         }
     }
 }
@@ -92,7 +94,7 @@ __device__ __forceinline__ void layer_norm_regs(const ew_f32x4 (&v)[R], int lane
 // this function.
 template <int R>
 __device__ __forceinline__ void rms_norm_regs(const ew_f32x4 (&v)[R], int lane, int n4, const float *w, float eps,
-                                              float *orow) {
+                                              float *orow, ew_f32x4 *copy = nullptr) {
     const float fn = (float)(4 * n4);
     float q = 0.f;
 #pragma unroll
@@ -117,6 +119,7 @@ __device__ __forceinline__ void rms_norm_regs(const ew_f32x4 (&v)[R], int lane, 
                 o[e] = r * wv[e];
             }
             reinterpret_cast<ew_f32x4 *>(orow)[c] = o;
+            if (copy) copy[c] = o;
         }
     }
 }
@@ -125,9 +128,9 @@ __device__ __forceinline__ void rms_norm_regs(const ew_f32x4 (&v)[R], int lane, 
 constexpr int kNormLayer = 0, kNormRms = 1;
 template <int KIND, int R>
 __device__ __forceinline__ void norm_regs(const ew_f32x4 (&v)[R], int lane, int n4, const float *w, const float *b,
-                                          float eps, float *orow) {
-    if constexpr (KIND == kNormRms) rms_norm_regs<R>(v, lane, n4, w, eps, orow);
-    else layer_norm_regs<R>(v, lane, n4, w, b, eps, orow);
+                                          float eps, float *orow, ew_f32x4 *copy = nullptr) {
+    if constexpr (KIND == kNormRms) rms_norm_regs<R>(v, lane, n4, w, eps, orow, copy);
+    else layer_norm_regs<R>(v, lane, n4, w, b, eps, orow, copy);
 }
 
 // ops.siluMul's element (src/ops.zig:429-439): gate / (1 + e^-gate) * up, rounded step by step in

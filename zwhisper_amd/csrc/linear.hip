@@ -283,10 +283,18 @@ struct Q8PartsOut {
     int max_parts;
     int n_split;
 };
+bool q8p_split_k(int64_t gx, int n_chunks) { return gx < ZWG_Q8P_SPLIT_BELOW && n_chunks > 1; }
+// 32-row calls split x inside the stream kernel; 64-row ones too when k is split (small calls,
+// where the separate pass's launch costs more than the fused split), otherwise in a pass of their
+// own first.
+template <int MT>
+bool q8p_splits_x_itself(int64_t gx, int n_chunks) {
+    return MT == 1 || (ZWG_Q8P_XS_SPLIT && q8p_split_k(gx, n_chunks));
+}
 template <int MT>
 int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
                   const zwg_lin::Q8KvStore *kvs = nullptr, const zwg_lin::Q8ResLn *resln = nullptr,
-                  Q8PartsOut *po = nullptr) {
+                  Q8PartsOut *po = nullptr, const _Float16 *xcvt_in = nullptr) {
     constexpr int kQ8pWaves = q8p_waves<MT>();
     zwg_lin::Q8Args a = base;
     const uint64_t m = (uint64_t)a.m;
@@ -304,12 +312,14 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
     g.elem_start[zwg_lin::kQ8MaxGroup] = (int64_t)(m * n_tot);
     const int n_chunks = (a.k + zwg_lin::kQ8Chunk - 1) / zwg_lin::kQ8Chunk;
     g.n_chunks = n_chunks;
-    // 32-row calls split x inside the stream kernel; 64-row ones too when k is split (small
-    // calls, where the separate pass's launch costs more than the fused split), otherwise in a
-    // pass of their own first
-    const bool split_k = gx < ZWG_Q8P_SPLIT_BELOW && n_chunks > 1;
-    const bool XS = MT == 1 || (ZWG_Q8P_XS_SPLIT && split_k);
-    const uint64_t xcvt_bytes = XS ? 0 : (uint64_t)n_chunks * zwg_lin::q8_chunk_halves<MT>() * 2;
+    const bool split_k = q8p_split_k(gx, n_chunks);
+    // xcvt_in (a 64-row call): x was split by the caller's previous launch.  The partial sums keep
+    // the place (and so the split count) the call has without it.
+    const bool xs_own = q8p_splits_x_itself<MT>(gx, n_chunks);
+    const bool XS = xs_own && !(MT == 2 && xcvt_in);
+    if (resln && resln->xcvt && (ZWG_ADDLN_WIDE == 0 || MT != 2))
+        return fail(ctx, "split rows for the next call come from 33..64-row calls' one-thread-per-column sums");
+    const uint64_t xcvt_bytes = xs_own ? 0 : (uint64_t)n_chunks * zwg_lin::q8_chunk_halves<MT>() * 2;
     const uint64_t part_off = (xcvt_bytes + 255) / 256 * 256;
     if (part_off > ctx->workspace_bytes) return fail(ctx, "workspace too small for this linear call");
     int n_split = 1;
@@ -334,13 +344,14 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
         g.part[0] = po->part;
         po->n_split = n_split;
     }
-    _Float16 *xcvt = XS ? nullptr : reinterpret_cast<_Float16 *>(ctx->workspace);
+    // xcvt_in: x already split in this layout by the previous call's row kernel
+    const _Float16 *xcvt = XS ? nullptr : xcvt_in ? xcvt_in : reinterpret_cast<_Float16 *>(ctx->workspace);
     hipError_t e;
-    if (!XS) {
+    if (!XS && !xcvt_in) {
         const int64_t prep_threads = (int64_t)n_chunks * MT * 32 * (zwg_lin::kQ8Chunk / 4);
         const int prep_bs = small_block(prep_threads);
         zwg_lin::linear_q8_xprep_kernel<MT><<<blocks_for(prep_threads, prep_bs), prep_bs, 0, ctx->stream>>>(
-            a.x, xcvt, a.m, a.k, n_chunks);
+            a.x, reinterpret_cast<_Float16 *>(ctx->workspace), a.m, a.k, n_chunks);
         e = hipGetLastError();
         if (e != hipSuccess) return fail_hip(ctx, "linear (int8) x preparation launch", e);
     }
@@ -548,7 +559,7 @@ void detach_q8w(void *obj) {
 int run_q8w_token_step(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t n_w, const zwg_q8w *const *w,
                        const float *const *bias, float *const *out, uint32_t epi,
                        const zwg_lin::Q8KvStore *kvs = nullptr, const zwg_lin::Q8ResLn *resln = nullptr,
-                       Q8PartsOut *po = nullptr) {
+                       Q8PartsOut *po = nullptr, const _Float16 *xcvt_in = nullptr) {
     zwg_lin::Q8Args a{};
     a.x = x;
     a.m = (int32_t)m;
@@ -565,7 +576,8 @@ int run_q8w_token_step(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t n_w, c
         g.bias[j] = bias ? bias[j] : nullptr;
         g.out[j] = out ? out[j] : nullptr;
     }
-    return m > 32 ? run_q8p_group<2>(ctx, a, g, kvs, resln, po) : run_q8p_group<1>(ctx, a, g, kvs, resln, po);
+    return m > 32 ? run_q8p_group<2>(ctx, a, g, kvs, resln, po, xcvt_in)
+                  : run_q8p_group<1>(ctx, a, g, kvs, resln, po, xcvt_in);
 }
 
 int run_linear_q8w(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, const float *bias, float *out,
@@ -647,9 +659,11 @@ int zwg_host::linear_q8w_qkv_kv(zwg_ctx *ctx, const float *x, uint64_t m, const 
 // x += xin . W^T + bias and ln_out = the norm of x (layer norm with ln_w, ln_b, or RMS norm with
 // ln_w; eps) for a decode step's rows (m <= 64, n <= 4096): one stream launch and
 // linear_split_sum_add_ln_kernel; a call too short to split k (k <= 256) runs the add epilogue and
-// the norm as two launches, with the same results.
+// the norm as two launches, with the same results.  xcvt_out (33..64 rows): ln_out also split for
+// the next call (q8w_xcvt_halves(n) halves), which takes it as xcvt_in.
 int zwg_host::linear_q8w_add_ln(zwg_ctx *ctx, const float *xin, uint64_t m, const zwg_q8w *w, const float *bias,
-                                float *x, const float *ln_w, const float *ln_b, float eps, float *ln_out, int norm) {
+                                float *x, const float *ln_w, const float *ln_b, float eps, float *ln_out, int norm,
+                                _Float16 *xcvt_out) {
     if (!w || !w->ctx) return fail(ctx, w ? kQ8wClosed : "null weights");
     const std::string msg = check_linear(m, w->k, ZWG_W_Q8, w->n);
     if (!msg.empty()) return fail(ctx, msg);
@@ -661,14 +675,50 @@ int zwg_host::linear_q8w_add_ln(zwg_ctx *ctx, const float *xin, uint64_t m, cons
     if (!xin || !x || !ln_w || (!rms && !ln_b) || !ln_out || !al16(xin) || !al16(x) || !al16(ln_w) ||
         (ln_b && !al16(ln_b)) || !al16(ln_out) || (bias && !al16(bias)))
         return fail(ctx, "null or unaligned buffer (all 16-byte aligned)");
+    if (xcvt_out && (m <= 32 || !al16(xcvt_out)))
+        return fail(ctx, "split rows for the next call are for 33..64-row steps (16-byte aligned)");
     if (w->n_chunks < 2) {
+        if (xcvt_out) return fail(ctx, "the split rows for the next call need k above 256");
         const int rc = run_linear_q8w(ctx, xin, m, w, bias, x, zwg_ew::kEpiAdd);
         if (rc != ZWG_OK) return rc;
         return rms ? rms_norm(ctx, x, m, w->n, ln_w, eps, ln_out) : layer_norm(ctx, x, m, w->n, ln_w, ln_b, eps, ln_out);
     }
-    zwg_lin::Q8ResLn r{x, ln_w, ln_b, ln_out, eps, rms ? zwg_ew::kNormRms : zwg_ew::kNormLayer};
+    zwg_lin::Q8ResLn r{x, ln_w, ln_b, ln_out, eps, rms ? zwg_ew::kNormRms : zwg_ew::kNormLayer, xcvt_out};
     float *outs[1] = {x};
     return run_q8w_token_step(ctx, xin, m, 1, &w, &bias, outs, zwg_ew::kEpiAdd, nullptr, &r);
+}
+
+bool zwg_host::q8w_group_reads_xcvt(uint64_t m, uint32_t n_w, const zwg_q8w *const *w) {
+    if (m <= 32 || m > 64 || n_w == 0 || n_w > (uint32_t)zwg_lin::kQ8MaxGroup) return false;
+    constexpr int kRows = 32 * q8p_waves<2>();
+    int64_t gx = 0;
+    for (uint32_t j = 0; j < n_w; ++j) gx += ((int64_t)w[j]->n + kRows - 1) / kRows;
+    const int n_chunks = (int)((w[0]->k + zwg_lin::kQ8Chunk - 1) / zwg_lin::kQ8Chunk);
+    return !q8p_splits_x_itself<2>(gx, n_chunks);
+}
+
+uint64_t zwg_host::q8w_xcvt_halves(uint64_t k) {
+    return (k + zwg_lin::kQ8Chunk - 1) / zwg_lin::kQ8Chunk * (uint64_t)zwg_lin::q8_chunk_halves<2>();
+}
+
+// A grouped token-step call (as zwg_linear_q8w_group_dev, m <= 64) whose x was split by the
+// previous call (linear_q8w_add_ln's xcvt_out, from the same rows); used where the call streams
+// its x from a split pass (33..64 rows, unsplit k), ignored where it splits x itself.
+int zwg_host::linear_q8w_group_xcvt(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t n_w, const zwg_q8w *const *w,
+                                    const float *const *bias, float *const *out, const _Float16 *xcvt_in) {
+    if (n_w == 0 || n_w > (uint32_t)zwg_lin::kQ8MaxGroup || !w || !out) return fail(ctx, "n_w must be 1..4");
+    const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    for (uint32_t j = 0; j < n_w; ++j) {
+        if (!w[j] || !w[j]->ctx) return fail(ctx, w[j] ? kQ8wClosed : "null weights");
+        if (w[j]->k != w[0]->k) return fail(ctx, "the weights of a group must share k");
+        const std::string msg = check_linear(m, w[j]->k, ZWG_W_Q8, w[j]->n);
+        if (!msg.empty()) return fail(ctx, msg);
+        if (m && (!out[j] || !al16(out[j]))) return fail(ctx, "outputs must be non-null and 16-byte aligned");
+    }
+    if (m == 0) return ZWG_OK;
+    if (m > 64 || !x || !al16(x) || (xcvt_in && (!al16(xcvt_in) || m <= 32)))
+        return fail(ctx, "a token-step group call: m <= 64, x 16-byte aligned, split rows for 33..64 rows");
+    return run_q8w_token_step(ctx, x, m, n_w, w, bias, out, zwg_ew::kEpiNone, nullptr, nullptr, nullptr, xcvt_in);
 }
 
 int zwg_host::linear_q8w_parts(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, float *parts,

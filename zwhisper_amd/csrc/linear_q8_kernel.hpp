@@ -85,6 +85,25 @@ __device__ __forceinline__ int q8_xs_at(int b, int i, int hl, int s, int lane) {
     return ((((b * MT + i) * 2 + hl) * 2 + s) * 64 + lane) * 8;
 }
 
+// x[row][gk .. gk + 3] (gk % 4 == 0) split into f16 hi/lo halves at its place in xcvt's chunk
+// layout above: hi = f16(v), lo = f16(v - hi)
+template <int MT>
+__device__ __forceinline__ void q8_xs_store(_Float16 *xcvt, int row, int gk, f32x4 v) {
+    const int c = gk / kQ8Chunk, kk = gk % kQ8Chunk;
+    const int b = kk >> 5, kb = kk & 31;
+    const int gg = kb >> 4, s = (kb >> 3) & 1, j = kb & 7;
+    const int i = row >> 5, l = (row & 31) + 32 * gg;
+    half4 hi, lo;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        hi[e] = (_Float16)v[e];
+        lo[e] = (_Float16)(v[e] - (float)hi[e]);
+    }
+    _Float16 *base = xcvt + (int64_t)c * q8_chunk_halves<MT>();
+    *reinterpret_cast<half4 *>(base + q8_xs_at<MT>(b, i, 0, s, l) + j) = hi;
+    *reinterpret_cast<half4 *>(base + q8_xs_at<MT>(b, i, 1, s, l) + j) = lo;
+}
+
 // x f32 [m][k] -> xcvt f16 [n_chunks][chunk layout above]; rows >= m and columns >= k are 0.
 // One thread per 4 consecutive k of one row.
 template <int MT>
@@ -98,18 +117,7 @@ __global__ __launch_bounds__(256) void linear_q8_xprep_kernel(const float *x, _F
     const int gk = c * kQ8Chunk + kk;
     f32x4 v = {0.f, 0.f, 0.f, 0.f};
     if (row < m && gk < k) v = *reinterpret_cast<const f32x4 *>(x + (int64_t)row * k + gk);
-    const int b = kk >> 5, kb = kk & 31;
-    const int gg = kb >> 4, s = (kb >> 3) & 1, j = kb & 7;
-    const int i = row >> 5, l = (row & 31) + 32 * gg;
-    half4 hi, lo;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        hi[e] = (_Float16)v[e];
-        lo[e] = (_Float16)(v[e] - (float)hi[e]);
-    }
-    _Float16 *base = xcvt + (int64_t)c * q8_chunk_halves<MT>();
-    *reinterpret_cast<half4 *>(base + q8_xs_at<MT>(b, i, 0, s, l) + j) = hi;
-    *reinterpret_cast<half4 *>(base + q8_xs_at<MT>(b, i, 1, s, l) + j) = lo;
+    q8_xs_store<MT>(xcvt, row, gk, v);
 }
 
 template <int MT, int S>
@@ -753,6 +761,10 @@ struct Q8ResLn {
     float *ln_out; // [m][n]
     float eps;
     int32_t norm; // zwg_ew::kNormLayer or kNormRms (host side: which instantiation)
+    // nullptr, or the normalised rows also split into f16 hi/lo halves for the next 64-row call
+    // (linear_q8_xprep_kernel's layout and values, rows m .. 63 zero); the one-thread-per-column
+    // kernel only
+    _Float16 *xcvt;
 };
 
 template <int R, int NORM>
@@ -865,7 +877,17 @@ __global__ __launch_bounds__(64 * R) void linear_split_sum_add_ln_wide_kernel(co
         zwg_ew::ew_f32x4 v[R];
 #pragma unroll
         for (int i = 0; i < R; ++i) v[i] = rowbuf[c + 64 * i];
-        zwg_ew::norm_regs<NORM, R>(v, c, n4, r.ln_w, r.ln_b, r.eps, r.ln_out + (int64_t)row * n);
+        // with xcvt the normalised row also goes back into rowbuf (past n4 it stays zero)
+        zwg_ew::norm_regs<NORM, R>(v, c, n4, r.ln_w, r.ln_b, r.eps, r.ln_out + (int64_t)row * n,
+                                   r.xcvt ? rowbuf : nullptr);
+    }
+    if (r.xcvt) {
+        __syncthreads();
+        const int n_cols = (n + kQ8Chunk - 1) / kQ8Chunk * (kQ8Chunk / 4); // float4 columns of whole chunks
+        if (c < n_cols) {
+            q8_xs_store<2>(r.xcvt, row, 4 * c, rowbuf[c]);
+            for (int z = row + m; z < 64; z += m) q8_xs_store<2>(r.xcvt, z, 4 * c, (f32x4){0.f, 0.f, 0.f, 0.f});
+        }
     }
 }
 

@@ -11,15 +11,18 @@
 //                                                    stream + linear_split_sum_qkv_kernel, which
 //                                                    also writes the key counts pos + 1
 //     T = attention(Q, caches[0 .. pos])             decode kernel over transposed keys (+ merge)
-//     X += o(T); H = rmsNorm(X, ffn_norm)            stream + linear_split_sum_add_ln_kernel (RMS)
-//     G, U = gate(H), up(H)                          one grouped call
+//     X += o(T); H = rmsNorm(X, ffn_norm)            stream + linear_split_sum_add_ln_wide_kernel
+//                                                    (RMS), which also splits H into f16 hi/lo
+//                                                    halves when the gate/up call reads a split x
+//     G, U = gate(H), up(H)                          one grouped call (no split launch of its own)
 //     G = silu(G) * U                                silu_mul_kernel
 //     X += down(G); H = next layer's attn_norm(X), or the output norm after the last layer
+//                                                    stream + the sum, residual add and norm
 //   logits = H . output^T
 //
 // The fused launches form the same values in the same order as the separate calls (the split
-// sums in split order, the residual add, zwg_ew::rms_norm_regs for every norm), so the results
-// are equal bit for bit.  The attention is the reference's causal call with one query, whose only
+// sums in split order, the residual add, zwg_ew::rms_norm_regs for every norm, the x split's f16
+// rounding), so the results are equal bit for bit.  The attention is the reference's causal call with one query, whose only
 // row sees every cached key: it runs non-causal over each sequence's own key count.
 #include <hip/hip_runtime.h>
 
@@ -94,7 +97,7 @@ std::string check_llm(const zwg_ctx *ctx, const zwg_llm &lm, uint64_t n_seq_need
 extern "C" {
 
 uint64_t zwg_llm_scratch(uint64_t m, uint64_t n_embd, uint64_t n_ff) {
-    return 4 * m * n_embd + 2 * m * n_ff + (m + 3) / 4 * 4;
+    return 4 * m * n_embd + 2 * m * n_ff + (m + 3) / 4 * 4 + q8w_xcvt_halves(n_embd) / 2;
 }
 
 int zwg_llm_step_dev(zwg_ctx *ctx, const zwg_llm *lm, const int32_t *tokens, const int32_t *pos, uint64_t m,
@@ -115,6 +118,9 @@ int zwg_llm_step_dev(zwg_ctx *ctx, const zwg_llm *lm, const int32_t *tokens, con
     const int rms = zwg_ew::kNormRms;
     float *X = scratch, *Hn = X + m * ne, *Q = Hn + m * ne, *T = Q + m * ne, *G = T + m * ne, *U = G + m * nff;
     int32_t *n_kv = reinterpret_cast<int32_t *>(U + m * nff);
+    // the ffn-normed rows split for the gate/up call, when that call reads a split pass (written by
+    // the o projection's sum kernel, so the call needs no split launch of its own)
+    _Float16 *xc = reinterpret_cast<_Float16 *>(reinterpret_cast<float *>(n_kv) + (m + 3) / 4 * 4);
     zwg_kv *kv = lm->kv;
     // src/llm.zig:175: embd.row, then the first block's attn_norm (:178)
     int rc = q8w_embed_ln(ctx, lm->embd, tokens, nullptr, pos, 0, m, X, lm->layers[0].attn_norm, nullptr, lm->eps, Hn,
@@ -141,6 +147,8 @@ int zwg_llm_step_dev(zwg_ctx *ctx, const zwg_llm *lm, const int32_t *tokens, con
     bt.out_bstride = ne;
     bt.n_kv_dev = n_kv;
 
+    const zwg_q8w *gu0[2] = {lm->layers[0].w_gate, lm->layers[0].w_up};
+    _Float16 *gu_xc = q8w_group_reads_xcvt(m, 2, gu0) ? xc : nullptr;
     for (uint64_t l = 0; l < lm->n_layer; ++l) {
         const zwg_llm_layer &L = lm->layers[l];
         // src/llm.zig:179-190: q/k/v, rotary positions, the cache writes
@@ -150,13 +158,14 @@ int zwg_llm_step_dev(zwg_ctx *ctx, const zwg_llm *lm, const int32_t *tokens, con
         const uint64_t at = (l * kv->desc.n_seq + seq0) * kv->per_seq;
         if ((rc = zwg_attention_batch_dev(ctx, Q, kv->k + at, kv->v + at, &sh, &bt, T)) != ZWG_OK) return rc;
         // :203-204 and the ffn norm (:206)
-        if ((rc = linear_q8w_add_ln(ctx, T, m, L.wo, nullptr, X, L.ffn_norm, nullptr, lm->eps, Hn, rms)) != ZWG_OK)
+        if ((rc = linear_q8w_add_ln(ctx, T, m, L.wo, nullptr, X, L.ffn_norm, nullptr, lm->eps, Hn, rms, gu_xc)) !=
+            ZWG_OK)
             return rc;
         // :207-211: gate and up, SiLU-gated, down, then the next block's attn_norm or the output
         // norm (:215)
         const zwg_q8w *gu[2] = {L.w_gate, L.w_up};
         float *gu_out[2] = {G, U};
-        if ((rc = zwg_linear_q8w_group_dev(ctx, Hn, m, 2, gu, nullptr, gu_out)) != ZWG_OK) return rc;
+        if ((rc = linear_q8w_group_xcvt(ctx, Hn, m, 2, gu, nullptr, gu_out, gu_xc)) != ZWG_OK) return rc;
         if ((rc = zwg_silu_mul_dev(ctx, G, U, m * nff)) != ZWG_OK) return rc;
         const float *nw = l + 1 == lm->n_layer ? lm->output_norm : lm->layers[l + 1].attn_norm;
         if ((rc = linear_q8w_add_ln(ctx, G, m, L.w_down, nullptr, X, nw, nullptr, lm->eps, Hn, rms)) != ZWG_OK)

@@ -94,9 +94,19 @@ int linear_q8w_qkv_kv(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *c
                       float *q_out, zwg_kv *kv, uint64_t layer, uint64_t seq0, const int32_t *pos_dev,
                       int32_t *n_kv_out);
 // A decode step's residual projection and the next norm: x += xin . W^T + bias, then ln_out =
-// the norm of x (norm 0: layer norm, 1: RMS norm; m <= 64, n <= 4096; linear.hip).
+// the norm of x (norm 0: layer norm, 1: RMS norm; m <= 64, n <= 4096; linear.hip).  xcvt_out
+// (33..64 rows): ln_out also split into f16 hi/lo halves for the next call (q8w_xcvt_halves(n)
+// halves), passed to it as xcvt_in.
 int linear_q8w_add_ln(zwg_ctx *ctx, const float *xin, uint64_t m, const zwg_q8w *w, const float *bias, float *x,
-                      const float *ln_w, const float *ln_b, float eps, float *ln_out, int norm = 0);
+                      const float *ln_w, const float *ln_b, float eps, float *ln_out, int norm = 0,
+                      _Float16 *xcvt_out = nullptr);
+uint64_t q8w_xcvt_halves(uint64_t k);
+// whether a token-step group call of these weights over m rows streams its x from a split pass
+// (and so takes linear_q8w_group_xcvt's xcvt_in)
+bool q8w_group_reads_xcvt(uint64_t m, uint32_t n_w, const zwg_q8w *const *w);
+// zwg_linear_q8w_group_dev over rows whose split was written by linear_q8w_add_ln (xcvt_in)
+int linear_q8w_group_xcvt(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t n_w, const zwg_q8w *const *w,
+                          const float *const *bias, float *const *out, const _Float16 *xcvt_in);
 // Token embeddings from packed int8 rows plus positional rows (pe may be null), and their norm:
 // x[i] = te.row(tok[i]) + pe[pos[i]], ln_out[i] = the norm of x[i] (n <= 4096; linear.hip).
 int q8w_embed_ln(zwg_ctx *ctx, const zwg_q8w *te, const int32_t *tok, const float *pe, const int32_t *pos,
