@@ -48,8 +48,11 @@ weights (HBM-bound; "qwen15_logits_q8_x64", "qwen15_decode_q8_linear_x64",
 "small_dec_q8_linear_x32") with the oracle's ops.linear over Q8 timed beside them, two decode
 steps' q/k/v projections with the new K/V rows written into the device caches by the projections
 themselves ("small_dec_qkv_cache_x32", "qwen15_qkv_cache_x64", with the unfused projections +
-append timed beside them), and one whole base.en encoder layer over the 16 windows
-("base_enc_layer_x16") with the oracle's layer beside it.
+append timed beside them), one whole base.en encoder layer over the 16 windows
+("base_enc_layer_x16") with the oracle's layer beside it, and the two callers' whole token steps
+on the device, the Whisper small.en decoder over 32 windows ("small_dec_step_x32") and Qwen2.5-1.5B
+over 64 sequences ("qwen15_step_x64"), each with the same step as separate calls and the oracle's
+forward for one token beside it.
 
 Each attention workload also carries "rate": windows/s for the encoders, tokens/s for the decoder
 step, the prefill and the LLM decode step, at wall time per step.  The prefill's CPU baseline runs
