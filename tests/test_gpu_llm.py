@@ -176,14 +176,15 @@ def test_step_bit_exact_with_composed_calls(torch, ctx, ne, H, Hk, nff):
 
 @pytest.mark.parametrize("m", [40, 64])
 def test_step_bit_exact_33_to_64_rows(torch, ctx, m):
-    """33..64 sequences take the 64-row kernels, and (n_ff 8192: the gate/up call streams a split
-    x) the o projection's sum kernel splits the ffn-normed rows for it, zero rows past m
-    included."""
+    """33..64 sequences take the 64-row kernels, and (n_ff 8192 and a 16400-token vocabulary: the
+    gate/up call and the logits stream a split x) the o projection's sum kernel splits the
+    ffn-normed rows for the gate/up call and the last down projection's the output-normed rows
+    for the logits, zero rows past m included."""
     import zwhisper_amd as z
     from zwhisper_amd import _lib
 
     rng = np.random.default_rng(m)
-    ne, H, Hk, nff, n_layer, n_vocab, n_ctx = 384, 6, 2, 8192, 2, 300, 16
+    ne, H, Hk, nff, n_layer, n_vocab, n_ctx = 384, 6, 2, 8192, 2, 16400, 16
     print(f"llm step n_embd={ne} heads {H}/{Hk} n_ff={nff} layers={n_layer} sequences {m}", flush=True)
     mdl = model(rng, ne, H, Hk, nff, n_layer, n_vocab)
     with contextlib.ExitStack() as st:

@@ -18,7 +18,8 @@
 //     G = silu(G) * U                                silu_mul_kernel
 //     X += down(G); H = next layer's attn_norm(X), or the output norm after the last layer
 //                                                    stream + the sum, residual add and norm
-//   logits = H . output^T
+//   logits = H . output^T                           one stream launch (33..64 sequences: x split by
+//                                                    the last down projection's sum kernel)
 //
 // The fused launches form the same values in the same order as the separate calls (the split
 // sums in split order, the residual add, zwg_ew::rms_norm_regs for every norm, the x split's f16
@@ -149,6 +150,8 @@ int zwg_llm_step_dev(zwg_ctx *ctx, const zwg_llm *lm, const int32_t *tokens, con
 
     const zwg_q8w *gu0[2] = {lm->layers[0].w_gate, lm->layers[0].w_up};
     _Float16 *gu_xc = q8w_group_reads_xcvt(m, 2, gu0) ? xc : nullptr;
+    // likewise the output-normed rows for the logits, from the last down projection's sum kernel
+    _Float16 *out_xc = q8w_group_reads_xcvt(m, 1, &lm->output) ? xc : nullptr;
     for (uint64_t l = 0; l < lm->n_layer; ++l) {
         const zwg_llm_layer &L = lm->layers[l];
         // src/llm.zig:179-190: q/k/v, rotary positions, the cache writes
@@ -167,12 +170,15 @@ int zwg_llm_step_dev(zwg_ctx *ctx, const zwg_llm *lm, const int32_t *tokens, con
         float *gu_out[2] = {G, U};
         if ((rc = linear_q8w_group_xcvt(ctx, Hn, m, 2, gu, nullptr, gu_out, gu_xc)) != ZWG_OK) return rc;
         if ((rc = zwg_silu_mul_dev(ctx, G, U, m * nff)) != ZWG_OK) return rc;
-        const float *nw = l + 1 == lm->n_layer ? lm->output_norm : lm->layers[l + 1].attn_norm;
-        if ((rc = linear_q8w_add_ln(ctx, G, m, L.w_down, nullptr, X, nw, nullptr, lm->eps, Hn, rms)) != ZWG_OK)
+        const bool last = l + 1 == lm->n_layer;
+        const float *nw = last ? lm->output_norm : lm->layers[l + 1].attn_norm;
+        if ((rc = linear_q8w_add_ln(ctx, G, m, L.w_down, nullptr, X, nw, nullptr, lm->eps, Hn, rms,
+                                    last ? out_xc : nullptr)) != ZWG_OK)
             return rc;
     }
     // the logits of every sequence's token (src/llm.zig:216)
-    return zwg_linear_q8w_dev(ctx, Hn, m, lm->output, nullptr, logits);
+    float *outs[1] = {logits};
+    return linear_q8w_group_xcvt(ctx, Hn, m, 1, &lm->output, nullptr, outs, out_xc);
 }
 
 } // extern "C"
