@@ -572,6 +572,24 @@ uint64_t zwg_llm_scratch(uint64_t m, uint64_t n_embd, uint64_t n_ff);
 int zwg_llm_step_dev(zwg_ctx *ctx, const zwg_llm *lm, const int32_t *tokens, const int32_t *pos, uint64_t m,
                      uint64_t seq0, float *logits, float *scratch);
 
+/* Floats of scratch a zwg_llm_forward_dev call over n tokens needs. */
+uint64_t zwg_llm_forward_scratch(uint64_t n, uint64_t n_embd, uint64_t n_ff);
+
+/*
+ * Qwen2's Model.forward (src/llm.zig:169-216) over n tokens of one sequence, the reference's
+ * prompt batch (Model.prompt, src/llm.zig:258-266, feeds a prompt in such batches): tokens[n]
+ * (device int32) at positions pos0 .. pos0 + n - 1 of sequence seq of lm->kv (pos0 + n <=
+ * n_ctx), written into the cache at those positions; logits[n_vocab] (device) are the last
+ * token's.  Each step is the library call of the reference's op (rmsNorm, the grouped q/k/v
+ * projections, zwg_kv_append with q, zwg_attention_dev causal over the pos0 + n cached keys, the
+ * int8 linears with the residual add in their store, siluMul), so a token's results match the
+ * one-token step's within f32 rounding (other kernels, other summation orders).  scratch:
+ * zwg_llm_forward_scratch(n, ...) floats, 16-byte aligned; the attention's key-split partials
+ * use the context's workspace.  Asynchronous.
+ */
+int zwg_llm_forward_dev(zwg_ctx *ctx, const zwg_llm *lm, const int32_t *tokens, uint64_t n, uint64_t seq,
+                        uint64_t pos0, float *logits, float *scratch);
+
 int zwg_version(void); /* ZWG_VERSION */
 
 #ifdef __cplusplus

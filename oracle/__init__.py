@@ -353,44 +353,49 @@ class Oracle:
         xl = self.layer_norm(x, 1, ns, dec["ln_w"], dec["ln_b"])
         return self.linear_q8(xl, 1, ns, te_q, te_s, None, n_vocab)
 
-    def llm_forward(self, lm: dict, cache: dict, token: int, pos: int) -> np.ndarray:
-        """Model.forward (src/llm.zig:169-216) for one sequence and one token at position pos
-        (n_past), as the reference runs it: x = embd.row(token); per layer rmsNorm, q/k/v with
-        their biases, NeoX rotary positions on q and k, k scattered into the transposed cache and v
-        into its rows at pos (oracle/kv.py llm_append), attentionEx over the pos + 1 cached keys
-        (causal, kt_stride = n_ctx), o added into x, rmsNorm, the SiLU-gated MLP added into x; then
-        the output norm and logits = norm(x) . output^T.  lm: {"embd": (q, scales), "output": (q,
-        scales), "output_norm", "n_head", "n_head_kv", "eps", "cos", "sin", "layers": [dict of the
-        layer's tensors, matrices as (q, scales)]}; cache: {"kt": [n_layer][n_head_kv * d *
-        n_ctx], "v": [n_layer][n_ctx][n_head_kv * d]} (updated at pos).  Returns the logits."""
+    def llm_forward(self, lm: dict, cache: dict, token, pos: int) -> np.ndarray:
+        """Model.forward (src/llm.zig:169-216) for one sequence and one token, or a list of n
+        tokens, at positions pos .. pos + n - 1 (n_past = pos), as the reference runs it: x =
+        embd.row(token) per row; per layer rmsNorm, q/k/v with their biases, NeoX rotary positions
+        on q and k, k scattered into the transposed cache and v into its rows (oracle/kv.py
+        llm_append), attentionEx over the pos + n cached keys (causal, kt_stride = n_ctx), o added
+        into x, rmsNorm, the SiLU-gated MLP added into x; then the output norm of the last row and
+        its logits = norm(x) . output^T.  lm: {"embd": (q, scales), "output": (q, scales),
+        "output_norm", "n_head", "n_head_kv", "eps", "cos", "sin", "layers": [dict of the layer's
+        tensors, matrices as (q, scales)]}; cache: {"kt": [n_layer][n_head_kv * d * n_ctx], "v":
+        [n_layer][n_ctx][n_head_kv * d]} (updated at pos ..).  Returns the last token's logits."""
         from types import SimpleNamespace
 
         from . import kv as kvo
 
+        toks = [int(token)] if np.ndim(token) == 0 else [int(t) for t in token]
+        n = len(toks)
         e_q, e_s = lm["embd"]
         n_vocab, ne = e_q.shape
         H, Hk, eps = lm["n_head"], lm["n_head_kv"], lm["eps"]
         d = ne // H
         kvw = Hk * d
         n_ctx = cache["v"].shape[1]
-        lin = lambda a, w, b, n, k: self.linear_q8(a, 1, k, *w, b, n)  # noqa: E731
-        x = (e_q[token].astype(np.float32).reshape(-1, Q8_BLOCK) * e_s[token].astype(np.float32)[:, None]).reshape(-1)
+        lin = lambda a, w, b, nn, k: self.linear_q8(a, n, k, *w, b, nn)  # noqa: E731
+        x = np.concatenate([(e_q[t].astype(np.float32).reshape(-1, Q8_BLOCK) *
+                             e_s[t].astype(np.float32)[:, None]).reshape(-1) for t in toks])
         for li, w in enumerate(lm["layers"]):
-            h = self.rms_norm(x, 1, ne, w["attn_norm"], eps)
+            h = self.rms_norm(x, n, ne, w["attn_norm"], eps)
             q = lin(h, w["wq"], w.get("bq"), ne, ne)
             k = lin(h, w["wk"], w.get("bk"), kvw, ne)
             v = lin(h, w["wv"], w.get("bv"), kvw, ne)
-            kvo.llm_append(q, k, v, 1, pos, H, Hk, d, ne, cache["kt"][li], cache["v"][li], n_ctx, lm["cos"], lm["sin"])
-            sh = SimpleNamespace(n_q=1, n_kv=pos + 1, n_head=H, n_head_kv=Hk, d=d, q_stride=ne, kv_stride=kvw,
+            kvo.llm_append(q, k, v, n, pos, H, Hk, d, ne, cache["kt"][li], cache["v"][li], n_ctx, lm["cos"], lm["sin"])
+            sh = SimpleNamespace(n_q=n, n_kv=pos + n, n_head=H, n_head_kv=Hk, d=d, q_stride=ne, kv_stride=kvw,
                                  out_stride=ne, causal=True, kt_stride=n_ctx)
-            att = self.attention_ex(q, cache["kt"][li], cache["v"][li][:pos + 1], sh)
+            att = self.attention_ex(q, cache["kt"][li], cache["v"][li][:pos + n], sh)
             x = x + lin(att, w["wo"], None, ne, ne)
-            h = self.rms_norm(x, 1, ne, w["ffn_norm"], eps)
-            g = lin(h, w["w_gate"], None, w["w_gate"][0].shape[0], ne)
-            u = lin(h, w["w_up"], None, w["w_up"][0].shape[0], ne)
+            h = self.rms_norm(x, n, ne, w["ffn_norm"], eps)
+            nff = w["w_gate"][0].shape[0]
+            g = lin(h, w["w_gate"], None, nff, ne)
+            u = lin(h, w["w_up"], None, nff, ne)
             g = self.silu_mul(g, u)
-            x = x + lin(g, w["w_down"], None, ne, g.size)
-        h = self.rms_norm(x, 1, ne, lm["output_norm"], eps)
+            x = x + lin(g, w["w_down"], None, ne, nff)
+        h = self.rms_norm(x[(n - 1) * ne:], 1, ne, lm["output_norm"], eps)
         return self.linear_q8(h, 1, ne, *lm["output"], None, n_vocab)
 
     def attention(self, q, k, v, n_q, n_kv, n_state, n_head, causal, out=None) -> np.ndarray:

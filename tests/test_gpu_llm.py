@@ -13,6 +13,9 @@ ops.siluMul (zwg_rms_norm_dev, zwg_silu_mul_dev).
 3. Against the oracle (Oracle.llm_forward, the reference's forward one sequence at a time):
    logits within 2e-5 of the largest |logit| (measured 4e-7).
 4. A step captured in a HIP graph and replayed equals the eager step; the shapes the call refuses.
+5. The n-token forward (zwg_llm_forward_dev, the reference's prompt batch) against the oracle's
+   forward over the same batches (40, 70 and 5 tokens), and against the same tokens one by one
+   through the step; its refusals.
 """
 from __future__ import annotations
 
@@ -250,6 +253,105 @@ def test_step_against_oracle(torch, ctx):
                 worst = max(worst, err)
                 assert err <= 2e-5, (step, w, err)
         print(f"worst logit error {worst:.2e} of the largest |logit|", flush=True)
+
+
+def _ora_model(z, mdl, H, Hk, n_ctx, d, base=1e6):
+    from oracle import kv as kvo
+
+    cos, sin = kvo.rope_tables(n_ctx, d, base)
+    out = mdl["output"] if mdl["output"] is not None else mdl["embd"]
+    return {"embd": (mdl["embd"].q, mdl["embd"].scales), "output": (out.q, out.scales),
+            "output_norm": mdl["output_norm"], "n_head": H, "n_head_kv": Hk, "eps": 1e-6, "cos": cos, "sin": sin,
+            "layers": [{k: ((v.q, v.scales) if isinstance(v, z.Q8) else v) for k, v in lw.items()}
+                       for lw in mdl["layers"]]}
+
+
+@pytest.mark.parametrize("ne,H,Hk,nff", [(384, 6, 2, 1024), (512, 4, 2, 1376)], ids=["d64", "d128"])
+def test_forward_against_oracle(torch, ctx, ne, H, Hk, nff):
+    """zwg_llm_forward_dev over prompt batches of 40, 70 (the tiled GEMMs past 64 rows) and 5
+    tokens of sequence 1 against Oracle.llm_forward over the same batches: the last token's
+    logits within 2e-5 of the largest |logit|, the cache rows within 2e-5 relative."""
+    import oracle
+    import zwhisper_amd as z
+
+    rng = np.random.default_rng(ne + 1)
+    n_layer, n_vocab, n_ctx, d = 2, 500, 128, ne // H
+    print(f"llm forward vs oracle n_embd={ne} heads {H}/{Hk} n_ff={nff} layers={n_layer}", flush=True)
+    mdl = model(rng, ne, H, Hk, nff, n_layer, n_vocab, tied=(ne == 512))
+    ora = _ora_model(z, mdl, H, Hk, n_ctx, d)
+    cache = {"kt": np.zeros((n_layer, Hk * d * n_ctx), np.float32), "v": np.zeros((n_layer, n_ctx, Hk * d), np.float32)}
+    with contextlib.ExitStack() as st:
+        o = st.enter_context(oracle.Oracle(4))
+        lm = st.enter_context(make_llm(z, ctx, mdl, H, Hk, nff, n_ctx, 2))
+        logits = torch.empty(n_vocab, device="cuda")
+        pos = 0
+        for n in (40, 70, 5):
+            toks = rng.integers(0, n_vocab, n).astype(np.int32)
+            lm.forward(torch.from_numpy(toks).cuda(), pos, logits, 1)
+            ref = o.llm_forward(ora, cache, toks, pos)
+            got = logits.cpu().numpy()
+            scale = max(1.0, np.max(np.abs(ref)))
+            err = np.max(np.abs(got - ref)) / scale
+            print(f"  batch of {n} at {pos}: logit error {err:.2e} of the largest |logit|", flush=True)
+            assert err <= 2e-5, (n, pos, err)
+            pos += n
+            for li in range(n_layer):
+                k, v = lm.kv.read(li, 1)
+                kr, vr = cache["kt"][li], cache["v"][li].reshape(-1)
+                assert np.max(np.abs(k - kr)) <= 2e-5 * max(1.0, np.max(np.abs(kr))), li
+                assert np.max(np.abs(v - vr)) <= 2e-5 * max(1.0, np.max(np.abs(vr))), li
+                k0, _ = lm.kv.read(li, 0)
+                assert not np.any(k0), "another sequence's cache was written"
+
+
+def test_forward_matches_steps(torch, ctx):
+    """A prompt batch through zwg_llm_forward_dev and the same tokens one by one through
+    zwg_llm_step_dev (other kernels): the last token's logits and the caches within f32
+    rounding."""
+    import zwhisper_amd as z
+
+    rng = np.random.default_rng(77)
+    ne, H, Hk, nff, n_layer, n_vocab, n_ctx = 384, 6, 2, 1024, 2, 400, 64
+    mdl = model(rng, ne, H, Hk, nff, n_layer, n_vocab)
+    toks = rng.integers(0, n_vocab, 33).astype(np.int32)
+    with contextlib.ExitStack() as st:
+        a = st.enter_context(make_llm(z, ctx, mdl, H, Hk, nff, n_ctx, 1))
+        b = st.enter_context(make_llm(z, ctx, mdl, H, Hk, nff, n_ctx, 1))
+        la = torch.empty(n_vocab, device="cuda")
+        lb = torch.empty(1, n_vocab, device="cuda")
+        a.forward(torch.from_numpy(toks).cuda(), 0, la, 0)
+        for p, t in enumerate(toks):
+            b.step(torch.tensor([t], dtype=torch.int32, device="cuda"), torch.tensor([p], dtype=torch.int32,
+                                                                                      device="cuda"), lb, 0)
+        torch.cuda.synchronize()
+        ga, gb = la.cpu().numpy(), lb[0].cpu().numpy()
+        assert np.max(np.abs(ga - gb)) <= 1e-5 * max(1.0, np.max(np.abs(gb)))
+        for li in range(n_layer):
+            ka, va = a.kv.read(li, 0)
+            kb, vb = b.kv.read(li, 0)
+            assert np.max(np.abs(ka - kb)) <= 1e-5 * max(1.0, np.max(np.abs(kb)))
+            assert np.max(np.abs(va - vb)) <= 1e-5 * max(1.0, np.max(np.abs(vb)))
+
+
+def test_forward_refusals(torch, ctx):
+    import ctypes
+
+    import zwhisper_amd as z
+    from zwhisper_amd import _lib
+
+    rng = np.random.default_rng(19)
+    mdl = model(rng, 384, 6, 2, 256, 1, 64)
+    L = _lib.lib()
+    with make_llm(z, ctx, mdl, 6, 2, 256, 16, 2) as lm:
+        logits = torch.empty(64, device="cuda")
+        with pytest.raises(z.ZwgError, match="past the cache"):
+            lm.forward(torch.zeros(10, dtype=torch.int32, device="cuda"), 7, logits, 0)
+        with pytest.raises(z.ZwgError, match="sequences out of range"):
+            lm.forward(torch.zeros(4, dtype=torch.int32, device="cuda"), 0, logits, 2)
+        scratch = torch.empty(int(L.zwg_llm_forward_scratch(4, 384, 256)), device="cuda")
+        rc = L.zwg_llm_forward_dev(ctx.handle, ctypes.byref(lm.c), None, 4, 0, 0, logits.data_ptr(),
+                                   scratch.data_ptr())
+        assert rc != 0 and "null tokens" in _lib.last_error(ctx.handle)
 
 
 def test_step_graph_replay(torch, ctx):

@@ -9,7 +9,8 @@ as a sum, eps outside the root, the tanh GELU in place of SiLU) that the closed-
 reject; and several decode steps of two sequences against an f64 model of the reference's
 forward, with planted mistakes (no rotary positions, rotary over interleaved pairs, the GQA map
 taken modulo, q's bias dropped, a self-attention one key short, no output norm), each of which
-the bar must reject.
+the bar must reject; and the n-token forward (a prompt batch) against the same model over all
+rows at once, with attention past a row's own position (no mask within the batch) rejected.
 """
 from __future__ import annotations
 
@@ -195,3 +196,67 @@ def test_llm_forward_against_f64(ora):
                     assert np.max(np.abs(got - bad)) / scale > 50 * max(err, 1e-7), bug
     print(f"worst relative error {worst:.2e}")
     assert worst < 2e-5
+
+
+def forward64_batch(lm, cache, toks, pos, bug=None):
+    """The reference's forward over n tokens at pos .. pos + n - 1 in f64: each layer over all rows,
+    query i attending to keys 0 .. pos + i (bug "noncausal": to all pos + n keys)."""
+    d = NE // H
+    n = len(toks)
+    x = deq(lm["embd"])[list(toks)]
+    for li, w in enumerate(lm["layers"]):
+        h = rms64(x, w["attn_norm"], EPS)
+        q = h @ deq(w["wq"]).T + w["bq"]
+        k = h @ deq(w["wk"]).T + w["bk"]
+        v = h @ deq(w["wv"]).T + w["bv"]
+        for i in range(n):
+            q[i] = rope64(q[i], H, d, pos + i)
+            k[i] = rope64(k[i], HK, d, pos + i)
+        cache["k"][li][pos:pos + n] = k
+        cache["v"][li][pos:pos + n] = v
+        att = np.zeros((n, NE))
+        for i in range(n):
+            end = pos + n if bug == "noncausal" else pos + i + 1
+            for hh in range(H):
+                hk = hh // (H // HK)
+                kk = cache["k"][li][:end, hk * d:(hk + 1) * d]
+                vv = cache["v"][li][:end, hk * d:(hk + 1) * d]
+                sc = kk @ q[i, hh * d:(hh + 1) * d] / math.sqrt(d)
+                p = np.exp(sc - sc.max())
+                att[i, hh * d:(hh + 1) * d] = (p / p.sum()) @ vv
+        x = x + att @ deq(w["wo"]).T
+        h = rms64(x, w["ffn_norm"], EPS)
+        g = h @ deq(w["w_gate"]).T
+        u = h @ deq(w["w_up"]).T
+        x = x + (g / (1 + np.exp(-g)) * u) @ deq(w["w_down"]).T
+    return deq(lm["output"]) @ rms64(x[-1], lm["output_norm"], EPS)
+
+
+def test_llm_forward_batch_against_f64(ora):
+    """The n-token forward (a prompt batch): the last token's logits and every cache row against
+    the f64 model over all rows at once, after a first batch; a batch attending past each row's
+    own position (no causal mask within the batch) fails the bar."""
+    rng = np.random.default_rng(5)
+    lm = model(rng)
+    d = NE // H
+    cache = {"kt": np.zeros((NL, HK * d * NCTX), np.float32), "v": np.zeros((NL, NCTX, HK * d), np.float32)}
+    c64 = {"k": np.zeros((NL, NCTX, HK * d)), "v": np.zeros((NL, NCTX, HK * d))}
+    worst = 0.0
+    for pos, n in ((0, 5), (5, 7), (12, 1)):
+        toks = rng.integers(0, NV, n)
+        before = {"k": c64["k"].copy(), "v": c64["v"].copy()}
+        got = ora.llm_forward(lm, cache, toks, pos)
+        ref = forward64_batch(lm, c64, toks, pos)
+        scale = max(1.0, np.max(np.abs(ref)))
+        err = np.max(np.abs(got - ref)) / scale
+        worst = max(worst, err)
+        assert err <= 2e-5, (pos, n, err)
+        for li in range(NL):
+            kt = cache["kt"][li].reshape(HK * d, NCTX)[:, pos:pos + n].T
+            assert np.max(np.abs(kt - c64["k"][li][pos:pos + n])) <= 2e-5 * scale
+            assert np.max(np.abs(cache["v"][li][pos:pos + n] - c64["v"][li][pos:pos + n])) <= 2e-5 * scale
+        if n > 1:
+            bad = forward64_batch(lm, {"k": before["k"].copy(), "v": before["v"].copy()}, toks, pos, bug="noncausal")
+            assert np.max(np.abs(got - bad)) / scale > 50 * max(err, 1e-7)
+    print(f"worst relative error {worst:.2e}")
+

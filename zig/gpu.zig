@@ -261,6 +261,9 @@ pub const Llm = extern struct {
 pub extern "zwgpu" fn zwg_llm_scratch(m: u64, n_embd: u64, n_ff: u64) u64;
 pub extern "zwgpu" fn zwg_llm_step_dev(ctx: *Ctx, lm: *const Llm, tokens: [*]const i32, pos: [*]const i32, m: u64,
     seq0: u64, logits: [*]f32, scratch: [*]f32) c_int;
+pub extern "zwgpu" fn zwg_llm_forward_scratch(n: u64, n_embd: u64, n_ff: u64) u64;
+pub extern "zwgpu" fn zwg_llm_forward_dev(ctx: *Ctx, lm: *const Llm, tokens: [*]const i32, n: u64, seq: u64,
+    pos0: u64, logits: [*]f32, scratch: [*]f32) c_int;
 
 // ---- the calling thread's context
 

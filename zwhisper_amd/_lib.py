@@ -260,6 +260,10 @@ def lib() -> ctypes.CDLL:
     L.zwg_llm_scratch.argtypes = [_u64, _u64, _u64]
     L.zwg_llm_step_dev.restype = c_int
     L.zwg_llm_step_dev.argtypes = [vp, ctypes.POINTER(LlmC), vp, vp, _u64, _u64, _fp, _fp]
+    L.zwg_llm_forward_scratch.restype = _u64
+    L.zwg_llm_forward_scratch.argtypes = [_u64, _u64, _u64]
+    L.zwg_llm_forward_dev.restype = c_int
+    L.zwg_llm_forward_dev.argtypes = [vp, ctypes.POINTER(LlmC), vp, _u64, _u64, _u64, _fp, _fp]
     L.zwg_decoder_set_audio_dev.restype = c_int
     L.zwg_decoder_set_audio_dev.argtypes = [vp, ctypes.POINTER(DecoderC), _fp, _u64, _u64]
     L.zwg_decoder_scratch.restype = _u64

@@ -746,7 +746,7 @@ int zwg_host::q8w_embed_ln(zwg_ctx *ctx, const zwg_q8w *te, const int32_t *tok, 
     if (te->k % 4 || te->k > (uint64_t)kMaxRowN || m > 0x7fffffffull || pe_rows > 0x7fffffffull)
         return fail(ctx, "embedding rows of at most 4096 floats, a multiple of 4");
     const bool rms = norm == zwg_ew::kNormRms;
-    if (!tok || !pos || !x || !ln_w || (!rms && !ln_b) || !ln_out || (pe_rows && !pe) || !al16(x) || !al16(ln_w) ||
+    if (!tok || !x || !ln_w || (!rms && !ln_b) || !ln_out || (pe_rows && (!pe || !pos)) || !al16(x) || !al16(ln_w) ||
         (ln_b && !al16(ln_b)) || !al16(ln_out) || (pe && !al16(pe)))
         return fail(ctx, "null or unaligned buffer (all 16-byte aligned)");
     zwg_lin::Q8Packed tp{te->q, te->scales, te->n_slabs, te->n_chunks};

@@ -896,7 +896,8 @@ __global__ __launch_bounds__(64 * R) void linear_split_sum_add_ln_wide_kernel(co
 // in f32) then ops.add (src/decoder.zig:171-174) -- and ln_out[i] = the norm of x[i] (the first
 // block's attn_ln, src/decoder.zig:178; for Qwen2, no position rows and the first block's RMS
 // norm, src/llm.zig:175-178).  A token outside
-// [0, n_vocab) gives a zero embedding row; a position outside [0, pe_rows) adds no position row.
+// [0, n_vocab) gives a zero embedding row; a position outside [0, pe_rows) adds no position row
+// (pos may be null when there are none).
 // One wave per row of n <= 256 R floats; a lane's float4 is 4 bytes of one 16-byte lane piece of
 // its block's tile (Q8Packed).
 template <int R, int NORM>
@@ -909,7 +910,7 @@ __global__ __launch_bounds__(64) void q8p_embed_ln_kernel(Q8Packed te, int32_t n
     const int row = (int)blockIdx.x; // one wave per workgroup, one row per wave
     if (row >= m) return;
     const int n4 = n >> 2;
-    const int t = tok[row], ps = pos[row];
+    const int t = tok[row], ps = pos ? pos[row] : -1;
     const bool t_ok = t >= 0 && t < n_vocab, p_ok = ps >= 0 && ps < pe_rows;
     const int slab = t_ok ? t >> 5 : 0, r32 = t & 31;
     const int nbp = te.n_chunks * kQ8ChunkBlocks;

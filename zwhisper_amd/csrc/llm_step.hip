@@ -181,4 +181,75 @@ int zwg_llm_step_dev(zwg_ctx *ctx, const zwg_llm *lm, const int32_t *tokens, con
     return linear_q8w_group_xcvt(ctx, Hn, m, 1, &lm->output, nullptr, outs, out_xc);
 }
 
+uint64_t zwg_llm_forward_scratch(uint64_t n, uint64_t n_embd, uint64_t n_ff) {
+    return n * (6 * n_embd + 2 * n_ff);
+}
+
+// Model.forward (src/llm.zig:169-216) over n tokens of one sequence at positions pos0 .. pos0 +
+// n - 1: the reference's prompt batch (Model.prompt feeds a prompt in such batches,
+// src/llm.zig:258-266), each step the library call of the reference's op: rmsNorm, the q/k/v
+// projections (one grouped call), the rotary cache append (q rotated in place), attentionEx over
+// the pos0 + n cached keys (causal, transposed keys), o with the residual add in its store, the
+// gate/up projections, siluMul, down with the add; then the output norm and the logits of the
+// last row only (:214-216).
+int zwg_llm_forward_dev(zwg_ctx *ctx, const zwg_llm *lm, const int32_t *tokens, uint64_t n, uint64_t seq,
+                        uint64_t pos0, float *logits, float *scratch) {
+    if (!ctx) return fail(nullptr, "null context");
+    if (!lm) return fail(ctx, "null model");
+    if (n == 0) return ZWG_OK;
+    const std::string msg = check_llm(ctx, *lm, seq + 1);
+    if (!msg.empty()) return fail(ctx, msg);
+    if (pos0 + n > lm->kv->desc.n_ctx || n > 0x7fffffffull) return fail(ctx, "pos0 + n is past the cache (n_ctx)");
+    if (!tokens) return fail(ctx, "null tokens");
+    if (!logits || !scratch || !aligned16(logits) || !aligned16(scratch))
+        return fail(ctx, "logits and scratch must be non-null and 16-byte aligned");
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
+
+    const uint64_t ne = lm->n_embd, nff = lm->n_ff, H = lm->n_head, Hk = lm->n_head_kv, d = ne / H;
+    const int rms = zwg_ew::kNormRms;
+    float *X = scratch, *Hn = X + n * ne, *Q = Hn + n * ne, *T = Q + n * ne, *Kb = T + n * ne, *Vb = Kb + n * ne,
+          *G = Vb + n * ne, *U = G + n * nff;
+    zwg_kv *kv = lm->kv;
+    // :175 and the first block's attn_norm (:178)
+    int rc = q8w_embed_ln(ctx, lm->embd, tokens, nullptr, nullptr, 0, n, X, lm->layers[0].attn_norm, nullptr,
+                          lm->eps, Hn, rms);
+    if (rc != ZWG_OK) return rc;
+    zwg_attn_shape sh{};
+    sh.n_q = n;
+    sh.n_kv = pos0 + n;
+    sh.n_head = H;
+    sh.n_head_kv = Hk;
+    sh.d = d;
+    sh.q_stride = ne;
+    sh.kv_stride = Hk * d;
+    sh.out_stride = ne;
+    sh.kt_stride = kv->desc.n_ctx;
+    sh.causal = 1;
+    for (uint64_t l = 0; l < lm->n_layer; ++l) {
+        const zwg_llm_layer &L = lm->layers[l];
+        if (l > 0 && (rc = rms_norm(ctx, X, n, ne, L.attn_norm, lm->eps, Hn)) != ZWG_OK) return rc;
+        // :179-190
+        const zwg_q8w *qkv[3] = {L.wq, L.wk, L.wv};
+        const float *qkv_b[3] = {L.bq, L.bk, L.bv};
+        float *qkv_out[3] = {Q, Kb, Vb};
+        if ((rc = zwg_linear_q8w_group_dev(ctx, Hn, n, 3, qkv, qkv_b, qkv_out)) != ZWG_OK) return rc;
+        if ((rc = zwg_kv_append(kv, l, seq, pos0, n, Kb, Vb, Q, H, ne, 0)) != ZWG_OK) return rc;
+        // :191-202
+        const uint64_t at = (l * kv->desc.n_seq + seq) * kv->per_seq;
+        if ((rc = zwg_attention_dev(ctx, Q, kv->k + at, kv->v + at, &sh, T)) != ZWG_OK) return rc;
+        // :203-211
+        if ((rc = zwg_linear_q8w_epi_dev(ctx, T, n, L.wo, nullptr, X, ZWG_EPI_ADD)) != ZWG_OK) return rc;
+        if ((rc = rms_norm(ctx, X, n, ne, L.ffn_norm, lm->eps, Hn)) != ZWG_OK) return rc;
+        const zwg_q8w *gu[2] = {L.w_gate, L.w_up};
+        float *gu_out[2] = {G, U};
+        if ((rc = zwg_linear_q8w_group_dev(ctx, Hn, n, 2, gu, nullptr, gu_out)) != ZWG_OK) return rc;
+        if ((rc = zwg_silu_mul_dev(ctx, G, U, n * nff)) != ZWG_OK) return rc;
+        if ((rc = zwg_linear_q8w_epi_dev(ctx, G, n, L.w_down, nullptr, X, ZWG_EPI_ADD)) != ZWG_OK) return rc;
+    }
+    // :214-216: the last row's output norm and logits
+    if ((rc = rms_norm(ctx, X + (n - 1) * ne, 1, ne, lm->output_norm, lm->eps, Hn)) != ZWG_OK) return rc;
+    return zwg_linear_q8w_dev(ctx, Hn, 1, lm->output, nullptr, logits);
+}
+
 } // extern "C"

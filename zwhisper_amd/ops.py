@@ -656,6 +656,25 @@ class LLM:
                                                  pos.data_ptr(), m, seq0, Context._dev_ptr(logits, "logits"),
                                                  Context._dev_ptr(self.scratch, "scratch")))
 
+    def forward(self, tokens, pos0: int, logits, seq: int = 0) -> None:
+        """Model.forward over the n tokens of `tokens` (a CUDA int32 tensor) of sequence seq at
+        positions pos0 .. pos0 + n - 1 (the reference's prompt batch); logits [n_vocab] (CUDA
+        float32) get the last token's (zwg_llm_forward_dev)."""
+        import torch
+
+        n = tokens.numel()
+        if not tokens.is_cuda or tokens.dtype != torch.int32:
+            raise ZwgError("tokens must be a CUDA int32 tensor")
+        if logits.numel() < self.n_vocab:
+            raise ZwgError("logits is shorter than n_vocab")
+        need = int(self._L.zwg_llm_forward_scratch(n, self.n_embd, self.n_ff))
+        if getattr(self, "_fwd_scratch", None) is None or self._fwd_scratch.numel() < need:
+            self._fwd_scratch = torch.empty(max(need, 4), device=f"cuda:{self.ctx.device}")
+        self.ctx._bind_torch_stream()
+        self.ctx._check(self._L.zwg_llm_forward_dev(self.ctx.handle, ctypes_byref(self.c), tokens.data_ptr(), n, seq,
+                                                    pos0, Context._dev_ptr(logits, "logits"),
+                                                    Context._dev_ptr(self._fwd_scratch, "scratch")))
+
     def close(self) -> None:
         for o in reversed(self._owned):
             o.close()
