@@ -1241,6 +1241,131 @@ class LlmStepWorkload:
         self.lm = self.kv = self._host_src = None
 
 
+class LlmPromptWorkload:
+    """Qwen2's prompt on the device as llm.prompt feeds it (src/llm.zig:258-266): one step is a
+    2048-token prompt of one sequence in 8 zwg_llm_forward_dev calls of 256 tokens (Model.forward,
+    src/llm.zig:169-216, over a batch: RMS norms, the q/k/v projections, the rotary cache append,
+    causal attention over the cache so far, o, the SwiGLU MLP, and the last token's logits), replayed
+    as one HIP graph.  Qwen2.5-0.5B shapes (24 layers, 896 wide, 14q/2kv heads of 64, n_ff 4864,
+    151936-token tied vocabulary), random int8 block weights, resident.
+
+    Algorithmic work per step: 2 flops per weight per token for every projection, 4 d H per
+    visible (query, key) pair for the attention (src/bench.zig:76), 2 flops per weight for the 8
+    calls' logits.  Its roofline is composite, as the encoder layer's: the projections at half
+    the 16-bit MFMA peak (two f16 products per f32 x int8 product), the attention at a third (x3)."""
+
+    dtype = ("f32 (projections: f32 x int8 block weights on f16 MFMA, x split into two f16 terms; attention: x3 "
+             "16-bit MFMA)")
+
+    def __init__(self, name: str, description: str, torch, ctx, n_tok: int = 2048, calls: int = 8, n_layer: int = 24,
+                 ne: int = 896, n_head: int = 14, n_head_kv: int = 2, n_ff: int = 4864, n_vocab: int = 151936,
+                 n_ctx: int = 2048):
+        import zwhisper_amd as z
+
+        self.name, self.description = name, description
+        self.torch, self.ctx = torch, ctx
+        self.n_tok, self.calls, self.rows = n_tok, calls, n_tok // calls
+        self.ne, self.H, self.Hk, self.n_ff, self.n_layer, self.n_vocab, self.n_ctx = (ne, n_head, n_head_kv, n_ff,
+                                                                                         n_layer, n_vocab, n_ctx)
+        d = ne // n_head
+        kvw = n_head_kv * d
+        g = torch.Generator(device="cuda").manual_seed(0x0C0C)
+
+        def q8(n, k):
+            q = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda", generator=g)
+            sc = torch.rand(n, k // 32, device="cuda", generator=g) * (2.0 / 127 / np.sqrt(k))
+            return z.Q8(q, sc, n, k)
+
+        def vec(n, base=0.0, scale=0.1):
+            return base + scale * torch.randn(n, device="cuda", generator=g)
+
+        layers = []
+        for _ in range(n_layer):
+            layers.append({"wq": q8(ne, ne), "wk": q8(kvw, ne), "wv": q8(kvw, ne), "wo": q8(ne, ne),
+                           "w_gate": q8(n_ff, ne), "w_up": q8(n_ff, ne), "w_down": q8(ne, n_ff),
+                           "bq": vec(ne, scale=0.3), "bk": vec(kvw, scale=0.3), "bv": vec(kvw),
+                           "attn_norm": vec(ne, 1.0), "ffn_norm": vec(ne, 1.0)})
+        embd = q8(n_vocab, ne)
+        output_norm = vec(ne, 1.0)
+        self.lm = z.LLM(ctx, embd, None, output_norm, layers, n_head, n_head_kv, n_ff, n_ctx, 1)
+        self._host_src = (embd, output_norm, layers)
+        self.tok = torch.randint(0, n_vocab, (n_tok,), dtype=torch.int32, device="cuda", generator=g)
+        self.logits = torch.empty(n_vocab, device="cuda")
+        per_tok = 2.0 * sum(w.n * w.k for w in layers[0].values() if isinstance(w, z.Q8)) * n_layer
+        self.linear_flops = per_tok * n_tok + calls * 2.0 * n_vocab * ne
+        pairs = n_tok * (n_tok + 1) / 2
+        self.attn_flops = 4.0 * d * n_head * pairs * n_layer
+        self.work = self.linear_flops + self.attn_flops
+        self.ideal_s = self.linear_flops / (PEAK_MFMA_F16 / 2) + self.attn_flops / (PEAK_MFMA_F16 / 3)
+        self._run()
+        torch.cuda.synchronize()
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self._run()
+        torch.cuda.synchronize()
+
+    def _run(self):
+        for c in range(self.calls):
+            self.lm.forward(self.tok[c * self.rows:(c + 1) * self.rows], c * self.rows, self.logits, 0)
+
+    def step(self, i: int):
+        self.graph.replay()
+
+    def extra_record(self, steps: int) -> dict:
+        """The step's calls eagerly (no graph), the graph's logits against them, tokens/s."""
+        torch = self.torch
+        self.graph.replay()
+        torch.cuda.synchronize()
+        ref = self.logits.clone()
+        t0 = time.perf_counter()
+        for _ in range(3):
+            self._run()
+        torch.cuda.synchronize()
+        eager_ms = (time.perf_counter() - t0) / 3 * 1e3
+        return {"eager": {"ms_per_step": eager_ms, "logits_equal_bitwise": bool(torch.equal(ref, self.logits)),
+                          "note": "the 8 calls launched from the host per step, no graph"},
+                "tokens_per_step": self.n_tok, "calls_per_step": self.calls,
+                "linear_flops": self.linear_flops, "attention_flops": self.attn_flops}
+
+    def cpu_baseline(self, threads: int) -> dict:
+        """The oracle's Model.forward (Oracle.llm_forward over a batch: ops.linear over Q8,
+        rmsNorm, the rotary cache writes, attentionEx causal over the transposed cache, siluMul)
+        for the prompt's first call of 256 tokens."""
+        import oracle
+        from oracle import kv as kvo
+
+        embd, output_norm, layers = self._host_src
+        d = self.ne // self.H
+        hl = [{nm: ((t.q.cpu().numpy(), t.scales.cpu().numpy()) if hasattr(t, "scales") else t.cpu().numpy())
+               for nm, t in lw.items()} for lw in layers]
+        e = (embd.q.cpu().numpy(), embd.scales.cpu().numpy())
+        cos, sin = kvo.rope_tables(self.n_ctx, d, 1e6)
+        lm = {"embd": e, "output": e, "output_norm": output_norm.cpu().numpy(), "n_head": self.H,
+              "n_head_kv": self.Hk, "eps": 1e-6, "cos": cos, "sin": sin, "layers": hl}
+        cache = {"kt": np.zeros((self.n_layer, self.Hk * d * self.n_ctx), np.float32),
+                 "v": np.zeros((self.n_layer, self.n_ctx, self.Hk * d), np.float32)}
+        toks = self.tok[:self.rows].cpu().numpy()
+        o = oracle.Oracle(threads)
+
+        def run():
+            o.llm_forward(lm, cache, toks, 0)
+
+        best, mean, runs = time_cpu(run, 2)
+        o.close()
+        per_tok = self.linear_flops / self.n_tok
+        work1 = per_tok * self.rows + 4.0 * d * self.H * self.rows * (self.rows + 1) / 2 * self.n_layer
+        return {"value": self.rows / best, "unit": "tokens/s", "cores": o.threads, "kind": "port",
+                "tflops": work1 / best / 1e12,
+                "sample": f"the prompt's first call: {self.rows} tokens through all {self.n_layer} layers and the last "
+                          "token's logits, oracle Model.forward over oracle/attn_oracle.c; " + cpu_timing(best, mean, runs),
+                "seconds": best}
+
+    def free(self):
+        self.graph = None
+        self.lm.close()
+        self.lm = self._host_src = None
+
+
 def q8_workloads(torch, ctx):
     """(name, constructor) of the int8 decode-step measurements."""
     qwen_layer = [(1536, 1536, True), (1536, 256, True), (1536, 256, True), (1536, 1536, False),
@@ -1564,7 +1689,8 @@ def _say(name: str, res: dict, peak_name: str) -> None:
 EXTRAS = ("qwen05_prefill_8x256", "small_dec_kv_append_x32", "qwen15_kv_append_x64", "qwen05_prefill_kv_append",
           "base_enc_linear_x16",
           "base_enc_layer_x16", "qwen15_logits_q8_x64", "qwen15_decode_q8_linear_x64", "small_dec_q8_linear_x32",
-          "small_dec_qkv_cache_x32", "qwen15_qkv_cache_x64", "small_dec_step_x32", "qwen15_step_x64")
+          "small_dec_qkv_cache_x32", "qwen15_qkv_cache_x64", "small_dec_step_x32", "qwen15_step_x64",
+          "qwen05_prompt_2048")
 
 
 def run_extra(name: str, torch, ctx, args, threads: int) -> dict:
@@ -1642,6 +1768,33 @@ def run_extra(name: str, torch, ctx, args, threads: int) -> dict:
             res["cpu_baseline"] = wl.cpu_baseline(threads)
         wl.free()
         _say(name, res, "the layer's mfma roofline")
+        return res
+    if name == "qwen05_prompt_2048":
+        wl = LlmPromptWorkload(name, "Qwen2.5-0.5B 2048-token prompt as llm.prompt feeds it (src/llm.zig:258-266): 8 "
+                               "zwg_llm_forward_dev calls of 256 tokens, each through 24 layers (RMS norms, int8 "
+                               "q/k/v with rotary positions into the transposed cache, causal GQA attention 14q/2kv "
+                               "x 64 over the cache so far, o, SwiGLU MLP) and the last token's logits over the "
+                               "151936-token vocabulary", torch, ctx)
+        r = time_workload(wl, args.steps, args.warmup)
+        achieved = wl.work / (r["kernel_ms_mean"] * 1e-3)
+        peak = wl.work / wl.ideal_s
+        res = {"workload": wl.name, "description": wl.description,
+               "value": wl.work / (r["ms_per_step"] * 1e-3) / 1e12, "unit": "TFLOP/s",
+               "ms_per_step": r["ms_per_step"], "kernel_ms_mean": r["kernel_ms_mean"],
+               "kernel_ms_median": r["kernel_ms_median"], "kernel_ms_min": r["kernel_ms_min"],
+               "algorithmic_work_per_step": wl.work, "dtype": wl.dtype,
+               "roofline": {"bound": "mfma", "achieved": achieved / 1e12, "peak": peak / 1e12, "unit": "TFLOP/s",
+                            "frac": achieved / peak, "traffic": traffic_for(wl.name),
+                            "note": "peak = the step's flops over the time they take at their own peaks: projections "
+                                    "at half the f16 MFMA peak, attention at a third of the 16-bit MFMA peak"},
+               "cold": cold(r, wl.work, "TFLOP/s", peak)}
+        res.update(wl.extra_record(args.steps))
+        res["tokens_per_s"] = wl.n_tok / (r["ms_per_step"] * 1e-3)
+        if not args.no_cpu:
+            res["cpu_baseline"] = wl.cpu_baseline(threads)
+        wl.free()
+        torch.cuda.empty_cache()
+        _say(name, res, "the step's mfma roofline")
         return res
     for q8_name, make in q8_workloads(torch, ctx):
         if q8_name != name:

@@ -213,6 +213,11 @@ constexpr int q8p_waves() { return MT == 1 ? ZWG_Q8P_WAVES_32 : ZWG_Q8P_WAVES; }
 #ifndef ZWG_Q8P_KS_BELOW
 #define ZWG_Q8P_KS_BELOW 256
 #endif
+// calls of up to this many rows stream the resident weights (64-row blocks of one launch); more
+// rows take the tiled GEMM
+#ifndef ZWG_Q8P_STREAM_ROWS
+#define ZWG_Q8P_STREAM_ROWS 256
+#endif
 
 
 // Row kernels of n <= 2048 floats (a wave per row, n / 256 float4 per lane, rounded up), one
@@ -312,10 +317,16 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
     g.elem_start[zwg_lin::kQ8MaxGroup] = (int64_t)(m * n_tot);
     const int n_chunks = (a.k + zwg_lin::kQ8Chunk - 1) / zwg_lin::kQ8Chunk;
     g.n_chunks = n_chunks;
-    const bool split_k = q8p_split_k(gx, n_chunks);
+    // calls of more than 64 rows: nz blocks of 64 rows in one launch (gridDim.z), x split in the
+    // kernel, and the k split chosen from all nz gx workgroups
+    const int nz = (int)((m + 32 * MT - 1) / (32 * MT));
+    if (nz > 1 && (MT != 2 || kvs || resln || po || xcvt_in))
+        return fail(ctx, "the fused token-step calls take at most 64 rows");
+    const int64_t gxz = gx * nz;
+    const bool split_k = q8p_split_k(gxz, n_chunks);
     // xcvt_in (a 64-row call): x was split by the caller's previous launch.  The partial sums keep
     // the place (and so the split count) the call has without it.
-    const bool xs_own = q8p_splits_x_itself<MT>(gx, n_chunks);
+    const bool xs_own = q8p_splits_x_itself<MT>(gxz, n_chunks) || nz > 1;
     const bool XS = xs_own && !(MT == 2 && xcvt_in);
     if (resln && resln->xcvt && (ZWG_ADDLN_WIDE == 0 || MT != 2))
         return fail(ctx, "split rows for the next call come from 33..64-row calls' one-thread-per-column sums");
@@ -323,7 +334,7 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
     const uint64_t part_off = (xcvt_bytes + 255) / 256 * 256;
     if (part_off > ctx->workspace_bytes) return fail(ctx, "workspace too small for this linear call");
     int n_split = 1;
-    if (split_k) n_split = (int)std::min<int64_t>(n_chunks, (ZWG_Q8P_SPLIT_TARGET + gx - 1) / gx);
+    if (split_k) n_split = (int)std::min<int64_t>(n_chunks, (ZWG_Q8P_SPLIT_TARGET + gxz - 1) / gxz);
     if (kvs || resln || po) {
         if (n_chunks < 2) return fail(ctx, "the fused split-sum calls need k above 256 (their sum is a k split)");
         n_split = std::max(n_split, 2);
@@ -355,9 +366,9 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
         e = hipGetLastError();
         if (e != hipSuccess) return fail_hip(ctx, "linear (int8) x preparation launch", e);
     }
-    dim3 grid((unsigned)gx, (unsigned)n_split);
+    dim3 grid((unsigned)gx, (unsigned)n_split, (unsigned)nz);
     // unsplit calls of too few workgroups to fill the chip: two stage groups per workgroup
-    const bool two_groups = n_split == 1 && gx < ZWG_Q8P_KS_BELOW && n_chunks > 1;
+    const bool two_groups = n_split == 1 && gxz < ZWG_Q8P_KS_BELOW && n_chunks > 1;
     if (two_groups) {
         if (XS) zwg_lin::linear_q8p_stream_kernel<MT, 1, kQ8pWaves, true, 2><<<grid, 128 * kQ8pWaves, 0, ctx->stream>>>(a, g, xcvt);
         else zwg_lin::linear_q8p_stream_kernel<MT, 1, kQ8pWaves, false, 2><<<grid, 128 * kQ8pWaves, 0, ctx->stream>>>(a, g, xcvt);
@@ -593,7 +604,7 @@ int run_linear_q8w(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, c
     if (!al16(x) || !al16(out)) return fail(ctx, "x and out must be 16-byte aligned");
     hipError_t e = hipSetDevice(ctx->device);
     if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
-    if (m <= 64) return run_q8w_token_step(ctx, x, m, 1, &w, &bias, &out, epi);
+    if (m <= ZWG_Q8P_STREAM_ROWS) return run_q8w_token_step(ctx, x, m, 1, &w, &bias, &out, epi);
     LinearArgs a{};
     a.x = x;
     a.w = w->q;
@@ -866,7 +877,7 @@ int zwg_linear_q8w_group_dev(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t 
     }
     if (m == 0) return ZWG_OK;
     if (!x || !al16(x)) return fail(ctx, "x must be non-null and 16-byte aligned");
-    if (m > 64) { // prefill sizes: the tiled kernel, one call per set
+    if (m > ZWG_Q8P_STREAM_ROWS) { // prefill sizes: the tiled kernel, one call per set
         for (uint32_t j = 0; j < n_w; ++j) {
             const int r = run_linear_q8w(ctx, x, m, w[j], bias ? bias[j] : nullptr, out[j], zwg_ew::kEpiNone);
             if (r != ZWG_OK) return r;

@@ -379,6 +379,13 @@ void linear_q8p_stream_kernel(Q8Args a, Q8Group grp, const _Float16 *xcvt) {
     a.bias = q8_pick(grp.bias, set);
     a.out = q8_pick(grp.out, set);
     a.part = q8_pick(grp.part, set);
+    // a call of more rows than one x stage holds runs gridDim.z blocks of 32 MT rows (XS only):
+    // block z takes rows r0 = 32 MT z .. of x and of the outputs; the partial sums keep the whole
+    // call's [split][m][n] layout
+    const int m_all = a.m;
+    const int r0 = (int)blockIdx.z * MT * 32;
+    a.m = min(MT * 32, m_all - r0);
+    a.x += (int64_t)r0 * a.k;
 
     const int lane = threadIdx.x & 63;
     const int wave_all = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6); // uniform: the LDS DMA base is per wave
@@ -568,7 +575,7 @@ void linear_q8p_stream_kernel(Q8Args a, Q8Group grp, const _Float16 *xcvt) {
                 for (int r = 0; r < 16; ++r) acc[i][s][r] += red[(((wave * MT + i) * S + s) * 16 + r) * 64 + lane];
     }
 
-    float *dst = a.n_split > 1 ? a.part + (int64_t)split * a.m * a.n : a.out;
+    float *dst = (a.n_split > 1 ? a.part + (int64_t)split * m_all * a.n : a.out) + (int64_t)r0 * a.n;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         const int col = (slab0 + s) * 32 + r32;
