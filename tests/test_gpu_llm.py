@@ -304,6 +304,64 @@ def test_forward_against_oracle(torch, ctx, ne, H, Hk, nff):
                 assert not np.any(k0), "another sequence's cache was written"
 
 
+def composed_forward(torch, ctx, lm, kv, embd, H, Hk, toks, pos0, seq, logits):
+    """zwg_llm_forward_dev as separate library calls over the model's own weights and its own cache."""
+    import zwhisper_amd as z
+    from zwhisper_amd import _lib
+
+    ne, nff, n = lm.n_embd, lm.n_ff, len(toks)
+    d, kvw = ne // H, Hk * (ne // H)
+    X, Hn, Q, T = (torch.empty(n, ne, device="cuda") for _ in range(4))
+    Kb, Vb = torch.empty(n, kvw, device="cuda"), torch.empty(n, kvw, device="cuda")
+    G, U = torch.empty(n, nff, device="cuda"), torch.empty(n, nff, device="cuda")
+    X.copy_(torch.from_numpy(embed_np(embd, toks)))
+    sh = z.AttnShape(n, pos0 + n, H, Hk, d, ne, kvw, ne, True, lm.n_ctx)
+    for li, L in enumerate(lm.layer_refs):
+        ctx.rms_norm_dev(X, n, ne, L["attn_norm"], lm.eps, Hn)
+        ctx.linear_q8w_group_dev(Hn, n, [L["wq"], L["wk"], L["wv"]], [L["bq"], L["bk"], L["bv"]], [Q, Kb, Vb])
+        kv.append(li, seq, pos0, Kb, Vb, Q, H, ne)
+        k, v = kv.ptrs(li, seq)
+        ctx.attention_dev(Q, k, v, sh, T)
+        ctx.linear_q8w_epi_dev(T, n, L["wo"], None, X, _lib.EPI_ADD)
+        ctx.rms_norm_dev(X, n, ne, L["ffn_norm"], lm.eps, Hn)
+        ctx.linear_q8w_group_dev(Hn, n, [L["w_gate"], L["w_up"]], None, [G, U])
+        ctx.silu_mul_dev(G, U)
+        ctx.linear_q8w_epi_dev(G, n, L["w_down"], None, X, _lib.EPI_ADD)
+    ctx.rms_norm_dev(X[n - 1:], 1, ne, lm.output_norm, lm.eps, Hn)
+    ctx.linear_q8w_dev(Hn, 1, lm.output, None, logits)
+
+
+@pytest.mark.parametrize("ne,H,Hk,nff", [(384, 6, 2, 1024), (480, 15, 5, 864)], ids=["d64", "d32"])
+def test_forward_bit_exact_with_composed_calls(torch, ctx, ne, H, Hk, nff):
+    """Prompt batches of at most 256 tokens (40, then 100: two 64-row blocks of the stream kernel,
+    then 5) through the fused launches (the q/k/v projections writing the cache, the split sums
+    adding into x and normalising it) equal the batch as separate calls bit for bit: the logits
+    and the cache."""
+    import zwhisper_amd as z
+    from zwhisper_amd import _lib
+
+    rng = np.random.default_rng(ne + nff)
+    n_layer, n_vocab, n_ctx, seq = 2, 600, 160, 1
+    mdl = model(rng, ne, H, Hk, nff, n_layer, n_vocab)
+    with contextlib.ExitStack() as st:
+        lm = st.enter_context(make_llm(z, ctx, mdl, H, Hk, nff, n_ctx, 2))
+        kv = st.enter_context(z.KVCache(ctx, n_layer, 2, n_ctx, Hk, ne // H, _lib.KV_KT, 1e6))
+        la = torch.empty(n_vocab, device="cuda")
+        lb = torch.empty(n_vocab, device="cuda")
+        pos = 0
+        for n in (40, 100, 5):
+            print(f"forward batch of {n} at {pos}", flush=True)
+            toks = rng.integers(0, n_vocab, n).astype(np.int32)
+            lm.forward(torch.from_numpy(toks).cuda(), pos, la, seq)
+            composed_forward(torch, ctx, lm, kv, mdl["embd"], H, Hk, toks, pos, seq, lb)
+            torch.cuda.synchronize()
+            assert torch.equal(la, lb), n
+            for li in range(n_layer):
+                a, b = lm.kv.read(li, seq), kv.read(li, seq)
+                assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1]), (n, li)
+            pos += n
+
+
 def test_forward_matches_steps(torch, ctx):
     """A prompt batch through zwg_llm_forward_dev and the same tokens one by one through
     zwg_llm_step_dev (other kernels): the last token's logits and the caches within f32

@@ -320,8 +320,8 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
     // calls of more than 64 rows: nz blocks of 64 rows in one launch (gridDim.z), x split in the
     // kernel, and the k split chosen from all nz gx workgroups
     const int nz = (int)((m + 32 * MT - 1) / (32 * MT));
-    if (nz > 1 && (MT != 2 || kvs || resln || po || xcvt_in))
-        return fail(ctx, "the fused token-step calls take at most 64 rows");
+    if (nz > 1 && (MT != 2 || po || xcvt_in || (resln && resln->xcvt)))
+        return fail(ctx, "the split rows and partials calls take at most 64 rows");
     const int64_t gxz = gx * nz;
     const bool split_k = q8p_split_k(gxz, n_chunks);
     // xcvt_in (a 64-row call): x was split by the caller's previous launch.  The partial sums keep
@@ -626,7 +626,7 @@ int run_linear_q8w(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w, c
 
 int zwg_host::linear_q8w_qkv_kv(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *const *w,
                                 const float *const *bias, float *q_out, zwg_kv *kv, uint64_t layer, uint64_t seq0,
-                                const int32_t *pos_dev, int32_t *n_kv_out) {
+                                const int32_t *pos_dev, int32_t *n_kv_out, int64_t pos0) {
     if (!ctx) return fail(nullptr, "null context");
     if (!w || !kv) return fail(ctx, "null weight array or cache");
     if (kv->ctx != ctx) return fail(ctx, "the cache belongs to another context (or its context is closed)");
@@ -643,10 +643,14 @@ int zwg_host::linear_q8w_qkv_kv(zwg_ctx *ctx, const float *x, uint64_t m, const 
     if (w[1]->n != kv->kvw || w[2]->n != kv->kvw) return fail(ctx, "k and v weights must have n_head_kv * d rows");
     if (w[0]->n % d.d || (w[0]->n / d.d) % d.n_head_kv) return fail(ctx, "q weights must have n_head * d rows, n_head a multiple of n_head_kv");
     if (layer >= d.n_layer) return fail(ctx, "kv layer out of range");
-    if (m > 64) return fail(ctx, "the cache-writing q/k/v call takes at most 64 tokens (one decode step)");
-    if (seq0 + m > d.n_seq) return fail(ctx, "kv sequences out of range");
+    const bool rows = pos_dev == nullptr; // one sequence's m tokens at pos0 ..
+    if (!rows && m > 64) return fail(ctx, "the cache-writing q/k/v call takes at most 64 tokens (one decode step)");
+    if (!rows && seq0 + m > d.n_seq) return fail(ctx, "kv sequences out of range");
+    if (rows && (seq0 >= d.n_seq || pos0 < 0 || (uint64_t)pos0 + m > d.n_ctx))
+        return fail(ctx, "kv sequence out of range, or pos0 + m past the cache");
+    if (rows && m > ZWG_Q8P_STREAM_ROWS) return fail(ctx, "one sequence's cache-writing q/k/v call takes at most 256 tokens");
     if (m == 0) return ZWG_OK;
-    if (!x || !al16(x) || !q_out || !al16(q_out) || !pos_dev) return fail(ctx, "x, q_out (16-byte aligned) and pos_dev must be non-null");
+    if (!x || !al16(x) || !q_out || !al16(q_out)) return fail(ctx, "x and q_out must be non-null and 16-byte aligned");
     const hipError_t e = hipSetDevice(ctx->device);
     if (e != hipSuccess) return fail_hip(ctx, "hipSetDevice", e);
     zwg_lin::Q8KvStore kvs{};
@@ -664,11 +668,13 @@ int zwg_host::linear_q8w_qkv_kv(zwg_ctx *ctx, const float *x, uint64_t m, const 
     kvs.n_head_kv = (int32_t)d.n_head_kv;
     kvs.kt = d.layout == ZWG_KV_KT;
     kvs.d = (int32_t)d.d;
+    kvs.pos0 = rows ? (int32_t)pos0 : 0;
+    kvs.seq_step = rows ? 0 : 1;
     return run_q8w_token_step(ctx, x, m, 3, w, bias, nullptr, zwg_ew::kEpiNone, &kvs);
 }
 
 // x += xin . W^T + bias and ln_out = the norm of x (layer norm with ln_w, ln_b, or RMS norm with
-// ln_w; eps) for a decode step's rows (m <= 64, n <= 4096): one stream launch and
+// ln_w; eps) for a decode step's or a prompt batch's rows (m <= 256, n <= 4096): one stream launch and
 // linear_split_sum_add_ln_kernel; a call too short to split k (k <= 256) runs the add epilogue and
 // the norm as two launches, with the same results.  xcvt_out (33..64 rows): ln_out also split for
 // the next call (q8w_xcvt_halves(n) halves), which takes it as xcvt_in.
@@ -680,8 +686,8 @@ int zwg_host::linear_q8w_add_ln(zwg_ctx *ctx, const float *xin, uint64_t m, cons
     if (!msg.empty()) return fail(ctx, msg);
     if (m == 0) return ZWG_OK;
     const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-    if (m > 64 || w->n % 4 || w->n > (uint64_t)kMaxRowN)
-        return fail(ctx, "the fused residual + norm call takes m <= 64 and n <= 4096, n % 4 == 0");
+    if (m > ZWG_Q8P_STREAM_ROWS || w->n % 4 || w->n > (uint64_t)kMaxRowN)
+        return fail(ctx, "the fused residual + norm call takes m <= 256 and n <= 4096, n % 4 == 0");
     const bool rms = norm == zwg_ew::kNormRms;
     if (!xin || !x || !ln_w || (!rms && !ln_b) || !ln_out || !al16(xin) || !al16(x) || !al16(ln_w) ||
         (ln_b && !al16(ln_b)) || !al16(ln_out) || (bias && !al16(bias)))
@@ -707,6 +713,8 @@ bool zwg_host::q8w_group_reads_xcvt(uint64_t m, uint32_t n_w, const zwg_q8w *con
     const int n_chunks = (int)((w[0]->k + zwg_lin::kQ8Chunk - 1) / zwg_lin::kQ8Chunk);
     return !q8p_splits_x_itself<2>(gx, n_chunks);
 }
+
+uint64_t zwg_host::q8w_stream_rows() { return ZWG_Q8P_STREAM_ROWS; }
 
 uint64_t zwg_host::q8w_xcvt_halves(uint64_t k) {
     return (k + zwg_lin::kQ8Chunk - 1) / zwg_lin::kQ8Chunk * (uint64_t)zwg_lin::q8_chunk_halves<2>();
@@ -893,6 +901,7 @@ int zwg_linear_q8w_qkv_kv_dev(zwg_ctx *ctx, const float *x, uint64_t m, const zw
                               const float *const *bias, float *q_out, zwg_kv *kv, uint64_t layer, uint64_t seq0,
                               const int32_t *pos_dev) {
     if (!ctx) return fail(nullptr, "null context");
+    if (!pos_dev) return fail(ctx, "null pos_dev");
     return linear_q8w_qkv_kv(ctx, x, m, w, bias, q_out, kv, layer, seq0, pos_dev, nullptr);
 }
 

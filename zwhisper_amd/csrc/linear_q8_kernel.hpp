@@ -673,10 +673,12 @@ struct Q8KvStore {
     float *v_cache;
     const float *cos;       // [n_ctx][D/2], or nullptr: no rotary positions
     const float *sin;
-    const int32_t *pos_dev; // [m] positions
+    const int32_t *pos_dev; // [m] positions, or nullptr: token i at pos0 + i
     int32_t *n_kv_out;      // or nullptr: [m] keys each sequence's cache then holds, pos + 1 (0 off the cache)
     int64_t per_seq;
     int32_t seq0, n_ctx, n_head, n_head_kv, kt;
+    int32_t pos0;     // the first position when pos_dev is nullptr
+    int32_t seq_step; // token i's sequence is seq0 + i seq_step: 1 (a decode step), 0 (one sequence's rows)
     int32_t d; // the kernel's D (host side: which instantiation)
 };
 
@@ -720,7 +722,7 @@ __global__ __launch_bounds__(256) void linear_split_sum_qkv_kernel(Q8Group grp, 
         lo += bl;
         hi += bh;
     }
-    const int p = kv.pos_dev[i];
+    const int p = kv.pos_dev ? kv.pos_dev[i] : kv.pos0 + i;
     const bool live = p >= 0 && p < kv.n_ctx;
     if (kv.n_kv_out && set == 0 && h == 0 && j == 0) kv.n_kv_out[i] = live ? p + 1 : 0;
     if (set < 2 && kv.cos && live) {
@@ -738,7 +740,7 @@ __global__ __launch_bounds__(256) void linear_split_sum_qkv_kernel(Q8Group grp, 
     }
     if (!live) return;
     const int kvw = kv.n_head_kv * D;
-    const int64_t seq = (int64_t)(kv.seq0 + i) * kv.per_seq;
+    const int64_t seq = (int64_t)(kv.seq0 + i * kv.seq_step) * kv.per_seq;
     if (set == 1 && kv.kt) {
         float *kc = kv.k_cache + seq + (int64_t)(h * D + j) * kv.n_ctx + p;
 #pragma unroll

@@ -226,30 +226,53 @@ int zwg_llm_forward_dev(zwg_ctx *ctx, const zwg_llm *lm, const int32_t *tokens, 
     sh.out_stride = ne;
     sh.kt_stride = kv->desc.n_ctx;
     sh.causal = 1;
+    // batches the int8 calls stream (at most q8w_stream_rows() rows) take the fused launches of the
+    // decode step: the q/k/v projections writing the cache, and the residual projections' split
+    // sums adding into x and normalising it for the next block, with the same results
+    const bool fused = n <= q8w_stream_rows();
     for (uint64_t l = 0; l < lm->n_layer; ++l) {
         const zwg_llm_layer &L = lm->layers[l];
-        if (l > 0 && (rc = rms_norm(ctx, X, n, ne, L.attn_norm, lm->eps, Hn)) != ZWG_OK) return rc;
+        if (l > 0 && !fused && (rc = rms_norm(ctx, X, n, ne, L.attn_norm, lm->eps, Hn)) != ZWG_OK) return rc;
         // :179-190
         const zwg_q8w *qkv[3] = {L.wq, L.wk, L.wv};
         const float *qkv_b[3] = {L.bq, L.bk, L.bv};
         float *qkv_out[3] = {Q, Kb, Vb};
-        if ((rc = zwg_linear_q8w_group_dev(ctx, Hn, n, 3, qkv, qkv_b, qkv_out)) != ZWG_OK) return rc;
-        if ((rc = zwg_kv_append(kv, l, seq, pos0, n, Kb, Vb, Q, H, ne, 0)) != ZWG_OK) return rc;
+        if (fused) {
+            if ((rc = linear_q8w_qkv_kv(ctx, Hn, n, qkv, qkv_b, Q, kv, l, seq, nullptr, nullptr, (int64_t)pos0)) !=
+                ZWG_OK)
+                return rc;
+        } else {
+            if ((rc = zwg_linear_q8w_group_dev(ctx, Hn, n, 3, qkv, qkv_b, qkv_out)) != ZWG_OK) return rc;
+            if ((rc = zwg_kv_append(kv, l, seq, pos0, n, Kb, Vb, Q, H, ne, 0)) != ZWG_OK) return rc;
+        }
         // :191-202
         const uint64_t at = (l * kv->desc.n_seq + seq) * kv->per_seq;
         if ((rc = zwg_attention_dev(ctx, Q, kv->k + at, kv->v + at, &sh, T)) != ZWG_OK) return rc;
         // :203-211
-        if ((rc = zwg_linear_q8w_epi_dev(ctx, T, n, L.wo, nullptr, X, ZWG_EPI_ADD)) != ZWG_OK) return rc;
-        if ((rc = rms_norm(ctx, X, n, ne, L.ffn_norm, lm->eps, Hn)) != ZWG_OK) return rc;
+        if (fused) {
+            if ((rc = linear_q8w_add_ln(ctx, T, n, L.wo, nullptr, X, L.ffn_norm, nullptr, lm->eps, Hn, rms)) != ZWG_OK)
+                return rc;
+        } else {
+            if ((rc = zwg_linear_q8w_epi_dev(ctx, T, n, L.wo, nullptr, X, ZWG_EPI_ADD)) != ZWG_OK) return rc;
+            if ((rc = rms_norm(ctx, X, n, ne, L.ffn_norm, lm->eps, Hn)) != ZWG_OK) return rc;
+        }
         const zwg_q8w *gu[2] = {L.w_gate, L.w_up};
         float *gu_out[2] = {G, U};
         if ((rc = zwg_linear_q8w_group_dev(ctx, Hn, n, 2, gu, nullptr, gu_out)) != ZWG_OK) return rc;
         if ((rc = zwg_silu_mul_dev(ctx, G, U, n * nff)) != ZWG_OK) return rc;
-        if ((rc = zwg_linear_q8w_epi_dev(ctx, G, n, L.w_down, nullptr, X, ZWG_EPI_ADD)) != ZWG_OK) return rc;
+        if (fused) {
+            // the next block's attn_norm, or the output norm (of every row; the logits take the last)
+            const float *nw = l + 1 == lm->n_layer ? lm->output_norm : lm->layers[l + 1].attn_norm;
+            if ((rc = linear_q8w_add_ln(ctx, G, n, L.w_down, nullptr, X, nw, nullptr, lm->eps, Hn, rms)) != ZWG_OK)
+                return rc;
+        } else if ((rc = zwg_linear_q8w_epi_dev(ctx, G, n, L.w_down, nullptr, X, ZWG_EPI_ADD)) != ZWG_OK) {
+            return rc;
+        }
     }
     // :214-216: the last row's output norm and logits
-    if ((rc = rms_norm(ctx, X + (n - 1) * ne, 1, ne, lm->output_norm, lm->eps, Hn)) != ZWG_OK) return rc;
-    return zwg_linear_q8w_dev(ctx, Hn, 1, lm->output, nullptr, logits);
+    if (!fused && (rc = rms_norm(ctx, X + (n - 1) * ne, 1, ne, lm->output_norm, lm->eps, Hn + (n - 1) * ne)) != ZWG_OK)
+        return rc;
+    return zwg_linear_q8w_dev(ctx, Hn + (n - 1) * ne, 1, lm->output, nullptr, logits);
 }
 
 } // extern "C"

@@ -90,11 +90,15 @@ int linear_q8w_parts(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *w,
                      int *n_split);
 // zwg_linear_q8w_qkv_kv_dev with, when n_kv_out is set, each sequence's key count after the
 // append (pos + 1, 0 for a position off the cache) written to n_kv_out[m] by the same launch.
+// pos_dev nullptr: the m rows are one sequence's (seq0) tokens at pos0 .. pos0 + m - 1 (a prompt
+// batch, m <= q8w_stream_rows()).
 int linear_q8w_qkv_kv(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *const *w, const float *const *bias,
                       float *q_out, zwg_kv *kv, uint64_t layer, uint64_t seq0, const int32_t *pos_dev,
-                      int32_t *n_kv_out);
+                      int32_t *n_kv_out, int64_t pos0 = -1);
+// rows up to which the int8 calls stream the resident weights (and the fused calls take)
+uint64_t q8w_stream_rows();
 // A decode step's residual projection and the next norm: x += xin . W^T + bias, then ln_out =
-// the norm of x (norm 0: layer norm, 1: RMS norm; m <= 64, n <= 4096; linear.hip).  xcvt_out
+// the norm of x (norm 0: layer norm, 1: RMS norm; m <= q8w_stream_rows(), n <= 4096; linear.hip).  xcvt_out
 // (33..64 rows): ln_out also split into f16 hi/lo halves for the next call (q8w_xcvt_halves(n)
 // halves), passed to it as xcvt_in.
 int linear_q8w_add_ln(zwg_ctx *ctx, const float *xin, uint64_t m, const zwg_q8w *w, const float *bias, float *x,
