@@ -52,7 +52,8 @@ append timed beside them), one whole base.en encoder layer over the 16 windows
 ("base_enc_layer_x16") with the oracle's layer beside it, and the two callers' whole token steps
 on the device, the Whisper small.en decoder over 32 windows ("small_dec_step_x32") and Qwen2.5-1.5B
 over 64 sequences ("qwen15_step_x64"), each with the same step as separate calls and the oracle's
-forward for one token beside it.
+forward for one token beside it, and Qwen2.5-0.5B's 2048-token prompt in 8 forward batches of 256
+("qwen05_prompt_2048", with the oracle's forward over the first batch beside it).
 
 Each attention workload also carries "rate": windows/s for the encoders, tokens/s for the decoder
 step, the prefill and the LLM decode step, at wall time per step.  The prefill's CPU baseline runs
