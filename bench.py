@@ -1837,6 +1837,8 @@ def main() -> int:
                     help="arithmetic of the dense kernel for the headline workload")
     ap.add_argument("--extra", choices=EXTRAS, default=None,
                     help="measure only this workload around the attention path (no attention workloads)")
+    ap.add_argument("--skip-extra", choices=EXTRAS, action="append", default=[],
+                    help="leave this workload around the attention path out of the full run (repeatable)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--no-parity", action="store_true", help="skip the f64 parity checks of the outputs")
     ap.add_argument("--calibrate-copy", type=int, metavar="MIB", default=0,
@@ -1938,7 +1940,8 @@ def main() -> int:
             torch.cuda.empty_cache()
         ctx32.close()
         for name in EXTRAS:
-            results[name] = run_extra(name, torch, ctx, args, threads)
+            if name not in args.skip_extra:
+                results[name] = run_extra(name, torch, ctx, args, threads)
     ctx.close()
     # every CPU baseline states the host it ran on
     for res in results.values():
