@@ -288,7 +288,18 @@ struct Q8PartsOut {
     int max_parts;
     int n_split;
 };
-bool q8p_split_k(int64_t gx, int n_chunks) { return gx < ZWG_Q8P_SPLIT_BELOW && n_chunks > 1; }
+// calls of several 64-row blocks (gridDim.z) take their own split rule: split below the same
+// count, up to about 256 workgroups (the Qwen2.5-0.5B prompt's 256-row calls, per 2048-token
+// prompt: 22.43 ms at 512, 22.19 at 256; splitting calls of up to 512 or 1024 workgroups: 23.9 ms)
+#ifndef ZWG_Q8P_SPLIT_BELOW_Z
+#define ZWG_Q8P_SPLIT_BELOW_Z ZWG_Q8P_SPLIT_BELOW
+#endif
+#ifndef ZWG_Q8P_SPLIT_TARGET_Z
+#define ZWG_Q8P_SPLIT_TARGET_Z 256
+#endif
+bool q8p_split_k(int64_t gx, int n_chunks, int nz = 1) {
+    return gx < (nz > 1 ? ZWG_Q8P_SPLIT_BELOW_Z : ZWG_Q8P_SPLIT_BELOW) && n_chunks > 1;
+}
 // 32-row calls split x inside the stream kernel; 64-row ones too when k is split (small calls,
 // where the separate pass's launch costs more than the fused split), otherwise in a pass of their
 // own first.
@@ -323,7 +334,7 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
     if (nz > 1 && (MT != 2 || po || xcvt_in || (resln && resln->xcvt)))
         return fail(ctx, "the split rows and partials calls take at most 64 rows");
     const int64_t gxz = gx * nz;
-    const bool split_k = q8p_split_k(gxz, n_chunks);
+    const bool split_k = q8p_split_k(gxz, n_chunks, nz);
     // xcvt_in (a 64-row call): x was split by the caller's previous launch.  The partial sums keep
     // the place (and so the split count) the call has without it.
     const bool xs_own = q8p_splits_x_itself<MT>(gxz, n_chunks) || nz > 1;
@@ -334,7 +345,8 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
     const uint64_t part_off = (xcvt_bytes + 255) / 256 * 256;
     if (part_off > ctx->workspace_bytes) return fail(ctx, "workspace too small for this linear call");
     int n_split = 1;
-    if (split_k) n_split = (int)std::min<int64_t>(n_chunks, (ZWG_Q8P_SPLIT_TARGET + gxz - 1) / gxz);
+    const int64_t target = nz > 1 ? ZWG_Q8P_SPLIT_TARGET_Z : ZWG_Q8P_SPLIT_TARGET;
+    if (split_k) n_split = (int)std::min<int64_t>(n_chunks, (target + gxz - 1) / gxz);
     if (kvs || resln || po) {
         if (n_chunks < 2) return fail(ctx, "the fused split-sum calls need k above 256 (their sum is a k split)");
         n_split = std::max(n_split, 2);
