@@ -177,12 +177,13 @@ def test_step_bit_exact_with_composed_calls(torch, ctx, ne, H, Hk, nff):
                     assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1]), (step, li, s)
 
 
-@pytest.mark.parametrize("m", [40, 64])
+@pytest.mark.parametrize("m", [40, 64, 24])
 def test_step_bit_exact_33_to_64_rows(torch, ctx, m):
     """33..64 sequences take the 64-row kernels, and (n_ff 8192 and a 16400-token vocabulary: the
     gate/up call and the logits stream a split x) the o projection's sum kernel splits the
     ffn-normed rows for the gate/up call and the last down projection's the output-normed rows
-    for the logits, zero rows past m included."""
+    for the logits, zero rows past m included.  At n_ff 8192 the SwiGLU pair is unsplit (its
+    gate waves take the up waves' values); 24 sequences: the same with the 32-row kernels."""
     import zwhisper_amd as z
     from zwhisper_amd import _lib
 
@@ -331,7 +332,8 @@ def composed_forward(torch, ctx, lm, kv, embd, H, Hk, toks, pos0, seq, logits):
     ctx.linear_q8w_dev(Hn, 1, lm.output, None, logits)
 
 
-@pytest.mark.parametrize("ne,H,Hk,nff", [(384, 6, 2, 1024), (480, 15, 5, 864)], ids=["d64", "d32"])
+@pytest.mark.parametrize("ne,H,Hk,nff", [(384, 6, 2, 1024), (480, 15, 5, 864), (384, 6, 2, 8192)],
+                         ids=["d64", "d32", "ff8192"])
 def test_forward_bit_exact_with_composed_calls(torch, ctx, ne, H, Hk, nff):
     """Prompt batches of at most 256 tokens (40, then 100: two 64-row blocks of the stream kernel,
     then 5) through the fused launches (the q/k/v projections writing the cache, the split sums

@@ -314,6 +314,9 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
     constexpr int kQ8pWaves = q8p_waves<MT>();
     zwg_lin::Q8Args a = base;
     const uint64_t m = (uint64_t)a.m;
+    const bool pair = g.swiglu != 0;
+    if (pair && (g.count != 2 || g.n[0] != g.n[1] || kvs || resln || po))
+        return fail(ctx, "a SwiGLU pair is two weight sets of the same shape, with no fused store");
     int64_t gx = 0;
     uint64_t n_tot = 0;
     for (int j = 0; j < zwg_lin::kQ8MaxGroup; ++j) {
@@ -328,6 +331,10 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
     g.elem_start[zwg_lin::kQ8MaxGroup] = (int64_t)(m * n_tot);
     const int n_chunks = (a.k + zwg_lin::kQ8Chunk - 1) / zwg_lin::kQ8Chunk;
     g.n_chunks = n_chunks;
+    // a SwiGLU pair's workgroups each take the same columns of both sets: the grid covers one
+    // set's columns at half the rows per workgroup, while every choice below is the two sets'
+    // unpaired one (so the sums are the same as the pair's two separate outputs')
+    const int64_t gx_launch = pair ? ((int64_t)g.n[0] + 16 * kQ8pWaves - 1) / (16 * kQ8pWaves) : gx;
     // calls of more than 64 rows: nz blocks of 64 rows in one launch (gridDim.z), x split in the
     // kernel, and the k split chosen from all nz gx workgroups
     const int nz = (int)((m + 32 * MT - 1) / (32 * MT));
@@ -378,15 +385,25 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
         e = hipGetLastError();
         if (e != hipSuccess) return fail_hip(ctx, "linear (int8) x preparation launch", e);
     }
-    dim3 grid((unsigned)gx, (unsigned)n_split, (unsigned)nz);
+    dim3 grid((unsigned)gx_launch, (unsigned)n_split, (unsigned)nz);
     // unsplit calls of too few workgroups to fill the chip: two stage groups per workgroup
     const bool two_groups = n_split == 1 && gxz < ZWG_Q8P_KS_BELOW && n_chunks > 1;
-    if (two_groups) {
-        if (XS) zwg_lin::linear_q8p_stream_kernel<MT, 1, kQ8pWaves, true, 2><<<grid, 128 * kQ8pWaves, 0, ctx->stream>>>(a, g, xcvt);
-        else zwg_lin::linear_q8p_stream_kernel<MT, 1, kQ8pWaves, false, 2><<<grid, 128 * kQ8pWaves, 0, ctx->stream>>>(a, g, xcvt);
+    using namespace zwg_lin;
+    constexpr int W = kQ8pWaves;
+    if (pair) {
+        if (two_groups) {
+            if (XS) linear_q8p_stream_kernel<MT, 1, W, true, 2, true><<<grid, 128 * W, 0, ctx->stream>>>(a, g, xcvt);
+            else linear_q8p_stream_kernel<MT, 1, W, false, 2, true><<<grid, 128 * W, 0, ctx->stream>>>(a, g, xcvt);
+        } else {
+            if (XS) linear_q8p_stream_kernel<MT, 1, W, true, 1, true><<<grid, 64 * W, 0, ctx->stream>>>(a, g, xcvt);
+            else linear_q8p_stream_kernel<MT, 1, W, false, 1, true><<<grid, 64 * W, 0, ctx->stream>>>(a, g, xcvt);
+        }
+    } else if (two_groups) {
+        if (XS) linear_q8p_stream_kernel<MT, 1, W, true, 2><<<grid, 128 * W, 0, ctx->stream>>>(a, g, xcvt);
+        else linear_q8p_stream_kernel<MT, 1, W, false, 2><<<grid, 128 * W, 0, ctx->stream>>>(a, g, xcvt);
     } else {
-        if (XS) zwg_lin::linear_q8p_stream_kernel<MT, 1, kQ8pWaves, true><<<grid, 64 * kQ8pWaves, 0, ctx->stream>>>(a, g, xcvt);
-        else zwg_lin::linear_q8p_stream_kernel<MT, 1, kQ8pWaves, false><<<grid, 64 * kQ8pWaves, 0, ctx->stream>>>(a, g, xcvt);
+        if (XS) linear_q8p_stream_kernel<MT, 1, W, true><<<grid, 64 * W, 0, ctx->stream>>>(a, g, xcvt);
+        else linear_q8p_stream_kernel<MT, 1, W, false><<<grid, 64 * W, 0, ctx->stream>>>(a, g, xcvt);
     }
     e = hipGetLastError();
     if (e != hipSuccess) return fail_hip(ctx, "linear (int8 stream) kernel launch", e);
@@ -410,6 +427,12 @@ int run_q8p_group(zwg_ctx *ctx, const zwg_lin::Q8Args &base, zwg_lin::Q8Group g,
                 : launch_rows<AddLnChosen, zwg_ew::kNormLayer>(g.n[0], a.m, ctx->stream, (const float *)g.part[0],
                                                                g.bias[0], *resln, a.m, g.n[0], n_split);
         if (e != hipSuccess) return fail_hip(ctx, "split-sum + residual + norm kernel launch", e);
+    } else if (n_split > 1 && pair) {
+        const int64_t elems = (int64_t)(m * (uint64_t)g.n[0]);
+        const int bs = small_block(elems);
+        zwg_lin::linear_split_sum_swiglu_kernel<<<blocks_for(elems, bs), bs, 0, ctx->stream>>>(g, a.m, n_split);
+        e = hipGetLastError();
+        if (e != hipSuccess) return fail_hip(ctx, "SwiGLU split-sum kernel launch", e);
     } else if (n_split > 1) {
         const int64_t elems = (int64_t)(m * n_tot);
         const int bs = small_block(elems);
@@ -582,7 +605,7 @@ void detach_q8w(void *obj) {
 int run_q8w_token_step(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t n_w, const zwg_q8w *const *w,
                        const float *const *bias, float *const *out, uint32_t epi,
                        const zwg_lin::Q8KvStore *kvs = nullptr, const zwg_lin::Q8ResLn *resln = nullptr,
-                       Q8PartsOut *po = nullptr, const _Float16 *xcvt_in = nullptr) {
+                       Q8PartsOut *po = nullptr, const _Float16 *xcvt_in = nullptr, bool swiglu = false) {
     zwg_lin::Q8Args a{};
     a.x = x;
     a.m = (int32_t)m;
@@ -591,6 +614,7 @@ int run_q8w_token_step(zwg_ctx *ctx, const float *x, uint64_t m, uint32_t n_w, c
     a.epi = epi;
     zwg_lin::Q8Group g{};
     g.count = (int32_t)n_w;
+    g.swiglu = swiglu ? 1 : 0;
     for (uint32_t j = 0; j < n_w; ++j) {
         g.q[j] = w[j]->q;
         g.scales[j] = w[j]->scales;
@@ -727,6 +751,28 @@ bool zwg_host::q8w_group_reads_xcvt(uint64_t m, uint32_t n_w, const zwg_q8w *con
 }
 
 uint64_t zwg_host::q8w_stream_rows() { return ZWG_Q8P_STREAM_ROWS; }
+
+// out = silu(x . gate^T) * (x . up^T) for at most q8w_stream_rows() rows (src/llm.zig:207-210):
+// one stream launch over both weight sets (a SwiGLU pair), plus one SwiGLU split sum when k is
+// split; the same values as the two projections' group call followed by the SiLU-mul kernel.
+// xcvt_in as for linear_q8w_group_xcvt.
+int zwg_host::linear_q8w_swiglu(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *gate, const zwg_q8w *up,
+                                float *out, const _Float16 *xcvt_in) {
+    const auto al16 = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    if (!gate || !up) return fail(ctx, "null weights");
+    if (!gate->ctx || !up->ctx) return fail(ctx, kQ8wClosed);
+    if (gate->n != up->n || gate->k != up->k) return fail(ctx, "gate and up weights must have one shape");
+    const std::string msg = check_linear(m, gate->k, ZWG_W_Q8, gate->n);
+    if (!msg.empty()) return fail(ctx, msg);
+    if (m == 0) return ZWG_OK;
+    if (m > ZWG_Q8P_STREAM_ROWS || !x || !out || !al16(x) || !al16(out) ||
+        (xcvt_in && (!al16(xcvt_in) || m <= 32 || m > 64)))
+        return fail(ctx, "a SwiGLU call: m <= 256, x and out 16-byte aligned, split rows for 33..64 rows");
+    const zwg_q8w *w[2] = {gate, up};
+    float *outs[2] = {out, nullptr};
+    return run_q8w_token_step(ctx, x, m, 2, w, nullptr, outs, zwg_ew::kEpiNone, nullptr, nullptr, nullptr, xcvt_in,
+                              true);
+}
 
 uint64_t zwg_host::q8w_xcvt_halves(uint64_t k) {
     return (k + zwg_lin::kQ8Chunk - 1) / zwg_lin::kQ8Chunk * (uint64_t)zwg_lin::q8_chunk_halves<2>();

@@ -266,6 +266,10 @@ struct Q8Group {
     const float *bias[kQ8MaxGroup];
     float *out[kQ8MaxGroup];
     float *part[kQ8MaxGroup]; // [n_split][m][n[j]] when the call is split
+    // 1: a SwiGLU pair (count 2, n[0] == n[1]: the MLP's gate and up, src/llm.zig:207-210): each
+    // workgroup takes the same columns of both sets and the call stores silu(gate) * up into
+    // out[0] (linear_q8p_stream_kernel; split calls through linear_split_sum_swiglu_kernel)
+    int32_t swiglu;
 };
 
 // entry j of a group field, by selects on the uniform j (no dynamic indexing of the kernel-
@@ -356,7 +360,8 @@ constexpr int kQ8StageK = kQ8StageBlocks * kQ8Block;
 // the first stores.  For calls whose weight rows give too few workgroups for the chip and are not
 // split: each wave then walks half the stages, and two waves share each SIMD, with no partial
 // sums in memory and no second launch.
-template <int MT, int S, int NW, bool XS, int KS = 1>
+// PAIR: a SwiGLU pair (Q8Group swiglu), a form of its own so the other calls carry none of it.
+template <int MT, int S, int NW, bool XS, int KS = 1, bool PAIR = false>
 __global__ __launch_bounds__(64 * NW * KS) __attribute__((amdgpu_waves_per_eu(2)))
 void linear_q8p_stream_kernel(Q8Args a, Q8Group grp, const _Float16 *xcvt) {
     static_assert(KS == 1 || KS == 2, "one or two stage groups");
@@ -371,9 +376,16 @@ void linear_q8p_stream_kernel(Q8Args a, Q8Group grp, const _Float16 *xcvt) {
     static_assert(!XS || XQ * 4 * NT == MT * 32 * kQ8StageK, "every thread loads whole quads of the x stage");
     __shared__ __align__(16) _Float16 xs_all[KS][2][STAGE_HALVES];
 
-    // this workgroup's weight set and its index within the set
-    const int set = q8_group_of_block(grp, (int)blockIdx.x);
-    const int bx = (int)blockIdx.x - q8_pick(grp.block_start, set);
+    const int lane = threadIdx.x & 63;
+    const int wave_all = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6); // uniform: the LDS DMA base is per wave
+    const int kg = KS == 1 ? 0 : wave_all / NW;                    // stage group
+    const int wave = KS == 1 ? wave_all : wave_all - kg * NW;      // wave within the group: its slabs
+    // this wave's weight set and its workgroup's index within the set.  A SwiGLU pair: the first
+    // NW / 2 waves take the gate's slabs and the others the up's slabs over the same columns.
+    constexpr bool pair = PAIR;
+    constexpr int HW = NW / 2;
+    const int set = pair ? (wave >= HW ? 1 : 0) : q8_group_of_block(grp, (int)blockIdx.x);
+    const int bx = (int)blockIdx.x - (pair ? 0 : q8_pick(grp.block_start, set));
     const Q8Packed w = {q8_pick(grp.q, set), q8_pick(grp.scales, set), q8_pick(grp.n_slabs, set), grp.n_chunks};
     a.n = q8_pick(grp.n, set);
     a.bias = q8_pick(grp.bias, set);
@@ -387,14 +399,11 @@ void linear_q8p_stream_kernel(Q8Args a, Q8Group grp, const _Float16 *xcvt) {
     a.m = min(MT * 32, m_all - r0);
     a.x += (int64_t)r0 * a.k;
 
-    const int lane = threadIdx.x & 63;
-    const int wave_all = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6); // uniform: the LDS DMA base is per wave
-    const int kg = KS == 1 ? 0 : wave_all / NW;                    // stage group
-    const int wave = KS == 1 ? wave_all : wave_all - kg * NW;      // wave within the group: its slabs
     const int tid = KS == 1 ? (int)threadIdx.x : (int)threadIdx.x - kg * NT; // thread within the group
     _Float16(&xs)[2][STAGE_HALVES] = xs_all[kg];
     const int r32 = lane & 31, g = lane >> 5;
-    const int slab0 = bx * SLABS + wave * S; // this wave's first slab
+    const int hw = pair ? wave - set * HW : wave;   // the wave's place among its set's waves
+    const int slab0 = bx * (pair ? HW * S : SLABS) + hw * S; // this wave's first slab
     const int split = blockIdx.y;
     const int n_stages = (a.k + NB * kQ8Block - 1) / (NB * kQ8Block);
     const int w_begin = split * a.chunks_per_split * 2;
@@ -566,21 +575,58 @@ void linear_q8p_stream_kernel(Q8Args a, Q8Group grp, const _Float16 *xcvt) {
                     for (int r = 0; r < 16; ++r) red[(((wave * MT + i) * S + s) * 16 + r) * 64 + lane] = acc[i][s][r];
         }
         __syncthreads();
-        if (kg == 1) return;
+        if (kg == 0) {
 #pragma unroll
-        for (int i = 0; i < MT; ++i)
+            for (int i = 0; i < MT; ++i)
 #pragma unroll
-            for (int s = 0; s < S; ++s)
+                for (int s = 0; s < S; ++s)
 #pragma unroll
-                for (int r = 0; r < 16; ++r) acc[i][s][r] += red[(((wave * MT + i) * S + s) * 16 + r) * 64 + lane];
+                    for (int r = 0; r < 16; ++r) acc[i][s][r] += red[(((wave * MT + i) * S + s) * 16 + r) * 64 + lane];
+        }
+        // an unsplit SwiGLU pair's second group stays for the barriers below
+        if (kg == 1 && !(PAIR && a.n_split == 1)) return;
     }
 
+    // an unsplit SwiGLU pair: the up waves hand their values (with bias, as the call would store
+    // them) to the gate waves through the freed x buffers (past the two groups' exchange), which
+    // store silu(gate) * up
+    constexpr int RED2 = KS == 2 ? NW * MT * S * 16 * 64 : 0;
+    float *red = reinterpret_cast<float *>(&xs_all[0][0][0]) + RED2;
+    static_assert((RED2 + HW * MT * S * 16 * 64) * 4 <= (int)sizeof(xs_all), "the up values fit in the x buffers");
+    if (PAIR && a.n_split == 1) {
+        __syncthreads(); // every wave is past its last compute (and the first group's sums are whole)
+        if (kg == 0 && set == 1) {
+#pragma unroll
+            for (int s = 0; s < S; ++s) {
+                const int col = (slab0 + s) * 32 + r32;
+                const float bj = (a.bias && col < a.n) ? a.bias[col] : 0.f;
+#pragma unroll
+                for (int i = 0; i < MT; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) red[(((hw * MT + i) * S + s) * 16 + r) * 64 + lane] = acc[i][s][r] + bj;
+            }
+        }
+        __syncthreads();
+        if (kg == 1 || set == 1) return;
+    }
     float *dst = (a.n_split > 1 ? a.part + (int64_t)split * m_all * a.n : a.out) + (int64_t)r0 * a.n;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
         const int col = (slab0 + s) * 32 + r32;
         if (col >= a.n) continue;
         const float bj = (a.n_split == 1 && a.bias) ? a.bias[col] : 0.f;
+        if (PAIR && a.n_split == 1) {
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int row = 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (row < a.m)
+                        dst[(int64_t)row * a.n + col] =
+                            zwg_ew::silu_mul(acc[i][s][r] + bj, red[(((hw * MT + i) * S + s) * 16 + r) * 64 + lane]);
+                }
+            continue;
+        }
 #pragma unroll
         for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -655,6 +701,35 @@ __global__ __launch_bounds__(256) void linear_split_sum_group_kernel(Q8Group grp
     }
     if (bias) s += bias[le % n];
     zwg_ew::epilogue_store(&q8_pick(grp.out, set)[le], s, epi);
+}
+
+// A split SwiGLU pair's sum (Q8Group swiglu): out[0][e] = silu(gate) * up, gate and up each their
+// splits added in split order then their bias, as linear_split_sum_group_kernel forms them, then
+// zwg_ew::silu_mul (the separate SiLU-mul kernel's function).  e over m n[0].
+__global__ __launch_bounds__(256) void linear_split_sum_swiglu_kernel(Q8Group grp, int32_t m, int32_t n_split) {
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int32_t n = grp.n[0];
+    const int64_t mn = (int64_t)m * n;
+    if (e >= mn) return;
+    float gu[2];
+#pragma unroll
+    for (int set = 0; set < 2; ++set) {
+        const float *p = (set ? grp.part[1] : grp.part[0]) + e;
+        float s = 0.f;
+        for (int q0 = 0; q0 < n_split; q0 += kSumBatch) {
+            float v[kSumBatch];
+#pragma unroll
+            for (int j = 0; j < kSumBatch; ++j)
+                if (q0 + j < n_split) v[j] = p[(q0 + j) * mn];
+#pragma unroll
+            for (int j = 0; j < kSumBatch; ++j)
+                if (q0 + j < n_split) s = q0 + j == 0 ? v[j] : s + v[j];
+        }
+        const float *bias = set ? grp.bias[1] : grp.bias[0];
+        if (bias) s += bias[e % n];
+        gu[set] = s;
+    }
+    grp.out[0][e] = zwg_ew::silu_mul(gu[0], gu[1]);
 }
 
 // The q/k/v group's split sum with the cache append fused into its stores (set 0 q, 1 k, 2 v of a

@@ -14,8 +14,10 @@
 //     X += o(T); H = rmsNorm(X, ffn_norm)            stream + linear_split_sum_add_ln_wide_kernel
 //                                                    (RMS), which also splits H into f16 hi/lo
 //                                                    halves when the gate/up call reads a split x
-//     G, U = gate(H), up(H)                          one grouped call (no split launch of its own)
-//     G = silu(G) * U                                silu_mul_kernel
+//     G = silu(gate(H)) * up(H)                      one stream launch over both weight sets, each
+//                                                    workgroup on the same columns of both (a
+//                                                    SwiGLU pair; + one split sum when k is split);
+//                                                    no x split launch of its own
 //     X += down(G); H = next layer's attn_norm(X), or the output norm after the last layer
 //                                                    stream + the sum, residual add and norm
 //   logits = H . output^T                           one stream launch (33..64 sequences: x split by
@@ -166,10 +168,7 @@ int zwg_llm_step_dev(zwg_ctx *ctx, const zwg_llm *lm, const int32_t *tokens, con
             return rc;
         // :207-211: gate and up, SiLU-gated, down, then the next block's attn_norm or the output
         // norm (:215)
-        const zwg_q8w *gu[2] = {L.w_gate, L.w_up};
-        float *gu_out[2] = {G, U};
-        if ((rc = linear_q8w_group_xcvt(ctx, Hn, m, 2, gu, nullptr, gu_out, gu_xc)) != ZWG_OK) return rc;
-        if ((rc = zwg_silu_mul_dev(ctx, G, U, m * nff)) != ZWG_OK) return rc;
+        if ((rc = linear_q8w_swiglu(ctx, Hn, m, L.w_gate, L.w_up, G, gu_xc)) != ZWG_OK) return rc;
         const bool last = l + 1 == lm->n_layer;
         const float *nw = last ? lm->output_norm : lm->layers[l + 1].attn_norm;
         if ((rc = linear_q8w_add_ln(ctx, G, m, L.w_down, nullptr, X, nw, nullptr, lm->eps, Hn, rms,
@@ -256,10 +255,14 @@ int zwg_llm_forward_dev(zwg_ctx *ctx, const zwg_llm *lm, const int32_t *tokens, 
             if ((rc = zwg_linear_q8w_epi_dev(ctx, T, n, L.wo, nullptr, X, ZWG_EPI_ADD)) != ZWG_OK) return rc;
             if ((rc = rms_norm(ctx, X, n, ne, L.ffn_norm, lm->eps, Hn)) != ZWG_OK) return rc;
         }
-        const zwg_q8w *gu[2] = {L.w_gate, L.w_up};
-        float *gu_out[2] = {G, U};
-        if ((rc = zwg_linear_q8w_group_dev(ctx, Hn, n, 2, gu, nullptr, gu_out)) != ZWG_OK) return rc;
-        if ((rc = zwg_silu_mul_dev(ctx, G, U, n * nff)) != ZWG_OK) return rc;
+        if (fused) {
+            if ((rc = linear_q8w_swiglu(ctx, Hn, n, L.w_gate, L.w_up, G)) != ZWG_OK) return rc;
+        } else {
+            const zwg_q8w *gu[2] = {L.w_gate, L.w_up};
+            float *gu_out[2] = {G, U};
+            if ((rc = zwg_linear_q8w_group_dev(ctx, Hn, n, 2, gu, nullptr, gu_out)) != ZWG_OK) return rc;
+            if ((rc = zwg_silu_mul_dev(ctx, G, U, n * nff)) != ZWG_OK) return rc;
+        }
         if (fused) {
             // the next block's attn_norm, or the output norm (of every row; the logits take the last)
             const float *nw = l + 1 == lm->n_layer ? lm->output_norm : lm->layers[l + 1].attn_norm;

@@ -97,6 +97,10 @@ int linear_q8w_qkv_kv(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *c
                       int32_t *n_kv_out, int64_t pos0 = -1);
 // rows up to which the int8 calls stream the resident weights (and the fused calls take)
 uint64_t q8w_stream_rows();
+// out = silu(x . gate^T) * (x . up^T), m <= q8w_stream_rows() (one stream launch over both sets);
+// xcvt_in as for linear_q8w_group_xcvt
+int linear_q8w_swiglu(zwg_ctx *ctx, const float *x, uint64_t m, const zwg_q8w *gate, const zwg_q8w *up, float *out,
+                      const _Float16 *xcvt_in = nullptr);
 // A decode step's residual projection and the next norm: x += xin . W^T + bias, then ln_out =
 // the norm of x (norm 0: layer norm, 1: RMS norm; m <= q8w_stream_rows(), n <= 4096; linear.hip).  xcvt_out
 // (33..64 rows): ln_out also split into f16 hi/lo halves for the next call (q8w_xcvt_halves(n)
