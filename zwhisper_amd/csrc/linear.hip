@@ -202,11 +202,12 @@ constexpr int q8p_waves() { return MT == 1 ? ZWG_Q8P_WAVES_32 : ZWG_Q8P_WAVES; }
 #define ZWG_Q8P_SPLIT_BELOW 128
 #endif
 // workgroups a split call is split up to (within its k chunks).  Only the Qwen2.5-1.5B down
-// projection (k = 8960, 35-way at 512) reaches it; its decode step measured 2163 / 2048 / 1960 /
-// 1964 / 1963 us at 128 / 192 / 256 / 512 / 1024: the partial sums' traffic (13.8 MB each way per
-// layer at 512) costs nothing that fewer splits would win back
+// projection (k = 8960: 18-way at 256, 35-way at 512) reaches it; its projections alone measured
+// 2163 / 2048 / 1960 / 1964 / 1963 us at 128 / 192 / 256 / 512 / 1024, and its whole token step,
+// whose down projection's sums add into x and normalise it in one row kernel, 4.117 / 4.073 /
+// 4.074 ms at 512 / 384 / 256 (paired runs): that kernel reads half the partials at 256
 #ifndef ZWG_Q8P_SPLIT_TARGET
-#define ZWG_Q8P_SPLIT_TARGET 512
+#define ZWG_Q8P_SPLIT_TARGET 256
 #endif
 // unsplit calls of fewer workgroups than this run two stage groups per workgroup (each over half
 // of k, summed through LDS at the end)
