@@ -131,9 +131,18 @@ std::string check_linear(uint64_t m, uint64_t k, uint32_t w_type, uint64_t n) {
 
 // Q8 with m <= 64: x split into hi/lo halves by linear_q8_xprep_kernel into the workspace, then
 // the weight-streaming kernel.  Four waves of S slabs of 32 weight rows per workgroup (S = 2 when
-// that alone makes >= 256 workgroups, else 1); k is split over more workgroups, at chunk
-// granularity, until there are about 512 of them, as long as the partial sums fit the workspace.
-// (Raw-layout weights; the resident packed ones go through run_q8p_group.)
+// that alone makes >= 256 workgroups, else 1); a call of fewer than 512 workgroups splits k over
+// more, at chunk granularity, up to about ZWG_Q8P_SPLIT_TARGET of them, as long as the partial
+// sums fit the workspace.  (Raw-layout weights; the resident packed ones go through run_q8p_group.)
+//
+// Workgroups a split call is split up to (within its k chunks).  Only the Qwen2.5-1.5B down
+// projection (k = 8960: 18-way at 256, 35-way at 512) reaches it; its projections alone measured
+// 2163 / 2048 / 1960 / 1964 / 1963 us at 128 / 192 / 256 / 512 / 1024, and its whole token step,
+// whose down projection's sums add into x and normalise it in one row kernel, 4.117 / 4.073 /
+// 4.074 ms at 512 / 384 / 256 (paired runs): that kernel reads half the partials at 256
+#ifndef ZWG_Q8P_SPLIT_TARGET
+#define ZWG_Q8P_SPLIT_TARGET 256
+#endif
 template <int MT>
 int run_q8_stream_mt(zwg_ctx *ctx, const zwg_lin::Q8Args &base) {
     zwg_lin::Q8Args a = base;
@@ -145,7 +154,8 @@ int run_q8_stream_mt(zwg_ctx *ctx, const zwg_lin::Q8Args &base) {
     const uint64_t part_off = (xcvt_bytes + 255) / 256 * 256;
     if (part_off > ctx->workspace_bytes) return fail(ctx, "workspace too small for this linear call");
     int n_split = 1;
-    if (gx < 512) n_split = (int)std::min<int64_t>(n_chunks, (512 + gx - 1) / gx);
+    // split up to the packed calls' target, so both layouts split a call into the same pieces
+    if (gx < 512) n_split = (int)std::min<int64_t>(n_chunks, (ZWG_Q8P_SPLIT_TARGET + gx - 1) / gx);
     while (n_split > 1 && part_off + (uint64_t)n_split * m * n * 4 > ctx->workspace_bytes) --n_split;
     a.chunks_per_split = (n_chunks + n_split - 1) / n_split;
     n_split = (n_chunks + a.chunks_per_split - 1) / a.chunks_per_split; // no empty splits
@@ -200,14 +210,6 @@ constexpr int q8p_waves() { return MT == 1 ? ZWG_Q8P_WAVES_32 : ZWG_Q8P_WAVES; }
 #endif
 #ifndef ZWG_Q8P_SPLIT_BELOW
 #define ZWG_Q8P_SPLIT_BELOW 128
-#endif
-// workgroups a split call is split up to (within its k chunks).  Only the Qwen2.5-1.5B down
-// projection (k = 8960: 18-way at 256, 35-way at 512) reaches it; its projections alone measured
-// 2163 / 2048 / 1960 / 1964 / 1963 us at 128 / 192 / 256 / 512 / 1024, and its whole token step,
-// whose down projection's sums add into x and normalise it in one row kernel, 4.117 / 4.073 /
-// 4.074 ms at 512 / 384 / 256 (paired runs): that kernel reads half the partials at 256
-#ifndef ZWG_Q8P_SPLIT_TARGET
-#define ZWG_Q8P_SPLIT_TARGET 256
 #endif
 // unsplit calls of fewer workgroups than this run two stage groups per workgroup (each over half
 // of k, summed through LDS at the end)
