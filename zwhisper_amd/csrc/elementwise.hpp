@@ -11,13 +11,18 @@ namespace zwg_ew {
 
 // ggml's GELU, tanh form (src/ops.zig:312-327): u = c (x + 0.044715 x^3), c = sqrt(2/pi),
 // tanh(u) = 1 - 2 / (1 + e^(2u)), gelu = 0.5 x (1 + tanh(u)).  Rounded step by step in the
-// reference's order (k x x x left to right), with no fused multiply-adds.
+// reference's order (k x x x left to right), with no fused multiply-adds.  e^(2u) is 2^(2u log2 e)
+// on v_exp_f32 and 2 / (1 + e) is 2 rcp(1 + e) on v_rcp_f32, each within about 1 ulp: the
+// rounding of 2u log2 e moves e by at most 2^-24 |2u| relatively, which changes tanh by at most
+// 2^-24 where it is not saturated (2e / (1 + e)^2 |2u| <= 1), far below the f32 sums feeding it.
+// Large |u| saturate exactly: e = inf gives t = 1, e = 0 gives t = -1.
 __device__ __forceinline__ float gelu(float x) {
 #pragma clang fp contract(off)
     const float c = 0.7978845608028654f;
     const float k = 0.044715f;
     const float u = c * (x + k * x * x * x);
-    const float t = 1.0f - 2.0f / (1.0f + expf(2.0f * u));
+    const float e = __builtin_amdgcn_exp2f(2.0f * u * 1.4426950408889634f);
+    const float t = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
     return 0.5f * x * (1.0f + t);
 }
 

@@ -340,6 +340,44 @@ __global__ __launch_bounds__(128 * NWN) void linear_mfma_kernel(LinearArgs a) {
             return;
         }
     }
+    if constexpr (!KSPLIT) {
+        const int rows_o = min(BM, a.m - m0);
+        const int64_t span = (int64_t)(rows_o - 1) * a.ldo + (a.n - n0); // elements from (m0, n0) on
+        if (a.epi == zwg_ew::kEpiAdd && span < 0x1fffffffll) {
+            // out + v: each row block's residual values are loaded before its first store.  Loads
+            // and stores interleaved per element (the compiler cannot move a load of out above a
+            // store to out it cannot tell apart) would wait one memory round trip each.  The loads
+            // go through a descriptor ending at the tile's last element (rows past m read 0), with
+            // the lane's part of the offset in one VGPR and the register's row in the SGPR part.
+            const __amdgpu_buffer_rsrc_t o_src = rsrc(a.out + (int64_t)m0 * a.ldo + n0, (uint32_t)(span * 4));
+            const int ld4 = (int)a.ldo * 4;
+            const int vo = (wm * WM + 4 * (lane >> 5)) * ld4 + (wn * WN + r32) * 4;
+#pragma unroll
+            for (int i = 0; i < TM; ++i) {
+                float res[TN][16];
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r)
+                        res[j][r] = __builtin_bit_cast(
+                            float, __builtin_amdgcn_raw_buffer_load_b32(
+                                       o_src, vo, (i * 32 + 8 * (r >> 2) + (r & 3)) * ld4 + j * 128, 0));
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int col = n0 + wn * WN + j * 32 + r32;
+                    if (col >= a.n) continue;
+                    const float bj = a.bias ? a.bias[col] : 0.f;
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                        if (row >= a.m) continue;
+                        a.out[(int64_t)row * a.ldo + col] = res[j][r] + (acc[i][j][r] + bj);
+                    }
+                }
+            }
+            return;
+        }
+    }
     float *part = KSPLIT ? a.part + (int64_t)split * a.m * a.n : nullptr;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
