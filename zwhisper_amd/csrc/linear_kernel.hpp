@@ -114,8 +114,10 @@ __device__ __forceinline__ int64_t xcd_logical_tile(int64_t hw, int64_t n) {
 // half index of (row, 8-half chunk) in a swizzled LDS tile
 __device__ __forceinline__ int lds_at(int row, int chunk) { return row * BK + ((chunk ^ ((row ^ (row >> 2)) & 3)) << 3); }
 
-template <int BM, int BN, int WMODE, int NWN = 2, bool KSPLIT = false>
-__global__ __launch_bounds__(128 * NWN) void linear_mfma_kernel(LinearArgs a) {
+// The kernel's body, taking the arguments by reference (measured 1-2% faster on the base.en
+// projections than the same code as the kernel itself, with its by-value argument).
+template <int BM, int BN, int WMODE, int NWN, bool KSPLIT>
+__device__ __forceinline__ void linear_mfma_body(const LinearArgs &a) {
     // 2 x NWN waves, each a (BM / 2) x (BN / NWN) block of the tile
     constexpr int kThreads = 128 * NWN;
     constexpr bool Q8 = WMODE != kWF16;
@@ -394,6 +396,11 @@ __global__ __launch_bounds__(128 * NWN) void linear_mfma_kernel(LinearArgs a) {
                 else zwg_ew::epilogue_store(&a.out[(int64_t)row * a.ldo + col], acc[i][j][r] + bj, a.epi);
             }
     }
+}
+
+template <int BM, int BN, int WMODE, int NWN = 2, bool KSPLIT = false>
+__global__ __launch_bounds__(128 * NWN) void linear_mfma_kernel(LinearArgs a) {
+    linear_mfma_body<BM, BN, WMODE, NWN, KSPLIT>(a);
 }
 
 // KSPLIT launches n_split workgroups per tile (a.k_split, a.part set); otherwise n_split is 1
