@@ -96,11 +96,14 @@ def test_add(torch, ctx):
     assert np.array_equal(t.cpu().numpy(), x + y)
 
 
-@pytest.mark.parametrize("m,k,n", [(1500, 384, 1536), (300, 512, 512), (7, 64, 40), (200, 2048, 512)])
+@pytest.mark.parametrize("m,k,n", [(8257, 512, 512), (8200, 512, 2048), (1500, 384, 1536), (300, 512, 512),
+                                   (7, 64, 40), (200, 2048, 512)])
 def test_linear_epilogues_exact(torch, ctx, m, k, n):
     """GELU and ADD epilogues equal the plain GEMM followed by zwg_gelu_dev / zwg_add_dev bit for bit,
-    and the output stride writes into a wider buffer without touching the other columns; the last
-    two shapes split k, so the split sum's epilogue and stride are the ones checked."""
+    and the output stride writes into a wider buffer without touching the other columns.  The first
+    two shapes run the 64 x 256 and 128 x 256 tiles with a last row block cut short (the ADD
+    epilogue's residual loads go through a descriptor ending at the tile's last element); the last
+    two split k, so the split sum's epilogue and stride are the ones checked."""
     from zwhisper_amd import _lib
 
     rng = np.random.default_rng(m)
@@ -116,14 +119,18 @@ def test_linear_epilogues_exact(torch, ctx, m, k, n):
     ctx.linear_epi_dev(x, m, k, w, b, n, acc, _lib.EPI_ADD)
     wide = torch.full((m, 3 * n), 7.0, device="cuda")
     ctx.linear_epi_dev(x, m, k, w, b, n, wide.view(-1)[n:], _lib.EPI_NONE, out_stride=3 * n)
+    wide_a = torch.full((m, 3 * n), 7.0, device="cuda")
+    wide_a[:, n:2 * n] = base
+    ctx.linear_epi_dev(x, m, k, w, b, n, wide_a.view(-1)[n:], _lib.EPI_ADD, out_stride=3 * n)
     ref_g = plain.clone()
     ctx.gelu_dev(ref_g)
     ref_a = base.clone()
     ctx.add_dev(ref_a, plain)
     torch.cuda.synchronize()
     assert torch.equal(g, ref_g) and torch.equal(acc, ref_a)
-    assert torch.equal(wide[:, n:2 * n], plain)
-    assert bool((wide[:, :n] == 7.0).all()) and bool((wide[:, 2 * n:] == 7.0).all())
+    assert torch.equal(wide[:, n:2 * n], plain) and torch.equal(wide_a[:, n:2 * n], ref_a)
+    for t in (wide, wide_a):
+        assert bool((t[:, :n] == 7.0).all()) and bool((t[:, 2 * n:] == 7.0).all())
 
 
 @pytest.mark.parametrize("m,k,n", [(32, 768, 3072), (64, 1536, 256), (64, 8960, 1536), (300, 768, 768),
