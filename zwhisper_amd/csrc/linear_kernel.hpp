@@ -393,7 +393,15 @@ __device__ __forceinline__ void linear_mfma_body(const LinearArgs &a) {
                 const int row = m0 + wm * WM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
                 if (row >= a.m) continue;
                 if constexpr (KSPLIT) part[(int64_t)row * a.n + col] = acc[i][j][r];
-                else zwg_ew::epilogue_store(&a.out[(int64_t)row * a.ldo + col], acc[i][j][r] + bj, a.epi);
+                else if (a.epi == zwg_ew::kEpiAdd) // a residual spanning 2^31 bytes or more
+                    zwg_ew::epilogue_store(&a.out[(int64_t)row * a.ldo + col], acc[i][j][r] + bj, a.epi);
+                else {
+                    // written once and not read again here: a non-temporal store keeps the x rows
+                    // that the neighbouring column tiles re-read in L2
+                    const float v = acc[i][j][r] + bj;
+                    __builtin_nontemporal_store(a.epi == zwg_ew::kEpiGelu ? zwg_ew::gelu(v) : v,
+                                                &a.out[(int64_t)row * a.ldo + col]);
+                }
             }
     }
 }
